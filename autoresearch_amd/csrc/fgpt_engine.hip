@@ -1,0 +1,770 @@
+// fgpt_engine.hip -- the C ABI of include/fgpt.h: model upload, workspace,
+// RoPE tables, KV caches and the orchestration of the gfx950 kernels for
+// gpt_forward / gpt_step / gpt_step_multi (14NGiestas/autoresearch
+// src/lib/fortran_gpt.f90:54-199, src/lib/fortran_kv.f90:26-289).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <atomic>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/fgpt.h"
+#include "fgpt_internal.h"
+
+using namespace fgpt;
+
+// ------------------------------------------------------------------ errors
+static thread_local int32_t g_err_code = FG_OK;
+static thread_local char g_err_msg[512] = "";
+
+static int32_t seterr(int32_t code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err_msg, sizeof g_err_msg, fmt, ap);
+  va_end(ap);
+  g_err_code = code;
+  return code;
+}
+
+#define HIPCHK(x)                                                                   \
+  do {                                                                              \
+    hipError_t e_ = (x);                                                            \
+    if (e_ != hipSuccess) return seterr(FG_EHIP, "%s: %s", #x, hipGetErrorString(e_)); \
+  } while (0)
+
+#define RCCHK(x)                   \
+  do {                             \
+    int32_t r_ = (x);              \
+    if (r_ != FG_OK) return r_;    \
+  } while (0)
+
+extern "C" int32_t fg_version(void) { return 100; }
+
+extern "C" int32_t fg_last_error(char* buf, int32_t len) {
+  if (buf && len > 0) {
+    strncpy(buf, g_err_msg, (size_t)len - 1);
+    buf[len - 1] = '\0';
+  }
+  return g_err_code;
+}
+
+// ------------------------------------------------------------------ handles
+struct fg_model {
+  Dims d{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  Weights w;
+  float* d_cos = nullptr;
+  float* d_sin = nullptr;
+  int rope_cap = 0, rope_n = 0;
+  Work ws;
+  float* fk = nullptr;  // forward-pass K/V scratch [rows][KH*hd]
+  float* fv = nullptr;
+  int64_t work_bytes = 0;
+  int64_t gen = 0;      // bumped whenever a buffer a captured graph uses moves
+  std::atomic<int> busy{0};
+};
+
+struct fg_kv {
+  fg_model* m = nullptr;
+  int B = 0, maxT = 0, len = 0;
+  float* k = nullptr;  // [L][B][maxT][KH*hd]
+  float* v = nullptr;
+  int32_t* d_len = nullptr;  // device copy of len for replayed steps
+  int32_t* d_ids = nullptr;  // [B] ids fed to the next step
+  int32_t* d_out = nullptr;  // [cap_out] greedy ids
+  int64_t cap_out = 0;
+  float* d_lgs = nullptr;    // [cap_lgs] per-step logits of fg_decode_greedy
+  int64_t cap_lgs = 0;
+  // captured greedy loops keyed by (n_steps, with_logits), valid for gen
+  std::map<std::pair<int, int>, hipGraphExec_t> graphs;
+  int64_t graphs_gen = -1;
+};
+
+namespace {
+
+struct Guard {
+  std::atomic<int>* f;
+  bool ok;
+  explicit Guard(fg_model* m) : f(&m->busy) {
+    int z = 0;
+    ok = f->compare_exchange_strong(z, 1);
+  }
+  ~Guard() {
+    if (ok) f->store(0);
+  }
+};
+
+#define GUARD(m)                                                                  \
+  Guard guard_(m);                                                                \
+  if (!guard_.ok) return seterr(FG_EBUSY, "handle in use by another thread");     \
+  HIPCHK(hipSetDevice((m)->device))
+
+int32_t check_device(int* dev_out) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n < 1) return seterr(FG_ENODEV, "no HIP device visible");
+  int dev = 0;
+  HIPCHK(hipGetDevice(&dev));
+  hipDeviceProp_t p;
+  HIPCHK(hipGetDeviceProperties(&p, dev));
+  if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+    return seterr(FG_ENODEV, "device %d is %s, this build targets gfx950", dev, p.gcnArchName);
+  *dev_out = dev;
+  return FG_OK;
+}
+
+int32_t check_dims(const fg_dims* in, Dims* d) {
+  if (!in) return seterr(FG_EARG, "dims is NULL");
+  d->L = in->n_layer;
+  d->D = in->d_model;
+  d->H = in->n_head;
+  d->KH = in->n_kv_head;
+  d->hd = in->head_dim;
+  d->V = in->vocab_size;
+  d->dff = 4 * in->d_model;
+  d->eps = in->eps;
+  if (d->L < 1 || d->D < 1 || d->H < 1 || d->KH < 1 || d->V < 1)
+    return seterr(FG_EDIMS, "dims must be positive");
+  if (d->hd != 64 && d->hd != 128)
+    return seterr(FG_EDIMS, "head_dim %d unsupported (64 or 128)", d->hd);
+  if (d->H * d->hd != d->D)
+    return seterr(FG_EDIMS, "n_head*head_dim (%d) must equal d_model (%d)", d->H * d->hd, d->D);
+  if (d->H % d->KH != 0) return seterr(FG_EDIMS, "n_head %% n_kv_head != 0");
+  if (d->D % 64 != 0) return seterr(FG_EDIMS, "d_model %d not a multiple of 64", d->D);
+  if (d->V % 64 != 0) return seterr(FG_EDIMS, "vocab %d not a multiple of 64", d->V);
+  if (!(d->eps > 0.f)) return seterr(FG_EDIMS, "eps must be > 0");
+  return FG_OK;
+}
+
+// fp32 -> bf16 bits, refusing values that are not exactly representable.
+int32_t to_bf16_exact(const float* src, size_t n, bf16_t* dst, const char* name) {
+  for (size_t i = 0; i < n; ++i) {
+    uint32_t u;
+    memcpy(&u, &src[i], 4);
+    if ((u & 0xFFFFu) != 0)
+      return seterr(FG_EWEIGHT, "%s[%zu] = %.9g is not bf16-representable", name, i, src[i]);
+    dst[i] = (bf16_t)(u >> 16);
+  }
+  return FG_OK;
+}
+
+int32_t upload_weights(fg_model* m, const float* const st[8]) {
+  const Dims& d = m->d;
+  static const char* names[8] = {"wte", "c_q", "c_k", "c_v", "c_proj", "c_fc", "c_proj2", "lm_head"};
+  for (int i = 0; i < 8; ++i)
+    if (!st[i]) return seterr(FG_EARG, "weight buffer %s is NULL", names[i]);
+  const size_t D = d.D, qd = d.qd(), kd = d.kvd(), dff = d.dff, V = d.V;
+  Weights& w = m->w;
+  w.off_qkv = 0;
+  w.off_proj = (size_t)d.nqkv() * D;
+  w.off_fc = w.off_proj + D * qd;
+  w.off_proj2 = w.off_fc + dff * D;
+  w.layer_stride = w.off_proj2 + D * dff;
+  const size_t n_total = w.layer_stride * d.L + 2 * V * D;
+  std::vector<bf16_t> h(n_total);
+  for (int l = 0; l < d.L; ++l) {
+    bf16_t* dst = h.data() + (size_t)l * w.layer_stride;
+    // fused, pair-interleaved QKV rows
+    const float* srcs[3] = {st[1] + (size_t)l * qd * D, st[2] + (size_t)l * kd * D,
+                            st[3] + (size_t)l * kd * D};
+    const int heads[3] = {d.H, d.KH, d.KH};
+    size_t row = 0;
+    for (int part = 0; part < 3; ++part) {
+      for (int hh = 0; hh < heads[part]; ++hh) {
+        for (int s = 0; s < d.hd; ++s) {
+          const float* src = srcs[part] + ((size_t)hh * d.hd + pair_dim(s, d.hd)) * D;
+          RCCHK(to_bf16_exact(src, D, dst + row * D, names[1 + part]));
+          ++row;
+        }
+      }
+    }
+    RCCHK(to_bf16_exact(st[4] + (size_t)l * D * qd, D * qd, dst + w.off_proj, "c_proj"));
+    RCCHK(to_bf16_exact(st[5] + (size_t)l * dff * D, dff * D, dst + w.off_fc, "c_fc"));
+    RCCHK(to_bf16_exact(st[6] + (size_t)l * D * dff, D * dff, dst + w.off_proj2, "c_proj2"));
+  }
+  bf16_t* tail = h.data() + w.layer_stride * d.L;
+  RCCHK(to_bf16_exact(st[7], V * D, tail, "lm_head"));
+  RCCHK(to_bf16_exact(st[0], V * D, tail + V * D, "wte"));
+  w.bytes = n_total * sizeof(bf16_t);
+  HIPCHK(hipMalloc((void**)&w.base, w.bytes));
+  HIPCHK(hipMemcpy(w.base, h.data(), w.bytes, hipMemcpyHostToDevice));
+  w.lm = w.base + w.layer_stride * d.L;
+  w.wte = w.lm + V * D;
+  return FG_OK;
+}
+
+void free_work(fg_model* m) {
+  Work& ws = m->ws;
+  void* ptrs[] = {ws.x, ws.q, ws.ao, ws.h, ws.logits, ws.ids, ws.tgt, ws.nll, ws.stat, ws.amax,
+                  m->fk, m->fv};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  ws = Work();
+  m->fk = m->fv = nullptr;
+  m->work_bytes = 0;
+}
+
+int32_t ensure_work(fg_model* m, int64_t rows) {
+  if (rows <= m->ws.rows) return FG_OK;
+  HIPCHK(hipStreamSynchronize(m->stream));
+  free_work(m);
+  const Dims& d = m->d;
+  Work& ws = m->ws;
+  int64_t total = 0;
+  auto alloc = [&](void** p, int64_t bytes) -> int32_t {
+    total += bytes;
+    HIPCHK(hipMalloc(p, (size_t)bytes));
+    return FG_OK;
+  };
+  RCCHK(alloc((void**)&ws.x, rows * d.D * 4));
+  RCCHK(alloc((void**)&ws.q, rows * d.qd() * 4));
+  RCCHK(alloc((void**)&ws.ao, rows * d.qd() * 4));
+  RCCHK(alloc((void**)&ws.h, rows * d.dff * 4));
+  RCCHK(alloc((void**)&ws.logits, rows * d.V * 4));
+  RCCHK(alloc((void**)&ws.ids, rows * 4));
+  RCCHK(alloc((void**)&ws.tgt, rows * 4));
+  RCCHK(alloc((void**)&ws.nll, rows * 4));
+  RCCHK(alloc((void**)&ws.stat, rows * 4));
+  RCCHK(alloc((void**)&ws.amax, rows * 4));
+  RCCHK(alloc((void**)&m->fk, rows * d.kvd() * 4));
+  RCCHK(alloc((void**)&m->fv, rows * d.kvd() * 4));
+  ws.rows = rows;
+  m->work_bytes = total;
+  m->gen++;
+  return FG_OK;
+}
+
+// y = epi(x W^T): GEMV for up to four token rows, MFMA GEMM beyond.
+void linear(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
+  if (a.M <= 4 && (int64_t)a.M * a.K * 4 <= 65536)
+    launch_gemv_pos(s, epi, a, d_pos);
+  else
+    launch_gemm_pos(s, epi, a, d_pos);
+}
+
+GemvArgs base_args(fg_model* m) {
+  GemvArgs a;
+  memset(&a, 0, sizeof a);
+  a.eps = m->d.eps;
+  a.cosb = m->d_cos;
+  a.sinb = m->d_sin;
+  a.H = m->d.H;
+  a.KH = m->d.KH;
+  a.hd = m->d.hd;
+  return a;
+}
+
+// One pass of the layer stack over rows = B*T token rows whose residual is
+// already in ws.x. Positions: pos0 (+ *d_pos if given) + row % T. K/V go to
+// kc/vc with [L][B][maxT][KH*hd] layout (layer stride lstride floats).
+// Attention: single-query kernel when T == 1 (attn_step), else the causal
+// chunk kernel (causal_attn / attn_chunk).
+void layer_stack(fg_model* m, hipStream_t s, int B, int T, int pos0, const int32_t* d_pos,
+                 float* kc, float* vc, int maxT, int64_t lstride, float* logits) {
+  const Dims& d = m->d;
+  Work& ws = m->ws;
+  const int rows = B * T;
+  for (int l = 0; l < d.L; ++l) {
+    float* lk = kc + l * lstride;
+    float* lv = vc + l * lstride;
+    GemvArgs a = base_args(m);
+    a.M = rows;
+    a.T = T;
+    a.pos0 = pos0;
+    a.kc = lk;
+    a.vc = lv;
+    a.maxT = maxT;
+    // q, k, v = rmsnorm(x) Wqkv^T, RoPE on q and k, k/v appended to the cache
+    a.x = ws.x; a.w = m->w.qkv(l); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
+    linear(s, GV_QKV, a, d_pos);
+    if (T == 1)
+      launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, ws.ao);
+    else
+      launch_attn_prefill(s, d, ws.q, lk, lv, B, T, maxT, pos0, ws.ao);
+    // x += attn_out Wproj^T
+    a.x = ws.ao; a.w = m->w.proj(l); a.N = d.D; a.K = d.qd(); a.norm = 0; a.y = ws.x;
+    linear(s, GV_RESID, a, d_pos);
+    // h = relu(rmsnorm(x) Wfc^T)^2
+    a.x = ws.x; a.w = m->w.fc(l); a.N = d.dff; a.K = d.D; a.norm = 1; a.y = ws.h;
+    linear(s, GV_RELU2, a, d_pos);
+    // x += h Wproj2^T
+    a.x = ws.h; a.w = m->w.proj2(l); a.N = d.D; a.K = d.dff; a.norm = 0; a.y = ws.x;
+    linear(s, GV_RESID, a, d_pos);
+  }
+  GemvArgs a = base_args(m);
+  a.M = rows; a.T = T; a.x = ws.x; a.w = m->w.lm; a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
+  linear(s, GV_STORE, a, d_pos);
+}
+
+int32_t check_rope(fg_model* m, int64_t upto) {
+  if (upto > m->rope_n)
+    return seterr(FG_EROPE, "RoPE rows set for positions < %d; position %lld needed",
+                  m->rope_n, (long long)upto - 1);
+  return FG_OK;
+}
+
+int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_logits,
+                     const int32_t* d_tgt, float* d_nll, hipStream_t s) {
+  if (B < 1 || T < 1) return seterr(FG_EARG, "B and T must be >= 1");
+  RCCHK(check_rope(m, T));
+  const int64_t rows = (int64_t)B * T;
+  if (rows > (1ll << 30) / m->d.V) return seterr(FG_EARG, "B*T too large");
+  RCCHK(ensure_work(m, rows));
+  float* logits = d_logits ? d_logits : m->ws.logits;
+  launch_embed_norm(s, m->d, m->w.wte, d_ids, rows, m->ws.x);
+  layer_stack(m, s, B, T, 0, nullptr, m->fk, m->fv, T, 0, logits);
+  if (d_tgt && d_nll) launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll);
+  HIPCHK(hipGetLastError());
+  return FG_OK;
+}
+
+int32_t model_new(const fg_dims* dims, fg_model** out, fg_model** pm) {
+  if (!out) return seterr(FG_EARG, "out is NULL");
+  *out = nullptr;
+  Dims d;
+  RCCHK(check_dims(dims, &d));
+  int dev = 0;
+  RCCHK(check_device(&dev));
+  fg_model* m = new fg_model();
+  m->d = d;
+  m->device = dev;
+  hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete m;
+    return seterr(FG_EHIP, "hipStreamCreate: %s", hipGetErrorString(e));
+  }
+  *pm = m;
+  return FG_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ model
+extern "C" int32_t fg_model_create(const fg_dims* dims, const float* wte, const float* c_q,
+                                   const float* c_k, const float* c_v, const float* c_proj,
+                                   const float* c_fc, const float* c_proj2,
+                                   const float* lm_head, fg_model** out) {
+  fg_model* m = nullptr;
+  RCCHK(model_new(dims, out, &m));
+  const float* st[8] = {wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head};
+  int32_t rc = upload_weights(m, st);
+  if (rc != FG_OK) {
+    fg_model_destroy(m);
+    return rc;
+  }
+  *out = m;
+  return FG_OK;
+}
+
+namespace {
+
+// Minimal .npy reader: version 1/2/3 header, dtype '<f4', C order, 1-D.
+int32_t read_npy_f32(const std::string& path, size_t want, float* dst) {
+  FILE* f = fopen(path.c_str(), "rb");
+  if (!f) return seterr(FG_EWEIGHT, "load failed (missing file): %s", path.c_str());
+  unsigned char mg[8];
+  int32_t rc = FG_OK;
+  std::string hdr;
+  uint32_t hlen = 0;
+  if (fread(mg, 1, 8, f) != 8 || memcmp(mg, "\x93NUMPY", 6) != 0) {
+    rc = seterr(FG_EWEIGHT, "not a .npy file (missing or empty): %s", path.c_str());
+  } else {
+    if (mg[6] == 1) {
+      unsigned char b[2];
+      if (fread(b, 1, 2, f) != 2) rc = seterr(FG_EWEIGHT, "truncated header: %s", path.c_str());
+      hlen = b[0] | (b[1] << 8);
+    } else {
+      unsigned char b[4];
+      if (fread(b, 1, 4, f) != 4) rc = seterr(FG_EWEIGHT, "truncated header: %s", path.c_str());
+      hlen = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
+    }
+    if (rc == FG_OK) {
+      hdr.resize(hlen);
+      if (hlen > 65536 || fread(&hdr[0], 1, hlen, f) != hlen)
+        rc = seterr(FG_EWEIGHT, "truncated header: %s", path.c_str());
+    }
+  }
+  if (rc == FG_OK) {
+    auto has = [&](const char* s) { return hdr.find(s) != std::string::npos; };
+    if (!has("'descr': '<f4'"))
+      rc = seterr(FG_EWEIGHT, "%s: dtype is not '<f4'", path.c_str());
+    else if (!has("'fortran_order': False"))
+      rc = seterr(FG_EWEIGHT, "%s: fortran_order arrays are not supported", path.c_str());
+    else {
+      size_t p = hdr.find("'shape': (");
+      unsigned long long n = 0;
+      char tail = 0;
+      if (p == std::string::npos ||
+          sscanf(hdr.c_str() + p + 10, "%llu%c", &n, &tail) != 2 || tail != ',')
+        rc = seterr(FG_EWEIGHT, "%s: shape is not 1-D", path.c_str());
+      else if (hdr.find(')', p) < hdr.find(',', p) || hdr.find(',', hdr.find(',', p) + 1) < hdr.find(')', p))
+        rc = seterr(FG_EWEIGHT, "%s: shape is not 1-D", path.c_str());
+      else if (n != want)
+        rc = seterr(FG_EWEIGHT, "%s: %llu values, expected %zu", path.c_str(), n, want);
+      else if (fread(dst, 4, want, f) != want)
+        rc = seterr(FG_EWEIGHT, "%s: truncated payload", path.c_str());
+    }
+  }
+  fclose(f);
+  return rc;
+}
+
+int32_t check_arch_txt(const std::string& dir, const Dims& d) {
+  FILE* f = fopen((dir + "/arch.txt").c_str(), "r");
+  if (!f) return FG_OK;  // absent = accepted, as read_arch_txt does
+  char line[256];
+  int32_t rc = FG_OK;
+  while (fgets(line, sizeof line, f)) {
+    if (line[0] == '#') continue;
+    char key[64];
+    long val;
+    if (sscanf(line, " %63[a-z_] = %ld", key, &val) != 2) continue;
+    long want = -1;
+    if (!strcmp(key, "d_model")) want = d.D;
+    else if (!strcmp(key, "n_head")) want = d.H;
+    else if (!strcmp(key, "n_kv")) want = d.KH;
+    else if (!strcmp(key, "n_layer")) want = d.L;
+    else if (!strcmp(key, "vocab")) want = d.V;
+    else if (!strcmp(key, "head_dim")) want = d.hd;
+    if (want >= 0 && want != val) {
+      rc = seterr(FG_EARCH, "arch.txt %s = %ld but the dims say %ld", key, val, want);
+      break;
+    }
+  }
+  fclose(f);
+  return rc;
+}
+
+}  // namespace
+
+extern "C" int32_t fg_model_load(const fg_dims* dims, const char* weights_dir, fg_model** out) {
+  if (!weights_dir) return seterr(FG_EARG, "weights_dir is NULL");
+  Dims d;
+  RCCHK(check_dims(dims, &d));
+  const std::string dir(weights_dir);
+  RCCHK(check_arch_txt(dir, d));
+  const size_t D = d.D, qd = d.qd(), kd = d.kvd(), dff = d.dff, V = d.V, L = d.L;
+  std::vector<float> wte(V * D), lm(V * D), cq(L * qd * D), ck(L * kd * D), cv(L * kd * D),
+      cp(L * D * qd), cf(L * dff * D), cp2(L * D * dff);
+  RCCHK(read_npy_f32(dir + "/transformer_wte_weight.npy", V * D, wte.data()));
+  RCCHK(read_npy_f32(dir + "/lm_head_weight.npy", V * D, lm.data()));
+  for (size_t l = 0; l < L; ++l) {
+    const std::string p = dir + "/transformer_h_" + std::to_string(l) + "_";
+    RCCHK(read_npy_f32(p + "attn_c_q_weight.npy", qd * D, cq.data() + l * qd * D));
+    RCCHK(read_npy_f32(p + "attn_c_k_weight.npy", kd * D, ck.data() + l * kd * D));
+    RCCHK(read_npy_f32(p + "attn_c_v_weight.npy", kd * D, cv.data() + l * kd * D));
+    RCCHK(read_npy_f32(p + "attn_c_proj_weight.npy", D * qd, cp.data() + l * D * qd));
+    RCCHK(read_npy_f32(p + "mlp_c_fc_weight.npy", dff * D, cf.data() + l * dff * D));
+    RCCHK(read_npy_f32(p + "mlp_c_proj_weight.npy", D * dff, cp2.data() + l * D * dff));
+  }
+  return fg_model_create(dims, wte.data(), cq.data(), ck.data(), cv.data(), cp.data(), cf.data(),
+                         cp2.data(), lm.data(), out);
+}
+
+extern "C" int32_t fg_model_destroy(fg_model* m) {
+  if (!m) return FG_OK;
+  (void)hipSetDevice(m->device);
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  free_work(m);
+  if (m->w.base) (void)hipFree(m->w.base);
+  if (m->d_cos) (void)hipFree(m->d_cos);
+  if (m->d_sin) (void)hipFree(m->d_sin);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_set_rope(fg_model* m, int32_t pos0, int32_t n_pos, const float* cos_buf,
+                               const float* sin_buf) {
+  if (!m || !cos_buf || !sin_buf) return seterr(FG_EARG, "NULL argument");
+  if (pos0 < 0 || n_pos < 1) return seterr(FG_EARG, "bad row range");
+  if (pos0 > m->rope_n)
+    return seterr(FG_EROPE, "RoPE rows must be set contiguously from 0 (have %d, asked %d)",
+                  m->rope_n, pos0);
+  GUARD(m);
+  const int half = m->d.hd / 2;
+  const int need = pos0 + n_pos;
+  if (need > m->rope_cap) {
+    int cap = m->rope_cap ? m->rope_cap : 64;
+    while (cap < need) cap *= 2;
+    float *nc = nullptr, *ns = nullptr;
+    HIPCHK(hipMalloc((void**)&nc, (size_t)cap * half * 4));
+    HIPCHK(hipMalloc((void**)&ns, (size_t)cap * half * 4));
+    HIPCHK(hipStreamSynchronize(m->stream));
+    if (m->rope_n > 0) {
+      HIPCHK(hipMemcpy(nc, m->d_cos, (size_t)m->rope_n * half * 4, hipMemcpyDeviceToDevice));
+      HIPCHK(hipMemcpy(ns, m->d_sin, (size_t)m->rope_n * half * 4, hipMemcpyDeviceToDevice));
+    }
+    if (m->d_cos) HIPCHK(hipFree(m->d_cos));
+    if (m->d_sin) HIPCHK(hipFree(m->d_sin));
+    m->d_cos = nc;
+    m->d_sin = ns;
+    m->rope_cap = cap;
+    m->gen++;
+  }
+  HIPCHK(hipStreamSynchronize(m->stream));
+  HIPCHK(hipMemcpy(m->d_cos + (size_t)pos0 * half, cos_buf, (size_t)n_pos * half * 4,
+                   hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(m->d_sin + (size_t)pos0 * half, sin_buf, (size_t)n_pos * half * 4,
+                   hipMemcpyHostToDevice));
+  if (need > m->rope_n) m->rope_n = need;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_forward(fg_model* m, const int32_t* ids, int32_t B, int32_t T,
+                              float* logits, const int32_t* targets, float* nll) {
+  if (!m || !ids) return seterr(FG_EARG, "NULL argument");
+  if (B < 1 || T < 1) return seterr(FG_EARG, "B and T must be >= 1");
+  const int64_t rows = (int64_t)B * T;
+  for (int64_t i = 0; i < rows; ++i)
+    if (ids[i] < 0 || ids[i] >= m->d.V)
+      return seterr(FG_EARG, "id %d at %lld outside [0, %d)", ids[i], (long long)i, m->d.V);
+  if (targets)
+    for (int64_t i = 0; i < rows; ++i)
+      if (targets[i] < 0 || targets[i] >= m->d.V)
+        return seterr(FG_EARG, "target %d at %lld outside [0, %d)", targets[i], (long long)i,
+                      m->d.V);
+  GUARD(m);
+  RCCHK(ensure_work(m, rows));
+  hipStream_t s = m->stream;
+  HIPCHK(hipMemcpyAsync(m->ws.ids, ids, rows * 4, hipMemcpyHostToDevice, s));
+  if (targets) HIPCHK(hipMemcpyAsync(m->ws.tgt, targets, rows * 4, hipMemcpyHostToDevice, s));
+  RCCHK(forward_core(m, m->ws.ids, B, T, m->ws.logits, targets ? m->ws.tgt : nullptr,
+                     targets ? m->ws.nll : nullptr, s));
+  if (logits)
+    HIPCHK(hipMemcpyAsync(logits, m->ws.logits, rows * m->d.V * 4, hipMemcpyDeviceToHost, s));
+  if (targets && nll) HIPCHK(hipMemcpyAsync(nll, m->ws.nll, rows * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return FG_OK;
+}
+
+extern "C" int32_t fg_forward_dev(fg_model* m, const int32_t* d_ids, int32_t B, int32_t T,
+                                  float* d_logits, const int32_t* d_targets, float* d_nll,
+                                  void* stream) {
+  if (!m || !d_ids) return seterr(FG_EARG, "NULL argument");
+  GUARD(m);
+  hipStream_t s = stream ? (hipStream_t)stream : m->stream;
+  return forward_core(m, d_ids, B, T, d_logits, d_targets, d_nll, s);
+}
+
+// ------------------------------------------------------------------ KV
+extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** out) {
+  if (!m || !out) return seterr(FG_EARG, "NULL argument");
+  *out = nullptr;
+  if (B < 1 || maxT < 1) return seterr(FG_EARG, "B and maxT must be >= 1");
+  // the decode attention keeps one score per cached position in LDS
+  if (maxT > 16000) return seterr(FG_EARG, "maxT %d above the 16000 this build supports", maxT);
+  GUARD(m);
+  fg_kv* kv = new fg_kv();
+  kv->m = m;
+  kv->B = B;
+  kv->maxT = maxT;
+  const size_t n = (size_t)m->d.L * B * maxT * m->d.kvd();
+  hipError_t e = hipMalloc((void**)&kv->k, n * 4);
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->v, n * 4);
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_len, 4);
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_ids, (size_t)B * 4);
+  if (e == hipSuccess) e = hipMemset(kv->k, 0, n * 4);  // the caller zeroes it in the reference
+  if (e == hipSuccess) e = hipMemset(kv->v, 0, n * 4);
+  if (e != hipSuccess) {
+    if (kv->k) (void)hipFree(kv->k);
+    if (kv->v) (void)hipFree(kv->v);
+    if (kv->d_len) (void)hipFree(kv->d_len);
+    if (kv->d_ids) (void)hipFree(kv->d_ids);
+    delete kv;
+    return seterr(FG_EHIP, "KV cache allocation (%zu bytes): %s", 2 * n * 4, hipGetErrorString(e));
+  }
+  *out = kv;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_kv_destroy(fg_kv* kv) {
+  if (!kv) return FG_OK;
+  (void)hipSetDevice(kv->m->device);
+  (void)hipStreamSynchronize(kv->m->stream);
+  for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
+  void* ptrs[] = {kv->k, kv->v, kv->d_len, kv->d_ids, kv->d_out, kv->d_lgs};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  delete kv;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_kv_len(const fg_kv* kv, int32_t* len) {
+  if (!kv || !len) return seterr(FG_EARG, "NULL argument");
+  *len = kv->len;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_kv_set_len(fg_kv* kv, int32_t len) {
+  if (!kv) return seterr(FG_EARG, "NULL argument");
+  if (len < 0 || len > kv->maxT) return seterr(FG_EARG, "len %d outside [0, %d]", len, kv->maxT);
+  kv->len = len;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_kv_read(fg_kv* kv, float* k_out, float* v_out) {
+  if (!kv) return seterr(FG_EARG, "NULL argument");
+  fg_model* m = kv->m;
+  GUARD(m);
+  const size_t n = (size_t)m->d.L * kv->B * kv->maxT * m->d.kvd();
+  HIPCHK(hipStreamSynchronize(m->stream));
+  if (k_out) HIPCHK(hipMemcpy(k_out, kv->k, n * 4, hipMemcpyDeviceToHost));
+  if (v_out) HIPCHK(hipMemcpy(v_out, kv->v, n * 4, hipMemcpyDeviceToHost));
+  return FG_OK;
+}
+
+namespace {
+
+int32_t check_ids(const fg_model* m, const int32_t* ids, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    if (ids[i] < 0 || ids[i] >= m->d.V)
+      return seterr(FG_EARG, "id %d at %lld outside [0, %d)", ids[i], (long long)i, m->d.V);
+  return FG_OK;
+}
+
+// TB tokens for each of the kv's B sequences at host position kv->len.
+int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* logits,
+                int32_t* next_ids) {
+  const int B = kv->B;
+  if (TB < 1) return seterr(FG_EARG, "TB must be >= 1");
+  if (kv->len + TB > kv->maxT)
+    return seterr(FG_EFULL, "cache full (raise maxT): len %d + %d > %d", kv->len, TB, kv->maxT);
+  RCCHK(check_rope(m, kv->len + TB));
+  const int64_t rows = (int64_t)B * TB;
+  RCCHK(ensure_work(m, rows));
+  hipStream_t s = m->stream;
+  HIPCHK(hipMemcpyAsync(m->ws.ids, h_ids, rows * 4, hipMemcpyHostToDevice, s));
+  launch_embed_norm(s, m->d, m->w.wte, m->ws.ids, rows, m->ws.x);
+  const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
+  layer_stack(m, s, B, TB, kv->len, nullptr, kv->k, kv->v, kv->maxT, lstride, m->ws.logits);
+  HIPCHK(hipGetLastError());
+  if (next_ids && TB == 1) {
+    launch_argmax(s, m->ws.logits, B, m->d.V, m->ws.amax);
+    HIPCHK(hipMemcpyAsync(next_ids, m->ws.amax, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+  } else if (next_ids) {
+    // argmax of each sequence's last row: rows b*TB + TB-1
+    for (int b = 0; b < B; ++b)
+      launch_argmax(s, m->ws.logits + ((int64_t)b * TB + TB - 1) * m->d.V, 1, m->d.V,
+                    m->ws.amax + b);
+    HIPCHK(hipMemcpyAsync(next_ids, m->ws.amax, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+  }
+  if (logits)
+    HIPCHK(hipMemcpyAsync(logits, m->ws.logits, rows * m->d.V * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  kv->len += TB;
+  return FG_OK;
+}
+
+// One greedy step whose position is read from kv->d_len on the device:
+// embed(d_ids) -> layers -> lm_head -> argmax into d_ids and out, len += 1.
+void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, float* logits, int32_t* out) {
+  const int B = kv->B;
+  launch_embed_norm(s, m->d, m->w.wte, kv->d_ids, B, m->ws.x);
+  const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
+  layer_stack(m, s, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, logits);
+  launch_argmax_step(s, logits, B, m->d.V, kv->d_ids, out, kv->d_len);
+}
+
+}  // namespace
+
+extern "C" int32_t fg_step(fg_model* m, fg_kv* kv, const int32_t* ids, float* logits,
+                           int32_t* next_ids) {
+  if (!m || !kv || !ids || kv->m != m) return seterr(FG_EARG, "bad argument");
+  RCCHK(check_ids(m, ids, kv->B));
+  GUARD(m);
+  return kv_pass(m, kv, ids, 1, logits, next_ids);
+}
+
+extern "C" int32_t fg_step_multi(fg_model* m, fg_kv* kv, const int32_t* ids, int32_t TB,
+                                 float* logits, int32_t* next_ids) {
+  if (!m || !kv || !ids || kv->m != m) return seterr(FG_EARG, "bad argument");
+  if (TB < 1) return seterr(FG_EARG, "TB must be >= 1");
+  RCCHK(check_ids(m, ids, (int64_t)kv->B * TB));
+  GUARD(m);
+  return kv_pass(m, kv, ids, TB, logits, next_ids);
+}
+
+extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, int32_t n_steps,
+                                    int32_t* ids_out, float* logits_out) {
+  if (!m || !kv || !ids || !ids_out || kv->m != m) return seterr(FG_EARG, "bad argument");
+  if (n_steps < 1) return seterr(FG_EARG, "n_steps must be >= 1");
+  RCCHK(check_ids(m, ids, kv->B));
+  GUARD(m);
+  const int B = kv->B;
+  if (kv->len + n_steps > kv->maxT)
+    return seterr(FG_EFULL, "cache full (raise maxT): len %d + %d > %d", kv->len, n_steps,
+                  kv->maxT);
+  RCCHK(check_rope(m, kv->len + n_steps));
+  RCCHK(ensure_work(m, B));
+  hipStream_t s = m->stream;
+  const int64_t nout = (int64_t)n_steps * B;
+  if (nout > kv->cap_out) {
+    if (kv->d_out) HIPCHK(hipFree(kv->d_out));
+    HIPCHK(hipMalloc((void**)&kv->d_out, nout * 4));
+    kv->cap_out = nout;
+    for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
+    kv->graphs.clear();
+  }
+  const int with_logits = logits_out ? 1 : 0;
+  const int64_t nlg = with_logits ? nout * m->d.V : (int64_t)B * m->d.V;
+  if (nlg > kv->cap_lgs) {
+    if (kv->d_lgs) HIPCHK(hipFree(kv->d_lgs));
+    HIPCHK(hipMalloc((void**)&kv->d_lgs, nlg * 4));
+    kv->cap_lgs = nlg;
+    for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
+    kv->graphs.clear();
+  }
+  if (kv->graphs_gen != m->gen) {
+    for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
+    kv->graphs.clear();
+    kv->graphs_gen = m->gen;
+  }
+  const int32_t len0 = kv->len;
+  HIPCHK(hipMemcpyAsync(kv->d_ids, ids, (size_t)B * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(kv->d_len, &len0, 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipStreamSynchronize(s));
+  // The whole n-step loop is one captured graph (positions come from d_len),
+  // replayed on later calls with the same step count.
+  const auto key = std::make_pair((int)n_steps, with_logits);
+  auto it = kv->graphs.find(key);
+  if (it == kv->graphs.end()) {
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    for (int st = 0; st < n_steps; ++st) {
+      float* lg = kv->d_lgs + (with_logits ? (int64_t)st * B * m->d.V : 0);
+      greedy_step_launches(m, kv, s, lg, kv->d_out + (int64_t)st * B);
+    }
+    HIPCHK(hipStreamEndCapture(s, &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return seterr(FG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    it = kv->graphs.emplace(key, ge).first;
+  }
+  HIPCHK(hipGraphLaunch(it->second, s));
+  HIPCHK(hipMemcpyAsync(ids_out, kv->d_out, nout * 4, hipMemcpyDeviceToHost, s));
+  if (logits_out)
+    HIPCHK(hipMemcpyAsync(logits_out, kv->d_lgs, nout * m->d.V * 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  kv->len += n_steps;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_sync(fg_model* m) {
+  if (!m) return seterr(FG_EARG, "NULL argument");
+  GUARD(m);
+  HIPCHK(hipStreamSynchronize(m->stream));
+  return FG_OK;
+}
+
+extern "C" int32_t fg_model_bytes(const fg_model* m, int64_t* weight_bytes, int64_t* work_bytes) {
+  if (!m) return seterr(FG_EARG, "NULL argument");
+  if (weight_bytes) *weight_bytes = (int64_t)m->w.bytes;
+  if (work_bytes) *work_bytes = m->work_bytes;
+  return FG_OK;
+}

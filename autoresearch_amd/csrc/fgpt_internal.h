@@ -1,0 +1,128 @@
+// fgpt_internal.h -- engine-internal types and kernel launchers (not part of
+// the C ABI). Everything here is gfx950-only HIP.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace fgpt {
+
+typedef uint16_t bf16_t;  // raw bf16 bits in HBM
+
+struct Dims {
+  int L, D, H, KH, hd, V, dff;
+  float eps;
+  int qd() const { return H * hd; }
+  int kvd() const { return KH * hd; }
+  int nqkv() const { return (H + 2 * KH) * hd; }
+};
+
+// Weight arena in HBM (bf16), one allocation:
+//   per layer l: Wqkv[(H+2KH)*hd][D]  rows permuted, see qkv_row_of()
+//                Wproj[D][H*hd], Wfc[4D][D], Wproj2[D][4D]
+//   then lm_head[V][D], wte[V][D]
+struct Weights {
+  bf16_t* base = nullptr;
+  size_t bytes = 0;
+  size_t layer_stride = 0;  // elements
+  size_t off_qkv = 0, off_proj = 0, off_fc = 0, off_proj2 = 0;  // within a layer
+  bf16_t* lm = nullptr;
+  bf16_t* wte = nullptr;
+  const bf16_t* qkv(int l) const { return base + l * layer_stride + off_qkv; }
+  const bf16_t* proj(int l) const { return base + l * layer_stride + off_proj; }
+  const bf16_t* fc(int l) const { return base + l * layer_stride + off_fc; }
+  const bf16_t* proj2(int l) const { return base + l * layer_stride + off_proj2; }
+};
+
+// Row order of the fused QKV matrix. Within every q or k head the rows are
+// interleaved in rotation pairs (d, d+hd/2) so one GEMV unit or one pair of
+// adjacent GEMM columns holds both halves RoPE mixes. Stored row s of a
+// head maps to head dimension: s even -> s/2, s odd -> hd/2 + s/2.
+__host__ __device__ inline int pair_dim(int s, int hd) {
+  return (s & 1) ? (hd / 2 + (s >> 1)) : (s >> 1);
+}
+
+// Activation workspace for up to `rows` token rows.
+struct Work {
+  int64_t rows = 0;
+  float* x = nullptr;       // residual stream [rows][D]
+  float* q = nullptr;       // rotated queries [rows][H*hd]
+  float* ao = nullptr;      // attention output [rows][H*hd]
+  float* h = nullptr;       // relu2(fc) [rows][4D]
+  float* logits = nullptr;  // [rows][V]
+  int32_t* ids = nullptr;   // [rows]
+  int32_t* tgt = nullptr;   // [rows]
+  float* nll = nullptr;     // [rows]
+  float* stat = nullptr;    // [rows] per-row scratch (argmax values etc.)
+  int32_t* amax = nullptr;  // [rows]
+};
+
+struct KVCacheDev {
+  int B = 0, maxT = 0;
+  float* k = nullptr;  // [L][B][maxT][KH*hd]
+  float* v = nullptr;
+};
+
+// ------------------------------------------------------------ launchers
+// All launches go to `s`; shapes are validated by the caller (engine).
+
+// x[r] = rmsnorm(wte[ids[r]])
+void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
+                       int64_t rows, float* x);
+
+// GEMV family for M <= 4 token rows, fp32 activations x bf16 weights.
+enum GemvEpi { GV_QKV = 0, GV_RESID = 1, GV_RELU2 = 2, GV_STORE = 3 };
+struct GemvArgs {
+  const float* x;   // [M][K] input rows
+  const bf16_t* w;  // [N][K]
+  int M, N, K;
+  int norm;         // apply rmsnorm(x) (scale by inv-rms of each x row)
+  float eps;
+  float* y;         // output [M][N] (RESID: y += ..., in place)
+  // QKV epilogue
+  const float* cosb;
+  const float* sinb;
+  int pos0;         // position of row 0 (row m is at pos0 + m % T)
+  int T;            // rows per sequence
+  float* kc;        // KV cache of this layer, [B][maxT][KH*hd]
+  float* vc;
+  int maxT;
+  int H, KH, hd;
+};
+void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
+
+// MFMA GEMM, C[M][N] = epi(rowscale * (A[M][K] . W[N][K]^T)), A fp32 split
+// into bf16 hi+lo on the fly, W bf16, fp32 accumulation.
+void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a);
+
+// Single-query attention over the cache: q [B][H][hd] at position len-1
+// (cache holds len positions) -> y [B][H*hd].
+void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const float* kc,
+                        const float* vc, int B, int maxT, int len, float* y, float* scratch,
+                        int64_t scratch_floats);
+
+// Causal chunk attention: q [B][T][H][hd] at positions pos0..pos0+T-1
+// against the cache positions 0..pos0+t -> y [B][T][H*hd].
+void launch_attn_prefill(hipStream_t s, const Dims& d, const float* q, const float* kc,
+                         const float* vc, int B, int T, int maxT, int pos0, float* y);
+
+// Variants whose position / cache length comes from device memory (so a
+// captured decode step replays at successive positions).
+void launch_gemv_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
+void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
+// d_len holds the cache length before the step; the query is at *d_len.
+void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
+                            const float* vc, int B, int maxT, const int32_t* d_len, int len,
+                            float* y);
+// argmax into out (and out2 if set); when d_len is set, row 0 increments it.
+void launch_argmax_step(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out,
+                        int32_t* out2, int32_t* d_len);
+
+// Per-row argmax (first max) of logits [rows][V] -> out [rows].
+void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out);
+// Per-row nll = logsumexp - logit[tgt].
+void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
+                float* out);
+
+}  // namespace fgpt

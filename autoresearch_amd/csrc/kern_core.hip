@@ -1,0 +1,499 @@
+// kern_core.hip -- embedding, small-M GEMV, decode attention, chunk
+// attention, argmax and NLL kernels for gfx950 (64-wide wavefronts).
+//
+// Reference semantics (14NGiestas/autoresearch):
+//   embedding + first norm  src/lib/fortran_gpt.f90:136-142, fortran_linear.f90:62-78
+//   rmsnorm0                src/lib/fortran_rmsnorm.f90:40-60
+//   y = x W^T               src/lib/fortran_blas.f90:39-57
+//   rope_4d (half split)    src/lib/fortran_rope.f90:25-52
+//   cache append            src/lib/fortran_kv.f90:112-116,292-300
+//   attn_step / attn_chunk  src/lib/fortran_attn.f90:317-425
+//   relu2                   src/lib/fortran_attn.f90:697-710
+//   greedy argmax           src/lib/sample.f90:271-277
+//   per-position NLL        src/app/eval_bpb.f90:165-181
+#include <float.h>
+
+#include "fgpt_internal.h"
+#include "kern_common.h"
+
+namespace fgpt {
+
+// ------------------------------------------------------------ block reduce
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += red[i];
+  return t;
+}
+
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) t = fmaxf(t, red[i]);
+  return t;
+}
+
+// ------------------------------------------------------------ embedding
+// x[r] = rmsnorm0(wte[ids[r]]): the embedding lookup and the norm that
+// gpt_forward copies back into the residual (fortran_gpt.f90:136-142).
+// An id outside [0, V) (possible only through the device-pointer entry
+// point, the host ones validate) yields a NaN row instead of a wild read.
+__global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ wte,
+                                                    const int32_t* __restrict__ ids, int D, int V,
+                                                    float eps, float* __restrict__ x) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const int id = ids[r];
+  if (id < 0 || id >= V) {
+    for (int k = threadIdx.x; k < D; k += 256) x[r * D + k] = __builtin_nanf("");
+    return;
+  }
+  const bf16_t* row = wte + (int64_t)id * D;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < D; k += 256) {
+    float v = bf16_to_f32(row[k]);
+    ss += v * v;
+  }
+  ss = block_sum<4>(ss, red);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  for (int k = threadIdx.x; k < D; k += 256) x[r * D + k] = bf16_to_f32(row[k]) * inv;
+}
+
+void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
+                       int64_t rows, float* x) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V, d.eps,
+                     x);
+}
+
+// ------------------------------------------------------------ epilogues
+// Shared by the GEMV and the MFMA GEMM: row m of the M token rows, stored
+// weight row r of N. The QKV epilogue receives a rotation pair (stored rows
+// r, r+1, i.e. head dims j and j+hd/2) at once.
+struct EpiCtx {
+  int b, pos;
+};
+
+__device__ __forceinline__ EpiCtx epi_ctx(const GemvArgs& a, int m, int pos0) {
+  EpiCtx c;
+  c.b = m / a.T;
+  c.pos = pos0 + (m % a.T);
+  return c;
+}
+
+// QKV pair epilogue: x1 = dim j, x2 = dim j+hd/2 of a q, k or v head row.
+__device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos0, int r, float x1,
+                                               float x2) {
+  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
+  const EpiCtx c = epi_ctx(a, m, pos0);
+  if (r < qd + kd) {
+    const int base = (r < qd) ? r : r - qd;
+    const int head = base / hd, j = (base % hd) >> 1;
+    const float cs = a.cosb[(int64_t)c.pos * (hd / 2) + j];
+    const float sn = a.sinb[(int64_t)c.pos * (hd / 2) + j];
+    const float y1 = x1 * cs + x2 * sn;
+    const float y2 = x1 * (-sn) + x2 * cs;
+    if (r < qd) {
+      float* q = a.y + (int64_t)m * qd + head * hd;
+      q[j] = y1;
+      q[j + hd / 2] = y2;
+    } else {
+      float* k = a.kc + ((int64_t)c.b * a.maxT + c.pos) * kd + head * hd;
+      k[j] = y1;
+      k[j + hd / 2] = y2;
+    }
+  } else {
+    const int base = r - qd - kd;
+    const int head = base / hd, j = (base % hd) >> 1;
+    float* v = a.vc + ((int64_t)c.b * a.maxT + c.pos) * kd + head * hd;
+    v[j] = x1;
+    v[j + hd / 2] = x2;
+  }
+}
+
+template <int EPI>
+__device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, float v) {
+  float* y = a.y + (int64_t)m * a.N + r;
+  if (EPI == GV_RESID) {
+    *y = *y + v;
+  } else if (EPI == GV_RELU2) {
+    const float t = v < 0.f ? 0.f : v;
+    *y = t * t;
+  } else {
+    *y = v;
+  }
+}
+
+// ------------------------------------------------------------ GEMV
+// M <= 4 token rows. x rows are staged in LDS (normalised there when
+// a.norm, so each product uses the rounded xn as the reference does). A
+// wavefront owns a pair of weight rows at a time; lanes stride the row in
+// 16-byte chunks (8 bf16), so each row is read as whole, coalesced lines.
+template <int M, int EPI>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restrict__ d_pos) {
+  extern __shared__ float sx[];  // [M][K]
+  __shared__ float sinv[4];
+  const int K = a.K, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  for (int i = tid; i < M * K; i += 256) sx[i] = a.x[i];
+  __syncthreads();
+  if (a.norm) {
+    if (wid < M) {
+      float ss = 0.f;
+      for (int k = lane; k < K; k += 64) ss += sx[wid * K + k] * sx[wid * K + k];
+      ss = wave_sum(ss);
+      if (lane == 0) sinv[wid] = 1.0f / sqrtf(ss / (float)K + a.eps);
+    }
+    __syncthreads();
+    for (int i = tid; i < M * K; i += 256) sx[i] = sx[i] * sinv[i / K];
+    __syncthreads();
+  }
+  const int pos0 = d_pos ? *d_pos : a.pos0;
+  const int nunits = a.N >> 1, nch = K >> 3;
+  for (int u = blockIdx.x * 4 + wid; u < nunits; u += gridDim.x * 4) {
+    const bf16_t* w0 = a.w + (int64_t)(2 * u) * K;
+    float acc0[M], acc1[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc0[m] = acc1[m] = 0.f;
+    for (int c = lane; c < nch; c += 64) {
+      const uint4 p0 = *(const uint4*)(w0 + c * 8);
+      const uint4 p1 = *(const uint4*)(w0 + K + c * 8);
+      float f0[8], f1[8];
+      unpack8(p0, f0);
+      unpack8(p1, f1);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float4 xa = *(const float4*)(sx + m * K + c * 8);
+        const float4 xb = *(const float4*)(sx + m * K + c * 8 + 4);
+        acc0[m] += f0[0] * xa.x + f0[1] * xa.y + f0[2] * xa.z + f0[3] * xa.w +
+                   f0[4] * xb.x + f0[5] * xb.y + f0[6] * xb.z + f0[7] * xb.w;
+        acc1[m] += f1[0] * xa.x + f1[1] * xa.y + f1[2] * xa.z + f1[3] * xa.w +
+                   f1[4] * xb.x + f1[5] * xb.y + f1[6] * xb.z + f1[7] * xb.w;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      acc0[m] = wave_sum(acc0[m]);
+      acc1[m] = wave_sum(acc1[m]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        if (EPI == GV_QKV) {
+          qkv_pair_store(a, m, pos0, 2 * u, acc0[m], acc1[m]);
+        } else {
+          single_store<EPI>(a, m, 2 * u, acc0[m]);
+          single_store<EPI>(a, m, 2 * u + 1, acc1[m]);
+        }
+      }
+    }
+  }
+}
+
+template <int EPI>
+static void gemv_m(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  const int nunits = a.N / 2;
+  int grid = (nunits + 3) / 4;
+  if (grid > 2048) grid = 2048;
+  const size_t lds = sizeof(float) * (size_t)a.M * a.K;
+  switch (a.M) {
+    case 1: hipLaunchKernelGGL((k_gemv<1, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
+    case 2: hipLaunchKernelGGL((k_gemv<2, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
+    case 3: hipLaunchKernelGGL((k_gemv<3, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
+    default: hipLaunchKernelGGL((k_gemv<4, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
+  }
+}
+
+void launch_gemv_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
+  switch (epi) {
+    case GV_QKV: gemv_m<GV_QKV>(s, a, d_pos); break;
+    case GV_RESID: gemv_m<GV_RESID>(s, a, d_pos); break;
+    case GV_RELU2: gemv_m<GV_RELU2>(s, a, d_pos); break;
+    default: gemv_m<GV_STORE>(s, a, d_pos); break;
+  }
+}
+
+void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a) {
+  launch_gemv_pos(s, epi, a, nullptr);
+}
+
+// ------------------------------------------------------------ decode attention
+// One block per (sequence b, query head h): the single query at position
+// len-1 against cache positions 0..len-1 (fortran_attn.f90:317-362). Scores
+// live in LDS; one wavefront per position computes a 64-lane dot product.
+__global__ __launch_bounds__(256) void k_attn_decode(const float* __restrict__ q,
+                                                     const float* __restrict__ kc,
+                                                     const float* __restrict__ vc, int H, int KH,
+                                                     int hd, int maxT,
+                                                     const int32_t* __restrict__ d_len, int len_imm,
+                                                     float* __restrict__ y) {
+  extern __shared__ float sm[];  // [hd] q, [2*hd] partial out, [len] scores
+  __shared__ float red[4];
+  const int bh = blockIdx.x, b = bh / H, h = bh % H, kvh = h / (H / KH);
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int len = d_len ? (*d_len + 1) : len_imm;
+  const int kd = KH * hd;
+  float* sq = sm;
+  float* so = sm + hd;
+  float* ss = sm + 3 * hd;
+  for (int i = tid; i < hd; i += 256) sq[i] = q[(int64_t)bh * hd + i];
+  __syncthreads();
+  const float scale = 1.0f / sqrtf((float)hd);
+  const float* K = kc + (int64_t)b * maxT * kd + kvh * hd;
+  const float* V = vc + (int64_t)b * maxT * kd + kvh * hd;
+  for (int p = wid; p < len; p += 4) {
+    const float* kr = K + (int64_t)p * kd;
+    float acc = 0.f;
+    for (int i = lane; i < hd; i += 64) acc += sq[i] * kr[i];
+    acc = wave_sum(acc);
+    if (lane == 0) ss[p] = acc * scale;
+  }
+  __syncthreads();
+  float m = -FLT_MAX;
+  for (int p = tid; p < len; p += 256) m = fmaxf(m, ss[p]);
+  m = block_max<4>(m, red);
+  float l = 0.f;
+  for (int p = tid; p < len; p += 256) {
+    const float e = expf(ss[p] - m);
+    ss[p] = e;
+    l += e;
+  }
+  l = block_sum<4>(l, red);
+  const float inv = 1.0f / l;
+  // two position groups of 128 threads; thread owns one head dim per pass
+  const int g = tid / 128, t = tid % 128;
+  for (int d0 = 0; d0 < hd; d0 += 128) {
+    const int dd = d0 + t;
+    float acc = 0.f;
+    if (dd < hd)
+      for (int p = g; p < len; p += 2) acc += ss[p] * inv * V[(int64_t)p * kd + dd];
+    __syncthreads();
+    if (dd < hd) so[g * hd + dd] = acc;
+    __syncthreads();
+    if (g == 0 && dd < hd) y[(int64_t)bh * hd + dd] = so[dd] + so[hd + dd];
+  }
+}
+
+void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
+                            const float* vc, int B, int maxT, const int32_t* d_len, int len,
+                            float* y) {
+  const size_t lds = sizeof(float) * (size_t)(3 * d.hd + maxT);
+  hipLaunchKernelGGL(k_attn_decode, dim3(B * d.H), dim3(256), lds, s, q, kc, vc, d.H, d.KH, d.hd,
+                     maxT, d_len, len, y);
+}
+
+void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const float* kc,
+                        const float* vc, int B, int maxT, int len, float* y, float*, int64_t) {
+  launch_attn_decode_pos(s, d, q, kc, vc, B, maxT, nullptr, len, y);
+}
+
+// ------------------------------------------------------------ chunk attention
+// Causal attention of T queries (positions pos0..pos0+T-1) against cache
+// positions 0..pos0+t (fortran_attn.f90:30-117 at pos0 = 0, :376-425 in
+// general), flash-style: 32 query rows per block, 64-position K/V tiles in
+// LDS, running max / sum per row. fp32 VALU arithmetic.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_chunk(const float* __restrict__ q,
+                                                    const float* __restrict__ kc,
+                                                    const float* __restrict__ vc, int H, int KH,
+                                                    int T, int maxT, int pos0,
+                                                    float* __restrict__ y) {
+  constexpr int QT = 32, KT = 64, KP = HD + 4;  // padded K row (floats)
+  constexpr int DPT = HD / 8;                   // output dims per thread
+  extern __shared__ float sm[];
+  float* sQ = sm;                 // [QT][HD]
+  float* sK = sQ + QT * HD;       // [KT][KP]
+  float* sV = sK + KT * KP;       // [KT][HD]
+  float* sP = sV + KT * HD;       // [QT][KT]
+  const int qt = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H, kvh = h / (H / KH);
+  const int tid = threadIdx.x, r = tid >> 3, c8 = tid & 7;
+  const int kd = KH * HD, qd = H * HD;
+  const int q0 = qt * QT;
+  const int nq = min(QT, T - q0);
+  for (int i = tid; i < QT * HD; i += 256) {
+    const int rr = i / HD, dd = i % HD;
+    sQ[i] = (rr < nq) ? q[((int64_t)b * T + q0 + rr) * qd + h * HD + dd] : 0.f;
+  }
+  const float scale = 1.0f / sqrtf((float)HD);
+  const int qpos = pos0 + q0 + r;  // this thread's query position
+  float m_run = -FLT_MAX, l_run = 0.f;
+  float o[DPT];
+#pragma unroll
+  for (int i = 0; i < DPT; ++i) o[i] = 0.f;
+  const int last_key = pos0 + q0 + nq - 1;
+  const float* Kb = kc + (int64_t)b * maxT * kd + kvh * HD;
+  const float* Vb = vc + (int64_t)b * maxT * kd + kvh * HD;
+  for (int k0 = 0; k0 <= last_key; k0 += KT) {
+    __syncthreads();
+    for (int i = tid; i < KT * HD; i += 256) {
+      const int kk = i / HD, dd = i % HD;
+      const bool ok = (k0 + kk) <= last_key;
+      sK[kk * KP + dd] = ok ? Kb[(int64_t)(k0 + kk) * kd + dd] : 0.f;
+      sV[kk * HD + dd] = ok ? Vb[(int64_t)(k0 + kk) * kd + dd] : 0.f;
+    }
+    __syncthreads();
+    float sc[KT / 8];
+    float mx = -FLT_MAX;
+#pragma unroll
+    for (int j = 0; j < KT / 8; ++j) {
+      const int kk = c8 + 8 * j;
+      const float* qr = sQ + r * HD;
+      const float* kr = sK + kk * KP;
+      float acc = 0.f;
+#pragma unroll 8
+      for (int dd = 0; dd < HD; dd += 4) {
+        const float4 a4 = *(const float4*)(qr + dd);
+        const float4 k4 = *(const float4*)(kr + dd);
+        acc += a4.x * k4.x + a4.y * k4.y + a4.z * k4.z + a4.w * k4.w;
+      }
+      float s = acc * scale;
+      if (k0 + kk > qpos) s = -INFINITY;
+      sc[j] = s;
+      mx = fmaxf(mx, s);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = expf(m_run - m_new);
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < KT / 8; ++j) {
+      const float p = expf(sc[j] - m_new);
+      ps += p;
+      sP[r * KT + c8 + 8 * j] = p;
+    }
+    ps += __shfl_xor(ps, 1, 64);
+    ps += __shfl_xor(ps, 2, 64);
+    ps += __shfl_xor(ps, 4, 64);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) o[i] *= alpha;
+    for (int kk = 0; kk < KT; ++kk) {
+      const float p = sP[r * KT + kk];
+#pragma unroll
+      for (int i = 0; i < DPT; ++i) o[i] += p * sV[kk * HD + c8 + 8 * i];
+    }
+  }
+  if (r < nq) {
+    const float inv = 1.0f / l_run;
+    float* yr = y + ((int64_t)b * T + q0 + r) * qd + h * HD;
+#pragma unroll
+    for (int i = 0; i < DPT; ++i) yr[c8 + 8 * i] = o[i] * inv;
+  }
+}
+
+void launch_attn_prefill(hipStream_t s, const Dims& d, const float* q, const float* kc,
+                         const float* vc, int B, int T, int maxT, int pos0, float* y) {
+  dim3 grid((T + 31) / 32, B * d.H);
+  static bool lds_set = false;
+  if (!lds_set) {  // the 128-wide variant stages 89 KiB of LDS
+    (void)hipFuncSetAttribute((const void*)k_attn_chunk<128>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipFuncSetAttribute((const void*)k_attn_chunk<64>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    lds_set = true;
+  }
+  if (d.hd == 128) {
+    const size_t lds = sizeof(float) * (32 * 128 + 64 * 132 + 64 * 128 + 32 * 64);
+    hipLaunchKernelGGL((k_attn_chunk<128>), grid, dim3(256), lds, s, q, kc, vc, d.H, d.KH, T,
+                       maxT, pos0, y);
+  } else {
+    const size_t lds = sizeof(float) * (32 * 64 + 64 * 68 + 64 * 64 + 32 * 64);
+    hipLaunchKernelGGL((k_attn_chunk<64>), grid, dim3(256), lds, s, q, kc, vc, d.H, d.KH, T, maxT,
+                       pos0, y);
+  }
+}
+
+// ------------------------------------------------------------ argmax / nll
+// First index of the maximum, as sample_token's strict > scan returns it.
+__device__ __forceinline__ void amax_merge(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, int V,
+                                                int32_t* __restrict__ out,
+                                                int32_t* __restrict__ out2,
+                                                int32_t* __restrict__ d_len) {
+  __shared__ float rv[4];
+  __shared__ int ri[4];
+  const int64_t row = blockIdx.x;
+  const float* l = logits + row * V;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const float v = l[j];
+    if (v > bv) {
+      bv = v;
+      bi = j;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(bv, o, 64);
+    const int i2 = __shfl_xor(bi, o, 64);
+    amax_merge(bv, bi, v2, i2);
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) {
+    rv[w] = bv;
+    ri[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 4; ++k) amax_merge(bv, bi, rv[k], ri[k]);
+    if (bi == 0x7fffffff) bi = 0;  // all -inf / NaN: position 1, as the scan starts there
+    out[row] = bi;
+    if (out2) out2[row] = bi;
+    if (d_len && row == 0) *d_len = *d_len + 1;
+  }
+}
+
+void launch_argmax_step(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out,
+                        int32_t* out2, int32_t* d_len) {
+  hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(256), 0, s, logits, V, out, out2, d_len);
+}
+
+void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out) {
+  launch_argmax_step(s, logits, rows, V, out, nullptr, nullptr);
+}
+
+__global__ __launch_bounds__(256) void k_nll(const float* __restrict__ logits,
+                                             const int32_t* __restrict__ tgt, int V,
+                                             float* __restrict__ out) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const float* l = logits + row * V;
+  float m = -FLT_MAX;
+  for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, l[j]);
+  m = block_max<4>(m, red);
+  float s = 0.f;
+  for (int j = threadIdx.x; j < V; j += 256) s += expf(l[j] - m);
+  s = block_sum<4>(s, red);
+  const int t = tgt[row];
+  if (threadIdx.x == 0) out[row] = (t >= 0 && t < V) ? (m + logf(s)) - l[t] : __builtin_nanf("");
+}
+
+void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
+                float* out) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(k_nll, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
+}
+
+}  // namespace fgpt

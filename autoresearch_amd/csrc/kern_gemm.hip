@@ -1,0 +1,186 @@
+// kern_gemm.hip -- bf16 MFMA GEMM for prefill and batched decode (gfx950).
+//
+// C[M][N] = epi( s_m * (A[M][K] . W[N][K]^T) ), the y = x W^T of
+// linear3d_sgemm (src/lib/fortran_blas.f90:39-57) with rmsnorm0's row scale
+// s_m = 1/sqrt(mean(A_m^2) + eps) (src/lib/fortran_rmsnorm.f90:40-60) applied
+// to the output rows when `norm` is set (rmsnorm is a per-row scale, so
+// norm(x) W^T = s * (x W^T)).
+//
+// Precision: W is bf16 and exact (the weights are bf16-representable). A is
+// fp32 and is split on the fly into two bf16 terms, A = hi + lo with
+// hi = bf16(A), lo = bf16(A - hi); both go through v_mfma_f32_32x32x16_bf16
+// with fp32 accumulation, so each product carries ~16 mantissa bits of A
+// instead of 8. A single bf16 term moves depth-12 logits by ~3e-3 of
+// max|logit|, more than the 2e-3 parity bound; the split keeps it ~5e-6.
+//
+// Tiling: 64x64 output tile per 256-thread block (four 64-wide wavefronts in
+// a 2x2 grid, each owning a 32x32 MFMA tile), K step 32 staged through LDS
+// with the next K step's global loads issued before the current MFMAs.
+#include "fgpt_internal.h"
+#include "kern_common.h"
+
+namespace fgpt {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+namespace {
+
+constexpr int BM = 64, BN = 64, BK = 32;
+constexpr int LDSK = BK + 8;  // bf16 elements per LDS row (pad: 80-byte stride)
+
+__device__ __forceinline__ void split_store(const float4 a, const float4 b, uint16_t* hi,
+                                            uint16_t* lo) {
+  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint16_t h[8], l[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    h[i] = f32_to_bf16_rne(v[i]);
+    l[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(h[i]));
+  }
+  uint4 ph, pl;
+  ph.x = h[0] | ((uint32_t)h[1] << 16);
+  ph.y = h[2] | ((uint32_t)h[3] << 16);
+  ph.z = h[4] | ((uint32_t)h[5] << 16);
+  ph.w = h[6] | ((uint32_t)h[7] << 16);
+  pl.x = l[0] | ((uint32_t)l[1] << 16);
+  pl.y = l[2] | ((uint32_t)l[3] << 16);
+  pl.z = l[4] | ((uint32_t)l[5] << 16);
+  pl.w = l[6] | ((uint32_t)l[7] << 16);
+  *(uint4*)hi = ph;
+  *(uint4*)lo = pl;
+}
+
+// Epilogue helpers (same semantics as the GEMV epilogues in kern_core.hip).
+__device__ __forceinline__ void g_qkv_pair(const GemvArgs& a, int m, int pos0, int r, float x1,
+                                           float x2) {
+  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
+  const int b = m / a.T, pos = pos0 + (m % a.T);
+  if (r < qd + kd) {
+    const int base = (r < qd) ? r : r - qd;
+    const int head = base / hd, j = (base % hd) >> 1;
+    const float cs = a.cosb[(int64_t)pos * (hd / 2) + j];
+    const float sn = a.sinb[(int64_t)pos * (hd / 2) + j];
+    const float y1 = x1 * cs + x2 * sn;
+    const float y2 = x1 * (-sn) + x2 * cs;
+    float* dst = (r < qd) ? (a.y + (int64_t)m * qd + head * hd)
+                          : (a.kc + ((int64_t)b * a.maxT + pos) * kd + head * hd);
+    dst[j] = y1;
+    dst[j + hd / 2] = y2;
+  } else {
+    const int base = r - qd - kd;
+    const int head = base / hd, j = (base % hd) >> 1;
+    float* v = a.vc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
+    v[j] = x1;
+    v[j + hd / 2] = x2;
+  }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm(GemvArgs a, const int32_t* __restrict__ d_pos) {
+  __shared__ __attribute__((aligned(16))) uint16_t sAh[BM * LDSK];
+  __shared__ __attribute__((aligned(16))) uint16_t sAl[BM * LDSK];
+  __shared__ __attribute__((aligned(16))) uint16_t sW[BN * LDSK];
+  __shared__ float sinv[BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int M = a.M, K = a.K;
+
+  // loader mapping: thread -> (row, 8-element chunk) of the 64x32 tiles
+  const int lr = tid >> 2, lc = (tid & 3) * 8;
+  const bool arow_ok = (m0 + lr) < M;
+  const float* ag = a.x + (int64_t)(arow_ok ? (m0 + lr) : 0) * K + lc;
+  const bf16_t* wg = a.w + (int64_t)(n0 + lr) * K + lc;
+
+  float4 ra0, ra1;
+  uint4 rw;
+  float ss = 0.f;
+  auto gload = [&](int k0) {
+    if (arow_ok) {
+      ra0 = *(const float4*)(ag + k0);
+      ra1 = *(const float4*)(ag + k0 + 4);
+    } else {
+      ra0 = make_float4(0.f, 0.f, 0.f, 0.f);
+      ra1 = ra0;
+    }
+    rw = *(const uint4*)(wg + k0);
+  };
+
+  f32x16_t acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+
+  gload(0);
+  for (int k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();
+    split_store(ra0, ra1, sAh + lr * LDSK + lc, sAl + lr * LDSK + lc);
+    *(uint4*)(sW + lr * LDSK + lc) = rw;
+    ss += ra0.x * ra0.x + ra0.y * ra0.y + ra0.z * ra0.z + ra0.w * ra0.w + ra1.x * ra1.x +
+          ra1.y * ra1.y + ra1.z * ra1.z + ra1.w * ra1.w;
+    __syncthreads();
+    if (k0 + BK < K) gload(k0 + BK);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 16) {
+      const int ar = wm * 32 + (lane & 31), br = wn * 32 + (lane & 31);
+      const int kc = kk + 8 * (lane >> 5);
+      const bf16x8_t ah = *(const bf16x8_t*)(sAh + ar * LDSK + kc);
+      const bf16x8_t al = *(const bf16x8_t*)(sAl + ar * LDSK + kc);
+      const bf16x8_t bw = *(const bf16x8_t*)(sW + br * LDSK + kc);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bw, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bw, acc, 0, 0, 0);
+    }
+  }
+  // row scale: 4 consecutive threads hold the partial sums of one A row
+  if (a.norm) {
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    if ((tid & 3) == 0) sinv[lr] = 1.0f / sqrtf(ss / (float)K + a.eps);
+    __syncthreads();
+  }
+
+  const int pos0 = d_pos ? *d_pos : a.pos0;
+  const int j = lane & 31;
+  const int n = n0 + wn * 32 + j;
+#pragma unroll
+  for (int rg = 0; rg < 16; ++rg) {
+    const int i = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
+    const int ml = wm * 32 + i;
+    const int m = m0 + ml;
+    float v = acc[rg];
+    if (a.norm) v *= sinv[ml];
+    if (EPI == GV_QKV) {
+      const float partner = __shfl_xor(v, 1, 64);
+      if (m < M && (j & 1) == 0) g_qkv_pair(a, m, pos0, n, v, partner);
+    } else if (m < M) {
+      float* y = a.y + (int64_t)m * a.N + n;
+      if (EPI == GV_RESID) {
+        *y = *y + v;
+      } else if (EPI == GV_RELU2) {
+        const float t = v < 0.f ? 0.f : v;
+        *y = t * t;
+      } else {
+        *y = v;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
+  dim3 grid(a.N / BN, (a.M + BM - 1) / BM);
+  switch (epi) {
+    case GV_QKV: hipLaunchKernelGGL(k_gemm<GV_QKV>, grid, dim3(256), 0, s, a, d_pos); break;
+    case GV_RESID: hipLaunchKernelGGL(k_gemm<GV_RESID>, grid, dim3(256), 0, s, a, d_pos); break;
+    case GV_RELU2: hipLaunchKernelGGL(k_gemm<GV_RELU2>, grid, dim3(256), 0, s, a, d_pos); break;
+    default: hipLaunchKernelGGL(k_gemm<GV_STORE>, grid, dim3(256), 0, s, a, d_pos); break;
+  }
+}
+
+void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a) {
+  launch_gemm_pos(s, epi, a, nullptr);
+}
+
+}  // namespace fgpt

@@ -1,0 +1,274 @@
+"""Python host side of the gfx950 engine: ctypes over include/fgpt.h.
+
+Mirrors the reference's model API (14NGiestas/autoresearch):
+  gpt_forward     src/lib/fortran_gpt.f90:54-199
+  gpt_step        src/lib/fortran_kv.f90:26-149
+  gpt_step_multi  src/lib/fortran_kv.f90:160-289
+  load_gpt_weights src/lib/load_weights.f90:830-874
+with the same argument meaning and the same loud failures (cache full,
+missing weights, arch mismatch) raised as exceptions. There is no CPU path:
+without libfgpt.so or a gfx950 device every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from .weights import Dims, STACK_NAMES
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libfgpt.so")
+
+FG_ERRORS = {
+    -1: "FG_EARG", -2: "FG_EDIMS", -3: "FG_EWEIGHT", -4: "FG_EHIP", -5: "FG_EFULL",
+    -6: "FG_EROPE", -7: "FG_ENODEV", -8: "FG_EBUSY", -9: "FG_EARCH",
+}
+
+# every symbol include/fgpt.h declares
+EXPORTS = (
+    "fg_version", "fg_last_error", "fg_model_create", "fg_model_load", "fg_model_destroy",
+    "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_destroy",
+    "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
+    "fg_decode_greedy", "fg_sync", "fg_model_bytes",
+)
+
+
+class FgptError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{FG_ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+class CacheFull(FgptError):
+    pass
+
+
+class _FgDims(C.Structure):
+    _fields_ = [("n_layer", C.c_int32), ("d_model", C.c_int32), ("n_head", C.c_int32),
+                ("n_kv_head", C.c_int32), ("head_dim", C.c_int32), ("vocab_size", C.c_int32),
+                ("eps", C.c_float)]
+
+
+_f = C.POINTER(C.c_float)
+_i = C.POINTER(C.c_int32)
+_vp = C.c_void_p
+_LIB = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libfgpt.so (fails loudly when it has not been built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is missing: build it with autoresearch_amd/build.py")
+    L = C.CDLL(path)
+    i32, i64 = C.c_int32, C.c_int64
+    sig = {
+        "fg_version": (i32, []),
+        "fg_last_error": (i32, [C.c_char_p, i32]),
+        "fg_model_create": (i32, [C.POINTER(_FgDims)] + [_f] * 8 + [C.POINTER(_vp)]),
+        "fg_model_load": (i32, [C.POINTER(_FgDims), C.c_char_p, C.POINTER(_vp)]),
+        "fg_model_destroy": (i32, [_vp]),
+        "fg_set_rope": (i32, [_vp, i32, i32, _f, _f]),
+        "fg_forward": (i32, [_vp, _i, i32, i32, _f, _i, _f]),
+        "fg_forward_dev": (i32, [_vp, _vp, i32, i32, _vp, _vp, _vp, _vp]),
+        "fg_kv_create": (i32, [_vp, i32, i32, C.POINTER(_vp)]),
+        "fg_kv_destroy": (i32, [_vp]),
+        "fg_kv_len": (i32, [_vp, _i]),
+        "fg_kv_set_len": (i32, [_vp, i32]),
+        "fg_kv_read": (i32, [_vp, _f, _f]),
+        "fg_step": (i32, [_vp, _vp, _i, _f, _i]),
+        "fg_step_multi": (i32, [_vp, _vp, _i, i32, _f, _i]),
+        "fg_decode_greedy": (i32, [_vp, _vp, _i, i32, _i, _f]),
+        "fg_sync": (i32, [_vp]),
+        "fg_model_bytes": (i32, [_vp, C.POINTER(i64), C.POINTER(i64)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = L
+    return L
+
+
+def _check(rc: int):
+    if rc != 0:
+        buf = C.create_string_buffer(512)
+        _LIB.fg_last_error(buf, 512)
+        msg = buf.value.decode(errors="replace")
+        raise (CacheFull if rc == -5 else FgptError)(rc, msg)
+
+
+def _fp(a):
+    return None if a is None else a.ctypes.data_as(_f)
+
+
+def _ip(a):
+    return None if a is None else a.ctypes.data_as(_i)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _cdims(d: Dims) -> _FgDims:
+    return _FgDims(d.n_layer, d.d_model, d.n_head, d.n_kv_head, d.head_dim, d.vocab, d.eps)
+
+
+class Model:
+    """One resident model: bf16 weight arena, workspace and RoPE tables in HBM."""
+
+    def __init__(self, d: Dims, stacks: dict | None = None, weights_dir: str | None = None):
+        L = load_library()
+        self.d = d
+        self._h = _vp()
+        cd = _cdims(d)
+        if weights_dir is not None:
+            _check(L.fg_model_load(C.byref(cd), weights_dir.encode(), C.byref(self._h)))
+        else:
+            bufs = [_f32(stacks[n]) for n in STACK_NAMES]
+            _check(L.fg_model_create(C.byref(cd), *[_fp(b) for b in bufs], C.byref(self._h)))
+
+    def close(self):
+        if self._h:
+            _LIB.fg_model_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    def set_rope(self, cos_buf, sin_buf, pos0: int = 0):
+        c, s = _f32(cos_buf).reshape(-1), _f32(sin_buf).reshape(-1)
+        n = c.size // (self.d.head_dim // 2)
+        _check(_LIB.fg_set_rope(self._h, pos0, n, _fp(c), _fp(s)))
+
+    def forward(self, ids, B: int, T: int, targets=None, want_logits: bool = True):
+        ids = _i32(ids).reshape(-1)
+        if ids.size != B * T:
+            raise ValueError("ids must hold B*T values")
+        lg = np.empty(B * T * self.d.vocab, np.float32) if want_logits else None
+        tg = _i32(targets).reshape(-1) if targets is not None else None
+        nll = np.empty(B * T, np.float32) if tg is not None else None
+        _check(_LIB.fg_forward(self._h, _ip(ids), B, T, _fp(lg), _ip(tg), _fp(nll)))
+        lg = lg.reshape(B, T, self.d.vocab) if lg is not None else None
+        return lg, (nll.reshape(B, T) if nll is not None else None)
+
+    def forward_dev(self, d_ids: int, B: int, T: int, d_logits: int = 0, d_targets: int = 0,
+                    d_nll: int = 0, stream: int = 0):
+        """Enqueue a forward on device pointers (ints), no host synchronisation."""
+        _check(_LIB.fg_forward_dev(self._h, d_ids, B, T, d_logits or None, d_targets or None,
+                                   d_nll or None, stream or None))
+
+    def sync(self):
+        _check(_LIB.fg_sync(self._h))
+
+    def bytes(self):
+        w, k = C.c_int64(), C.c_int64()
+        _check(_LIB.fg_model_bytes(self._h, C.byref(w), C.byref(k)))
+        return w.value, k.value
+
+    def kv(self, B: int, maxT: int) -> "KV":
+        return KV(self, B, maxT)
+
+
+class KV:
+    """A KV cache of B sequences x maxT positions resident in HBM."""
+
+    def __init__(self, m: Model, B: int, maxT: int):
+        self.m, self.B, self.maxT = m, B, maxT
+        self._h = _vp()
+        _check(_LIB.fg_kv_create(m.handle, B, maxT, C.byref(self._h)))
+
+    def close(self):
+        if self._h:
+            _LIB.fg_kv_destroy(self._h)
+            self._h = _vp()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def len(self) -> int:
+        v = C.c_int32()
+        _check(_LIB.fg_kv_len(self._h, C.byref(v)))
+        return v.value
+
+    @len.setter
+    def len(self, v: int):
+        _check(_LIB.fg_kv_set_len(self._h, v))
+
+    def read(self):
+        d = self.m.d
+        n = d.n_layer * self.B * self.maxT * d.n_kv_head * d.head_dim
+        k, v = np.empty(n, np.float32), np.empty(n, np.float32)
+        _check(_LIB.fg_kv_read(self._h, _fp(k), _fp(v)))
+        return k, v
+
+    def step(self, ids, want_logits: bool = True):
+        ids = _i32(ids).reshape(-1)
+        lg = np.empty(self.B * self.m.d.vocab, np.float32) if want_logits else None
+        nxt = np.empty(self.B, np.int32)
+        _check(_LIB.fg_step(self.m.handle, self._h, _ip(ids), _fp(lg), _ip(nxt)))
+        return (lg.reshape(self.B, -1) if lg is not None else None), nxt
+
+    def step_multi(self, ids, want_logits: bool = True):
+        ids = _i32(ids).reshape(self.B, -1)
+        TB = ids.shape[1]
+        lg = np.empty(self.B * TB * self.m.d.vocab, np.float32) if want_logits else None
+        nxt = np.empty(self.B, np.int32)
+        _check(_LIB.fg_step_multi(self.m.handle, self._h, _ip(ids), TB, _fp(lg), _ip(nxt)))
+        return (lg.reshape(self.B, TB, -1) if lg is not None else None), nxt
+
+    def decode_greedy(self, ids, n_steps: int, want_logits: bool = False):
+        ids = _i32(ids).reshape(-1)
+        out = np.empty(n_steps * self.B, np.int32)
+        lg = np.empty(n_steps * self.B * self.m.d.vocab, np.float32) if want_logits else None
+        _check(_LIB.fg_decode_greedy(self.m.handle, self._h, _ip(ids), n_steps, _ip(out), _fp(lg)))
+        out = out.reshape(n_steps, self.B)
+        return out, (lg.reshape(n_steps, self.B, -1) if lg is not None else None)
+
+
+# ------------------------------------------------------- reference-shaped API
+
+def load_gpt_weights(wdir: str, d: Dims) -> Model:
+    """load_gpt_weights + require_arch (src/lib/load_weights.f90:830-874,
+    src/lib/fortran_arch.f90:238-246), uploading straight to HBM."""
+    return Model(d, weights_dir=wdir)
+
+
+def greedy_generate(m: Model, prompt, n_gen: int, cos_buf, sin_buf, pchunk: int = 64):
+    """The ids-in/ids-out loop of src/app/chat_text.f90:257-278,423-462 with
+    plain argmax: prompt[:-1] through chunked cached passes (gpt_step_multi,
+    pchunk tokens each), then n_gen device-side greedy steps fed from
+    prompt[-1]. Returns the generated ids."""
+    prompt = _i32(prompt).reshape(-1)
+    ntot = prompt.size + n_gen
+    m.set_rope(np.asarray(cos_buf).reshape(-1)[: ntot * m.d.head_dim // 2],
+               np.asarray(sin_buf).reshape(-1)[: ntot * m.d.head_dim // 2])
+    kv = m.kv(1, ntot)
+    npre = prompt.size - 1
+    s = 0
+    while s < npre:
+        tb = min(pchunk, npre - s)
+        kv.step_multi(prompt[s:s + tb], want_logits=False)
+        s += tb
+    out, _ = kv.decode_greedy(prompt[-1:], n_gen)
+    kv.close()
+    return out[:, 0]

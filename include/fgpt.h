@@ -1,0 +1,137 @@
+/* fgpt.h -- C ABI of the MI355X (gfx950) engine for the fortran_gpt forward
+ * path of 14NGiestas/autoresearch: gpt_forward (prefill), gpt_step and
+ * gpt_step_multi (KV-cache decode).
+ *
+ * The library (autoresearch_amd/libfgpt.so) is bound from Fortran through
+ * iso_c_binding (autoresearch_amd/fortran/fgpt_c.f90) exactly as the
+ * reference binds its rocBLAS shim (src/lib/fortran_blas_gpu.f90:30-59 ->
+ * src/lib/gpu_shim.cpp:98-122), and from Python through ctypes.
+ *
+ * Conventions
+ *  - Every function returns int32_t: FG_OK (0) or a negative FG_E* code;
+ *    fg_last_error() returns the message of the calling thread's last error.
+ *  - Host buffers are row-major flats, as in the reference (fortran_gpt.f90:
+ *    94-96). Ids are 0-based int32 (fortran_linear.f90:59-61). Logits are
+ *    fp32, one row of vocab_size per token.
+ *  - Weights are the reference loader's eight stacked fp32 buffers
+ *    (load_weights.f90:830-874); every value must be exactly bf16
+ *    representable. They are uploaded once, as bf16, into one HBM arena.
+ *  - A handle is single-stream and not reentrant: a call made while another
+ *    thread is inside a call on the same handle fails with FG_EBUSY.
+ *  - There is no CPU fallback: without a usable gfx950 device every call that
+ *    needs one fails with FG_ENODEV.
+ */
+#ifndef FGPT_H
+#define FGPT_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FG_OK = 0,
+  FG_EARG = -1,     /* bad argument (null pointer, size out of range)      */
+  FG_EDIMS = -2,    /* model dims the engine does not support              */
+  FG_EWEIGHT = -3,  /* weight file missing/empty/malformed, not bf16-exact */
+  FG_EHIP = -4,     /* HIP runtime error                                   */
+  FG_EFULL = -5,    /* KV cache full (fortran_kv.f90:74-77, :213-216)      */
+  FG_EROPE = -6,    /* RoPE table row not set for a position in use        */
+  FG_ENODEV = -7,   /* no usable gfx950 device                             */
+  FG_EBUSY = -8,    /* handle in use by another thread                     */
+  FG_EARCH = -9     /* arch.txt disagrees with the dims (fortran_arch.f90:238-246) */
+};
+
+typedef struct fg_model fg_model;
+typedef struct fg_kv fg_kv;
+
+/* Model dims: the integer arguments of gpt_forward / gpt_step
+ * (fortran_gpt.f90:58-64, fortran_kv.f90:31-39). d_ff is 4*d_model. */
+typedef struct fg_dims {
+  int32_t n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size;
+  float eps;
+} fg_dims;
+
+/* ABI version (major*100 + minor). */
+int32_t fg_version(void);
+
+/* Copies the calling thread's last error message (NUL-terminated,
+ * truncated to len) and returns its code. */
+int32_t fg_last_error(char *buf, int32_t len);
+
+/* Upload from the reference's eight stacked host buffers (the outputs of
+ * load_gpt_weights, src/lib/load_weights.f90:830-874; replaces the per-call
+ * weight registration of gpublas_sgemm_fwd, src/lib/gpu_shim.cpp:76-95).
+ * The host buffers may be freed after the call. */
+int32_t fg_model_create(const fg_dims *dims, const float *wte, const float *c_q,
+                        const float *c_k, const float *c_v, const float *c_proj,
+                        const float *c_fc, const float *c_proj2,
+                        const float *lm_head, fg_model **out);
+
+/* Load a reference weight directory (.npy flats with the file names of
+ * src/lib/load_weights.f90:7-9, :853-873) and check arch.txt against dims
+ * when present (require_arch, src/lib/fortran_arch.f90:238-246). */
+int32_t fg_model_load(const fg_dims *dims, const char *weights_dir, fg_model **out);
+
+int32_t fg_model_destroy(fg_model *m);
+
+/* Set RoPE table rows [pos0, pos0+n_pos) from host fp32 (n_pos, head_dim/2)
+ * cos/sin tables (src/app/chat_text.f90:225-235): the engine uses the
+ * caller's tables rather than recomputing sin/cos on the device. */
+int32_t fg_set_rope(fg_model *m, int32_t pos0, int32_t n_pos, const float *cos_buf,
+                    const float *sin_buf);
+
+/* gpt_forward (src/lib/fortran_gpt.f90:54-199): B rows of T ids, positions
+ * 0..T-1. logits (B*T*V, host) may be NULL. When targets (B*T) is given,
+ * nll (B*T, host) receives logsumexp(logits) - logits[target] in nats
+ * (src/app/eval_bpb.f90:165-181). RoPE rows 0..T-1 must be set. */
+int32_t fg_forward(fg_model *m, const int32_t *ids, int32_t B, int32_t T, float *logits,
+                   const int32_t *targets, float *nll);
+
+/* fg_forward on device buffers, enqueued on `stream` (a hipStream_t, NULL =
+ * the handle's stream) without host synchronisation. d_logits may be NULL
+ * (the handle keeps them in its workspace); d_targets/d_nll as above. */
+int32_t fg_forward_dev(fg_model *m, const int32_t *d_ids, int32_t B, int32_t T,
+                       float *d_logits, const int32_t *d_targets, float *d_nll,
+                       void *stream);
+
+/* KV cache for B sequences of up to maxT positions, fp32, resident in HBM
+ * (replaces the caller-owned host cache_k/cache_v of fortran_kv.f90:9-12). */
+int32_t fg_kv_create(fg_model *m, int32_t B, int32_t maxT, fg_kv **out);
+int32_t fg_kv_destroy(fg_kv *kv);
+/* cache_len in/out of gpt_step: the number of filled positions. */
+int32_t fg_kv_len(const fg_kv *kv, int32_t *len);
+int32_t fg_kv_set_len(fg_kv *kv, int32_t len);
+/* Copy the cache back in the reference layout (L, B, maxT, KVH*hd) fp32. */
+int32_t fg_kv_read(fg_kv *kv, float *k_out, float *v_out);
+
+/* gpt_step (src/lib/fortran_kv.f90:26-149) for B sequences at position
+ * cache_len: ids (B), logits (B*V, nullable), next_ids (B, nullable) =
+ * greedy argmax (src/lib/sample.f90:271-277). Advances cache_len by 1. */
+int32_t fg_step(fg_model *m, fg_kv *kv, const int32_t *ids, float *logits, int32_t *next_ids);
+
+/* gpt_step_multi (src/lib/fortran_kv.f90:160-289): TB tokens of each of the
+ * B sequences at positions cache_len..cache_len+TB-1; logits (B*TB*V,
+ * nullable), next_ids (B, nullable) = argmax of each sequence's last row.
+ * Advances cache_len by TB. */
+int32_t fg_step_multi(fg_model *m, fg_kv *kv, const int32_t *ids, int32_t TB, float *logits,
+                      int32_t *next_ids);
+
+/* The greedy loop of src/app/chat_text.f90:423-462 (plain argmax, no byte
+ * mask): n_steps cached steps fed back on the device, starting from ids
+ * (B). ids_out (n_steps*B) receives the chosen ids; logits_out
+ * (n_steps*B*V) is optional. */
+int32_t fg_decode_greedy(fg_model *m, fg_kv *kv, const int32_t *ids, int32_t n_steps,
+                         int32_t *ids_out, float *logits_out);
+
+/* Block until the handle's queued work is done. */
+int32_t fg_sync(fg_model *m);
+
+/* Bytes of HBM the handle holds (weights, workspace, tables). Diagnostic,
+ * the counterpart of gpublas_count / gpublas_bufs (gpu_shim.cpp:172-186). */
+int32_t fg_model_bytes(const fg_model *m, int64_t *weight_bytes, int64_t *work_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
