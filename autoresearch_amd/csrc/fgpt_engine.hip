@@ -66,6 +66,15 @@ struct fg_model {
   int64_t work_bytes = 0;
   int64_t gen = 0;      // bumped whenever a buffer a captured graph uses moves
   std::atomic<int> busy{0};
+  // per-launch HIP-event timing (fg_timing): off unless asked for
+  bool timing = false;
+  struct TRec {
+    int kind;
+    hipEvent_t a, b;
+    double flops, bytes;
+  };
+  std::vector<TRec> trecs;
+  std::vector<hipEvent_t> evpool;
 };
 
 struct fg_kv {
@@ -73,13 +82,14 @@ struct fg_kv {
   int B = 0, maxT = 0, len = 0;
   float* k = nullptr;  // [L][B][maxT][KH*hd]
   float* v = nullptr;
-  int32_t* d_len = nullptr;  // device copy of len for replayed steps
+  int32_t* d_len = nullptr;  // device copy of len for replayed steps; d_len[1] = len at
+                             // the start of the current fg_decode_greedy call
   int32_t* d_ids = nullptr;  // [B] ids fed to the next step
   int32_t* d_out = nullptr;  // [cap_out] greedy ids
   int64_t cap_out = 0;
   float* d_lgs = nullptr;    // [cap_lgs] per-step logits of fg_decode_greedy
   int64_t cap_lgs = 0;
-  // captured greedy loops keyed by (n_steps, with_logits), valid for gen
+  // captured runs of greedy steps keyed by (steps, with_logits), valid for gen
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
   int64_t graphs_gen = -1;
 };
@@ -102,6 +112,32 @@ struct Guard {
   Guard guard_(m);                                                                \
   if (!guard_.ok) return seterr(FG_EBUSY, "handle in use by another thread");     \
   HIPCHK(hipSetDevice((m)->device))
+
+hipEvent_t get_event(fg_model* m) {
+  if (!m->evpool.empty()) {
+    hipEvent_t e = m->evpool.back();
+    m->evpool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  (void)hipEventCreate(&e);
+  return e;
+}
+
+// Launch f on s; with timing on, bracket it with events and keep the
+// algorithmic flops / bytes of the launch for fg_timing_read.
+template <class F>
+void timed(fg_model* m, hipStream_t s, int kind, double flops, double bytes, F&& f) {
+  if (!m->timing) {
+    f();
+    return;
+  }
+  hipEvent_t a = get_event(m), b = get_event(m);
+  (void)hipEventRecord(a, s);
+  f();
+  (void)hipEventRecord(b, s);
+  m->trecs.push_back({kind, a, b, flops, bytes});
+}
 
 int32_t check_device(int* dev_out) {
   int n = 0;
@@ -239,11 +275,16 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
 }
 
 // y = epi(x W^T): GEMV for up to four token rows, MFMA GEMM beyond.
-void linear(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
+// Algorithmic traffic: weights once, activations in and out once (RESID
+// reads the residual it adds to).
+void linear(fg_model* m, hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
+  const double M = a.M, N = a.N, K = a.K;
+  const double flops = 2.0 * M * N * K;
+  const double bytes = N * K * 2 + M * K * 4 + M * N * 4 * (epi == GV_RESID ? 2 : 1);
   if (a.M <= 4 && (int64_t)a.M * a.K * 4 <= 65536)
-    launch_gemv_pos(s, epi, a, d_pos);
+    timed(m, s, FG_K_GEMV, flops, bytes, [&] { launch_gemv_pos(s, epi, a, d_pos); });
   else
-    launch_gemm_pos(s, epi, a, d_pos);
+    timed(m, s, FG_K_GEMM, flops, bytes, [&] { launch_gemm_pos(s, epi, a, d_pos); });
 }
 
 GemvArgs base_args(fg_model* m) {
@@ -264,10 +305,16 @@ GemvArgs base_args(fg_model* m) {
 // Attention: single-query kernel when T == 1 (attn_step), else the causal
 // chunk kernel (causal_attn / attn_chunk).
 void layer_stack(fg_model* m, hipStream_t s, int B, int T, int pos0, const int32_t* d_pos,
-                 float* kc, float* vc, int maxT, int64_t lstride, float* logits) {
+                 float* kc, float* vc, int maxT, int64_t lstride, float* logits,
+                 int pos_host = -1) {
   const Dims& d = m->d;
   Work& ws = m->ws;
   const int rows = B * T;
+  if (pos_host < 0) pos_host = pos0;
+  // causal (query, key) pairs per (sequence, head) and the attention traffic
+  const double pairs = (double)T * pos_host + 0.5 * (double)T * (T + 1);
+  const double at_flops = 4.0 * d.hd * d.H * B * pairs;
+  const double at_bytes = (double)B * (2.0 * T * d.qd() + 2.0 * (pos_host + T) * d.kvd()) * 4;
   for (int l = 0; l < d.L; ++l) {
     float* lk = kc + l * lstride;
     float* lv = vc + l * lstride;
@@ -280,24 +327,28 @@ void layer_stack(fg_model* m, hipStream_t s, int B, int T, int pos0, const int32
     a.maxT = maxT;
     // q, k, v = rmsnorm(x) Wqkv^T, RoPE on q and k, k/v appended to the cache
     a.x = ws.x; a.w = m->w.qkv(l); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
-    linear(s, GV_QKV, a, d_pos);
+    linear(m, s, GV_QKV, a, d_pos);
     if (T == 1)
-      launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, ws.ao);
+      timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
+        launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, ws.ao);
+      });
     else
-      launch_attn_prefill(s, d, ws.q, lk, lv, B, T, maxT, pos0, ws.ao);
+      timed(m, s, FG_K_ATTN_CHUNK, at_flops, at_bytes, [&] {
+        launch_attn_prefill(s, d, ws.q, lk, lv, B, T, maxT, pos0, ws.ao);
+      });
     // x += attn_out Wproj^T
     a.x = ws.ao; a.w = m->w.proj(l); a.N = d.D; a.K = d.qd(); a.norm = 0; a.y = ws.x;
-    linear(s, GV_RESID, a, d_pos);
+    linear(m, s, GV_RESID, a, d_pos);
     // h = relu(rmsnorm(x) Wfc^T)^2
     a.x = ws.x; a.w = m->w.fc(l); a.N = d.dff; a.K = d.D; a.norm = 1; a.y = ws.h;
-    linear(s, GV_RELU2, a, d_pos);
+    linear(m, s, GV_RELU2, a, d_pos);
     // x += h Wproj2^T
     a.x = ws.h; a.w = m->w.proj2(l); a.N = d.D; a.K = d.dff; a.norm = 0; a.y = ws.x;
-    linear(s, GV_RESID, a, d_pos);
+    linear(m, s, GV_RESID, a, d_pos);
   }
   GemvArgs a = base_args(m);
   a.M = rows; a.T = T; a.x = ws.x; a.w = m->w.lm; a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
-  linear(s, GV_STORE, a, d_pos);
+  linear(m, s, GV_STORE, a, d_pos);
 }
 
 int32_t check_rope(fg_model* m, int64_t upto) {
@@ -315,9 +366,11 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   if (rows > (1ll << 30) / m->d.V) return seterr(FG_EARG, "B*T too large");
   RCCHK(ensure_work(m, rows));
   float* logits = d_logits ? d_logits : m->ws.logits;
-  launch_embed_norm(s, m->d, m->w.wte, d_ids, rows, m->ws.x);
+  const double eb = (double)rows * m->d.D * 6, vb = (double)rows * m->d.V * 4;
+  timed(m, s, FG_K_OTHER, 0, eb, [&] { launch_embed_norm(s, m->d, m->w.wte, d_ids, rows, m->ws.x); });
   layer_stack(m, s, B, T, 0, nullptr, m->fk, m->fv, T, 0, logits);
-  if (d_tgt && d_nll) launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll);
+  if (d_tgt && d_nll)
+    timed(m, s, FG_K_OTHER, 0, vb, [&] { launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll); });
   HIPCHK(hipGetLastError());
   return FG_OK;
 }
@@ -473,6 +526,11 @@ extern "C" int32_t fg_model_destroy(fg_model* m) {
   if (m->w.base) (void)hipFree(m->w.base);
   if (m->d_cos) (void)hipFree(m->d_cos);
   if (m->d_sin) (void)hipFree(m->d_sin);
+  for (auto& r : m->trecs) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  for (auto e : m->evpool) (void)hipEventDestroy(e);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
   return FG_OK;
@@ -566,7 +624,7 @@ extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** ou
   const size_t n = (size_t)m->d.L * B * maxT * m->d.kvd();
   hipError_t e = hipMalloc((void**)&kv->k, n * 4);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->v, n * 4);
-  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_len, 4);
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_len, 8);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_ids, (size_t)B * 4);
   if (e == hipSuccess) e = hipMemset(kv->k, 0, n * 4);  // the caller zeroes it in the reference
   if (e == hipSuccess) e = hipMemset(kv->v, 0, n * 4);
@@ -639,7 +697,8 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
   RCCHK(ensure_work(m, rows));
   hipStream_t s = m->stream;
   HIPCHK(hipMemcpyAsync(m->ws.ids, h_ids, rows * 4, hipMemcpyHostToDevice, s));
-  launch_embed_norm(s, m->d, m->w.wte, m->ws.ids, rows, m->ws.x);
+  timed(m, s, FG_K_OTHER, 0, (double)rows * m->d.D * 6,
+        [&] { launch_embed_norm(s, m->d, m->w.wte, m->ws.ids, rows, m->ws.x); });
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
   layer_stack(m, s, B, TB, kv->len, nullptr, kv->k, kv->v, kv->maxT, lstride, m->ws.logits);
   HIPCHK(hipGetLastError());
@@ -661,13 +720,40 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
 }
 
 // One greedy step whose position is read from kv->d_len on the device:
-// embed(d_ids) -> layers -> lm_head -> argmax into d_ids and out, len += 1.
-void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, float* logits, int32_t* out) {
+// embed(d_ids) -> layers -> lm_head -> argmax into d_ids and d_out[(len -
+// len0) * B], logits copied to d_lgs at the same slot when wanted, len += 1.
+// Nothing in it depends on the step index, so a captured run of steps can
+// be replayed back to back.
+void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logits,
+                          int pos_host) {
   const int B = kv->B;
-  launch_embed_norm(s, m->d, m->w.wte, kv->d_ids, B, m->ws.x);
+  timed(m, s, FG_K_OTHER, 0, (double)B * m->d.D * 6,
+        [&] { launch_embed_norm(s, m->d, m->w.wte, kv->d_ids, B, m->ws.x); });
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
-  layer_stack(m, s, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, logits);
-  launch_argmax_step(s, logits, B, m->d.V, kv->d_ids, out, kv->d_len);
+  layer_stack(m, s, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, m->ws.logits, pos_host);
+  timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
+    launch_argmax_step(s, m->ws.logits, B, m->d.V, kv->d_ids, kv->d_out, kv->d_len,
+                       kv->d_len + 1, with_logits ? kv->d_lgs : nullptr);
+  });
+}
+
+// Replay (capturing on first use) a graph of `steps` greedy steps.
+int32_t run_greedy_graph(fg_model* m, fg_kv* kv, hipStream_t s, int steps, bool with_logits) {
+  const auto key = std::make_pair(steps, with_logits ? 1 : 0);
+  auto it = kv->graphs.find(key);
+  if (it == kv->graphs.end()) {
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    for (int st = 0; st < steps; ++st) greedy_step_launches(m, kv, s, with_logits, -1);
+    HIPCHK(hipStreamEndCapture(s, &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return seterr(FG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    it = kv->graphs.emplace(key, ge).first;
+  }
+  HIPCHK(hipGraphLaunch(it->second, s));
+  return FG_OK;
 }
 
 }  // namespace
@@ -724,29 +810,22 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
     kv->graphs.clear();
     kv->graphs_gen = m->gen;
   }
-  const int32_t len0 = kv->len;
+  const int32_t lens[2] = {kv->len, kv->len};
   HIPCHK(hipMemcpyAsync(kv->d_ids, ids, (size_t)B * 4, hipMemcpyHostToDevice, s));
-  HIPCHK(hipMemcpyAsync(kv->d_len, &len0, 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(kv->d_len, lens, 8, hipMemcpyHostToDevice, s));
   HIPCHK(hipStreamSynchronize(s));
-  // The whole n-step loop is one captured graph (positions come from d_len),
-  // replayed on later calls with the same step count.
-  const auto key = std::make_pair((int)n_steps, with_logits);
-  auto it = kv->graphs.find(key);
-  if (it == kv->graphs.end()) {
-    hipGraph_t g = nullptr;
-    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-    for (int st = 0; st < n_steps; ++st) {
-      float* lg = kv->d_lgs + (with_logits ? (int64_t)st * B * m->d.V : 0);
-      greedy_step_launches(m, kv, s, lg, kv->d_out + (int64_t)st * B);
+  if (m->timing) {  // eager launches so every kernel can be bracketed by events
+    for (int st = 0; st < n_steps; ++st) greedy_step_launches(m, kv, s, with_logits, lens[0] + st);
+  } else {
+    // runs of up to kGraphSteps captured steps, replayed back to back
+    const int kGraphSteps = 32;
+    int done = 0;
+    while (done < n_steps) {
+      const int run = n_steps - done < kGraphSteps ? n_steps - done : kGraphSteps;
+      RCCHK(run_greedy_graph(m, kv, s, run, with_logits));
+      done += run;
     }
-    HIPCHK(hipStreamEndCapture(s, &g));
-    hipGraphExec_t ge = nullptr;
-    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    if (e != hipSuccess) return seterr(FG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
-    it = kv->graphs.emplace(key, ge).first;
   }
-  HIPCHK(hipGraphLaunch(it->second, s));
   HIPCHK(hipMemcpyAsync(ids_out, kv->d_out, nout * 4, hipMemcpyDeviceToHost, s));
   if (logits_out)
     HIPCHK(hipMemcpyAsync(logits_out, kv->d_lgs, nout * m->d.V * 4, hipMemcpyDeviceToHost, s));
@@ -759,6 +838,43 @@ extern "C" int32_t fg_sync(fg_model* m) {
   if (!m) return seterr(FG_EARG, "NULL argument");
   GUARD(m);
   HIPCHK(hipStreamSynchronize(m->stream));
+  return FG_OK;
+}
+
+extern "C" int32_t fg_timing(fg_model* m, int32_t enable) {
+  if (!m) return seterr(FG_EARG, "NULL argument");
+  GUARD(m);
+  HIPCHK(hipStreamSynchronize(m->stream));
+  for (auto& r : m->trecs) {
+    m->evpool.push_back(r.a);
+    m->evpool.push_back(r.b);
+  }
+  m->trecs.clear();
+  m->timing = enable != 0;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_timing_read(fg_model* m, int32_t kind, int64_t* launches, double* ms,
+                                  double* flops, double* bytes) {
+  if (!m) return seterr(FG_EARG, "NULL argument");
+  if (kind < 0 || kind >= FG_K_NKINDS) return seterr(FG_EARG, "kind %d out of range", kind);
+  GUARD(m);
+  HIPCHK(hipStreamSynchronize(m->stream));
+  int64_t n = 0;
+  double t = 0, f = 0, b = 0;
+  for (auto& r : m->trecs) {
+    if (r.kind != kind) continue;
+    float e = 0.f;
+    HIPCHK(hipEventElapsedTime(&e, r.a, r.b));
+    ++n;
+    t += e;
+    f += r.flops;
+    b += r.bytes;
+  }
+  if (launches) *launches = n;
+  if (ms) *ms = t;
+  if (flops) *flops = f;
+  if (bytes) *bytes = b;
   return FG_OK;
 }
 

@@ -115,9 +115,11 @@ void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
                             float* y);
-// argmax into out (and out2 if set); when d_len is set, row 0 increments it.
+// argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +
+// row] (and the logits row into lgs_out at that slot, when set), then
+// *d_len += 1.
 void launch_argmax_step(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out,
-                        int32_t* out2, int32_t* d_len);
+                        int32_t* out2, int32_t* d_len, const int32_t* d_len0, float* lgs_out);
 
 // Per-row argmax (first max) of logits [rows][V] -> out [rows].
 void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out);

@@ -427,18 +427,27 @@ __device__ __forceinline__ void amax_merge(float& v, int& i, float v2, int i2) {
   }
 }
 
+// One block per row. With a step record (d_len/d_len0 set), the chosen id
+// also goes to out2[(len - len0) * rows + row] and, when lgs_out is set, the
+// whole logits row is copied to lgs_out at the same slot: a replayed greedy
+// graph then needs no per-step pointers.
 __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits, int V,
                                                 int32_t* __restrict__ out,
                                                 int32_t* __restrict__ out2,
-                                                int32_t* __restrict__ d_len) {
+                                                const int32_t* __restrict__ d_len,
+                                                const int32_t* __restrict__ d_len0,
+                                                float* __restrict__ lgs_out) {
   __shared__ float rv[4];
   __shared__ int ri[4];
-  const int64_t row = blockIdx.x;
+  const int64_t row = blockIdx.x, rows = gridDim.x;
   const float* l = logits + row * V;
+  const int64_t slot = d_len ? (int64_t)(*d_len - *d_len0) * rows + row : 0;
+  float* cp = (d_len && lgs_out) ? lgs_out + slot * V : nullptr;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int j = threadIdx.x; j < V; j += 256) {
     const float v = l[j];
+    if (cp) cp[j] = v;
     if (v > bv) {
       bv = v;
       bi = j;
@@ -460,18 +469,24 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
     for (int k = 1; k < 4; ++k) amax_merge(bv, bi, rv[k], ri[k]);
     if (bi == 0x7fffffff) bi = 0;  // all -inf / NaN: position 1, as the scan starts there
     out[row] = bi;
-    if (out2) out2[row] = bi;
-    if (d_len && row == 0) *d_len = *d_len + 1;
+    if (out2 && d_len) out2[slot] = bi;
   }
 }
 
+// Advance the device-side cache length after a replayed step.
+__global__ void k_advance(int32_t* d_len) {
+  if (threadIdx.x == 0) *d_len = *d_len + 1;
+}
+
 void launch_argmax_step(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out,
-                        int32_t* out2, int32_t* d_len) {
-  hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(256), 0, s, logits, V, out, out2, d_len);
+                        int32_t* out2, int32_t* d_len, const int32_t* d_len0, float* lgs_out) {
+  hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(256), 0, s, logits, V, out, out2, d_len,
+                     d_len0, lgs_out);
+  if (d_len) hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, d_len);
 }
 
 void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out) {
-  launch_argmax_step(s, logits, rows, V, out, nullptr, nullptr);
+  launch_argmax_step(s, logits, rows, V, out, nullptr, nullptr, nullptr, nullptr);
 }
 
 __global__ __launch_bounds__(256) void k_nll(const float* __restrict__ logits,

@@ -31,8 +31,10 @@ EXPORTS = (
     "fg_version", "fg_last_error", "fg_model_create", "fg_model_load", "fg_model_destroy",
     "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_destroy",
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
-    "fg_decode_greedy", "fg_sync", "fg_model_bytes",
+    "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
 )
+
+KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other"}
 
 
 class FgptError(RuntimeError):
@@ -85,6 +87,9 @@ def load_library(path: str = LIB_PATH):
         "fg_decode_greedy": (i32, [_vp, _vp, _i, i32, _i, _f]),
         "fg_sync": (i32, [_vp]),
         "fg_model_bytes": (i32, [_vp, C.POINTER(i64), C.POINTER(i64)]),
+        "fg_timing": (i32, [_vp, i32]),
+        "fg_timing_read": (i32, [_vp, i32, C.POINTER(i64), C.POINTER(C.c_double),
+                                 C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -180,6 +185,18 @@ class Model:
         w, k = C.c_int64(), C.c_int64()
         _check(_LIB.fg_model_bytes(self._h, C.byref(w), C.byref(k)))
         return w.value, k.value
+
+    def timing(self, enable: bool):
+        _check(_LIB.fg_timing(self._h, 1 if enable else 0))
+
+    def timing_read(self) -> dict:
+        """{kind: (launches, ms, flops, bytes)} of the launches recorded so far."""
+        out = {}
+        for k, name in KERNEL_KINDS.items():
+            n, ms, fl, by = C.c_int64(), C.c_double(), C.c_double(), C.c_double()
+            _check(_LIB.fg_timing_read(self._h, k, C.byref(n), C.byref(ms), C.byref(fl), C.byref(by)))
+            out[name] = (n.value, ms.value, fl.value, by.value)
+        return out
 
     def kv(self, B: int, maxT: int) -> "KV":
         return KV(self, B, maxT)

@@ -127,6 +127,24 @@ int32_t fg_decode_greedy(fg_model *m, fg_kv *kv, const int32_t *ids, int32_t n_s
 /* Block until the handle's queued work is done. */
 int32_t fg_sync(fg_model *m);
 
+/* Kernel timing, the device-side counterpart of chat_text --stats
+ * (src/app/chat_text.f90:250-282,465-468). With timing on, every launch the
+ * handle makes outside graph capture (fg_decode_greedy then runs its steps
+ * eagerly) is bracketed by HIP events on the stream it runs on, and tagged
+ * with its kernel kind and its algorithmic flops and HBM bytes. Enabling or
+ * disabling clears the records. fg_timing_read sums one kind. */
+enum {
+  FG_K_GEMM = 0,        /* MFMA GEMM (prefill, batched decode linears)   */
+  FG_K_GEMV = 1,        /* small-M GEMV (B=1 decode linears)             */
+  FG_K_ATTN_CHUNK = 2,  /* causal chunk attention (prefill)              */
+  FG_K_ATTN_DECODE = 3, /* single-query attention (decode)               */
+  FG_K_OTHER = 4,       /* embedding+norm, argmax, NLL                   */
+  FG_K_NKINDS = 5
+};
+int32_t fg_timing(fg_model *m, int32_t enable);
+int32_t fg_timing_read(fg_model *m, int32_t kind, int64_t *launches, double *ms, double *flops,
+                       double *bytes);
+
 /* Bytes of HBM the handle holds (weights, workspace, tables). Diagnostic,
  * the counterpart of gpublas_count / gpublas_bufs (gpu_shim.cpp:172-186). */
 int32_t fg_model_bytes(const fg_model *m, int64_t *weight_bytes, int64_t *work_bytes);
