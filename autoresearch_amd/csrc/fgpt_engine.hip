@@ -61,8 +61,12 @@ struct fg_model {
   float* d_sin = nullptr;
   int rope_cap = 0, rope_n = 0;
   Work ws;
-  float* fk = nullptr;  // forward-pass K/V scratch [rows][KH*hd]
-  float* fv = nullptr;
+  // bf16 hi/lo planes for the MFMA chunk attention: q [rows][qd], and
+  // k / v^T for up to split_kv_elems elements per plane
+  uint16_t* qs = nullptr;
+  uint16_t* ks = nullptr;
+  uint16_t* vt = nullptr;
+  int64_t split_kv_elems = 0;
   int64_t work_bytes = 0;
   int64_t gen = 0;      // bumped whenever a buffer a captured graph uses moves
   std::atomic<int> busy{0};
@@ -236,11 +240,11 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
 void free_work(fg_model* m) {
   Work& ws = m->ws;
   void* ptrs[] = {ws.x, ws.q, ws.ao, ws.h, ws.logits, ws.ids, ws.tgt, ws.nll, ws.stat, ws.amax,
-                  m->fk, m->fv};
+                  m->qs};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   ws = Work();
-  m->fk = m->fv = nullptr;
+  m->qs = nullptr;
   m->work_bytes = 0;
 }
 
@@ -266,13 +270,29 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
   RCCHK(alloc((void**)&ws.nll, rows * 4));
   RCCHK(alloc((void**)&ws.stat, rows * 4));
   RCCHK(alloc((void**)&ws.amax, rows * 4));
-  RCCHK(alloc((void**)&m->fk, rows * d.kvd() * 4));
-  RCCHK(alloc((void**)&m->fv, rows * d.kvd() * 4));
+  RCCHK(alloc((void**)&m->qs, rows * d.qd() * 2 * 2));
   ws.rows = rows;
   m->work_bytes = total;
   m->gen++;
   return FG_OK;
 }
+
+// hi/lo key and value planes for B sequences of npos (padded) positions.
+int32_t ensure_split(fg_model* m, int64_t elems) {
+  if (elems <= m->split_kv_elems) return FG_OK;
+  HIPCHK(hipStreamSynchronize(m->stream));
+  if (m->ks) HIPCHK(hipFree(m->ks));
+  if (m->vt) HIPCHK(hipFree(m->vt));
+  m->ks = m->vt = nullptr;
+  m->split_kv_elems = 0;
+  HIPCHK(hipMalloc((void**)&m->ks, (size_t)elems * 2 * 2));
+  HIPCHK(hipMalloc((void**)&m->vt, (size_t)elems * 2 * 2));
+  m->split_kv_elems = elems;
+  m->gen++;
+  return FG_OK;
+}
+
+int npos_pad(int n) { return (n + 63) / 64 * 64; }
 
 // y = epi(x W^T): GEMV for up to four token rows, MFMA GEMM beyond.
 // Algorithmic traffic: weights once, activations in and out once (RESID
@@ -316,8 +336,8 @@ void layer_stack(fg_model* m, hipStream_t s, int B, int T, int pos0, const int32
   const double at_flops = 4.0 * d.hd * d.H * B * pairs;
   const double at_bytes = (double)B * (2.0 * T * d.qd() + 2.0 * (pos_host + T) * d.kvd()) * 4;
   for (int l = 0; l < d.L; ++l) {
-    float* lk = kc + l * lstride;
-    float* lv = vc + l * lstride;
+    float* lk = kc ? kc + l * lstride : nullptr;  // null: no persistent cache (gpt_forward)
+    float* lv = vc ? vc + l * lstride : nullptr;
     GemvArgs a = base_args(m);
     a.M = rows;
     a.T = T;
@@ -326,16 +346,37 @@ void layer_stack(fg_model* m, hipStream_t s, int B, int T, int pos0, const int32
     a.vc = lv;
     a.maxT = maxT;
     // q, k, v = rmsnorm(x) Wqkv^T, RoPE on q and k, k/v appended to the cache
+    // (and, for a chunk, written as bf16 hi/lo planes for the MFMA attention)
+    // single-query kernel only for a cached step; a cache-less forward
+    // (gpt_forward, kc == null) always takes the chunk kernel
+    const bool one = (T == 1 && lk != nullptr);
+    const int npos = npos_pad(pos0 + T);
+    if (!one) {
+      a.qs = m->qs;
+      a.q_plane = (int64_t)rows * d.qd();
+      a.ks = m->ks;
+      a.vt = m->vt;
+      a.npos = npos;
+      a.kv_plane = (int64_t)B * npos * d.kvd();
+    }
     a.x = ws.x; a.w = m->w.qkv(l); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
     linear(m, s, GV_QKV, a, d_pos);
-    if (T == 1)
+    if (one) {
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
         launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, ws.ao);
       });
-    else
+    } else {
+      if (pos0 > 0)  // earlier cache positions enter the chunk's key planes
+        timed(m, s, FG_K_OTHER, 0, (double)B * pos0 * d.kvd() * 16, [&] {
+          launch_split_cache(s, d, lk, lv, B, maxT, pos0, npos, a.kv_plane, m->ks, m->vt);
+        });
       timed(m, s, FG_K_ATTN_CHUNK, at_flops, at_bytes, [&] {
-        launch_attn_prefill(s, d, ws.q, lk, lv, B, T, maxT, pos0, ws.ao);
+        launch_attn_mfma(s, d, m->qs, m->ks, m->vt, B, T, npos, pos0, a.q_plane, a.kv_plane,
+                         ws.ao);
       });
+    }
+    a.qs = nullptr;
+    a.ks = a.vt = nullptr;
     // x += attn_out Wproj^T
     a.x = ws.ao; a.w = m->w.proj(l); a.N = d.D; a.K = d.qd(); a.norm = 0; a.y = ws.x;
     linear(m, s, GV_RESID, a, d_pos);
@@ -365,10 +406,11 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   const int64_t rows = (int64_t)B * T;
   if (rows > (1ll << 30) / m->d.V) return seterr(FG_EARG, "B*T too large");
   RCCHK(ensure_work(m, rows));
+  RCCHK(ensure_split(m, (int64_t)B * npos_pad(T) * m->d.kvd()));
   float* logits = d_logits ? d_logits : m->ws.logits;
   const double eb = (double)rows * m->d.D * 6, vb = (double)rows * m->d.V * 4;
   timed(m, s, FG_K_OTHER, 0, eb, [&] { launch_embed_norm(s, m->d, m->w.wte, d_ids, rows, m->ws.x); });
-  layer_stack(m, s, B, T, 0, nullptr, m->fk, m->fv, T, 0, logits);
+  layer_stack(m, s, B, T, 0, nullptr, nullptr, nullptr, T, 0, logits);
   if (d_tgt && d_nll)
     timed(m, s, FG_K_OTHER, 0, vb, [&] { launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll); });
   HIPCHK(hipGetLastError());
@@ -523,6 +565,8 @@ extern "C" int32_t fg_model_destroy(fg_model* m) {
   (void)hipSetDevice(m->device);
   if (m->stream) (void)hipStreamSynchronize(m->stream);
   free_work(m);
+  if (m->ks) (void)hipFree(m->ks);
+  if (m->vt) (void)hipFree(m->vt);
   if (m->w.base) (void)hipFree(m->w.base);
   if (m->d_cos) (void)hipFree(m->d_cos);
   if (m->d_sin) (void)hipFree(m->d_sin);
@@ -695,6 +739,8 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
   RCCHK(check_rope(m, kv->len + TB));
   const int64_t rows = (int64_t)B * TB;
   RCCHK(ensure_work(m, rows));
+  if (TB > 1) RCCHK(ensure_split(m, (int64_t)B * npos_pad(kv->len + TB) * m->d.kvd()));
+  // (TB == 1 runs the single-query kernel on the fp32 cache)
   hipStream_t s = m->stream;
   HIPCHK(hipMemcpyAsync(m->ws.ids, h_ids, rows * 4, hipMemcpyHostToDevice, s));
   timed(m, s, FG_K_OTHER, 0, (double)rows * m->d.D * 6,

@@ -85,10 +85,17 @@ struct GemvArgs {
   const float* sinb;
   int pos0;         // position of row 0 (row m is at pos0 + m % T)
   int T;            // rows per sequence
-  float* kc;        // KV cache of this layer, [B][maxT][KH*hd]
+  float* kc;        // KV cache of this layer, [B][maxT][KH*hd] (nullable)
   float* vc;
   int maxT;
   int H, KH, hd;
+  // bf16 hi/lo copies for the MFMA chunk attention (nullable):
+  // qs [B][H][T][hd], ks [B][KH][npos][hd], vt [B][KH][hd][npos]
+  uint16_t* qs;
+  uint16_t* ks;
+  uint16_t* vt;
+  int npos;
+  int64_t q_plane, kv_plane;  // elements between the hi and lo planes
 };
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 
@@ -102,10 +109,17 @@ void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const floa
                         const float* vc, int B, int maxT, int len, float* y, float* scratch,
                         int64_t scratch_floats);
 
-// Causal chunk attention: q [B][T][H][hd] at positions pos0..pos0+T-1
-// against the cache positions 0..pos0+t -> y [B][T][H*hd].
-void launch_attn_prefill(hipStream_t s, const Dims& d, const float* q, const float* kc,
-                         const float* vc, int B, int T, int maxT, int pos0, float* y);
+// Causal chunk attention of T queries at positions pos0..pos0+T-1 against
+// keys 0..pos0+t, on MFMA from the bf16 hi/lo planes (layouts of
+// GemvArgs::qs/ks/vt; npos = padded row stride of the key planes) ->
+// y [B][T][H*hd].
+void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
+                      const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
+                      int64_t kv_plane, float* y);
+// Fill the hi/lo key/value planes for cache positions [0, n) from the fp32
+// cache of one layer ([B][maxT][KH*hd]).
+void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const float* vc, int B,
+                        int maxT, int n, int npos, int64_t kv_plane, uint16_t* ks, uint16_t* vt);
 
 // Variants whose position / cache length comes from device memory (so a
 // captured decode step replays at successive positions).

@@ -15,6 +15,7 @@
 
 #include "fgpt_internal.h"
 #include "kern_common.h"
+#include "kern_epi.h"
 
 namespace fgpt {
 
@@ -79,50 +80,6 @@ void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const in
 }
 
 // ------------------------------------------------------------ epilogues
-// Shared by the GEMV and the MFMA GEMM: row m of the M token rows, stored
-// weight row r of N. The QKV epilogue receives a rotation pair (stored rows
-// r, r+1, i.e. head dims j and j+hd/2) at once.
-struct EpiCtx {
-  int b, pos;
-};
-
-__device__ __forceinline__ EpiCtx epi_ctx(const GemvArgs& a, int m, int pos0) {
-  EpiCtx c;
-  c.b = m / a.T;
-  c.pos = pos0 + (m % a.T);
-  return c;
-}
-
-// QKV pair epilogue: x1 = dim j, x2 = dim j+hd/2 of a q, k or v head row.
-__device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos0, int r, float x1,
-                                               float x2) {
-  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
-  const EpiCtx c = epi_ctx(a, m, pos0);
-  if (r < qd + kd) {
-    const int base = (r < qd) ? r : r - qd;
-    const int head = base / hd, j = (base % hd) >> 1;
-    const float cs = a.cosb[(int64_t)c.pos * (hd / 2) + j];
-    const float sn = a.sinb[(int64_t)c.pos * (hd / 2) + j];
-    const float y1 = x1 * cs + x2 * sn;
-    const float y2 = x1 * (-sn) + x2 * cs;
-    if (r < qd) {
-      float* q = a.y + (int64_t)m * qd + head * hd;
-      q[j] = y1;
-      q[j + hd / 2] = y2;
-    } else {
-      float* k = a.kc + ((int64_t)c.b * a.maxT + c.pos) * kd + head * hd;
-      k[j] = y1;
-      k[j + hd / 2] = y2;
-    }
-  } else {
-    const int base = r - qd - kd;
-    const int head = base / hd, j = (base % hd) >> 1;
-    float* v = a.vc + ((int64_t)c.b * a.maxT + c.pos) * kd + head * hd;
-    v[j] = x1;
-    v[j + hd / 2] = x2;
-  }
-}
-
 template <int EPI>
 __device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, float v) {
   float* y = a.y + (int64_t)m * a.N + r;
@@ -191,7 +148,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restr
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         if (EPI == GV_QKV) {
-          qkv_pair_store(a, m, pos0, 2 * u, acc0[m], acc1[m]);
+          qkv_pair_epilogue(a, m, pos0, 2 * u, acc0[m], acc1[m]);
         } else {
           single_store<EPI>(a, m, 2 * u, acc0[m]);
           single_store<EPI>(a, m, 2 * u + 1, acc1[m]);
@@ -296,126 +253,6 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
 void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const float* kc,
                         const float* vc, int B, int maxT, int len, float* y, float*, int64_t) {
   launch_attn_decode_pos(s, d, q, kc, vc, B, maxT, nullptr, len, y);
-}
-
-// ------------------------------------------------------------ chunk attention
-// Causal attention of T queries (positions pos0..pos0+T-1) against cache
-// positions 0..pos0+t (fortran_attn.f90:30-117 at pos0 = 0, :376-425 in
-// general), flash-style: 32 query rows per block, 64-position K/V tiles in
-// LDS, running max / sum per row. fp32 VALU arithmetic.
-template <int HD>
-__global__ __launch_bounds__(256) void k_attn_chunk(const float* __restrict__ q,
-                                                    const float* __restrict__ kc,
-                                                    const float* __restrict__ vc, int H, int KH,
-                                                    int T, int maxT, int pos0,
-                                                    float* __restrict__ y) {
-  constexpr int QT = 32, KT = 64, KP = HD + 4;  // padded K row (floats)
-  constexpr int DPT = HD / 8;                   // output dims per thread
-  extern __shared__ float sm[];
-  float* sQ = sm;                 // [QT][HD]
-  float* sK = sQ + QT * HD;       // [KT][KP]
-  float* sV = sK + KT * KP;       // [KT][HD]
-  float* sP = sV + KT * HD;       // [QT][KT]
-  const int qt = blockIdx.x, bh = blockIdx.y, b = bh / H, h = bh % H, kvh = h / (H / KH);
-  const int tid = threadIdx.x, r = tid >> 3, c8 = tid & 7;
-  const int kd = KH * HD, qd = H * HD;
-  const int q0 = qt * QT;
-  const int nq = min(QT, T - q0);
-  for (int i = tid; i < QT * HD; i += 256) {
-    const int rr = i / HD, dd = i % HD;
-    sQ[i] = (rr < nq) ? q[((int64_t)b * T + q0 + rr) * qd + h * HD + dd] : 0.f;
-  }
-  const float scale = 1.0f / sqrtf((float)HD);
-  const int qpos = pos0 + q0 + r;  // this thread's query position
-  float m_run = -FLT_MAX, l_run = 0.f;
-  float o[DPT];
-#pragma unroll
-  for (int i = 0; i < DPT; ++i) o[i] = 0.f;
-  const int last_key = pos0 + q0 + nq - 1;
-  const float* Kb = kc + (int64_t)b * maxT * kd + kvh * HD;
-  const float* Vb = vc + (int64_t)b * maxT * kd + kvh * HD;
-  for (int k0 = 0; k0 <= last_key; k0 += KT) {
-    __syncthreads();
-    for (int i = tid; i < KT * HD; i += 256) {
-      const int kk = i / HD, dd = i % HD;
-      const bool ok = (k0 + kk) <= last_key;
-      sK[kk * KP + dd] = ok ? Kb[(int64_t)(k0 + kk) * kd + dd] : 0.f;
-      sV[kk * HD + dd] = ok ? Vb[(int64_t)(k0 + kk) * kd + dd] : 0.f;
-    }
-    __syncthreads();
-    float sc[KT / 8];
-    float mx = -FLT_MAX;
-#pragma unroll
-    for (int j = 0; j < KT / 8; ++j) {
-      const int kk = c8 + 8 * j;
-      const float* qr = sQ + r * HD;
-      const float* kr = sK + kk * KP;
-      float acc = 0.f;
-#pragma unroll 8
-      for (int dd = 0; dd < HD; dd += 4) {
-        const float4 a4 = *(const float4*)(qr + dd);
-        const float4 k4 = *(const float4*)(kr + dd);
-        acc += a4.x * k4.x + a4.y * k4.y + a4.z * k4.z + a4.w * k4.w;
-      }
-      float s = acc * scale;
-      if (k0 + kk > qpos) s = -INFINITY;
-      sc[j] = s;
-      mx = fmaxf(mx, s);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = expf(m_run - m_new);
-    float ps = 0.f;
-#pragma unroll
-    for (int j = 0; j < KT / 8; ++j) {
-      const float p = expf(sc[j] - m_new);
-      ps += p;
-      sP[r * KT + c8 + 8 * j] = p;
-    }
-    ps += __shfl_xor(ps, 1, 64);
-    ps += __shfl_xor(ps, 2, 64);
-    ps += __shfl_xor(ps, 4, 64);
-    l_run = l_run * alpha + ps;
-    m_run = m_new;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < DPT; ++i) o[i] *= alpha;
-    for (int kk = 0; kk < KT; ++kk) {
-      const float p = sP[r * KT + kk];
-#pragma unroll
-      for (int i = 0; i < DPT; ++i) o[i] += p * sV[kk * HD + c8 + 8 * i];
-    }
-  }
-  if (r < nq) {
-    const float inv = 1.0f / l_run;
-    float* yr = y + ((int64_t)b * T + q0 + r) * qd + h * HD;
-#pragma unroll
-    for (int i = 0; i < DPT; ++i) yr[c8 + 8 * i] = o[i] * inv;
-  }
-}
-
-void launch_attn_prefill(hipStream_t s, const Dims& d, const float* q, const float* kc,
-                         const float* vc, int B, int T, int maxT, int pos0, float* y) {
-  dim3 grid((T + 31) / 32, B * d.H);
-  static bool lds_set = false;
-  if (!lds_set) {  // the 128-wide variant stages 89 KiB of LDS
-    (void)hipFuncSetAttribute((const void*)k_attn_chunk<128>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute((const void*)k_attn_chunk<64>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    lds_set = true;
-  }
-  if (d.hd == 128) {
-    const size_t lds = sizeof(float) * (32 * 128 + 64 * 132 + 64 * 128 + 32 * 64);
-    hipLaunchKernelGGL((k_attn_chunk<128>), grid, dim3(256), lds, s, q, kc, vc, d.H, d.KH, T,
-                       maxT, pos0, y);
-  } else {
-    const size_t lds = sizeof(float) * (32 * 64 + 64 * 68 + 64 * 64 + 32 * 64);
-    hipLaunchKernelGGL((k_attn_chunk<64>), grid, dim3(256), lds, s, q, kc, vc, d.H, d.KH, T, maxT,
-                       pos0, y);
-  }
 }
 
 // ------------------------------------------------------------ argmax / nll

@@ -1,0 +1,75 @@
+// kern_epi.h -- the fused QKV epilogue shared by the GEMV and the MFMA GEMM.
+//
+// A rotation pair (stored rows r, r+1 of the pair-interleaved QKV matrix:
+// head dims j and j+hd/2) arrives for token row m. q and k are rotated
+// (src/lib/fortran_rope.f90:45-46: y1 = x1 c + x2 s, y2 = -x1 s + x2 c);
+// k and the un-rotated v are appended to the fp32 cache at the row's
+// position (src/lib/fortran_kv.f90:112-116). When the split pointers are set
+// (chunk attention follows), q, k and v are also written as bf16 hi/lo
+// planes in the layouts the MFMA attention kernel reads:
+//   qs [B][H][T][hd], ks [B][KH][npos][hd], vt [B][KH][hd][npos]
+// (hi plane first, lo plane `*_plane` elements later).
+#pragma once
+#include "fgpt_internal.h"
+#include "kern_common.h"
+
+namespace fgpt {
+
+// v = hi + lo in bf16: hi at p, lo at p + plane.
+__device__ __forceinline__ void split_bf16(float v, uint16_t* p, int64_t plane) {
+  const uint16_t h = f32_to_bf16_rne(v);
+  p[0] = h;
+  p[plane] = f32_to_bf16_rne(v - bf16_to_f32(h));
+}
+
+__device__ __forceinline__ void qkv_pair_epilogue(const GemvArgs& a, int m, int pos0, int r,
+                                                  float x1, float x2) {
+  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
+  const int b = m / a.T, t = m % a.T, pos = pos0 + t;
+  if (r < qd + kd) {
+    const bool isq = r < qd;
+    const int base = isq ? r : r - qd;
+    const int head = base / hd, j = (base % hd) >> 1;
+    const float cs = a.cosb[(int64_t)pos * (hd / 2) + j];
+    const float sn = a.sinb[(int64_t)pos * (hd / 2) + j];
+    const float y1 = x1 * cs + x2 * sn;
+    const float y2 = x1 * (-sn) + x2 * cs;
+    if (isq) {
+      if (a.qs) {
+        uint16_t* p = a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd;
+        split_bf16(y1, p + j, a.q_plane);
+        split_bf16(y2, p + j + hd / 2, a.q_plane);
+      } else {
+        float* q = a.y + (int64_t)m * qd + head * hd;
+        q[j] = y1;
+        q[j + hd / 2] = y2;
+      }
+    } else {
+      if (a.kc) {
+        float* k = a.kc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
+        k[j] = y1;
+        k[j + hd / 2] = y2;
+      }
+      if (a.ks) {
+        uint16_t* p = a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd;
+        split_bf16(y1, p + j, a.kv_plane);
+        split_bf16(y2, p + j + hd / 2, a.kv_plane);
+      }
+    }
+  } else {
+    const int base = r - qd - kd;
+    const int head = base / hd, j = (base % hd) >> 1;
+    if (a.vc) {
+      float* v = a.vc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
+      v[j] = x1;
+      v[j + hd / 2] = x2;
+    }
+    if (a.vt) {
+      uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
+      split_bf16(x1, p + (int64_t)j * a.npos, a.kv_plane);
+      split_bf16(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
+    }
+  }
+}
+
+}  // namespace fgpt

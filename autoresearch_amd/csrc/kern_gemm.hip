@@ -18,6 +18,7 @@
 // with the next K step's global loads issued before the current MFMAs.
 #include "fgpt_internal.h"
 #include "kern_common.h"
+#include "kern_epi.h"
 
 namespace fgpt {
 
@@ -49,31 +50,6 @@ __device__ __forceinline__ void split_store(const float4 a, const float4 b, uint
   pl.w = l[6] | ((uint32_t)l[7] << 16);
   *(uint4*)hi = ph;
   *(uint4*)lo = pl;
-}
-
-// Epilogue helpers (same semantics as the GEMV epilogues in kern_core.hip).
-__device__ __forceinline__ void g_qkv_pair(const GemvArgs& a, int m, int pos0, int r, float x1,
-                                           float x2) {
-  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
-  const int b = m / a.T, pos = pos0 + (m % a.T);
-  if (r < qd + kd) {
-    const int base = (r < qd) ? r : r - qd;
-    const int head = base / hd, j = (base % hd) >> 1;
-    const float cs = a.cosb[(int64_t)pos * (hd / 2) + j];
-    const float sn = a.sinb[(int64_t)pos * (hd / 2) + j];
-    const float y1 = x1 * cs + x2 * sn;
-    const float y2 = x1 * (-sn) + x2 * cs;
-    float* dst = (r < qd) ? (a.y + (int64_t)m * qd + head * hd)
-                          : (a.kc + ((int64_t)b * a.maxT + pos) * kd + head * hd);
-    dst[j] = y1;
-    dst[j + hd / 2] = y2;
-  } else {
-    const int base = r - qd - kd;
-    const int head = base / hd, j = (base % hd) >> 1;
-    float* v = a.vc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
-    v[j] = x1;
-    v[j + hd / 2] = x2;
-  }
 }
 
 template <int EPI>
@@ -152,7 +128,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemvArgs a, const int32_t* __restr
     if (a.norm) v *= sinv[ml];
     if (EPI == GV_QKV) {
       const float partner = __shfl_xor(v, 1, 64);
-      if (m < M && (j & 1) == 0) g_qkv_pair(a, m, pos0, n, v, partner);
+      if (m < M && (j & 1) == 0) qkv_pair_epilogue(a, m, pos0, n, v, partner);
     } else if (m < M) {
       float* y = a.y + (int64_t)m * a.N + n;
       if (EPI == GV_RESID) {

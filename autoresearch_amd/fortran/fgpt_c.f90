@@ -1,0 +1,154 @@
+! fgpt_c.f90 -- iso_c_binding interface to the gfx950 engine (include/fgpt.h).
+!
+! The binding style is the reference's own for its rocBLAS shim
+! (src/lib/fortran_blas_gpu.f90:30-59 binding src/lib/gpu_shim.cpp:98-122):
+! plain bind(C) interfaces, integer return codes, pointers passed as
+! assumed-size arrays or type(c_ptr).
+module fgpt_c
+  use, intrinsic :: iso_c_binding
+  implicit none
+  private
+
+  integer(c_int32_t), parameter, public :: FG_OK = 0, FG_EARG = -1, FG_EDIMS = -2, &
+      FG_EWEIGHT = -3, FG_EHIP = -4, FG_EFULL = -5, FG_EROPE = -6, FG_ENODEV = -7, &
+      FG_EBUSY = -8, FG_EARCH = -9
+
+  type, bind(C), public :: fg_dims
+    integer(c_int32_t) :: n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size
+    real(c_float) :: eps
+  end type fg_dims
+
+  public :: fg_version, fg_last_error, fg_model_create, fg_model_load, fg_model_destroy, &
+      fg_set_rope, fg_forward, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
+      fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_error_message
+
+  interface
+    integer(c_int32_t) function fg_version() bind(C, name="fg_version")
+      import :: c_int32_t
+    end function
+
+    integer(c_int32_t) function fg_last_error(buf, len) bind(C, name="fg_last_error")
+      import :: c_int32_t, c_char
+      character(kind=c_char), intent(out) :: buf(*)
+      integer(c_int32_t), value :: len
+    end function
+
+    integer(c_int32_t) function fg_model_create(dims, wte, c_q, c_k, c_v, c_proj, c_fc, &
+        c_proj2, lm_head, out) bind(C, name="fg_model_create")
+      import :: c_int32_t, c_float, c_ptr, fg_dims
+      type(fg_dims), intent(in) :: dims
+      real(c_float), intent(in) :: wte(*), c_q(*), c_k(*), c_v(*), c_proj(*), c_fc(*), &
+          c_proj2(*), lm_head(*)
+      type(c_ptr), intent(out) :: out
+    end function
+
+    integer(c_int32_t) function fg_model_load(dims, weights_dir, out) &
+        bind(C, name="fg_model_load")
+      import :: c_int32_t, c_char, c_ptr, fg_dims
+      type(fg_dims), intent(in) :: dims
+      character(kind=c_char), intent(in) :: weights_dir(*)
+      type(c_ptr), intent(out) :: out
+    end function
+
+    integer(c_int32_t) function fg_model_destroy(m) bind(C, name="fg_model_destroy")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: m
+    end function
+
+    integer(c_int32_t) function fg_set_rope(m, pos0, n_pos, cos_buf, sin_buf) &
+        bind(C, name="fg_set_rope")
+      import :: c_int32_t, c_float, c_ptr
+      type(c_ptr), value :: m
+      integer(c_int32_t), value :: pos0, n_pos
+      real(c_float), intent(in) :: cos_buf(*), sin_buf(*)
+    end function
+
+    integer(c_int32_t) function fg_forward(m, ids, B, T, logits, targets, nll) &
+        bind(C, name="fg_forward")
+      import :: c_int32_t, c_float, c_ptr
+      type(c_ptr), value :: m
+      integer(c_int32_t), intent(in) :: ids(*)
+      integer(c_int32_t), value :: B, T
+      real(c_float), intent(out) :: logits(*)
+      type(c_ptr), value :: targets, nll
+    end function
+
+    integer(c_int32_t) function fg_kv_create(m, B, maxT, out) bind(C, name="fg_kv_create")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: m
+      integer(c_int32_t), value :: B, maxT
+      type(c_ptr), intent(out) :: out
+    end function
+
+    integer(c_int32_t) function fg_kv_destroy(kv) bind(C, name="fg_kv_destroy")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: kv
+    end function
+
+    integer(c_int32_t) function fg_kv_len(kv, len) bind(C, name="fg_kv_len")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: kv
+      integer(c_int32_t), intent(out) :: len
+    end function
+
+    integer(c_int32_t) function fg_kv_set_len(kv, len) bind(C, name="fg_kv_set_len")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: kv
+      integer(c_int32_t), value :: len
+    end function
+
+    integer(c_int32_t) function fg_step(m, kv, ids, logits, next_ids) bind(C, name="fg_step")
+      import :: c_int32_t, c_float, c_ptr
+      type(c_ptr), value :: m, kv
+      integer(c_int32_t), intent(in) :: ids(*)
+      real(c_float), intent(out) :: logits(*)
+      type(c_ptr), value :: next_ids
+    end function
+
+    integer(c_int32_t) function fg_step_multi(m, kv, ids, TB, logits, next_ids) &
+        bind(C, name="fg_step_multi")
+      import :: c_int32_t, c_float, c_ptr
+      type(c_ptr), value :: m, kv
+      integer(c_int32_t), intent(in) :: ids(*)
+      integer(c_int32_t), value :: TB
+      real(c_float), intent(out) :: logits(*)
+      type(c_ptr), value :: next_ids
+    end function
+
+    integer(c_int32_t) function fg_decode_greedy(m, kv, ids, n_steps, ids_out, logits_out) &
+        bind(C, name="fg_decode_greedy")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: m, kv
+      integer(c_int32_t), intent(in) :: ids(*)
+      integer(c_int32_t), value :: n_steps
+      integer(c_int32_t), intent(out) :: ids_out(*)
+      type(c_ptr), value :: logits_out
+    end function
+
+    integer(c_int32_t) function fg_sync(m) bind(C, name="fg_sync")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: m
+    end function
+  end interface
+
+contains
+
+  ! The engine's message for the calling thread's last error.
+  function fg_error_message() result(msg)
+    character(len=:), allocatable :: msg
+    character(kind=c_char) :: buf(512)
+    integer(c_int32_t) :: rc
+    integer :: i, n
+    rc = fg_last_error(buf, 512_c_int32_t)
+    n = 0
+    do i = 1, 512
+      if (buf(i) == c_null_char) exit
+      n = i
+    end do
+    allocate (character(len=n) :: msg)
+    do i = 1, n
+      msg(i:i) = buf(i)
+    end do
+  end function fg_error_message
+
+end module fgpt_c

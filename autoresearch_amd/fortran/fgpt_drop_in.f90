@@ -1,0 +1,344 @@
+! fgpt_drop_in.f90 -- the fortran_gpt model API, routed to the gfx950 engine.
+!
+! gpt_forward, gpt_step and gpt_step_multi keep the names and argument lists
+! of the reference (src/lib/fortran_gpt.f90:54-92, src/lib/fortran_kv.f90:
+! 26-55 and :160-189), so an app switches by changing its `use` line.
+! load_gpt_weights keeps the reference loader's signature and .npy layout
+! (src/lib/load_weights.f90:830-874) with its loud failures.
+!
+! What changes under the same arguments:
+!  - The weights are uploaded to HBM (bf16, exact) on the first call and kept
+!    there. Later calls with the same arrays (same addresses and dims) reuse
+!    them; different arrays re-upload. Weights changed in place are not seen:
+!    call fgpt_release() after changing them.
+!  - The KV cache lives in HBM. cache_k / cache_v are accepted and left
+!    untouched; cache_len is honoured in and out exactly as in the reference
+!    (resetting it to 0 starts a new sequence).
+!  - RoPE rows are taken from the caller's tables on every call (the rows of
+!    the positions being computed), as the reference uses them.
+!  - Errors stop the program with the engine's message, the reference's
+!    loud-failure convention (print + exit, or error stop).
+module fgpt_drop_in_mod
+  use, intrinsic :: iso_c_binding
+  use, intrinsic :: iso_fortran_env, only: int8, error_unit
+  use fgpt_c
+  implicit none
+  private
+  public :: gpt_forward, gpt_step, gpt_step_multi, load_gpt_weights, fgpt_release, &
+      fgpt_handles
+
+  type(c_ptr), save :: g_model = c_null_ptr
+  type(c_ptr), save :: g_kv = c_null_ptr
+  integer(c_intptr_t), save :: g_key(8) = 0
+  integer, save :: g_dims(6) = -1
+  integer, save :: g_kv_b = -1, g_kv_maxt = -1
+
+contains
+
+  subroutine die(what, rc)
+    character(*), intent(in) :: what
+    integer(c_int32_t), intent(in) :: rc
+    write (error_unit, '(4A,I0,A)') what, ': ', fg_error_message(), ' (rc ', rc, ')'
+    error stop 1
+  end subroutine die
+
+  ! Bind the engine model to these weight arrays (upload on first use or
+  ! when the arrays or dims change).
+  subroutine bind_model(wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, &
+      vocab_size, d_model, n_head, n_kv_head, head_dim, n_layer, eps)
+    real(c_float), intent(in), target :: wte(:), c_q(:), c_k(:), c_v(:), c_proj(:), &
+        c_fc(:), c_proj2(:), lm_head(:)
+    integer(c_int), intent(in) :: vocab_size, d_model, n_head, n_kv_head, head_dim, n_layer
+    real(c_float), intent(in) :: eps
+    integer(c_intptr_t) :: key(8)
+    integer :: dims(6)
+    type(fg_dims) :: fd
+    integer(c_int32_t) :: rc
+
+    key = [transfer(c_loc(wte), 0_c_intptr_t), transfer(c_loc(c_q), 0_c_intptr_t), &
+        transfer(c_loc(c_k), 0_c_intptr_t), transfer(c_loc(c_v), 0_c_intptr_t), &
+        transfer(c_loc(c_proj), 0_c_intptr_t), transfer(c_loc(c_fc), 0_c_intptr_t), &
+        transfer(c_loc(c_proj2), 0_c_intptr_t), transfer(c_loc(lm_head), 0_c_intptr_t)]
+    dims = [n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size]
+    if (c_associated(g_model) .and. all(key == g_key) .and. all(dims == g_dims)) return
+    call fgpt_release()
+    if (size(wte) < vocab_size*d_model .or. size(lm_head) < vocab_size*d_model .or. &
+        size(c_q) < n_layer*n_head*head_dim*d_model .or. &
+        size(c_k) < n_layer*n_kv_head*head_dim*d_model .or. &
+        size(c_v) < n_layer*n_kv_head*head_dim*d_model .or. &
+        size(c_proj) < n_layer*d_model*n_head*head_dim .or. &
+        size(c_fc) < n_layer*4*d_model*d_model .or. size(c_proj2) < n_layer*4*d_model*d_model) then
+      write (error_unit, '(A)') 'fgpt: weight arrays smaller than the dims require'
+      error stop 1
+    end if
+    fd = fg_dims(n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size, eps)
+    rc = fg_model_create(fd, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, g_model)
+    if (rc /= FG_OK) call die('fgpt: weight upload', rc)
+    g_key = key
+    g_dims = dims
+  end subroutine bind_model
+
+  subroutine bind_kv(bb, maxt)
+    integer(c_int), intent(in) :: bb, maxt
+    integer(c_int32_t) :: rc
+    if (c_associated(g_kv) .and. g_kv_b == bb .and. g_kv_maxt == maxt) return
+    if (c_associated(g_kv)) rc = fg_kv_destroy(g_kv)
+    g_kv = c_null_ptr
+    rc = fg_kv_create(g_model, bb, maxt, g_kv)
+    if (rc /= FG_OK) call die('fgpt: KV cache', rc)
+    g_kv_b = bb
+    g_kv_maxt = maxt
+  end subroutine bind_kv
+
+  ! Drop the device model and cache (the next call re-uploads).
+  subroutine fgpt_release()
+    integer(c_int32_t) :: rc
+    if (c_associated(g_kv)) rc = fg_kv_destroy(g_kv)
+    if (c_associated(g_model)) rc = fg_model_destroy(g_model)
+    g_kv = c_null_ptr
+    g_model = c_null_ptr
+    g_key = 0
+    g_dims = -1
+    g_kv_b = -1
+    g_kv_maxt = -1
+  end subroutine fgpt_release
+
+  ! The engine handles behind the drop-in calls (for callers that also use
+  ! the C API directly, e.g. the device-side greedy loop).
+  subroutine fgpt_handles(model, kv)
+    type(c_ptr), intent(out) :: model, kv
+    model = g_model
+    kv = g_kv
+  end subroutine fgpt_handles
+
+  ! src/lib/fortran_gpt.f90:54-199. attn_blas selects another summation
+  ! order in the reference; here there is one attention kernel, so it is
+  ! accepted and has no effect. attn_qk (QK-hop) is not part of this path.
+  ! pos_frac / pos_n are attention statistics of the attn_blas path and are
+  ! left untouched.
+  subroutine gpt_forward(idx, cos_buf, sin_buf, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, &
+      lm_head, outp, BB, TT, vocab_size, d_model, n_head, n_kv_head, head_dim, n_layer, eps, &
+      attn_blas, attn_qk, pos_frac, pos_n)
+    integer(c_int), intent(in) :: BB, TT, vocab_size, d_model
+    integer(c_int), intent(in) :: n_head, n_kv_head, head_dim, n_layer
+    real(c_float), value :: eps
+    logical, intent(in), optional :: attn_blas, attn_qk
+    real(c_float), intent(inout), optional :: pos_frac(:)
+    integer, intent(inout), optional :: pos_n(:)
+    integer(c_int), intent(in) :: idx(:)
+    real(c_float), intent(in) :: cos_buf(:), sin_buf(:)
+    real(c_float), intent(in), target :: wte(:), c_q(:), c_k(:), c_v(:), c_proj(:), c_fc(:), &
+        c_proj2(:), lm_head(:)
+    real(c_float), intent(out) :: outp(:)
+    integer(c_int32_t) :: rc
+
+    if (present(attn_qk)) then
+      if (attn_qk) then
+        write (error_unit, '(A)') 'gpt_forward: attn_qk (QK-hop) is not supported by this engine'
+        error stop 1
+      end if
+    end if
+    if (size(outp) < BB*TT*vocab_size .or. size(idx) < BB*TT .or. &
+        size(cos_buf) < TT*(head_dim/2) .or. size(sin_buf) < TT*(head_dim/2)) then
+      write (error_unit, '(A)') 'gpt_forward: array smaller than B*T requires'
+      error stop 1
+    end if
+    call bind_model(wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, vocab_size, d_model, &
+        n_head, n_kv_head, head_dim, n_layer, eps)
+    rc = fg_set_rope(g_model, 0_c_int32_t, TT, cos_buf, sin_buf)
+    if (rc /= FG_OK) call die('gpt_forward: RoPE tables', rc)
+    rc = fg_forward(g_model, idx, BB, TT, outp, c_null_ptr, c_null_ptr)
+    if (rc /= FG_OK) call die('gpt_forward', rc)
+  end subroutine gpt_forward
+
+  ! src/lib/fortran_kv.f90:26-149
+  subroutine gpt_step(idx1, cos1, sin1, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, &
+      cache_k, cache_v, cache_len, maxT, out1, BB, vocab_size, d_model, n_head, n_kv_head, &
+      head_dim, n_layer, eps)
+    integer(c_int), intent(in) :: BB, vocab_size, d_model
+    integer(c_int), intent(in) :: n_head, n_kv_head, head_dim, n_layer
+    integer(c_int), intent(in) :: maxT
+    integer(c_int), intent(inout) :: cache_len
+    real(c_float), value :: eps
+    integer(c_int), intent(in) :: idx1(:)
+    real(c_float), intent(in) :: cos1(:), sin1(:)
+    real(c_float), intent(in), target :: wte(:), c_q(:), c_k(:), c_v(:), c_proj(:), c_fc(:), &
+        c_proj2(:), lm_head(:)
+    real(c_float), intent(inout) :: cache_k(:), cache_v(:)
+    real(c_float), intent(out) :: out1(:)
+    integer(c_int32_t) :: rc
+
+    if (cache_len >= maxT) then
+      print '(A)', "gpt_step: cache full (raise maxT)"
+      error stop 1
+    end if
+    call bind_model(wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, vocab_size, d_model, &
+        n_head, n_kv_head, head_dim, n_layer, eps)
+    call bind_kv(BB, maxT)
+    rc = fg_kv_set_len(g_kv, cache_len)
+    if (rc /= FG_OK) call die('gpt_step', rc)
+    rc = fg_set_rope(g_model, cache_len, 1_c_int32_t, cos1, sin1)
+    if (rc /= FG_OK) call die('gpt_step: RoPE row', rc)
+    rc = fg_step(g_model, g_kv, idx1, out1, c_null_ptr)
+    if (rc /= FG_OK) call die('gpt_step', rc)
+    cache_len = cache_len + 1
+  end subroutine gpt_step
+
+  ! src/lib/fortran_kv.f90:160-289
+  subroutine gpt_step_multi(idx, cos_buf, sin_buf, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, &
+      lm_head, cache_k, cache_v, cache_len, maxT, out, BB, vocab_size, d_model, n_head, &
+      n_kv_head, head_dim, n_layer, TB, eps)
+    integer(c_int), intent(in) :: BB, vocab_size, d_model
+    integer(c_int), intent(in) :: n_head, n_kv_head, head_dim, n_layer
+    integer(c_int), intent(in) :: maxT, TB
+    integer(c_int), intent(inout) :: cache_len
+    real(c_float), value :: eps
+    integer(c_int), intent(in) :: idx(:)
+    real(c_float), intent(in) :: cos_buf(:), sin_buf(:)
+    real(c_float), intent(in), target :: wte(:), c_q(:), c_k(:), c_v(:), c_proj(:), c_fc(:), &
+        c_proj2(:), lm_head(:)
+    real(c_float), intent(inout) :: cache_k(:), cache_v(:)
+    real(c_float), intent(out) :: out(:)
+    integer(c_int32_t) :: rc
+
+    if (TB < 1) then
+      print '(A)', "gpt_step_multi: TB must be >= 1"
+      error stop 1
+    end if
+    if (cache_len + TB > maxT) then
+      print '(A)', "gpt_step_multi: cache full (raise maxT)"
+      error stop 1
+    end if
+    call bind_model(wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, vocab_size, d_model, &
+        n_head, n_kv_head, head_dim, n_layer, eps)
+    call bind_kv(BB, maxT)
+    rc = fg_kv_set_len(g_kv, cache_len)
+    if (rc /= FG_OK) call die('gpt_step_multi', rc)
+    rc = fg_set_rope(g_model, cache_len, TB, cos_buf, sin_buf)
+    if (rc /= FG_OK) call die('gpt_step_multi: RoPE rows', rc)
+    rc = fg_step_multi(g_model, g_kv, idx, TB, out, c_null_ptr)
+    if (rc /= FG_OK) call die('gpt_step_multi', rc)
+    cache_len = cache_len + TB
+  end subroutine gpt_step_multi
+
+  ! ------------------------------------------------------------ weights
+  ! One 1-D '<f4' C-order .npy file of exactly n values (the exporter's
+  ! format, scripts/export_weights.py:22-24,151-166); missing, empty or
+  ! malformed files stop the program, as load1 does (load_weights.f90:139-159).
+  subroutine load1(path, a, at, n)
+    character(*), intent(in) :: path
+    real(c_float), intent(inout) :: a(:)
+    integer, intent(in) :: at, n
+    integer :: u, ios, sz, hlen, hstart
+    character(len=6) :: magic
+    integer(int8) :: ver(2), hl(2)
+    character(len=:), allocatable :: hdr
+    logical :: ex
+
+    inquire (file=path, exist=ex, size=sz)
+    if (.not. ex .or. sz <= 0) then
+      print '(2A)', "load failed (missing or empty file): ", trim(path)
+      error stop 1
+    end if
+    open (newunit=u, file=path, access='stream', form='unformatted', status='old', &
+        action='read', iostat=ios)
+    if (ios /= 0) then
+      print '(2A)', "load failed: ", trim(path)
+      error stop 1
+    end if
+    read (u, iostat=ios) magic, ver, hl
+    if (ios /= 0 .or. magic(2:6) /= 'NUMPY' .or. ver(1) /= 1) then
+      print '(2A)', "load failed (not a version-1 .npy): ", trim(path)
+      error stop 1
+    end if
+    hlen = iand(int(hl(1)), 255) + 256*iand(int(hl(2)), 255)
+    allocate (character(len=hlen) :: hdr)
+    read (u, iostat=ios) hdr
+    hstart = 10 + hlen
+    if (ios /= 0 .or. index(hdr, "'descr': '<f4'") == 0 .or. &
+        index(hdr, "'fortran_order': False") == 0) then
+      print '(2A)', "load failed (need a '<f4' C-order array): ", trim(path)
+      error stop 1
+    end if
+    if (sz /= hstart + 4*n) then
+      print '(2A,I0,A)', "load failed (size mismatch, expected ", trim(path), n, " values)"
+      error stop 1
+    end if
+    read (u, pos=hstart + 1, iostat=ios) a(at:at + n - 1)
+    if (ios /= 0) then
+      print '(2A)', "load failed (short read): ", trim(path)
+      error stop 1
+    end if
+    close (u)
+  end subroutine load1
+
+  ! arch.txt, when present, must agree with the dims (read_arch_txt /
+  ! require_arch, src/lib/fortran_arch.f90:121-159,238-246).
+  subroutine require_arch(wdir, dims)
+    character(*), intent(in) :: wdir
+    integer, intent(in) :: dims(6)   ! n_layer, d_model, n_head, n_kv_head, head_dim, vocab
+    character(len=128) :: line
+    character(len=64) :: key
+    integer :: u, ios, eq, val, want
+    open (newunit=u, file=trim(wdir)//'/arch.txt', status='old', action='read', iostat=ios)
+    if (ios /= 0) return
+    do
+      read (u, '(A)', iostat=ios) line
+      if (ios /= 0) exit
+      eq = index(line, '=')
+      if (eq == 0 .or. line(1:1) == '#') cycle
+      key = trim(adjustl(line(:eq - 1)))
+      read (line(eq + 1:), *, iostat=ios) val
+      if (ios /= 0) cycle
+      select case (key)
+      case ('n_layer'); want = dims(1)
+      case ('d_model'); want = dims(2)
+      case ('n_head'); want = dims(3)
+      case ('n_kv'); want = dims(4)
+      case ('head_dim'); want = dims(5)
+      case ('vocab'); want = dims(6)
+      case default; cycle
+      end select
+      if (want /= val) then
+        print '(A,A,A,I0,A,I0)', 'FATAL: shape mismatch in arch.txt ', trim(key), &
+            ': expected ', want, ', checkpoint has ', val
+        error stop 1
+      end if
+    end do
+    close (u)
+  end subroutine require_arch
+
+  ! src/lib/load_weights.f90:830-874 (.npy branch) plus require_arch.
+  subroutine load_gpt_weights(wdir, n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size, &
+      wte, lm_head, c_q, c_k, c_v, c_pr, c_fc, c_pr2)
+    character(*), intent(in) :: wdir
+    integer, intent(in) :: n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size
+    real(c_float), allocatable, intent(out) :: wte(:), lm_head(:)
+    real(c_float), allocatable, intent(out) :: c_q(:), c_k(:), c_v(:), c_pr(:), c_fc(:), c_pr2(:)
+    integer :: ll, qsz, ksz, psz, fsz
+    character(len=16) :: ls
+    character(len=:), allocatable :: p
+
+    call require_arch(wdir, [n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size])
+    qsz = n_head*head_dim*d_model
+    ksz = n_kv_head*head_dim*d_model
+    psz = d_model*n_head*head_dim
+    fsz = 4*d_model*d_model
+    allocate (wte(vocab_size*d_model), lm_head(vocab_size*d_model))
+    allocate (c_q(n_layer*qsz), c_k(n_layer*ksz), c_v(n_layer*ksz), c_pr(n_layer*psz))
+    allocate (c_fc(n_layer*fsz), c_pr2(n_layer*fsz))
+    call load1(trim(wdir)//"/transformer_wte_weight.npy", wte, 1, vocab_size*d_model)
+    call load1(trim(wdir)//"/lm_head_weight.npy", lm_head, 1, vocab_size*d_model)
+    do ll = 0, n_layer - 1
+      write (ls, '(I0)') ll
+      p = trim(wdir)//"/transformer_h_"//trim(ls)//"_"
+      call load1(p//"attn_c_q_weight.npy", c_q, ll*qsz + 1, qsz)
+      call load1(p//"attn_c_k_weight.npy", c_k, ll*ksz + 1, ksz)
+      call load1(p//"attn_c_v_weight.npy", c_v, ll*ksz + 1, ksz)
+      call load1(p//"attn_c_proj_weight.npy", c_pr, ll*psz + 1, psz)
+      call load1(p//"mlp_c_fc_weight.npy", c_fc, ll*fsz + 1, fsz)
+      call load1(p//"mlp_c_proj_weight.npy", c_pr2, ll*fsz + 1, fsz)
+    end do
+  end subroutine load_gpt_weights
+
+end module fgpt_drop_in_mod

@@ -1,0 +1,367 @@
+! fgpt_run.f90 -- ids-in / ids-out harness over the drop-in model API.
+!
+! Reproduces the call semantics of the reference's inference apps with the
+! gfx950 engine underneath:
+!   greedy   the decode loop of src/app/chat_text.f90:225-278,423-462: RoPE
+!            tables built on the host in fp32, the prompt (minus its last id)
+!            through gpt_step_multi chunks of pchunk, then one gpt_step per
+!            generated id with a host argmax (src/lib/sample.f90:271-277,
+!            first maximum; no byte mask). With loop=device the generated
+!            ids come from the engine's device-side greedy loop instead.
+!   eval     the per-position NLL of src/app/eval_bpb.f90:117-126,156-181:
+!            B rows of T+1 ids, gpt_forward on the first T, nats per
+!            position = logsumexp - logit[target].
+!   selftest cached steps == full forward (src/test/test_kernels.f90:720-779)
+!            through the drop-in subroutines on frand-filled weights.
+!
+! Usage:
+!   fgpt_run greedy WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [PCHUNK] [host|device]
+!   fgpt_run eval   WDIR L D H KH HD V ROWS_FILE B T OUT_FILE
+!   fgpt_run selftest
+! Ids files are whitespace-separated 0-based integers. Timing goes to stderr.
+program fgpt_run
+  use, intrinsic :: iso_c_binding
+  use, intrinsic :: iso_fortran_env, only: error_unit, int64
+  use fgpt_c
+  use fgpt_drop_in_mod
+  implicit none
+
+  character(len=512) :: mode
+  integer :: nargs
+
+  nargs = command_argument_count()
+  if (nargs < 1) call usage()
+  call get_command_argument(1, mode)
+  select case (trim(mode))
+  case ('greedy')
+    call run_greedy()
+  case ('eval')
+    call run_eval()
+  case ('selftest')
+    call run_selftest()
+  case default
+    call usage()
+  end select
+
+contains
+
+  subroutine usage()
+    write (error_unit, '(A)') 'usage: fgpt_run greedy WDIR L D H KH HD V IDS NGEN OUT [PCHUNK] [host|device]'
+    write (error_unit, '(A)') '       fgpt_run eval WDIR L D H KH HD V ROWS B T OUT'
+    write (error_unit, '(A)') '       fgpt_run selftest'
+    stop 2
+  end subroutine usage
+
+  integer function iarg(i)
+    integer, intent(in) :: i
+    character(len=64) :: s
+    integer :: ios
+    call get_command_argument(i, s)
+    read (s, *, iostat=ios) iarg
+    if (ios /= 0) then
+      write (error_unit, '(A,I0,2A)') 'bad integer argument ', i, ': ', trim(s)
+      stop 2
+    end if
+  end function iarg
+
+  character(len=512) function sarg(i)
+    integer, intent(in) :: i
+    call get_command_argument(i, sarg)
+  end function sarg
+
+  subroutine read_ids(path, ids, n)
+    character(*), intent(in) :: path
+    integer(c_int), allocatable, intent(out) :: ids(:)
+    integer, intent(out) :: n
+    integer :: u, ios, v
+    integer(c_int), allocatable :: tmp(:)
+    allocate (ids(1024))
+    n = 0
+    open (newunit=u, file=path, status='old', action='read', iostat=ios)
+    if (ios /= 0) then
+      write (error_unit, '(2A)') 'cannot open ', trim(path)
+      stop 1
+    end if
+    do
+      read (u, *, iostat=ios) v
+      if (ios /= 0) exit
+      n = n + 1
+      if (n > size(ids)) then
+        allocate (tmp(2*size(ids)))
+        tmp(1:size(ids)) = ids
+        call move_alloc(tmp, ids)
+      end if
+      ids(n) = v
+    end do
+    close (u)
+  end subroutine read_ids
+
+  ! chat_text.f90:225-235 / eval_bpb.f90:117-126
+  subroutine rope_tables(ntot, hd, cos_b, sin_b)
+    integer, intent(in) :: ntot, hd
+    real(c_float), allocatable, intent(out) :: cos_b(:), sin_b(:)
+    integer :: i, j
+    real(c_float) :: theta, ang
+    allocate (cos_b(ntot*(hd/2)), sin_b(ntot*(hd/2)))
+    do i = 1, ntot
+      do j = 1, hd/2
+        theta = 10000.0_c_float ** (-2.0_c_float * real(j-1, c_float) / real(hd, c_float))
+        ang = real(i-1, c_float) * theta
+        cos_b((i-1)*(hd/2)+j) = cos(ang)
+        sin_b((i-1)*(hd/2)+j) = sin(ang)
+      end do
+    end do
+  end subroutine rope_tables
+
+  ! RoPE rows [pos0, pos0+n) of the host tables into the engine (the device
+  ! loop reads them without a host round trip per step)
+  subroutine set_rope_rows(model, pos0, n, hd, cos_b, sin_b)
+    type(c_ptr), intent(in) :: model
+    integer(c_int), intent(in) :: pos0
+    integer, intent(in) :: n, hd
+    real(c_float), intent(in) :: cos_b(:), sin_b(:)
+    integer(c_int32_t) :: rc
+    if (n < 1) return
+    rc = fg_set_rope(model, pos0, n, cos_b(pos0*(hd/2)+1:), sin_b(pos0*(hd/2)+1:))
+    if (rc /= FG_OK) then
+      write (error_unit, '(2A)') 'fg_set_rope: ', fg_error_message()
+      stop 1
+    end if
+  end subroutine set_rope_rows
+
+  real(8) function now()
+    integer(int64) :: c, r
+    call system_clock(c, r)
+    now = real(c, 8) / real(r, 8)
+  end function now
+
+  subroutine run_greedy()
+    character(len=512) :: wdir, ids_file, out_file, loop
+    integer :: L, D, H, KH, HD, V, ngen, pchunk, nprompt, ntot, npre, srow, tb, step, tc, i, u, best
+    integer(c_int) :: clen
+    real(c_float), allocatable :: wte(:), lm(:), c_q(:), c_k(:), c_v(:), c_pr(:), c_fc(:), c_pr2(:)
+    real(c_float), allocatable :: cos_b(:), sin_b(:), out1(:), outc(:), ck(:), cv(:)
+    integer(c_int), allocatable :: prompt(:), idx(:), gen(:)
+    type(c_ptr) :: model, kv
+    integer(c_int32_t) :: rc
+    real(8) :: t0, t1, t2
+
+    if (command_argument_count() < 11) call usage()
+    wdir = sarg(2); L = iarg(3); D = iarg(4); H = iarg(5); KH = iarg(6); HD = iarg(7); V = iarg(8)
+    ids_file = sarg(9); ngen = iarg(10); out_file = sarg(11)
+    pchunk = 64
+    if (command_argument_count() >= 12) pchunk = iarg(12)
+    loop = 'host'
+    if (command_argument_count() >= 13) loop = sarg(13)
+
+    call load_gpt_weights(trim(wdir), L, D, H, KH, HD, V, wte, lm, c_q, c_k, c_v, c_pr, c_fc, c_pr2)
+    call read_ids(trim(ids_file), prompt, nprompt)
+    if (nprompt < 1) then
+      write (error_unit, '(A)') 'empty prompt'
+      stop 1
+    end if
+    ntot = nprompt + ngen
+    allocate (idx(ntot), out1(V), ck(1), cv(1))
+    idx(1:nprompt) = prompt(1:nprompt)
+    call rope_tables(ntot, HD, cos_b, sin_b)
+    clen = 0
+
+    t0 = now()
+    npre = nprompt - 1
+    if (npre >= 1) then
+      allocate (outc(max(1, min(pchunk, npre))*V))
+      srow = 1
+      do while (srow <= npre)
+        tb = min(pchunk, npre - srow + 1)
+        call gpt_step_multi(idx(srow:srow+tb-1), cos_b((srow-1)*(HD/2)+1:), &
+            sin_b((srow-1)*(HD/2)+1:), wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, &
+            ck, cv, clen, ntot, outc, 1, V, D, H, KH, HD, L, tb, 1.0e-5_c_float)
+        srow = srow + tb
+      end do
+    end if
+    t1 = now()
+    if (trim(loop) == 'device') then
+      ! one host call: the engine feeds each argmax back on the device
+      if (npre < 1) then
+        ! bind the model and cache through a zero-length-free first step
+        call gpt_step(idx(1:1), cos_b, sin_b, wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, &
+            ck, cv, clen, ntot, out1, 1, V, D, H, KH, HD, L, 1.0e-5_c_float)
+        best = 1
+        do i = 2, V
+          if (out1(i) > out1(best)) best = i
+        end do
+        idx(nprompt+1) = best - 1
+        call fgpt_handles(model, kv)
+        call set_rope_rows(model, clen, ngen - 1, HD, cos_b, sin_b)
+        allocate (gen(max(ngen-1, 1)))
+        if (ngen > 1) then
+          rc = fg_decode_greedy(model, kv, idx(nprompt+1:nprompt+1), ngen-1, gen, c_null_ptr)
+          if (rc /= FG_OK) then
+            write (error_unit, '(2A)') 'fg_decode_greedy: ', fg_error_message()
+            stop 1
+          end if
+          idx(nprompt+2:ntot) = gen(1:ngen-1)
+        end if
+      else
+        call fgpt_handles(model, kv)
+        call set_rope_rows(model, clen, ngen, HD, cos_b, sin_b)
+        allocate (gen(ngen))
+        rc = fg_decode_greedy(model, kv, idx(nprompt:nprompt), ngen, gen, c_null_ptr)
+        if (rc /= FG_OK) then
+          write (error_unit, '(2A)') 'fg_decode_greedy: ', fg_error_message()
+          stop 1
+        end if
+        idx(nprompt+1:ntot) = gen(1:ngen)
+      end if
+    else
+      do step = nprompt, ntot - 1
+        tc = step
+        call gpt_step(idx(tc:tc), cos_b((tc-1)*(HD/2)+1:), sin_b((tc-1)*(HD/2)+1:), &
+            wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, ck, cv, clen, ntot, out1, &
+            1, V, D, H, KH, HD, L, 1.0e-5_c_float)
+        if (out1(1) /= out1(1)) then
+          print '(A)', "NaN logit - abort"
+          stop 1
+        end if
+        best = 1
+        do i = 2, V
+          if (out1(i) > out1(best)) best = i
+        end do
+        idx(tc+1) = best - 1
+      end do
+    end if
+    t2 = now()
+    open (newunit=u, file=trim(out_file), status='replace', action='write')
+    do i = nprompt + 1, ntot
+      write (u, '(I0)') idx(i)
+    end do
+    close (u)
+    write (error_unit, '(A,F10.3,A,F10.3,A,F12.1,2A)') 'stats: prefill_ms=', 1000*(t1-t0), &
+        ' decode_ms=', 1000*(t2-t1), ' tok_s=', real(ngen, 8)/max(t2-t1, 1d-9), ' loop=', trim(loop)
+    call fgpt_release()
+  end subroutine run_greedy
+
+  subroutine run_eval()
+    character(len=512) :: wdir, rows_file, out_file
+    integer :: L, D, H, KH, HD, V, B, T, n, r, tcc, j, u, tgt, base
+    real(c_float), allocatable :: wte(:), lm(:), c_q(:), c_k(:), c_v(:), c_pr(:), c_fc(:), c_pr2(:)
+    real(c_float), allocatable :: cos_b(:), sin_b(:), outp(:), nll(:,:)
+    integer(c_int), allocatable :: rows(:), idx(:)
+    real(c_float) :: m, s
+    real(8) :: t0, t1, tot
+
+    if (command_argument_count() < 12) call usage()
+    wdir = sarg(2); L = iarg(3); D = iarg(4); H = iarg(5); KH = iarg(6); HD = iarg(7); V = iarg(8)
+    rows_file = sarg(9); B = iarg(10); T = iarg(11); out_file = sarg(12)
+    call load_gpt_weights(trim(wdir), L, D, H, KH, HD, V, wte, lm, c_q, c_k, c_v, c_pr, c_fc, c_pr2)
+    call read_ids(trim(rows_file), rows, n)
+    if (n /= B*(T+1)) then
+      write (error_unit, '(A,I0,A,I0)') 'rows file holds ', n, ' ids, need ', B*(T+1)
+      stop 1
+    end if
+    allocate (idx(B*T), outp(B*T*V), nll(B, T))
+    do r = 1, B
+      idx((r-1)*T+1:r*T) = rows((r-1)*(T+1)+1:(r-1)*(T+1)+T)
+    end do
+    call rope_tables(T, HD, cos_b, sin_b)
+    t0 = now()
+    call gpt_forward(idx, cos_b, sin_b, wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, outp, &
+        B, T, V, D, H, KH, HD, L, 1.0e-5_c_float)
+    t1 = now()
+    do r = 1, B
+      base = (r-1)*T*V
+      do tcc = 1, T
+        tgt = rows((r-1)*(T+1) + tcc + 1) + 1
+        m = outp(base+(tcc-1)*V+1)
+        do j = 2, V
+          if (outp(base+(tcc-1)*V+j) > m) m = outp(base+(tcc-1)*V+j)
+        end do
+        s = 0.0_c_float
+        do j = 1, V
+          s = s + exp(outp(base+(tcc-1)*V+j) - m)
+        end do
+        nll(r, tcc) = (m + log(s)) - outp(base+(tcc-1)*V+tgt)
+      end do
+    end do
+    open (newunit=u, file=trim(out_file), status='replace', action='write')
+    do r = 1, B
+      tot = 0
+      do tcc = 1, T
+        tot = tot + nll(r, tcc)
+      end do
+      write (u, '(ES24.16)') tot
+    end do
+    close (u)
+    write (error_unit, '(A,F10.3,A,F14.1)') 'stats: forward_ms=', 1000*(t1-t0), &
+        ' tok_s=', real(B*T, 8)/max(t1-t0, 1d-9)
+    call fgpt_release()
+  end subroutine run_eval
+
+  ! frand of src/test/test_kernels.f90:115-119, explicit 32-bit wrap
+  real(c_float) function frand(seed)
+    integer, intent(inout) :: seed
+    integer(int64) :: t
+    t = int(seed, int64) * 1103515245_int64 + 12345_int64
+    t = iand(t, int(z'FFFFFFFF', int64))
+    if (t >= 2147483648_int64) t = t - 4294967296_int64
+    seed = int(mod(t, 2147483647_int64))
+    frand = real(mod(seed / 65536, 32768), c_float) / 32768.0_c_float - 0.5_c_float
+  end function frand
+
+  subroutine fill(x, scale, seed)
+    real(c_float), intent(out) :: x(:)
+    real(c_float), intent(in) :: scale
+    integer, intent(inout) :: seed
+    integer :: i
+    do i = 1, size(x)
+      ! bf16-exact values: the engine stores weights as bf16
+      x(i) = transfer(iand(transfer(frand(seed)*scale, 0), -65536), 0.0_c_float)
+    end do
+  end subroutine fill
+
+  ! cached steps == full forward, the reference's test_kv_equiv, at dims the
+  ! engine supports (head_dim 64, d_model 128)
+  subroutine run_selftest()
+    integer, parameter :: TC = 6, VV = 128, DD = 128, NH = 2, NKV = 1, HDm = 64, NL = 2
+    integer(c_int) :: idx(TC), clen
+    real(c_float) :: wte(VV*DD), c_q(NL*NH*HDm*DD), c_k(NL*NKV*HDm*DD), c_v(NL*NKV*HDm*DD)
+    real(c_float) :: c_proj(NL*DD*NH*HDm), c_fc(NL*4*DD*DD), c_proj2(NL*DD*4*DD), lm(VV*DD)
+    real(c_float) :: out_full(TC*VV), out_steps(TC*VV), out1(VV), ck(1), cv(1)
+    real(c_float), allocatable :: cos_b(:), sin_b(:)
+    real(c_float) :: err
+    integer :: i, t, seed
+
+    seed = 42
+    do i = 1, TC
+      idx(i) = 1 + mod(i, 7)
+    end do
+    call fill(wte, 0.1_c_float, seed)
+    call fill(c_q, 0.05_c_float, seed)
+    call fill(c_k, 0.05_c_float, seed)
+    call fill(c_v, 0.05_c_float, seed)
+    call fill(c_proj, 0.05_c_float, seed)
+    call fill(c_fc, 0.05_c_float, seed)
+    call fill(c_proj2, 0.05_c_float, seed)
+    call fill(lm, 0.05_c_float, seed)
+    call rope_tables(TC, HDm, cos_b, sin_b)
+    call gpt_forward(idx, cos_b, sin_b, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm, &
+        out_full, 1, TC, VV, DD, NH, NKV, HDm, NL, 1.0e-5_c_float)
+    clen = 0
+    do t = 1, TC
+      call gpt_step(idx(t:t), cos_b((t-1)*(HDm/2)+1:), sin_b((t-1)*(HDm/2)+1:), &
+          wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm, ck, cv, clen, TC, out1, &
+          1, VV, DD, NH, NKV, HDm, NL, 1.0e-5_c_float)
+      out_steps((t-1)*VV+1:t*VV) = out1
+    end do
+    err = maxval(abs(out_full - out_steps)) / maxval(abs(out_full))
+    print '(A,ES10.3,A,I0)', 'selftest: cached steps vs forward, max rel err = ', err, &
+        '  cache_len=', clen
+    call fgpt_release()
+    if (clen /= TC .or. .not. (err < 1.0e-5)) then
+      print '(A)', 'selftest: FAIL'
+      stop 1
+    end if
+    print '(A)', 'selftest: ok'
+  end subroutine run_selftest
+
+end program fgpt_run

@@ -1,0 +1,121 @@
+"""The Fortran host layer: the iso_c_binding module, the drop-in
+gpt_forward / gpt_step / gpt_step_multi and the ids-in/ids-out harness
+(autoresearch_amd/fgpt_run), checked against the CPU oracle."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from autoresearch_amd.weights import (D12, Dims, seeded_weights, uniform_ids, write_npy_dir,
+                                      zipf_ids, BOS_ID)
+from oracle import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXE = os.path.join(ROOT, "autoresearch_amd", "fgpt_run")
+SMALL = Dims(n_layer=2, d_model=128, n_head=2, n_kv_head=1, head_dim=64, vocab=512)
+
+
+def dims_args(d):
+    return [str(x) for x in (d.n_layer, d.d_model, d.n_head, d.n_kv_head, d.head_dim, d.vocab)]
+
+
+def run(args, timeout=300):
+    return subprocess.run([EXE, *args], capture_output=True, text=True, timeout=timeout)
+
+
+def test_harness_built_and_fails_loudly_without_device():
+    import torch
+    assert os.path.exists(EXE), "build() must compile the Fortran harness"
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    r = run(["selftest"], timeout=60)
+    assert r.returncode != 0
+    assert "no HIP device" in r.stderr or "gfx950" in r.stderr
+
+
+def test_harness_usage_error():
+    r = run(["nonsense"], timeout=30)
+    assert r.returncode == 2 and "usage" in r.stderr
+
+
+@pytest.mark.gpu
+def test_fortran_selftest_steps_equal_forward():
+    r = run(["selftest"], timeout=120)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "selftest: ok" in r.stdout
+
+
+def oracle_greedy(d, w, prompt, ngen):
+    c, s = O.rope_tables(prompt.size + ngen, d.head_dim)
+    return O.greedy_decode(prompt, w, d, ngen, c, s, maxT=prompt.size + ngen)[0]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("loop,pchunk", [("host", 64), ("device", 4)])
+def test_fortran_greedy_small(tmp_path, loop, pchunk):
+    d = SMALL
+    w = seeded_weights(d, 21)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=64)
+    prompt = uniform_ids(31, 11, d.vocab)
+    np.savetxt(tmp_path / "ids.txt", prompt, fmt="%d")
+    r = run(["greedy", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "ids.txt"), "20",
+             str(tmp_path / "out.txt"), str(pchunk), loop])
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0
+    got = np.loadtxt(tmp_path / "out.txt", dtype=np.int32)
+    assert np.array_equal(got, oracle_greedy(d, w, prompt, 20))
+
+
+@pytest.mark.gpu
+def test_fortran_greedy_depth12(tmp_path):
+    """The B=1 decode workload through the Fortran drop-in: 16 prompt ids,
+    32 greedy steps, host argmax per step as chat_text does."""
+    d = D12
+    w = seeded_weights(d, 1234)
+    write_npy_dir(str(tmp_path / "w"), d, w)
+    prompt = uniform_ids(42, 16, d.vocab)
+    np.savetxt(tmp_path / "ids.txt", prompt, fmt="%d")
+    ref = oracle_greedy(d, w, prompt, 32)
+    for loop in ("host", "device"):
+        r = run(["greedy", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "ids.txt"), "32",
+                 str(tmp_path / f"out_{loop}.txt"), "64", loop])
+        print(r.stderr)
+        assert r.returncode == 0
+        got = np.loadtxt(tmp_path / f"out_{loop}.txt", dtype=np.int32)
+        assert np.array_equal(got, ref), loop
+
+
+@pytest.mark.gpu
+def test_fortran_eval_rows(tmp_path):
+    d = SMALL
+    w = seeded_weights(d, 22)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=128)
+    B, T = 3, 96
+    rows = zipf_ids(5, B * (T + 1), d.vocab).reshape(B, T + 1)
+    rows[:, 0] = BOS_ID % d.vocab
+    np.savetxt(tmp_path / "rows.txt", rows.reshape(-1), fmt="%d")
+    r = run(["eval", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"), str(B),
+             str(T), str(tmp_path / "nll.txt")])
+    print(r.stderr)
+    assert r.returncode == 0
+    got = np.loadtxt(tmp_path / "nll.txt")
+    c, s = O.rope_tables(T, d.head_dim)
+    for b in range(B):
+        lg = O.gpt_forward(rows[b, :T], c, s, w, d, 1, T)
+        ref = float(O.nll(lg.reshape(T, -1), rows[b, 1:], d.vocab).astype(np.float64).sum())
+        assert abs(got[b] - ref) < 2 * 2e-3 * np.abs(lg).max() * T
+        assert abs(got[b] - ref) < 1e-3 * T
+
+
+@pytest.mark.gpu
+def test_fortran_arch_mismatch_stops(tmp_path):
+    d = SMALL
+    w = seeded_weights(d, 23)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=64)
+    np.savetxt(tmp_path / "ids.txt", [1, 2, 3], fmt="%d")
+    wrong = dims_args(d)
+    wrong[3] = "2"  # n_kv_head 2 vs arch.txt n_kv = 1
+    r = run(["greedy", str(tmp_path / "w"), *wrong, str(tmp_path / "ids.txt"), "2",
+             str(tmp_path / "o.txt")])
+    assert r.returncode != 0 and "arch.txt" in r.stdout
