@@ -174,7 +174,7 @@ int32_t check_dims(const fg_dims* in, Dims* d) {
   if (d->H * d->hd != d->D)
     return seterr(FG_EDIMS, "n_head*head_dim (%d) must equal d_model (%d)", d->H * d->hd, d->D);
   if (d->H % d->KH != 0) return seterr(FG_EDIMS, "n_head %% n_kv_head != 0");
-  if (d->D % 64 != 0) return seterr(FG_EDIMS, "d_model %d not a multiple of 64", d->D);
+  if (d->D % 128 != 0) return seterr(FG_EDIMS, "d_model %d not a multiple of 128", d->D);
   if (d->V % 64 != 0) return seterr(FG_EDIMS, "vocab %d not a multiple of 64", d->V);
   if (!(d->eps > 0.f)) return seterr(FG_EDIMS, "eps must be > 0");
   return FG_OK;
@@ -240,7 +240,7 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
 void free_work(fg_model* m) {
   Work& ws = m->ws;
   void* ptrs[] = {ws.x, ws.q, ws.ao, ws.h, ws.logits, ws.ids, ws.tgt, ws.nll, ws.stat, ws.amax,
-                  m->qs};
+                  ws.xs, ws.aos, ws.hs, ws.ssq, m->qs};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   ws = Work();
@@ -271,6 +271,10 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
   RCCHK(alloc((void**)&ws.stat, rows * 4));
   RCCHK(alloc((void**)&ws.amax, rows * 4));
   RCCHK(alloc((void**)&m->qs, rows * d.qd() * 2 * 2));
+  RCCHK(alloc((void**)&ws.xs, rows * d.D * 2 * 2));
+  RCCHK(alloc((void**)&ws.aos, rows * d.qd() * 2 * 2));
+  RCCHK(alloc((void**)&ws.hs, rows * d.dff * 2 * 2));
+  RCCHK(alloc((void**)&ws.ssq, rows * (d.D / 64) * 4));
   ws.rows = rows;
   m->work_bytes = total;
   m->gen++;
@@ -294,17 +298,23 @@ int32_t ensure_split(fg_model* m, int64_t elems) {
 
 int npos_pad(int n) { return (n + 63) / 64 * 64; }
 
-// y = epi(x W^T): GEMV for up to four token rows, MFMA GEMM beyond.
-// Algorithmic traffic: weights once, activations in and out once (RESID
-// reads the residual it adds to).
-void linear(fg_model* m, hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
+// The fp32 GEMV serves up to four token rows (its rows sit in LDS); beyond
+// that every linear of the pass runs on the MFMA GEMM with split operands.
+bool use_gemm(const Dims& d, int64_t rows) {
+  return rows > 4 || rows * (int64_t)d.dff * 4 > 65536;
+}
+
+// y = epi(x W^T) on the path chosen for the pass. Algorithmic traffic:
+// weights once, activations in and out once (RESID reads the residual).
+void linear(fg_model* m, hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos,
+            bool gm) {
   const double M = a.M, N = a.N, K = a.K;
   const double flops = 2.0 * M * N * K;
   const double bytes = N * K * 2 + M * K * 4 + M * N * 4 * (epi == GV_RESID ? 2 : 1);
-  if (a.M <= 4 && (int64_t)a.M * a.K * 4 <= 65536)
-    timed(m, s, FG_K_GEMV, flops, bytes, [&] { launch_gemv_pos(s, epi, a, d_pos); });
-  else
+  if (gm)
     timed(m, s, FG_K_GEMM, flops, bytes, [&] { launch_gemm_pos(s, epi, a, d_pos); });
+  else
+    timed(m, s, FG_K_GEMV, flops, bytes, [&] { launch_gemv_pos(s, epi, a, d_pos); });
 }
 
 GemvArgs base_args(fg_model* m) {
@@ -319,22 +329,33 @@ GemvArgs base_args(fg_model* m) {
   return a;
 }
 
-// One pass of the layer stack over rows = B*T token rows whose residual is
-// already in ws.x. Positions: pos0 (+ *d_pos if given) + row % T. K/V go to
-// kc/vc with [L][B][maxT][KH*hd] layout (layer stride lstride floats).
-// Attention: single-query kernel when T == 1 (attn_step), else the causal
+// One pass over rows = B*T token rows: embedding of ids, the layer stack,
+// lm_head into logits. Positions: pos0 (+ *d_pos if given) + row % T. K/V
+// go to kc/vc with [L][B][maxT][KH*hd] layout (layer stride lstride floats),
+// or only to the split planes when kc is null (gpt_forward). Attention: the
+// single-query kernel for a cached step (T == 1, attn_step), else the causal
 // chunk kernel (causal_attn / attn_chunk).
-void layer_stack(fg_model* m, hipStream_t s, int B, int T, int pos0, const int32_t* d_pos,
-                 float* kc, float* vc, int maxT, int64_t lstride, float* logits,
-                 int pos_host = -1) {
+void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, int pos0,
+                 const int32_t* d_pos, float* kc, float* vc, int maxT, int64_t lstride,
+                 float* logits, int pos_host = -1) {
   const Dims& d = m->d;
   Work& ws = m->ws;
   const int rows = B * T;
+  const bool gm = use_gemm(d, rows);
   if (pos_host < 0) pos_host = pos0;
   // causal (query, key) pairs per (sequence, head) and the attention traffic
   const double pairs = (double)T * pos_host + 0.5 * (double)T * (T + 1);
   const double at_flops = 4.0 * d.hd * d.H * B * pairs;
   const double at_bytes = (double)B * (2.0 * T * d.qd() + 2.0 * (pos_host + T) * d.kvd()) * 4;
+  const int64_t xplane = (int64_t)rows * d.D, aplane = (int64_t)rows * d.qd();
+  const int64_t hplane = (int64_t)rows * d.dff;
+  const int nt_resid = d.D / gemm_tile_n(rows, d.D);  // ssq partials per row after a RESID
+
+  timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
+    launch_embed_norm(s, d, m->w.wte, ids, rows, ws.x, gm ? ws.xs : nullptr, xplane,
+                      gm ? ws.ssq : nullptr);
+  });
+  int nt = 1;  // partial sums of squares per row of the current residual
   for (int l = 0; l < d.L; ++l) {
     float* lk = kc ? kc + l * lstride : nullptr;  // null: no persistent cache (gpt_forward)
     float* lv = vc ? vc + l * lstride : nullptr;
@@ -347,49 +368,60 @@ void layer_stack(fg_model* m, hipStream_t s, int B, int T, int pos0, const int32
     a.maxT = maxT;
     // q, k, v = rmsnorm(x) Wqkv^T, RoPE on q and k, k/v appended to the cache
     // (and, for a chunk, written as bf16 hi/lo planes for the MFMA attention)
-    // single-query kernel only for a cached step; a cache-less forward
-    // (gpt_forward, kc == null) always takes the chunk kernel
     const bool one = (T == 1 && lk != nullptr);
     const int npos = npos_pad(pos0 + T);
     if (!one) {
       a.qs = m->qs;
-      a.q_plane = (int64_t)rows * d.qd();
+      a.q_plane = aplane;
       a.ks = m->ks;
       a.vt = m->vt;
       a.npos = npos;
       a.kv_plane = (int64_t)B * npos * d.kvd();
     }
-    a.x = ws.x; a.w = m->w.qkv(l); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
-    linear(m, s, GV_QKV, a, d_pos);
+    a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
+    a.w = m->w.qkv(l); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
+    linear(m, s, GV_QKV, a, d_pos, gm);
+    a.qs = nullptr;
+    a.ks = a.vt = nullptr;
+    uint16_t* aos = gm ? ws.aos : nullptr;
     if (one) {
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
-        launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, ws.ao);
+        launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, ws.ao, aos, aplane);
       });
     } else {
       if (pos0 > 0)  // earlier cache positions enter the chunk's key planes
         timed(m, s, FG_K_OTHER, 0, (double)B * pos0 * d.kvd() * 16, [&] {
-          launch_split_cache(s, d, lk, lv, B, maxT, pos0, npos, a.kv_plane, m->ks, m->vt);
+          launch_split_cache(s, d, lk, lv, B, maxT, pos0, npos, (int64_t)B * npos * d.kvd(),
+                             m->ks, m->vt);
         });
       timed(m, s, FG_K_ATTN_CHUNK, at_flops, at_bytes, [&] {
-        launch_attn_mfma(s, d, m->qs, m->ks, m->vt, B, T, npos, pos0, a.q_plane, a.kv_plane,
-                         ws.ao);
+        launch_attn_mfma(s, d, m->qs, m->ks, m->vt, B, T, npos, pos0, aplane,
+                         (int64_t)B * npos * d.kvd(), ws.ao, aos, aplane);
       });
     }
-    a.qs = nullptr;
-    a.ks = a.vt = nullptr;
-    // x += attn_out Wproj^T
-    a.x = ws.ao; a.w = m->w.proj(l); a.N = d.D; a.K = d.qd(); a.norm = 0; a.y = ws.x;
-    linear(m, s, GV_RESID, a, d_pos);
+    // x += attn_out Wproj^T (GEMM path: also the split x and its row sums)
+    a.x = ws.ao; a.xs = ws.aos; a.xs_plane = aplane; a.ssq_n = 0;
+    a.w = m->w.proj(l); a.N = d.D; a.K = d.qd(); a.norm = 0; a.y = ws.x;
+    a.ys = ws.xs; a.ys_plane = xplane; a.ssq_out = ws.ssq;
+    linear(m, s, GV_RESID, a, d_pos, gm);
+    nt = nt_resid;
     // h = relu(rmsnorm(x) Wfc^T)^2
-    a.x = ws.x; a.w = m->w.fc(l); a.N = d.dff; a.K = d.D; a.norm = 1; a.y = ws.h;
-    linear(m, s, GV_RELU2, a, d_pos);
+    a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
+    a.w = m->w.fc(l); a.N = d.dff; a.K = d.D; a.norm = 1; a.y = ws.h;
+    a.ys = ws.hs; a.ys_plane = hplane; a.ssq_out = nullptr;
+    linear(m, s, GV_RELU2, a, d_pos, gm);
     // x += h Wproj2^T
-    a.x = ws.h; a.w = m->w.proj2(l); a.N = d.D; a.K = d.dff; a.norm = 0; a.y = ws.x;
-    linear(m, s, GV_RESID, a, d_pos);
+    a.x = ws.h; a.xs = ws.hs; a.xs_plane = hplane; a.ssq_n = 0;
+    a.w = m->w.proj2(l); a.N = d.D; a.K = d.dff; a.norm = 0; a.y = ws.x;
+    a.ys = ws.xs; a.ys_plane = xplane; a.ssq_out = ws.ssq;
+    linear(m, s, GV_RESID, a, d_pos, gm);
+    nt = nt_resid;
   }
   GemvArgs a = base_args(m);
-  a.M = rows; a.T = T; a.x = ws.x; a.w = m->w.lm; a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
-  linear(m, s, GV_STORE, a, d_pos);
+  a.M = rows; a.T = T;
+  a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
+  a.w = m->w.lm; a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
+  linear(m, s, GV_STORE, a, d_pos, gm);
 }
 
 int32_t check_rope(fg_model* m, int64_t upto) {
@@ -408,9 +440,8 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   RCCHK(ensure_work(m, rows));
   RCCHK(ensure_split(m, (int64_t)B * npos_pad(T) * m->d.kvd()));
   float* logits = d_logits ? d_logits : m->ws.logits;
-  const double eb = (double)rows * m->d.D * 6, vb = (double)rows * m->d.V * 4;
-  timed(m, s, FG_K_OTHER, 0, eb, [&] { launch_embed_norm(s, m->d, m->w.wte, d_ids, rows, m->ws.x); });
-  layer_stack(m, s, B, T, 0, nullptr, nullptr, nullptr, T, 0, logits);
+  const double vb = (double)rows * m->d.V * 4;
+  layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, logits);
   if (d_tgt && d_nll)
     timed(m, s, FG_K_OTHER, 0, vb, [&] { launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll); });
   HIPCHK(hipGetLastError());
@@ -743,10 +774,9 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
   // (TB == 1 runs the single-query kernel on the fp32 cache)
   hipStream_t s = m->stream;
   HIPCHK(hipMemcpyAsync(m->ws.ids, h_ids, rows * 4, hipMemcpyHostToDevice, s));
-  timed(m, s, FG_K_OTHER, 0, (double)rows * m->d.D * 6,
-        [&] { launch_embed_norm(s, m->d, m->w.wte, m->ws.ids, rows, m->ws.x); });
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
-  layer_stack(m, s, B, TB, kv->len, nullptr, kv->k, kv->v, kv->maxT, lstride, m->ws.logits);
+  layer_stack(m, s, m->ws.ids, B, TB, kv->len, nullptr, kv->k, kv->v, kv->maxT, lstride,
+              m->ws.logits);
   HIPCHK(hipGetLastError());
   if (next_ids && TB == 1) {
     launch_argmax(s, m->ws.logits, B, m->d.V, m->ws.amax);
@@ -773,10 +803,9 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
 void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logits,
                           int pos_host) {
   const int B = kv->B;
-  timed(m, s, FG_K_OTHER, 0, (double)B * m->d.D * 6,
-        [&] { launch_embed_norm(s, m->d, m->w.wte, kv->d_ids, B, m->ws.x); });
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
-  layer_stack(m, s, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, m->ws.logits, pos_host);
+  layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, m->ws.logits,
+              pos_host);
   timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
     launch_argmax_step(s, m->ws.logits, B, m->d.V, kv->d_ids, kv->d_out, kv->d_len,
                        kv->d_len + 1, with_logits ? kv->d_lgs : nullptr);

@@ -56,6 +56,13 @@ struct Work {
   float* nll = nullptr;     // [rows]
   float* stat = nullptr;    // [rows] per-row scratch (argmax values etc.)
   int32_t* amax = nullptr;  // [rows]
+  // the MFMA path's activations in the split format (hi plane, lo plane
+  // rows*width elements later) and the residual's per-row partial sums of
+  // squares [rows][D/64]
+  uint16_t* xs = nullptr;   // residual [rows][D]
+  uint16_t* aos = nullptr;  // attention output [rows][H*hd]
+  uint16_t* hs = nullptr;   // relu2(fc) [rows][4D]
+  float* ssq = nullptr;
 };
 
 struct KVCacheDev {
@@ -67,9 +74,11 @@ struct KVCacheDev {
 // ------------------------------------------------------------ launchers
 // All launches go to `s`; shapes are validated by the caller (engine).
 
-// x[r] = rmsnorm(wte[ids[r]])
+// x[r] = rmsnorm(wte[ids[r]]); when xs is set, also the split copy of x
+// (hi plane, lo plane `plane` elements later) and ssq[r] = sum_k x[r][k]^2.
 void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
-                       int64_t rows, float* x);
+                       int64_t rows, float* x, uint16_t* xs = nullptr, int64_t plane = 0,
+                       float* ssq = nullptr);
 
 // GEMV family for M <= 4 token rows, fp32 activations x bf16 weights.
 enum GemvEpi { GV_QKV = 0, GV_RESID = 1, GV_RELU2 = 2, GV_STORE = 3 };
@@ -96,12 +105,28 @@ struct GemvArgs {
   uint16_t* vt;
   int npos;
   int64_t q_plane, kv_plane;  // elements between the hi and lo planes
+  // MFMA GEMM operands in the split format (bf16 hi plane, lo plane
+  // `*_plane` elements later). xs: A rows [M][K]. ssq_in: per-row partial
+  // sums of squares of A, [M][ssq_n] (the row norm). ys: split output
+  // (RESID: the updated residual, RELU2: relu^2). ssq_out: RESID only,
+  // per-row partial sums of squares of the updated residual, one per
+  // N tile, [M][N / tile_n].
+  const uint16_t* xs;
+  int64_t xs_plane;
+  const float* ssq_in;
+  int ssq_n;
+  uint16_t* ys;
+  int64_t ys_plane;
+  float* ssq_out;
 };
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 
-// MFMA GEMM, C[M][N] = epi(rowscale * (A[M][K] . W[N][K]^T)), A fp32 split
-// into bf16 hi+lo on the fly, W bf16, fp32 accumulation.
+// MFMA GEMM, C[M][N] = epi(rowscale * (A[M][K] . W[N][K]^T)), A in the
+// split format (xs), W bf16, fp32 accumulation. K must be a multiple of 64.
 void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a);
+// Width of the N tile the GEMM uses for an M x N problem (the number of
+// ssq_out partials per row is N / gemm_tile_n(M, N)).
+int gemm_tile_n(int64_t M, int N);
 
 // Single-query attention over the cache: q [B][H][hd] at position len-1
 // (cache holds len positions) -> y [B][H*hd].
@@ -115,7 +140,7 @@ void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const floa
 // y [B][T][H*hd].
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
-                      int64_t kv_plane, float* y);
+                      int64_t kv_plane, float* y, uint16_t* ys = nullptr, int64_t ys_plane = 0);
 // Fill the hi/lo key/value planes for cache positions [0, n) from the fp32
 // cache of one layer ([B][maxT][KH*hd]).
 void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const float* vc, int B,
@@ -126,9 +151,10 @@ void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const flo
 void launch_gemv_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
 void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
 // d_len holds the cache length before the step; the query is at *d_len.
+// ys (nullable): write the output in the split format instead of fp32 y.
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* y);
+                            float* y, uint16_t* ys = nullptr, int64_t ys_plane = 0);
 // argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +
 // row] (and the logits row into lgs_out at that slot, when set), then
 // *d_len += 1.

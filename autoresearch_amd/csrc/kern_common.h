@@ -28,6 +28,13 @@ __device__ __forceinline__ void unpack8(const uint4 v, float* f) {
   f[7] = __uint_as_float(v.w & 0xFFFF0000u);
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations (lgkmcnt) but, unlike __syncthreads(), not for its outstanding
+// global loads, so prefetches issued before it stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Sum across the 64 lanes of a wavefront (result valid in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

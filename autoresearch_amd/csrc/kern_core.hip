@@ -53,12 +53,15 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // point, the host ones validate) yields a NaN row instead of a wild read.
 __global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ wte,
                                                     const int32_t* __restrict__ ids, int D, int V,
-                                                    float eps, float* __restrict__ x) {
+                                                    float eps, float* __restrict__ x,
+                                                    uint16_t* __restrict__ xs, int64_t plane,
+                                                    float* __restrict__ ssq) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
   const int id = ids[r];
   if (id < 0 || id >= V) {
     for (int k = threadIdx.x; k < D; k += 256) x[r * D + k] = __builtin_nanf("");
+    if (ssq && threadIdx.x == 0) ssq[r] = __builtin_nanf("");
     return;
   }
   const bf16_t* row = wte + (int64_t)id * D;
@@ -69,14 +72,24 @@ __global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ w
   }
   ss = block_sum<4>(ss, red);
   const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  for (int k = threadIdx.x; k < D; k += 256) x[r * D + k] = bf16_to_f32(row[k]) * inv;
+  float s2 = 0.f;
+  for (int k = threadIdx.x; k < D; k += 256) {
+    const float v = bf16_to_f32(row[k]) * inv;
+    x[r * D + k] = v;
+    if (xs) split_bf16(v, xs + r * D + k, plane);
+    s2 += v * v;
+  }
+  if (ssq) {
+    s2 = block_sum<4>(s2, red);
+    if (threadIdx.x == 0) ssq[r] = s2;
+  }
 }
 
 void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
-                       int64_t rows, float* x) {
+                       int64_t rows, float* x, uint16_t* xs, int64_t plane, float* ssq) {
   if (rows <= 0) return;
   hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V, d.eps,
-                     x);
+                     x, xs, plane, ssq);
 }
 
 // ------------------------------------------------------------ epilogues
@@ -194,7 +207,8 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float* __restrict__ q
                                                      const float* __restrict__ vc, int H, int KH,
                                                      int hd, int maxT,
                                                      const int32_t* __restrict__ d_len, int len_imm,
-                                                     float* __restrict__ y) {
+                                                     float* __restrict__ y,
+                                                     uint16_t* __restrict__ ys, int64_t ys_plane) {
   extern __shared__ float sm[];  // [hd] q, [2*hd] partial out, [len] scores
   __shared__ float red[4];
   const int bh = blockIdx.x, b = bh / H, h = bh % H, kvh = h / (H / KH);
@@ -238,16 +252,22 @@ __global__ __launch_bounds__(256) void k_attn_decode(const float* __restrict__ q
     __syncthreads();
     if (dd < hd) so[g * hd + dd] = acc;
     __syncthreads();
-    if (g == 0 && dd < hd) y[(int64_t)bh * hd + dd] = so[dd] + so[hd + dd];
+    if (g == 0 && dd < hd) {
+      const float o = so[dd] + so[hd + dd];
+      if (ys)
+        split_bf16(o, ys + (int64_t)bh * hd + dd, ys_plane);
+      else
+        y[(int64_t)bh * hd + dd] = o;
+    }
   }
 }
 
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* y) {
+                            float* y, uint16_t* ys, int64_t ys_plane) {
   const size_t lds = sizeof(float) * (size_t)(3 * d.hd + maxT);
   hipLaunchKernelGGL(k_attn_decode, dim3(B * d.H), dim3(256), lds, s, q, kc, vc, d.H, d.KH, d.hd,
-                     maxT, d_len, len, y);
+                     maxT, d_len, len, y, ys, ys_plane);
 }
 
 void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const float* kc,

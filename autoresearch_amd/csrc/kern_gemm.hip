@@ -7,15 +7,25 @@
 // norm(x) W^T = s * (x W^T)).
 //
 // Precision: W is bf16 and exact (the weights are bf16-representable). A is
-// fp32 and is split on the fly into two bf16 terms, A = hi + lo with
-// hi = bf16(A), lo = bf16(A - hi); both go through v_mfma_f32_32x32x16_bf16
-// with fp32 accumulation, so each product carries ~16 mantissa bits of A
-// instead of 8. A single bf16 term moves depth-12 logits by ~3e-3 of
-// max|logit|, more than the 2e-3 parity bound; the split keeps it ~5e-6.
+// an fp32 activation carried as two bf16 terms, A = hi + lo with
+// hi = bf16(A), lo = bf16(A - hi), written in that form once by the kernel
+// that produced it; both terms go through v_mfma_f32_32x32x16_bf16 with
+// fp32 accumulation, so each product carries ~16 mantissa bits of A instead
+// of 8. A single bf16 term moves depth-12 logits by ~3e-3 of max|logit|,
+// more than the 2e-3 parity bound; the split keeps it ~5e-6. The row norm
+// comes from per-row sums of squares of the fp32 values, also written by
+// the producer (one partial per producer N tile, summed here in order).
 //
-// Tiling: 64x64 output tile per 256-thread block (four 64-wide wavefronts in
-// a 2x2 grid, each owning a 32x32 MFMA tile), K step 32 staged through LDS
-// with the next K step's global loads issued before the current MFMAs.
+// Pipeline: NST stages of 32-wide K slices in LDS, filled by
+// global_load_lds_dwordx4 (memory -> LDS without registers), NST-1 slices in
+// flight while the MFMAs consume the oldest. Each 64-byte LDS row (32 bf16)
+// holds its four 16-byte chunks XOR-swizzled by row so the MFMA operand
+// reads (32 rows x one chunk per half-wavefront) do not collide in banks.
+// Tiling: BM x BN per block of NWM x NWN 64-wide wavefronts, each owning
+// (BM/NWM) x (BN/NWN) as 32x32 MFMA blocks. The epilogue is staged through
+// LDS 64 rows at a time so each thread owns a column pair (coalesced stores;
+// a QKV rotation pair in one thread). The host picks the largest tile that
+// still gives every CU work.
 #include "fgpt_internal.h"
 #include "kern_common.h"
 #include "kern_epi.h"
@@ -27,131 +37,261 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int BM = 64, BN = 64, BK = 32;
-constexpr int LDSK = BK + 8;  // bf16 elements per LDS row (pad: 80-byte stride)
+constexpr int BK = 32;    // K slice per stage (bf16 elements = 64 bytes per row)
+constexpr int NST = 4;    // pipeline stages
 
-__device__ __forceinline__ void split_store(const float4 a, const float4 b, uint16_t* hi,
-                                            uint16_t* lo) {
-  const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  uint16_t h[8], l[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    h[i] = f32_to_bf16_rne(v[i]);
-    l[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(h[i]));
-  }
-  uint4 ph, pl;
-  ph.x = h[0] | ((uint32_t)h[1] << 16);
-  ph.y = h[2] | ((uint32_t)h[3] << 16);
-  ph.z = h[4] | ((uint32_t)h[5] << 16);
-  ph.w = h[6] | ((uint32_t)h[7] << 16);
-  pl.x = l[0] | ((uint32_t)l[1] << 16);
-  pl.y = l[2] | ((uint32_t)l[3] << 16);
-  pl.z = l[4] | ((uint32_t)l[5] << 16);
-  pl.w = l[6] | ((uint32_t)l[7] << 16);
-  *(uint4*)hi = ph;
-  *(uint4*)lo = pl;
+// chunk slot of logical 16-byte chunk c in row r
+__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
+
+// 16 bytes per lane, memory -> LDS at m0 + 16*lane (the wavefront's 1 KB
+// block starting at LDS offset `lds`). Issued from asm so that the compiler,
+// which cannot tell which stage a DMA fills, does not drain every load in
+// flight before each LDS read; the kernel orders them with explicit
+// vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
 }
 
-template <int EPI>
-__global__ __launch_bounds__(256) void k_gemm(GemvArgs a, const int32_t* __restrict__ d_pos) {
-  __shared__ __attribute__((aligned(16))) uint16_t sAh[BM * LDSK];
-  __shared__ __attribute__((aligned(16))) uint16_t sAl[BM * LDSK];
-  __shared__ __attribute__((aligned(16))) uint16_t sW[BN * LDSK];
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Stage hand-over: this wavefront's slice loads older than the newest N are
+// in LDS, and its LDS reads of the stage it consumed last have returned
+// (lgkmcnt(0): the compiler may sink the MFMAs that use them below this
+// point, and the stage is refilled by another wavefront right after the
+// barrier), then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void stage_sync() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int EPI, int BM, int BN, int NWM, int NWN>
+__global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
+                                                        const int32_t* __restrict__ d_pos) {
+  constexpr int NW = NWM * NWN, NT = 64 * NW;
+  constexpr int WM = BM / (32 * NWM), WN = BN / (32 * NWN);  // 32x32 blocks per wave
+  // a stage: A hi rows, A lo rows, W rows; 64 bytes each; loaded 16 rows (1 KB)
+  // per wavefront instruction
+  constexpr int ROWS = 2 * BM + BN;
+  constexpr int GROUPS = ROWS / 16;          // 1 KB load groups per stage
+  constexpr int GPW = GROUPS / NW;           // groups per wavefront per stage
+  static_assert(GROUPS % NW == 0 && WM >= 1 && WN >= 1, "tile / wave grid mismatch");
+  constexpr int STAGE_BYTES = ROWS * 64;
+  constexpr int SSTR = BN + 4;  // epilogue staging row stride (floats)
+  // one object per stage: the compiler can then tell a stage being filled
+  // by DMA from the stage being read and need not drain the loads in flight
+  __shared__ __attribute__((aligned(1024))) uint8_t stg0[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t stg1[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t stg2[STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t stg3[STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) float stage[64 * SSTR];
   __shared__ float sinv[BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid >> 1, wn = wid & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int wm = wid / NWN, wn = wid % NWN;
+  // Blocks go to the 8 XCDs round-robin by linear id. Remap so that XCD x
+  // runs a contiguous run of tiles in row-major order: tiles sharing an A
+  // row-block (and the weight panel sweep) stay in one XCD's L2.
+  const int nbn = gridDim.x, ntile = gridDim.x * gridDim.y;
+  int lin = blockIdx.x + nbn * blockIdx.y;
+  if ((ntile & 7) == 0) lin = (lin & 7) * (ntile >> 3) + (lin >> 3);
+  const int m0 = (lin / nbn) * BM, n0 = (lin % nbn) * BN;
   const int M = a.M, K = a.K;
 
-  // loader mapping: thread -> (row, 8-element chunk) of the 64x32 tiles
-  const int lr = tid >> 2, lc = (tid & 3) * 8;
-  const bool arow_ok = (m0 + lr) < M;
-  const float* ag = a.x + (int64_t)(arow_ok ? (m0 + lr) : 0) * K + lc;
-  const bf16_t* wg = a.w + (int64_t)(n0 + lr) * K + lc;
-
-  float4 ra0, ra1;
-  uint4 rw;
-  float ss = 0.f;
-  auto gload = [&](int k0) {
-    if (arow_ok) {
-      ra0 = *(const float4*)(ag + k0);
-      ra1 = *(const float4*)(ag + k0 + 4);
+  // This lane's source rows for each of its load groups (fixed for the whole
+  // K loop): group g covers stage rows 16g .. 16g+15; lane -> row 16g + l/4,
+  // LDS slot l%4, which holds logical chunk swz(row, slot).
+  const uint16_t* src[GPW];
+#pragma unroll
+  for (int q = 0; q < GPW; ++q) {
+    const int g = wid + NW * q;
+    const int r = 16 * g + (lane >> 2), slot = lane & 3;
+    const int c = swz(r, slot);
+    if (r < 2 * BM) {  // A hi (r < BM) or A lo
+      const int ar = r < BM ? r : r - BM;
+      const int row = min(m0 + ar, M - 1);  // rows past M are never stored
+      src[q] = a.xs + (r < BM ? 0 : a.xs_plane) + (int64_t)row * K + c * 8;
     } else {
-      ra0 = make_float4(0.f, 0.f, 0.f, 0.f);
-      ra1 = ra0;
+      src[q] = a.w + (int64_t)(n0 + r - 2 * BM) * K + c * 8;
     }
-    rw = *(const uint4*)(wg + k0);
+  }
+
+  f32x16_t acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = K / BK;  // a multiple of NST (K % 128 == 0, checked by the host)
+  const int klast = K - BK;
+  auto fill = [&](uint8_t* base, int k0) {
+    const uint32_t b = __builtin_amdgcn_readfirstlane(lds_off(base) + wid * 1024);
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) dma16(src[q] + k0, b + NW * q * 1024);
   };
-
-  f32x16_t acc;
+  auto consume = [&](const uint8_t* stg) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-
-  gload(0);
-  for (int k0 = 0; k0 < K; k0 += BK) {
-    __syncthreads();
-    split_store(ra0, ra1, sAh + lr * LDSK + lc, sAl + lr * LDSK + lc);
-    *(uint4*)(sW + lr * LDSK + lc) = rw;
-    ss += ra0.x * ra0.x + ra0.y * ra0.y + ra0.z * ra0.z + ra0.w * ra0.w + ra1.x * ra1.x +
-          ra1.y * ra1.y + ra1.z * ra1.z + ra1.w * ra1.w;
-    __syncthreads();
-    if (k0 + BK < K) gload(k0 + BK);
+    for (int kk = 0; kk < 2; ++kk) {
+      const int c = 2 * kk + (lane >> 5);  // logical chunk of this half-wave
+      bf16x8_t ah[WM], al[WM], bw[WN];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 16) {
-      const int ar = wm * 32 + (lane & 31), br = wn * 32 + (lane & 31);
-      const int kc = kk + 8 * (lane >> 5);
-      const bf16x8_t ah = *(const bf16x8_t*)(sAh + ar * LDSK + kc);
-      const bf16x8_t al = *(const bf16x8_t*)(sAl + ar * LDSK + kc);
-      const bf16x8_t bw = *(const bf16x8_t*)(sW + br * LDSK + kc);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bw, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bw, acc, 0, 0, 0);
+      for (int i = 0; i < WM; ++i) {
+        const int r = (wm * WM + i) * 32 + (lane & 31);
+        ah[i] = *(const bf16x8_t*)(stg + r * 64 + swz(r, c) * 16);
+        al[i] = *(const bf16x8_t*)(stg + (BM + r) * 64 + swz(BM + r, c) * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int r = 2 * BM + (wn * WN + j) * 32 + (lane & 31);
+        bw[j] = *(const bf16x8_t*)(stg + r * 64 + swz(r, c) * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
     }
+  };
+  // prologue: slices 0, 1, 2 in flight; then each step waits for its slice,
+  // refills the stage consumed one step earlier (NST-1 = 3 slices ahead; loads
+  // past the end re-read the last slice so the outstanding count is fixed)
+  fill(stg0, 0);
+  fill(stg1, min(BK, klast));
+  fill(stg2, min(2 * BK, klast));
+  for (int kt = 0; kt < nk; kt += NST) {
+    stage_sync<(NST - 2) * GPW>();
+    fill(stg3, min((kt + 3) * BK, klast));
+    consume(stg0);
+    stage_sync<(NST - 2) * GPW>();
+    fill(stg0, min((kt + 4) * BK, klast));
+    consume(stg1);
+    stage_sync<(NST - 2) * GPW>();
+    fill(stg1, min((kt + 5) * BK, klast));
+    consume(stg2);
+    stage_sync<(NST - 2) * GPW>();
+    fill(stg2, min((kt + 6) * BK, klast));
+    consume(stg3);
   }
-  // row scale: 4 consecutive threads hold the partial sums of one A row
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  // row scale from the producer's partial sums of squares
   if (a.norm) {
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
-    if ((tid & 3) == 0) sinv[lr] = 1.0f / sqrtf(ss / (float)K + a.eps);
+    for (int r = tid; r < BM; r += NT) {
+      float ssum = 0.f;
+      if (m0 + r < M)
+        for (int t = 0; t < a.ssq_n; ++t) ssum += a.ssq_in[(int64_t)(m0 + r) * a.ssq_n + t];
+      sinv[r] = 1.0f / sqrtf(ssum / (float)K + a.eps);
+    }
     __syncthreads();
   }
 
+  // epilogue through LDS, 64 tile rows (two 32-row blocks) per pass
   const int pos0 = d_pos ? *d_pos : a.pos0;
-  const int j = lane & 31;
-  const int n = n0 + wn * 32 + j;
 #pragma unroll
-  for (int rg = 0; rg < 16; ++rg) {
-    const int i = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
-    const int ml = wm * 32 + i;
-    const int m = m0 + ml;
-    float v = acc[rg];
-    if (a.norm) v *= sinv[ml];
-    if (EPI == GV_QKV) {
-      const float partner = __shfl_xor(v, 1, 64);
-      if (m < M && (j & 1) == 0) qkv_pair_epilogue(a, m, pos0, n, v, partner);
-    } else if (m < M) {
-      float* y = a.y + (int64_t)m * a.N + n;
-      if (EPI == GV_RESID) {
-        *y = *y + v;
+  for (int q = 0; q < BM / 64; ++q) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int rb = wm * WM + i;  // 32-row block of the tile
+      if (rb / 2 != q) continue;
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int rg = 0; rg < 16; ++rg) {
+          const int r = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
+          stage[((rb & 1) * 32 + r) * SSTR + (wn * WN + j) * 32 + (lane & 31)] = acc[i][j][rg];
+        }
+    }
+    __syncthreads();
+    // BN/2 consecutive e cover one row; with BN = 128 that is one
+    // wavefront, with BN = 64 half of one (reductions stay in the wave)
+    for (int e = tid; e < 64 * (BN / 2); e += NT) {
+      const int srow = e / (BN / 2), pc = 2 * (e % (BN / 2));
+      const int ml = q * 64 + srow;
+      const int m = m0 + ml, n = n0 + pc;
+      const bool live = m < M;
+      float v0 = stage[srow * SSTR + pc], v1 = stage[srow * SSTR + pc + 1];
+      if (a.norm) {
+        v0 *= sinv[ml];
+        v1 *= sinv[ml];
+      }
+      if (EPI == GV_QKV) {
+        if (live) qkv_pair_epilogue(a, m, pos0, n, v0, v1);
+      } else if (EPI == GV_RESID) {
+        float2 o = make_float2(0.f, 0.f);
+        float* y = a.y + (int64_t)(live ? m : 0) * a.N + n;
+        if (live) {
+          o = *reinterpret_cast<float2*>(y);
+          o.x += v0;
+          o.y += v1;
+          *reinterpret_cast<float2*>(y) = o;
+          uint16_t* ys = a.ys + (int64_t)m * a.N + n;
+          split_bf16(o.x, ys, a.ys_plane);
+          split_bf16(o.y, ys + 1, a.ys_plane);
+        }
+        float sq = o.x * o.x + o.y * o.y;
+#pragma unroll
+        for (int off = BN / 4; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+        if (live && pc == 0) a.ssq_out[(int64_t)m * (a.N / BN) + n0 / BN] = sq;
       } else if (EPI == GV_RELU2) {
-        const float t = v < 0.f ? 0.f : v;
-        *y = t * t;
+        if (live) {
+          const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
+          uint16_t* ys = a.ys + (int64_t)m * a.N + n;
+          split_bf16(t0 * t0, ys, a.ys_plane);
+          split_bf16(t1 * t1, ys + 1, a.ys_plane);
+        }
       } else {
-        *y = v;
+        if (live) *reinterpret_cast<float2*>(a.y + (int64_t)m * a.N + n) = make_float2(v0, v1);
       }
     }
+    __syncthreads();
+  }
+}
+
+template <int EPI>
+void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  const int bn = gemm_tile_n(a.M, a.N);
+  const int64_t mt128 = (a.M + 127) / 128, mt64 = (a.M + 63) / 64;
+  if (bn == 128 && mt128 * (a.N / 128) >= 256) {
+    dim3 g(a.N / 128, (unsigned)mt128);
+    hipLaunchKernelGGL((k_gemm<EPI, 128, 128, 4, 2>), g, dim3(512), 0, s, a, d_pos);
+  } else if (bn == 128) {
+    dim3 g(a.N / 128, (unsigned)mt64);
+    hipLaunchKernelGGL((k_gemm<EPI, 64, 128, 2, 2>), g, dim3(256), 0, s, a, d_pos);
+  } else {
+    dim3 g(a.N / 64, (unsigned)mt64);
+    hipLaunchKernelGGL((k_gemm<EPI, 64, 64, 2, 2>), g, dim3(256), 0, s, a, d_pos);
   }
 }
 
 }  // namespace
 
+// largest tile that still leaves >= 256 blocks (one per CU), else 64 wide
+int gemm_tile_n(int64_t M, int N) {
+  const int64_t mt64 = (M + 63) / 64;
+  return (N % 128 == 0 && mt64 * (N / 128) >= 256) ? 128 : 64;
+}
+
 void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
-  dim3 grid(a.N / BN, (a.M + BM - 1) / BM);
   switch (epi) {
-    case GV_QKV: hipLaunchKernelGGL(k_gemm<GV_QKV>, grid, dim3(256), 0, s, a, d_pos); break;
-    case GV_RESID: hipLaunchKernelGGL(k_gemm<GV_RESID>, grid, dim3(256), 0, s, a, d_pos); break;
-    case GV_RELU2: hipLaunchKernelGGL(k_gemm<GV_RELU2>, grid, dim3(256), 0, s, a, d_pos); break;
-    default: hipLaunchKernelGGL(k_gemm<GV_STORE>, grid, dim3(256), 0, s, a, d_pos); break;
+    case GV_QKV: launch_tile<GV_QKV>(s, a, d_pos); break;
+    case GV_RESID: launch_tile<GV_RESID>(s, a, d_pos); break;
+    case GV_RELU2: launch_tile<GV_RELU2>(s, a, d_pos); break;
+    default: launch_tile<GV_STORE>(s, a, d_pos); break;
   }
 }
 
