@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <map>
 #include <string>
@@ -67,6 +68,9 @@ struct fg_model {
   uint16_t* ks = nullptr;
   uint16_t* vt = nullptr;
   int64_t split_kv_elems = 0;
+  // partial results of the chunk attention
+  float* attn_part = nullptr;
+  int64_t attn_floats = 0;
   int64_t work_bytes = 0;
   int64_t gen = 0;      // bumped whenever a buffer a captured graph uses moves
   std::atomic<int> busy{0};
@@ -291,7 +295,25 @@ int32_t ensure_split(fg_model* m, int64_t elems) {
   m->split_kv_elems = 0;
   HIPCHK(hipMalloc((void**)&m->ks, (size_t)elems * 2 * 2));
   HIPCHK(hipMalloc((void**)&m->vt, (size_t)elems * 2 * 2));
+  // the attention reads whole 64-key steps: padding positions must hold
+  // finite values (zero here; later only values this engine wrote)
+  HIPCHK(hipMemset(m->ks, 0, (size_t)elems * 2 * 2));
+  HIPCHK(hipMemset(m->vt, 0, (size_t)elems * 2 * 2));
   m->split_kv_elems = elems;
+  m->gen++;
+  return FG_OK;
+}
+
+// Scratch of the chunk attention for B x T queries after pos0 cached ones.
+int32_t ensure_attn(fg_model* m, int B, int T, int pos0) {
+  const int64_t floats = attn_scratch_floats(m->d, B, T, pos0);
+  if (floats <= m->attn_floats) return FG_OK;
+  HIPCHK(hipStreamSynchronize(m->stream));
+  if (m->attn_part) HIPCHK(hipFree(m->attn_part));
+  m->attn_part = nullptr;
+  m->attn_floats = 0;
+  HIPCHK(hipMalloc((void**)&m->attn_part, (size_t)floats * 4));
+  m->attn_floats = floats;
   m->gen++;
   return FG_OK;
 }
@@ -396,7 +418,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
         });
       timed(m, s, FG_K_ATTN_CHUNK, at_flops, at_bytes, [&] {
         launch_attn_mfma(s, d, m->qs, m->ks, m->vt, B, T, npos, pos0, aplane,
-                         (int64_t)B * npos * d.kvd(), ws.ao, aos, aplane);
+                         (int64_t)B * npos * d.kvd(), m->attn_part, ws.ao, aos, aplane);
       });
     }
     // x += attn_out Wproj^T (GEMM path: also the split x and its row sums)
@@ -439,6 +461,7 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   if (rows > (1ll << 30) / m->d.V) return seterr(FG_EARG, "B*T too large");
   RCCHK(ensure_work(m, rows));
   RCCHK(ensure_split(m, (int64_t)B * npos_pad(T) * m->d.kvd()));
+  RCCHK(ensure_attn(m, B, T, 0));
   float* logits = d_logits ? d_logits : m->ws.logits;
   const double vb = (double)rows * m->d.V * 4;
   layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, logits);
@@ -598,6 +621,7 @@ extern "C" int32_t fg_model_destroy(fg_model* m) {
   free_work(m);
   if (m->ks) (void)hipFree(m->ks);
   if (m->vt) (void)hipFree(m->vt);
+  if (m->attn_part) (void)hipFree(m->attn_part);
   if (m->w.base) (void)hipFree(m->w.base);
   if (m->d_cos) (void)hipFree(m->d_cos);
   if (m->d_sin) (void)hipFree(m->d_sin);
@@ -770,7 +794,10 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
   RCCHK(check_rope(m, kv->len + TB));
   const int64_t rows = (int64_t)B * TB;
   RCCHK(ensure_work(m, rows));
-  if (TB > 1) RCCHK(ensure_split(m, (int64_t)B * npos_pad(kv->len + TB) * m->d.kvd()));
+  if (TB > 1) {
+    RCCHK(ensure_split(m, (int64_t)B * npos_pad(kv->len + TB) * m->d.kvd()));
+    RCCHK(ensure_attn(m, B, TB, kv->len));
+  }
   // (TB == 1 runs the single-query kernel on the fp32 cache)
   hipStream_t s = m->stream;
   HIPCHK(hipMemcpyAsync(m->ws.ids, h_ids, rows * 4, hipMemcpyHostToDevice, s));

@@ -122,7 +122,7 @@ struct GemvArgs {
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 
 // MFMA GEMM, C[M][N] = epi(rowscale * (A[M][K] . W[N][K]^T)), A in the
-// split format (xs), W bf16, fp32 accumulation. K must be a multiple of 64.
+// split format (xs), W bf16, fp32 accumulation. K must be a multiple of 128.
 void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 // Width of the N tile the GEMM uses for an M x N problem (the number of
 // ssq_out partials per row is N / gemm_tile_n(M, N)).
@@ -136,11 +136,16 @@ void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const floa
 
 // Causal chunk attention of T queries at positions pos0..pos0+T-1 against
 // keys 0..pos0+t, on MFMA from the bf16 hi/lo planes (layouts of
-// GemvArgs::qs/ks/vt; npos = padded row stride of the key planes) ->
-// y [B][T][H*hd].
+// GemvArgs::qs/ks/vt; npos = padded row stride of the key planes, a
+// multiple of 64, with finite values in the padding) -> y [B][T][H*hd]
+// (or its split format in ys). Long key ranges are split over workgroups;
+// their partial results go through `scratch` (attn_scratch_floats floats)
+// and a merge kernel on the same stream.
+int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0);
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
-                      int64_t kv_plane, float* y, uint16_t* ys = nullptr, int64_t ys_plane = 0);
+                      int64_t kv_plane, float* scratch, float* y, uint16_t* ys = nullptr,
+                      int64_t ys_plane = 0);
 // Fill the hi/lo key/value planes for cache positions [0, n) from the fp32
 // cache of one layer ([B][maxT][KH*hd]).
 void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const float* vc, int B,

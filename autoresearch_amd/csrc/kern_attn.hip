@@ -5,13 +5,25 @@
 // head mapping h -> h / (H/KH): causal_attn (src/lib/fortran_attn.f90:30-117)
 // when pos0 = 0 and attn_chunk (:376-425) in general.
 //
-// Formulation: each 64-wide wavefront owns 32 queries and walks 64-key
-// tiles staged in LDS (keys and transposed values, shared by the block's two
-// wavefronts). It forms S^T = K Q^T with v_mfma_f32_32x32x16_bf16 (keys as
-// MFMA rows, queries as columns), so the probabilities come out in exactly
-// the register layout the B operand of O^T = V^T P^T needs: no LDS round
-// trip for P. Online softmax (running max and sum per query) replaces the
-// reference's two passes; the result differs from it only by rounding.
+// Formulation: each 64-wide wavefront owns 32 queries and forms S^T = K Q^T
+// with v_mfma_f32_32x32x16_bf16 (keys as MFMA rows, queries as columns), so
+// the probabilities come out in the register layout the B operand of
+// O^T = V^T P^T needs: no LDS round trip for P. The key rows of each 32-key
+// tile are permuted (bits 2 and 3 of the row index swapped) so that the 8
+// probabilities a lane holds per 16-key step belong to 8 consecutive keys,
+// and the matching V^T operand is one 16-byte LDS read. Online softmax
+// (running max and sum per query, log2 domain) replaces the reference's two
+// passes; the result differs from it only by rounding.
+//
+// Work split: a workgroup (8 wavefronts: 4 query groups x 2 key parities)
+// takes 128 queries against one chunk of at most 512 keys, so a T=2048
+// prefill gives ~40 items per head instead of 16 uneven query blocks. K and
+// V^T tiles (64 keys per step) stream memory -> LDS by global_load_lds into
+// two XOR-swizzled buffers, the next step loading while the current one is
+// consumed. When a query block spans several chunks, each item leaves its
+// unnormalised (O, max, sum) in scratch and a second kernel merges them in
+// chunk order (a device-scope fence per workgroup, needed to merge in the
+// same kernel, costs more than the extra launch).
 //
 // Precision: q, k, v and p are fp32 quantities carried as bf16 hi + lo
 // pairs; each product uses hi*hi + lo*hi + hi*lo (the lo*lo term is below
@@ -31,17 +43,45 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int QG = 32;   // queries per wavefront (MFMA columns)
-constexpr int KT = 32;   // keys per tile (MFMA rows)
+constexpr int QB = 128;  // queries per workgroup (4 groups of 32 MFMA columns)
+constexpr int CK = 512;  // keys per work item
+constexpr int SK = 64;   // keys per pipeline step (two 32-key tiles)
 constexpr float LOG2E = 1.4426950408889634f;
 
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+struct AttnArgs {
+  const uint16_t* qs;
+  const uint16_t* ks;
+  const uint16_t* vt;
+  int H, KH, T, npos, nvalid, pos0;
+  int nbh;  // B * H
+  int nqb;  // query blocks per (sequence, head)
+  int iph;  // work items per (sequence, head)
+  int64_t q_plane, kv_plane;
+  float* y;
+  uint16_t* ys;
+  int64_t ys_plane;
+  float* part;
+};
 
-__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
-  return (uint32_t)lo | ((uint32_t)hi << 16);
+// key chunks of query block j (queries j*QB .. j*QB+QB-1)
+__host__ __device__ inline int chunk_count(int j, int T, int pos0, int nvalid) {
+  const int tl = (j + 1) * QB < T ? (j + 1) * QB : T;
+  const int kend = nvalid < pos0 + tl ? nvalid : pos0 + tl;
+  return (kend + CK - 1) / CK;
 }
 
-// hi/lo bf16 halves of 8 floats, packed as the 8-element MFMA operand.
+// key offset held by row i of a 32-key tile: bits 2 and 3 swapped
+__device__ __forceinline__ int tile_key(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+// 16-byte chunk slot of logical chunk c in LDS row r: K rows (HD*2 bytes)
+// and V^T rows (64 keys = 128 bytes), swizzled so that 16 consecutive rows
+// read at one logical chunk hit distinct banks
+template <int HD>
+__device__ __forceinline__ int kslot(int r, int c) {
+  return HD == 128 ? c ^ (r & 15) : c ^ ((r >> 1) & 7);
+}
+__device__ __forceinline__ int vslot(int d, int c) { return c ^ ((d >> 1) & 7); }
+
 __device__ __forceinline__ void split8(const float* v, bf16x8_t& h, bf16x8_t& l) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -51,142 +91,143 @@ __device__ __forceinline__ void split8(const float* v, bf16x8_t& h, bf16x8_t& l)
   }
 }
 
-// Block = 4 wavefronts = 2 query groups (32 queries each) x 2 key parities.
-// Each step stages two 32-key tiles (one per parity) in LDS; the wavefront
-// of parity p takes tile p, so both query groups share every tile and the
-// key range is walked two tiles at a time. The two parities' running
-// (max, sum, O) are merged through LDS at the end.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ qs,
-                                                   const uint16_t* __restrict__ ks,
-                                                   const uint16_t* __restrict__ vt, int H, int KH,
-                                                   int T, int npos, int nvalid, int pos0,
-                                                   int64_t q_plane, int64_t kv_plane,
-                                                   float* __restrict__ y,
-                                                   uint16_t* __restrict__ ys, int64_t ys_plane) {
-  constexpr int KSTR = HD + 8;  // bf16 per LDS key row
-  constexpr int VSTR = KT + 8;  // bf16 per LDS value-dim row
-  constexpr int NS = HD / 16;   // k-steps over the head dim
-  constexpr int ND = HD / 32;   // 32-row blocks of O^T
-  constexpr int PAR = 2 * KT * KSTR + 2 * HD * VSTR;  // bf16 per parity
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+__device__ __forceinline__ void store_out(const AttnArgs& p, int64_t yo, int d, const float* v) {
+  if (p.ys) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) split_bf16(v[e], p.ys + yo + d + e, p.ys_plane);
+  } else {
+    *(float4*)(p.y + yo + d) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, g = lane >> 5, qi = lane & 31;
-  const int qg = wv & 1, kp = wv >> 1;
-  uint16_t* sKh = lds + kp * PAR;
-  uint16_t* sKl = sKh + KT * KSTR;
-  uint16_t* sVh = sKl + KT * KSTR;
-  uint16_t* sVl = sVh + HD * VSTR;
+template <int HD>
+__global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
+  constexpr int NS = HD / 16;          // k-steps over the head dim
+  constexpr int ND = HD / 32;          // 32-row blocks of O^T
+  constexpr int RBK = HD * 2;          // bytes per K row in LDS
+  constexpr int REG = SK * RBK;        // bytes per region (K hi, K lo, V^T hi, V^T lo)
+  constexpr int STAGE = 4 * REG;
+  constexpr int GPR = REG / 1024;      // 1 KB DMA groups per region
+  constexpr int GPW = 4 * GPR / 8;     // groups per wavefront per stage
+  constexpr int PSTR = QB * (HD + 2);  // floats per scratch item: O, then (max, sum)
+  static_assert(GPR >= 8 && GPR % 8 == 0, "region / wavefront mismatch");
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
 
-  const int nqb = (T + 2 * QG - 1) / (2 * QG);
-  const int qb = nqb - 1 - (int)blockIdx.x;  // longest causal rows first
-  const int bh = blockIdx.y, b = bh / H, h = bh % H, kvh = h / (H / KH);
-  const int64_t bk = (int64_t)b * KH + kvh;
-  const int t = qb * 2 * QG + qg * QG + qi;  // this lane's query (column)
-  const bool tok = t < T;
-  const int qpos = pos0 + t;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int qg = wv & 3, kp = wv >> 2, g = lane >> 5, qi = lane & 31;
+
+  // work item: (sequence*head, query block j, key chunk c); items of one
+  // index across heads are adjacent, heaviest query blocks first
+  const int bh = blockIdx.x % p.nbh;
+  int it = blockIdx.x / p.nbh, j = p.nqb - 1, base = 0, nch;
+  for (;;) {
+    nch = chunk_count(j, p.T, p.pos0, p.nvalid);
+    if (it < nch) break;
+    it -= nch;
+    base += nch;
+    --j;
+  }
+  const int c = it;
+  const int b = bh / p.H, h = bh % p.H, kvh = h / (p.H / p.KH);
+  const int64_t bk = (int64_t)b * p.KH + kvh;
+  const int tq0 = j * QB;
+  const int kend = min(p.nvalid, p.pos0 + min(tq0 + QB, p.T));
+  const int kbeg = c * CK, kstop = min(kend, kbeg + CK);
+  const int nsteps = (kstop - kbeg + SK - 1) / SK;
+
+  const int t = tq0 + qg * 32 + qi;  // this lane's query (column)
+  const bool tok = t < p.T;
+  const int qpos = p.pos0 + t;
+  const bool wact = tq0 + qg * 32 < p.T;  // the wavefront has queries
+  const int wq0 = p.pos0 + tq0 + qg * 32;
+  const int wq1 = p.pos0 + min(tq0 + qg * 32 + 32, p.T) - 1;
 
   bf16x8_t qh[NS], ql[NS];
   {
-    const uint16_t* qp = qs + ((int64_t)bh * T + (tok ? t : 0)) * HD + 8 * g;
+    const uint16_t* qp = p.qs + ((int64_t)bh * p.T + (tok ? t : 0)) * HD + 8 * g;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       uint4 vh = *(const uint4*)(qp + 16 * s);
-      uint4 vl = *(const uint4*)(qp + 16 * s + q_plane);
+      uint4 vl = *(const uint4*)(qp + 16 * s + p.q_plane);
       if (!tok) vh = vl = make_uint4(0, 0, 0, 0);
-      qh[s] = as_bf16x8(vh);
-      ql[s] = as_bf16x8(vl);
+      qh[s] = __builtin_bit_cast(bf16x8_t, vh);
+      ql[s] = __builtin_bit_cast(bf16x8_t, vl);
     }
   }
+
+  // DMA sources of this lane, one per 1 KB group the wavefront fills:
+  // group G = wv + 8q lies in region G / GPR = 8q / GPR (compile time)
+  const uint16_t* src[GPW];
+  int koff[GPW];
+#pragma unroll
+  for (int q = 0; q < GPW; ++q) {
+    const int region = 8 * q / GPR, gi = (wv + 8 * q) % GPR;
+    if (region < 2) {  // K rows: 1024 / RBK rows per group
+      const int row = gi * (1024 / RBK) + lane / (HD / 8), slot = lane % (HD / 8);
+      koff[q] = 32 * (row >> 5) + tile_key(row & 31);
+      src[q] = p.ks + (region ? p.kv_plane : 0) + bk * p.npos * HD + kslot<HD>(row, slot) * 8;
+    } else {  // V^T rows (dims): 8 rows of 64 keys per group
+      const int d = gi * 8 + lane / 8, slot = lane & 7;
+      koff[q] = 0;
+      src[q] = p.vt + (region == 3 ? p.kv_plane : 0) + (bk * HD + d) * p.npos + vslot(d, slot) * 8;
+    }
+  }
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_off(lds) + wv * 1024);
+  auto fill = [&](int stg, int k0) {
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) {
+      const int region = 8 * q / GPR;
+      const uint16_t* g0 =
+          region < 2 ? src[q] + (int64_t)min(k0 + koff[q], p.nvalid - 1) * HD : src[q] + k0;
+      dma16(g0, lds0 + stg * STAGE + 8 * q * 1024);
+    }
+  };
 
   f32x16_t o[ND];
 #pragma unroll
   for (int i = 0; i < ND; ++i)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
-  float m_run = -FLT_MAX, l_run = 0.f;           // in the log2 domain
-  const float c = LOG2E / sqrtf((float)HD);
+  float m_run = -FLT_MAX, l_run = 0.f;  // in the log2 domain
+  const float cs = LOG2E / sqrtf((float)HD);
 
-  const int t_last = min(qb * 2 * QG + 2 * QG, T) - 1;
-  const int kend = min(nvalid, pos0 + t_last + 1);
-  const int wq0 = pos0 + qb * 2 * QG + qg * QG;              // first query position of the wave
-  const int wq1 = pos0 + min(qb * 2 * QG + qg * QG + QG, T) - 1;  // last
-
-  for (int k0 = 0; k0 < kend; k0 += 2 * KT) {
-    __syncthreads();
-    // both parities' K tiles (KT keys x HD) and V^T tiles (HD x KT)
-#pragma unroll
-    for (int i = 0; i < 2 * KT * HD / 8 / 256; ++i) {
-      const int cc = tid + 256 * i, p = cc / (KT * HD / 8), rem = cc % (KT * HD / 8);
-      const int row = rem / (HD / 8), col = (rem % (HD / 8)) * 8;
-      const int key = k0 + p * KT + row;
-      uint4 vh = make_uint4(0, 0, 0, 0), vl = vh;
-      if (key < nvalid) {
-        const uint16_t* src = ks + (bk * npos + key) * HD + col;
-        vh = *(const uint4*)src;
-        vl = *(const uint4*)(src + kv_plane);
-      }
-      uint16_t* dh = lds + p * PAR + row * KSTR + col;
-      *(uint4*)dh = vh;
-      *(uint4*)(dh + KT * KSTR) = vl;
-    }
-#pragma unroll
-    for (int i = 0; i < 2 * HD * KT / 8 / 256; ++i) {
-      const int cc = tid + 256 * i, p = cc / (HD * KT / 8), rem = cc % (HD * KT / 8);
-      const int d = rem / (KT / 8), col = (rem % (KT / 8)) * 8;
-      const int key = k0 + p * KT + col;
-      const uint16_t* src = vt + (bk * HD + d) * npos + key;
-      uint4 vh, vl;
-      if (key + 8 <= nvalid) {
-        vh = *(const uint4*)src;
-        vl = *(const uint4*)(src + kv_plane);
-      } else {
-        uint16_t eh[8], el[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const bool ok = key + e < nvalid;
-          eh[e] = ok ? src[e] : 0;
-          el[e] = ok ? src[e + kv_plane] : 0;
-        }
-        vh = make_uint4(pack2(eh[0], eh[1]), pack2(eh[2], eh[3]), pack2(eh[4], eh[5]),
-                        pack2(eh[6], eh[7]));
-        vl = make_uint4(pack2(el[0], el[1]), pack2(el[2], el[3]), pack2(el[4], el[5]),
-                        pack2(el[6], el[7]));
-      }
-      uint16_t* dh = lds + p * PAR + 2 * KT * KSTR + d * VSTR + col;
-      *(uint4*)dh = vh;
-      *(uint4*)(dh + HD * VSTR) = vl;
-    }
-    __syncthreads();
-    const int kt0 = k0 + kp * KT;       // this wavefront's tile
-    if (kt0 > wq1 || kt0 >= kend) continue;
+  fill(0, kbeg);
+  for (int st = 0; st < nsteps; ++st) {
+    // this step's buffer has landed and every wavefront is done with the other
+    stage_sync<0>();
+    if (st + 1 < nsteps) fill((st + 1) & 1, kbeg + (st + 1) * SK);
+    const int kt0 = kbeg + st * SK + 32 * kp;  // this wavefront's tile
+    if (!wact || kt0 > wq1 || kt0 >= kstop) continue;
+    const uint8_t* S = lds + (st & 1) * STAGE;
 
     // S^T (32 keys x 32 queries) = K Q^T with hi*hi + lo*hi + hi*lo
     f32x16_t sc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[r] = 0.f;
     {
-      const uint16_t* kh = sKh + qi * KSTR + 8 * g;
-      const uint16_t* kl = sKl + qi * KSTR + 8 * g;
+      const int row = 32 * kp + qi;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const bf16x8_t ah = as_bf16x8(*(const uint4*)(kh + 16 * s));
-        const bf16x8_t al = as_bf16x8(*(const uint4*)(kl + 16 * s));
+        const int off = row * RBK + kslot<HD>(row, 2 * s + g) * 16;
+        const bf16x8_t ah = *(const bf16x8_t*)(S + off);
+        const bf16x8_t al = *(const bf16x8_t*)(S + REG + off);
         sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[s], sc, 0, 0, 0);
         sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[s], sc, 0, 0, 0);
         sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[s], sc, 0, 0, 0);
       }
     }
-    // scores in the log2 domain; mask only tiles that reach the diagonal or
+    // scores in the log2 domain; accumulator r of this lane is key
+    // kt0 + 16(r/8) + 8g + (r%8); mask only tiles that reach the diagonal or
     // the end of the valid keys
-    const bool need_mask = (kt0 + KT - 1 > wq0) || (kt0 + KT > nvalid);
+    const bool need_mask = (kt0 + 31 > wq0) || (kt0 + 32 > p.nvalid);
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      float v = sc[r] * c;
+      float v = sc[r] * cs;
       if (need_mask) {
-        const int key = kt0 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (key > qpos || key >= nvalid) v = -INFINITY;
+        const int key = kt0 + 16 * (r >> 3) + 8 * g + (r & 7);
+        if (key > qpos || key >= p.nvalid) v = -INFINITY;
       }
       sc[r] = v;
       mx = fmaxf(mx, v);
@@ -205,13 +246,14 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p = exp2f(sc[r] - m_new);
-      sc[r] = p;
-      ps += p;
+      const float pr = exp2f(sc[r] - m_new);
+      sc[r] = pr;
+      ps += pr;
     }
     l_run += ps + __shfl_xor(ps, 32, 64);
 
-    // O^T += V^T P^T over two 16-key steps
+    // O^T += V^T P^T over two 16-key steps: this lane's 8 probabilities are
+    // keys 16s + 8g .. +7, one 16-byte chunk of each V^T row
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       float pv[8];
@@ -219,17 +261,12 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
       for (int e = 0; e < 8; ++e) pv[e] = sc[8 * s + e];
       bf16x8_t bh8, bl8;
       split8(pv, bh8, bl8);
-      // A operand: V^T row d, keys 16s + {4g..4g+3, 8+4g..8+4g+3}, the key
-      // order the S^T accumulator hands to this lane group
 #pragma unroll
       for (int i = 0; i < ND; ++i) {
         const int d = 32 * i + qi;
-        const uint16_t* vh = sVh + d * VSTR + 16 * s + 4 * g;
-        const uint16_t* vl = sVl + d * VSTR + 16 * s + 4 * g;
-        const uint2 h0 = *(const uint2*)vh, h1 = *(const uint2*)(vh + 8);
-        const uint2 l0 = *(const uint2*)vl, l1 = *(const uint2*)(vl + 8);
-        const bf16x8_t avh = as_bf16x8(make_uint4(h0.x, h0.y, h1.x, h1.y));
-        const bf16x8_t avl = as_bf16x8(make_uint4(l0.x, l0.y, l1.x, l1.y));
+        const int off = 2 * REG + d * 128 + vslot(d, 4 * kp + 2 * s + g) * 16;
+        const bf16x8_t avh = *(const bf16x8_t*)(S + off);
+        const bf16x8_t avl = *(const bf16x8_t*)(S + REG + off);
         o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avh, bh8, o[i], 0, 0, 0);
         o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avl, bh8, o[i], 0, 0, 0);
         o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avh, bl8, o[i], 0, 0, 0);
@@ -237,7 +274,8 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
     }
   }
 
-  // merge the two key parities of each query group through LDS
+  // merge the two key parities of each query group through LDS (no DMA is
+  // in flight: the last step issued none and waited for its own)
   __syncthreads();
   float* xo = reinterpret_cast<float*>(lds) + qg * (ND * 16 * 64 + 128);
   if (kp == 1) {
@@ -249,28 +287,83 @@ __global__ __launch_bounds__(256) void k_attn_mfma(const uint16_t* __restrict__ 
     xo[ND * 16 * 64 + 64 + lane] = l_run;
   }
   __syncthreads();
-  if (kp == 0 && tok) {
+  const int64_t yrow = (int64_t)p.H * HD;
+  if (kp == 0 && wact) {
     const float m1 = xo[ND * 16 * 64 + lane], l1 = xo[ND * 16 * 64 + 64 + lane];
     const float m = fmaxf(m_run, m1);
     const float a0 = exp2f(m_run - m), a1 = exp2f(m1 - m);
-    const float inv = 1.0f / (l_run * a0 + l1 * a1);
-    const int64_t yo = ((int64_t)b * T + t) * ((int64_t)H * HD) + h * HD;
+    const float l = l_run * a0 + l1 * a1;
+    if (nch == 1) {
+      if (tok) {
+        const float inv = 1.0f / l;
+        const int64_t yo = ((int64_t)b * p.T + t) * yrow + h * HD;
 #pragma unroll
-    for (int i = 0; i < ND; ++i)
+        for (int i = 0; i < ND; ++i)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int d = 32 * i + 8 * r4 + 4 * g;
-        float v[4];
+          for (int r4 = 0; r4 < 4; ++r4) {
+            float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          v[e] = (o[i][4 * r4 + e] * a0 + xo[(i * 16 + 4 * r4 + e) * 64 + lane] * a1) * inv;
-        if (ys) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) split_bf16(v[e], ys + yo + d + e, ys_plane);
-        } else {
-          *(float4*)(y + yo + d) = make_float4(v[0], v[1], v[2], v[3]);
-        }
+            for (int e = 0; e < 4; ++e)
+              v[e] = (o[i][4 * r4 + e] * a0 + xo[(i * 16 + 4 * r4 + e) * 64 + lane] * a1) * inv;
+            store_out<HD>(p, yo, 32 * i + 8 * r4 + 4 * g, v);
+          }
       }
+    } else {
+      float* P = p.part + ((int64_t)bh * p.iph + base + c) * PSTR;
+      const int q = qg * 32 + qi;
+#pragma unroll
+      for (int i = 0; i < ND; ++i)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[e] = o[i][4 * r4 + e] * a0 + xo[(i * 16 + 4 * r4 + e) * 64 + lane] * a1;
+          *(float4*)(P + q * HD + 32 * i + 8 * r4 + 4 * g) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+      if (g == 0) *(float2*)(P + QB * HD + 2 * q) = make_float2(m, l);
+    }
+  }
+}
+
+// Query blocks that span several key chunks: combine the chunks' partial
+// (O, max, sum) in chunk order. One workgroup per (sequence*head, block,
+// 32-query quarter); a thread owns 4 dims of 4 queries.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
+  constexpr int PSTR = QB * (HD + 2), D4 = HD / 4;
+  const int bh = blockIdx.x % p.nbh, rest = blockIdx.x / p.nbh;
+  const int j = p.nqb - 1 - rest / 4, quarter = rest % 4;  // heaviest blocks first
+  const int nch = chunk_count(j, p.T, p.pos0, p.nvalid);
+  if (nch == 1) return;  // written by the attention kernel itself
+  int base = 0;
+  for (int i = p.nqb - 1; i > j; --i) base += chunk_count(i, p.T, p.pos0, p.nvalid);
+  const int b = bh / p.H, h = bh % p.H;
+  const int64_t yrow = (int64_t)p.H * HD;
+  const float* P0 = p.part + ((int64_t)bh * p.iph + base) * PSTR;
+#pragma unroll
+  for (int u = 0; u < 32 * D4 / 256; ++u) {
+    const int e = threadIdx.x + 256 * u;
+    const int q = quarter * 32 + e / D4, d = 4 * (e % D4), tt = j * QB + q;
+    if (tt >= p.T) continue;
+    float m = -FLT_MAX;
+    for (int k = 0; k < nch; ++k) m = fmaxf(m, P0[k * PSTR + QB * HD + 2 * q]);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float l = 0.f;
+#pragma unroll 4
+    for (int k = 0; k < nch; ++k) {
+      const float2 ml = *(const float2*)(P0 + k * PSTR + QB * HD + 2 * q);
+      const float4 ov = *(const float4*)(P0 + k * PSTR + q * HD + d);
+      const float w = exp2f(ml.x - m);
+      l += w * ml.y;
+      acc.x += w * ov.x;
+      acc.y += w * ov.y;
+      acc.z += w * ov.z;
+      acc.w += w * ov.w;
+    }
+    const float inv = 1.0f / l;
+    const float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+    store_out<HD>(p, ((int64_t)b * p.T + tt) * yrow + h * HD, d, v);
   }
 }
 
@@ -300,27 +393,57 @@ __global__ __launch_bounds__(256) void k_split_cache(const float* __restrict__ k
 
 }  // namespace
 
+int attn_items_per_head(int T, int pos0) {
+  const int nqb = (T + QB - 1) / QB, nvalid = pos0 + T;
+  int n = 0;
+  for (int j = 0; j < nqb; ++j) n += chunk_count(j, T, pos0, nvalid);
+  return n;
+}
+
+int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0) {
+  return (int64_t)B * d.H * attn_items_per_head(T, pos0) * QB * (d.hd + 2);
+}
+
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
-                      int64_t kv_plane, float* y, uint16_t* ys, int64_t ys_plane) {
+                      int64_t kv_plane, float* scratch, float* y, uint16_t* ys,
+                      int64_t ys_plane) {
   static bool lds_set = false;
   if (!lds_set) {
     (void)hipFuncSetAttribute((const void*)k_attn_mfma<128>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
     (void)hipFuncSetAttribute((const void*)k_attn_mfma<64>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
     lds_set = true;
   }
-  const int nvalid = pos0 + T;
-  dim3 grid((T + 2 * QG - 1) / (2 * QG), B * d.H);
+  AttnArgs p;
+  p.qs = qs;
+  p.ks = ks;
+  p.vt = vt;
+  p.H = d.H;
+  p.KH = d.KH;
+  p.T = T;
+  p.npos = npos;
+  p.nvalid = pos0 + T;
+  p.pos0 = pos0;
+  p.nbh = B * d.H;
+  p.nqb = (T + QB - 1) / QB;
+  p.iph = attn_items_per_head(T, pos0);
+  p.q_plane = q_plane;
+  p.kv_plane = kv_plane;
+  p.y = y;
+  p.ys = ys;
+  p.ys_plane = ys_plane;
+  p.part = scratch;
+  const dim3 grid((unsigned)(p.nbh * p.iph));
+  const bool split = p.iph > p.nqb;  // some query block spans several chunks
+  const dim3 mgrid((unsigned)(p.nbh * p.nqb * 4));
   if (d.hd == 128) {
-    const size_t lds = 2 * (2 * KT * (128 + 8) + 2 * 128 * (KT + 8)) * sizeof(uint16_t);
-    hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(256), lds, s, qs, ks, vt, d.H, d.KH, T,
-                       npos, nvalid, pos0, q_plane, kv_plane, y, ys, ys_plane);
+    hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(512), 2 * 4 * SK * 256, s, p);
+    if (split) hipLaunchKernelGGL(k_attn_merge<128>, mgrid, dim3(256), 0, s, p);
   } else {
-    const size_t lds = 2 * (2 * KT * (64 + 8) + 2 * 64 * (KT + 8)) * sizeof(uint16_t);
-    hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(256), lds, s, qs, ks, vt, d.H, d.KH, T, npos,
-                       nvalid, pos0, q_plane, kv_plane, y, ys, ys_plane);
+    hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(512), 2 * 4 * SK * 128, s, p);
+    if (split) hipLaunchKernelGGL(k_attn_merge<64>, mgrid, dim3(256), 0, s, p);
   }
 }
 

@@ -35,6 +35,30 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// 16 bytes per lane, memory -> LDS at m0 + 16*lane (the wavefront's 1 KB
+// block starting at LDS byte offset `lds`, which must be wave-uniform).
+// Issued from asm so that the compiler, which cannot tell which buffer a
+// DMA fills, does not drain every load in flight before each LDS read; the
+// kernels order them with stage_sync().
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_off(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Stage hand-over for DMA-filled LDS buffers: this wavefront's loads older
+// than the newest N have landed, and its own LDS reads have returned
+// (lgkmcnt(0): the compiler may sink the MFMAs that use them below this
+// point, and a buffer is refilled by another wavefront right after the
+// barrier); then the workgroup barrier.
+template <int N>
+__device__ __forceinline__ void stage_sync() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // Sum across the 64 lanes of a wavefront (result valid in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

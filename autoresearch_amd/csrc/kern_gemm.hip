@@ -43,33 +43,9 @@ constexpr int NST = 4;    // pipeline stages
 // chunk slot of logical 16-byte chunk c in row r
 __device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
 
-// 16 bytes per lane, memory -> LDS at m0 + 16*lane (the wavefront's 1 KB
-// block starting at LDS offset `lds`). Issued from asm so that the compiler,
-// which cannot tell which stage a DMA fills, does not drain every load in
-// flight before each LDS read; the kernel orders them with explicit
-// vmcnt waits and barriers.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
-               : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_off(const void* p) {
-  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
-}
-
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Stage hand-over: this wavefront's slice loads older than the newest N are
-// in LDS, and its LDS reads of the stage it consumed last have returned
-// (lgkmcnt(0): the compiler may sink the MFMAs that use them below this
-// point, and the stage is refilled by another wavefront right after the
-// barrier), then the workgroup barrier.
-template <int N>
-__device__ __forceinline__ void stage_sync() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 template <int EPI, int BM, int BN, int NWM, int NWN>
@@ -202,6 +178,10 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
 
   // epilogue through LDS, 64 tile rows (two 32-row blocks) per pass
   const int pos0 = d_pos ? *d_pos : a.pos0;
+  // Tiles holding v columns that go to the transposed bf16 layout
+  // ([..][hd][npos]: positions contiguous) walk the staged tile row-fastest,
+  // so a wavefront's stores cover 64 consecutive positions of one dim.
+  const bool rows_fast = EPI == GV_QKV && a.vt && n0 + BN > (a.H + a.KH) * a.hd;
 #pragma unroll
   for (int q = 0; q < BM / 64; ++q) {
 #pragma unroll
@@ -220,7 +200,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
     // BN/2 consecutive e cover one row; with BN = 128 that is one
     // wavefront, with BN = 64 half of one (reductions stay in the wave)
     for (int e = tid; e < 64 * (BN / 2); e += NT) {
-      const int srow = e / (BN / 2), pc = 2 * (e % (BN / 2));
+      const int srow = rows_fast ? e % 64 : e / (BN / 2);
+      const int pc = rows_fast ? 2 * (e / 64) : 2 * (e % (BN / 2));
       const int ml = q * 64 + srow;
       const int m = m0 + ml, n = n0 + pc;
       const bool live = m < M;
@@ -280,10 +261,11 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 
 }  // namespace
 
-// largest tile that still leaves >= 256 blocks (one per CU), else 64 wide
+// 128 wide while that still leaves half the CUs a block (the wider tile
+// reads the A panel half as often), else 64 wide
 int gemm_tile_n(int64_t M, int N) {
   const int64_t mt64 = (M + 63) / 64;
-  return (N % 128 == 0 && mt64 * (N / 128) >= 256) ? 128 : 64;
+  return (N % 128 == 0 && mt64 * (N / 128) >= 128) ? 128 : 64;
 }
 
 void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {

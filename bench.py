@@ -178,6 +178,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b64", action="store_true")
+    ap.add_argument("--only", choices=("prefill", "decode_b1", "decode_b64"),
+                    help="run one workload and print its record (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "
@@ -194,6 +196,15 @@ def main():
     m = engine.Model(d, stacks=w)
     c, s = rope_tables(2304, d.head_dim)
     m.set_rope(c.reshape(-1), s.reshape(-1))
+
+    if args.only:
+        rec = {"prefill": lambda: bench_prefill(m, d, args.steps, args.warmup, torch),
+               "decode_b1": lambda: bench_decode(m, d, 1, 16, 32, reps=max(args.steps, 5),
+                                                 warmup=args.warmup),
+               "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0)}[
+            args.only]()
+        print(json.dumps({"only": args.only, **rec}), flush=True)
+        return
 
     log("bench: prefill B=1 T=2048")
     pre = bench_prefill(m, d, args.steps, args.warmup, torch)
