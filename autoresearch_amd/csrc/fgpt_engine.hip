@@ -96,6 +96,7 @@ struct fg_kv {
   int32_t* d_out = nullptr;  // [cap_out] greedy ids
   int64_t cap_out = 0;
   float* d_lgs = nullptr;    // [cap_lgs] per-step logits of fg_decode_greedy
+  float* d_part = nullptr;   // per-chunk partials of the single-query attention
   int64_t cap_lgs = 0;
   // captured runs of greedy steps keyed by (steps, with_logits), valid for gen
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
@@ -359,7 +360,7 @@ GemvArgs base_args(fg_model* m) {
 // chunk kernel (causal_attn / attn_chunk).
 void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, int pos0,
                  const int32_t* d_pos, float* kc, float* vc, int maxT, int64_t lstride,
-                 float* logits, int pos_host = -1) {
+                 float* dec_part, float* logits, int pos_host = -1) {
   const Dims& d = m->d;
   Work& ws = m->ws;
   const int rows = B * T;
@@ -408,7 +409,8 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     uint16_t* aos = gm ? ws.aos : nullptr;
     if (one) {
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
-        launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, ws.ao, aos, aplane);
+        launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, dec_part, ws.ao, aos,
+                               aplane);
       });
     } else {
       if (pos0 > 0)  // earlier cache positions enter the chunk's key planes
@@ -464,7 +466,7 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   RCCHK(ensure_attn(m, B, T, 0));
   float* logits = d_logits ? d_logits : m->ws.logits;
   const double vb = (double)rows * m->d.V * 4;
-  layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, logits);
+  layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, nullptr, logits);
   if (d_tgt && d_nll)
     timed(m, s, FG_K_OTHER, 0, vb, [&] { launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll); });
   HIPCHK(hipGetLastError());
@@ -713,7 +715,7 @@ extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** ou
   if (!m || !out) return seterr(FG_EARG, "NULL argument");
   *out = nullptr;
   if (B < 1 || maxT < 1) return seterr(FG_EARG, "B and maxT must be >= 1");
-  // the decode attention keeps one score per cached position in LDS
+  // the largest cache this build is tested with
   if (maxT > 16000) return seterr(FG_EARG, "maxT %d above the 16000 this build supports", maxT);
   GUARD(m);
   fg_kv* kv = new fg_kv();
@@ -725,6 +727,8 @@ extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** ou
   if (e == hipSuccess) e = hipMalloc((void**)&kv->v, n * 4);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_len, 8);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_ids, (size_t)B * 4);
+  if (e == hipSuccess)
+    e = hipMalloc((void**)&kv->d_part, (size_t)attn_decode_scratch_floats(m->d, B, maxT) * 4);
   if (e == hipSuccess) e = hipMemset(kv->k, 0, n * 4);  // the caller zeroes it in the reference
   if (e == hipSuccess) e = hipMemset(kv->v, 0, n * 4);
   if (e != hipSuccess) {
@@ -732,6 +736,7 @@ extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** ou
     if (kv->v) (void)hipFree(kv->v);
     if (kv->d_len) (void)hipFree(kv->d_len);
     if (kv->d_ids) (void)hipFree(kv->d_ids);
+    if (kv->d_part) (void)hipFree(kv->d_part);
     delete kv;
     return seterr(FG_EHIP, "KV cache allocation (%zu bytes): %s", 2 * n * 4, hipGetErrorString(e));
   }
@@ -744,7 +749,7 @@ extern "C" int32_t fg_kv_destroy(fg_kv* kv) {
   (void)hipSetDevice(kv->m->device);
   (void)hipStreamSynchronize(kv->m->stream);
   for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
-  void* ptrs[] = {kv->k, kv->v, kv->d_len, kv->d_ids, kv->d_out, kv->d_lgs};
+  void* ptrs[] = {kv->k, kv->v, kv->d_len, kv->d_ids, kv->d_out, kv->d_lgs, kv->d_part};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   delete kv;
@@ -803,7 +808,7 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
   HIPCHK(hipMemcpyAsync(m->ws.ids, h_ids, rows * 4, hipMemcpyHostToDevice, s));
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
   layer_stack(m, s, m->ws.ids, B, TB, kv->len, nullptr, kv->k, kv->v, kv->maxT, lstride,
-              m->ws.logits);
+              kv->d_part, m->ws.logits);
   HIPCHK(hipGetLastError());
   if (next_ids && TB == 1) {
     launch_argmax(s, m->ws.logits, B, m->d.V, m->ws.amax);
@@ -831,8 +836,8 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
                           int pos_host) {
   const int B = kv->B;
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
-  layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, m->ws.logits,
-              pos_host);
+  layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, kv->d_part,
+              m->ws.logits, pos_host);
   timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
     launch_argmax_step(s, m->ws.logits, B, m->d.V, kv->d_ids, kv->d_out, kv->d_len,
                        kv->d_len + 1, with_logits ? kv->d_lgs : nullptr);

@@ -128,12 +128,6 @@ void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 // ssq_out partials per row is N / gemm_tile_n(M, N)).
 int gemm_tile_n(int64_t M, int N);
 
-// Single-query attention over the cache: q [B][H][hd] at position len-1
-// (cache holds len positions) -> y [B][H*hd].
-void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const float* kc,
-                        const float* vc, int B, int maxT, int len, float* y, float* scratch,
-                        int64_t scratch_floats);
-
 // Causal chunk attention of T queries at positions pos0..pos0+T-1 against
 // keys 0..pos0+t, on MFMA from the bf16 hi/lo planes (layouts of
 // GemvArgs::qs/ks/vt; npos = padded row stride of the key planes, a
@@ -155,11 +149,16 @@ void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const flo
 // captured decode step replays at successive positions).
 void launch_gemv_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
 void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
-// d_len holds the cache length before the step; the query is at *d_len.
-// ys (nullable): write the output in the split format instead of fp32 y.
+// Single-query attention over the cache: q [B][H][hd] at position len-1
+// -> y [B][H*hd] (or its split format in ys). d_len (nullable) holds the
+// cache length before the step (the query is at *d_len), else len is the
+// length including the query. scratch: attn_decode_scratch_floats(d, B,
+// maxT) floats (a multi-chunk step also launches a merge kernel).
+int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT);
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* y, uint16_t* ys = nullptr, int64_t ys_plane = 0);
+                            float* scratch, float* y, uint16_t* ys = nullptr,
+                            int64_t ys_plane = 0);
 // argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +
 // row] (and the logits row into lgs_out at that slot, when set), then
 // *d_len += 1.

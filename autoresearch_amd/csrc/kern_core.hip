@@ -199,80 +199,180 @@ void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a) {
 }
 
 // ------------------------------------------------------------ decode attention
-// One block per (sequence b, query head h): the single query at position
-// len-1 against cache positions 0..len-1 (fortran_attn.f90:317-362). Scores
-// live in LDS; one wavefront per position computes a 64-lane dot product.
-__global__ __launch_bounds__(256) void k_attn_decode(const float* __restrict__ q,
-                                                     const float* __restrict__ kc,
-                                                     const float* __restrict__ vc, int H, int KH,
-                                                     int hd, int maxT,
-                                                     const int32_t* __restrict__ d_len, int len_imm,
-                                                     float* __restrict__ y,
-                                                     uint16_t* __restrict__ ys, int64_t ys_plane) {
-  extern __shared__ float sm[];  // [hd] q, [2*hd] partial out, [len] scores
-  __shared__ float red[4];
-  const int bh = blockIdx.x, b = bh / H, h = bh % H, kvh = h / (H / KH);
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int len = d_len ? (*d_len + 1) : len_imm;
-  const int kd = KH * hd;
-  float* sq = sm;
-  float* so = sm + hd;
-  float* ss = sm + 3 * hd;
-  for (int i = tid; i < hd; i += 256) sq[i] = q[(int64_t)bh * hd + i];
-  __syncthreads();
-  const float scale = 1.0f / sqrtf((float)hd);
-  const float* K = kc + (int64_t)b * maxT * kd + kvh * hd;
-  const float* V = vc + (int64_t)b * maxT * kd + kvh * hd;
-  for (int p = wid; p < len; p += 4) {
-    const float* kr = K + (int64_t)p * kd;
-    float acc = 0.f;
-    for (int i = lane; i < hd; i += 64) acc += sq[i] * kr[i];
-    acc = wave_sum(acc);
-    if (lane == 0) ss[p] = acc * scale;
+// Single-query attention over the cache (attn_step,
+// src/lib/fortran_attn.f90:317-362): the query at position len-1 against
+// cache positions 0..len-1, softmax in the natural domain as the reference
+// has it. Work item = (sequence b, query head h, chunk of DPC positions), so
+// B=64 at len 1536 gives ~9k workgroups instead of 384 serial scans. Each
+// lane holds a float4 of the head dim: hd/4 lanes cover one cached row, a
+// wavefront covers 64/(hd/4) positions per load, and every K and V row of
+// the chunk is loaded up front (V does not depend on the scores), so a
+// chunk costs one memory round trip. A single-chunk call writes the result;
+// otherwise each chunk leaves (max, sum, O) in scratch for k_attn_dec_merge.
+constexpr int DPC = 64;  // positions per chunk
+
+struct DecArgs {
+  const float* q;  // [B][H][hd]
+  const float* kc;  // [B][maxT][KH*hd]
+  const float* vc;
+  int H, KH, maxT, nchunk;
+  const int32_t* d_len;  // cache length before the step (query at *d_len), or null
+  int len_imm;           // cache length including the query's position, if d_len is null
+  float* y;
+  uint16_t* ys;
+  int64_t ys_plane;
+  float* part;  // [B*H][nchunk][hd + 2]: O, then max and sum
+};
+
+template <int HD>
+__device__ __forceinline__ void dec_store(const DecArgs& a, int64_t o, int d, float4 v) {
+  if (a.ys) {
+    split_bf16(v.x, a.ys + o + d, a.ys_plane);
+    split_bf16(v.y, a.ys + o + d + 1, a.ys_plane);
+    split_bf16(v.z, a.ys + o + d + 2, a.ys_plane);
+    split_bf16(v.w, a.ys + o + d + 3, a.ys_plane);
+  } else {
+    *(float4*)(a.y + o + d) = v;
   }
-  __syncthreads();
-  float m = -FLT_MAX;
-  for (int p = tid; p < len; p += 256) m = fmaxf(m, ss[p]);
-  m = block_max<4>(m, red);
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
+  constexpr int LPP = HD / 4;         // lanes per cached row
+  constexpr int PPW = 64 / LPP;       // positions per wavefront load
+  constexpr int IT = DPC / 4 / PPW;   // loads per wavefront
+  __shared__ float red[8];
+  __shared__ float4 so[4][LPP];
+  const int bh = blockIdx.x, c = blockIdx.y;
+  const int len = a.d_len ? *a.d_len + 1 : a.len_imm;
+  const int p0 = c * DPC;
+  if (p0 >= len) return;
+  const int nch = (len + DPC - 1) / DPC;
+  const int b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.KH);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int sub = lane / LPP, dl = lane % LPP;
+  const int64_t kd = (int64_t)a.KH * HD;
+  const float* K = a.kc + (int64_t)b * a.maxT * kd + kvh * HD + 4 * dl;
+  const float* V = a.vc + (int64_t)b * a.maxT * kd + kvh * HD + 4 * dl;
+  const float4 qv = *(const float4*)(a.q + (int64_t)bh * HD + 4 * dl);
+  float4 kr[IT], vr[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const int p = min(p0 + wv * (DPC / 4) + i * PPW + sub, len - 1);
+    kr[i] = *(const float4*)(K + p * kd);
+    vr[i] = *(const float4*)(V + p * kd);
+  }
+  const float scale = 1.0f / sqrtf((float)HD);
+  float sc[IT], mx = -FLT_MAX;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    float v = qv.x * kr[i].x + qv.y * kr[i].y + qv.z * kr[i].z + qv.w * kr[i].w;
+#pragma unroll
+    for (int o = LPP / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    const int p = p0 + wv * (DPC / 4) + i * PPW + sub;
+    sc[i] = p < len ? v * scale : -INFINITY;
+    mx = fmaxf(mx, sc[i]);
+  }
+  const float m = block_max<4>(mx, red);
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
   float l = 0.f;
-  for (int p = tid; p < len; p += 256) {
-    const float e = expf(ss[p] - m);
-    ss[p] = e;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    const float e = expf(sc[i] - m);
     l += e;
+    o.x += e * vr[i].x;
+    o.y += e * vr[i].y;
+    o.z += e * vr[i].z;
+    o.w += e * vr[i].w;
   }
-  l = block_sum<4>(l, red);
+  // every lane of a row group holds the same e: count each position once
+  l = block_sum<4>(dl == 0 ? l : 0.f, red + 4);
+#pragma unroll
+  for (int off = LPP; off < 64; off <<= 1) {
+    o.x += __shfl_xor(o.x, off, 64);
+    o.y += __shfl_xor(o.y, off, 64);
+    o.z += __shfl_xor(o.z, off, 64);
+    o.w += __shfl_xor(o.w, off, 64);
+  }
+  if (sub == 0) so[wv][dl] = o;
+  __syncthreads();
+  if (tid >= LPP) return;
+  float4 t = so[0][tid];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    t.x += so[w][tid].x;
+    t.y += so[w][tid].y;
+    t.z += so[w][tid].z;
+    t.w += so[w][tid].w;
+  }
+  if (nch == 1) {
+    const float inv = 1.0f / l;
+    dec_store<HD>(a, (int64_t)bh * HD, 4 * tid, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
+  } else {
+    float* P = a.part + ((int64_t)bh * a.nchunk + c) * (HD + 2);
+    *(float4*)(P + 4 * tid) = t;
+    if (tid == 0) *(float2*)(P + HD) = make_float2(m, l);
+  }
+}
+
+// Combine the chunks of a multi-chunk step in chunk order.
+template <int HD>
+__global__ __launch_bounds__(64) void k_attn_dec_merge(DecArgs a) {
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int len = a.d_len ? *a.d_len + 1 : a.len_imm;
+  const int nch = (len + DPC - 1) / DPC;
+  if (nch == 1 || tid >= HD / 4) return;
+  const float* P = a.part + (int64_t)bh * a.nchunk * (HD + 2);
+  float m = -FLT_MAX;
+  for (int c = 0; c < nch; ++c) m = fmaxf(m, P[c * (HD + 2) + HD]);
+  float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+  float l = 0.f;
+  for (int c = 0; c < nch; ++c) {
+    const float2 ml = *(const float2*)(P + c * (HD + 2) + HD);
+    const float4 ov = *(const float4*)(P + c * (HD + 2) + 4 * tid);
+    const float w = expf(ml.x - m);
+    l += w * ml.y;
+    t.x += w * ov.x;
+    t.y += w * ov.y;
+    t.z += w * ov.z;
+    t.w += w * ov.w;
+  }
   const float inv = 1.0f / l;
-  // two position groups of 128 threads; thread owns one head dim per pass
-  const int g = tid / 128, t = tid % 128;
-  for (int d0 = 0; d0 < hd; d0 += 128) {
-    const int dd = d0 + t;
-    float acc = 0.f;
-    if (dd < hd)
-      for (int p = g; p < len; p += 2) acc += ss[p] * inv * V[(int64_t)p * kd + dd];
-    __syncthreads();
-    if (dd < hd) so[g * hd + dd] = acc;
-    __syncthreads();
-    if (g == 0 && dd < hd) {
-      const float o = so[dd] + so[hd + dd];
-      if (ys)
-        split_bf16(o, ys + (int64_t)bh * hd + dd, ys_plane);
-      else
-        y[(int64_t)bh * hd + dd] = o;
-    }
-  }
+  dec_store<HD>(a, (int64_t)bh * HD, 4 * tid, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
+}
+
+int attn_decode_chunks(int maxT) { return (maxT + DPC - 1) / DPC; }
+
+int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT) {
+  return (int64_t)B * d.H * attn_decode_chunks(maxT) * (d.hd + 2);
 }
 
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* y, uint16_t* ys, int64_t ys_plane) {
-  const size_t lds = sizeof(float) * (size_t)(3 * d.hd + maxT);
-  hipLaunchKernelGGL(k_attn_decode, dim3(B * d.H), dim3(256), lds, s, q, kc, vc, d.H, d.KH, d.hd,
-                     maxT, d_len, len, y, ys, ys_plane);
-}
-
-void launch_attn_decode(hipStream_t s, const Dims& d, const float* q, const float* kc,
-                        const float* vc, int B, int maxT, int len, float* y, float*, int64_t) {
-  launch_attn_decode_pos(s, d, q, kc, vc, B, maxT, nullptr, len, y);
+                            float* scratch, float* y, uint16_t* ys, int64_t ys_plane) {
+  DecArgs a;
+  a.q = q;
+  a.kc = kc;
+  a.vc = vc;
+  a.H = d.H;
+  a.KH = d.KH;
+  a.maxT = maxT;
+  // chunks that can be live: all of maxT for a replayed step, else those of len
+  a.nchunk = attn_decode_chunks(d_len ? maxT : len);
+  a.d_len = d_len;
+  a.len_imm = len;
+  a.y = y;
+  a.ys = ys;
+  a.ys_plane = ys_plane;
+  a.part = scratch;
+  const dim3 grid((unsigned)(B * d.H), (unsigned)a.nchunk);
+  if (d.hd == 128) {
+    hipLaunchKernelGGL(k_attn_dec<128>, grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<128>, dim3(B * d.H), dim3(64), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(k_attn_dec<64>, grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<64>, dim3(B * d.H), dim3(64), 0, s, a);
+  }
 }
 
 // ------------------------------------------------------------ argmax / nll
