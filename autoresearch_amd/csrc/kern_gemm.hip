@@ -37,37 +37,38 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int BK = 32;    // K slice per stage (bf16 elements = 64 bytes per row)
-constexpr int NST = 4;    // pipeline stages
-
-// chunk slot of logical 16-byte chunk c in row r
-__device__ __forceinline__ int swz(int r, int c) { return c ^ ((r >> 1) & 3); }
+// 16-byte chunk slot of logical chunk c in row r of a stage whose rows hold
+// BK bf16 (BK/8 chunks): rows r and r+1 share a slot pattern, so 16 rows
+// read at one logical chunk spread over the banks
+template <int BK>
+__device__ __forceinline__ int swz(int r, int c) {
+  return c ^ ((r >> 1) & (BK / 8 - 1));
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int EPI, int BM, int BN, int NWM, int NWN>
+template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST>
 __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
                                                         const int32_t* __restrict__ d_pos) {
   constexpr int NW = NWM * NWN, NT = 64 * NW;
   constexpr int WM = BM / (32 * NWM), WN = BN / (32 * NWN);  // 32x32 blocks per wave
-  // a stage: A hi rows, A lo rows, W rows; 64 bytes each; loaded 16 rows (1 KB)
-  // per wavefront instruction
+  // a stage: A hi rows, A lo rows, W rows of RB bytes each, loaded 1 KB
+  // (1024 / RB rows) per wavefront instruction
+  constexpr int RB = 2 * BK, CPR = BK / 8, RPG = 1024 / RB;
   constexpr int ROWS = 2 * BM + BN;
-  constexpr int GROUPS = ROWS / 16;          // 1 KB load groups per stage
+  constexpr int GROUPS = ROWS / RPG;         // 1 KB load groups per stage
   constexpr int GPW = GROUPS / NW;           // groups per wavefront per stage
   static_assert(GROUPS % NW == 0 && WM >= 1 && WN >= 1, "tile / wave grid mismatch");
-  constexpr int STAGE_BYTES = ROWS * 64;
+  constexpr int STAGE_BYTES = ROWS * RB;
   constexpr int SSTR = BN + 4;  // epilogue staging row stride (floats)
-  // one object per stage: the compiler can then tell a stage being filled
-  // by DMA from the stage being read and need not drain the loads in flight
-  __shared__ __attribute__((aligned(1024))) uint8_t stg0[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t stg1[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t stg2[STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) uint8_t stg3[STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) float stage[64 * SSTR];
+  // NST stages of STAGE_BYTES; after the K loop the same memory (sized for
+  // the larger of the two) stages the epilogue (the DMA is issued from asm, so the compiler never waits on it
+  // for an LDS read: the stage_sync() calls order them)
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  float* stage = reinterpret_cast<float*>(smem);
   __shared__ float sinv[BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -82,14 +83,14 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   const int M = a.M, K = a.K;
 
   // This lane's source rows for each of its load groups (fixed for the whole
-  // K loop): group g covers stage rows 16g .. 16g+15; lane -> row 16g + l/4,
-  // LDS slot l%4, which holds logical chunk swz(row, slot).
+  // K loop): group g covers stage rows RPG*g .. RPG*g+RPG-1; lane -> row
+  // RPG*g + l/CPR, LDS slot l%CPR, which holds logical chunk swz(row, slot).
   const uint16_t* src[GPW];
 #pragma unroll
   for (int q = 0; q < GPW; ++q) {
     const int g = wid + NW * q;
-    const int r = 16 * g + (lane >> 2), slot = lane & 3;
-    const int c = swz(r, slot);
+    const int r = RPG * g + lane / CPR, slot = lane % CPR;
+    const int c = swz<BK>(r, slot);
     if (r < 2 * BM) {  // A hi (r < BM) or A lo
       const int ar = r < BM ? r : r - BM;
       const int row = min(m0 + ar, M - 1);  // rows past M are never stored
@@ -107,28 +108,29 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = K / BK;  // a multiple of NST (K % 128 == 0, checked by the host)
+  const int nk = K / BK;  // K % BK == 0 (checked by the host)
   const int klast = K - BK;
-  auto fill = [&](uint8_t* base, int k0) {
-    const uint32_t b = __builtin_amdgcn_readfirstlane(lds_off(base) + wid * 1024);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_off(smem) + wid * 1024);
+  auto fill = [&](int stg, int k0) {
 #pragma unroll
-    for (int q = 0; q < GPW; ++q) dma16(src[q] + k0, b + NW * q * 1024);
+    for (int q = 0; q < GPW; ++q) dma16(src[q] + k0, lds0 + stg * STAGE_BYTES + NW * q * 1024);
   };
-  auto consume = [&](const uint8_t* stg) {
+  auto consume = [&](int si) {
+    const uint8_t* stg = smem + si * STAGE_BYTES;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < BK / 16; ++kk) {
       const int c = 2 * kk + (lane >> 5);  // logical chunk of this half-wave
       bf16x8_t ah[WM], al[WM], bw[WN];
 #pragma unroll
       for (int i = 0; i < WM; ++i) {
         const int r = (wm * WM + i) * 32 + (lane & 31);
-        ah[i] = *(const bf16x8_t*)(stg + r * 64 + swz(r, c) * 16);
-        al[i] = *(const bf16x8_t*)(stg + (BM + r) * 64 + swz(BM + r, c) * 16);
+        ah[i] = *(const bf16x8_t*)(stg + r * RB + swz<BK>(r, c) * 16);
+        al[i] = *(const bf16x8_t*)(stg + (BM + r) * RB + swz<BK>(BM + r, c) * 16);
       }
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
         const int r = 2 * BM + (wn * WN + j) * 32 + (lane & 31);
-        bw[j] = *(const bf16x8_t*)(stg + r * 64 + swz(r, c) * 16);
+        bw[j] = *(const bf16x8_t*)(stg + r * RB + swz<BK>(r, c) * 16);
       }
 #pragma unroll
       for (int i = 0; i < WM; ++i)
@@ -142,25 +144,21 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
     }
   };
-  // prologue: slices 0, 1, 2 in flight; then each step waits for its slice,
-  // refills the stage consumed one step earlier (NST-1 = 3 slices ahead; loads
-  // past the end re-read the last slice so the outstanding count is fixed)
-  fill(stg0, 0);
-  fill(stg1, min(BK, klast));
-  fill(stg2, min(2 * BK, klast));
+  // prologue: slices 0 .. NST-2 in flight; then each step waits for its
+  // slice and refills the stage consumed one step earlier (NST-1 slices
+  // ahead; loads past the end re-read the last slice so the outstanding
+  // count is fixed)
+#pragma unroll
+  for (int si = 0; si < NST - 1; ++si) fill(si, min(si * BK, klast));
   for (int kt = 0; kt < nk; kt += NST) {
-    stage_sync<(NST - 2) * GPW>();
-    fill(stg3, min((kt + 3) * BK, klast));
-    consume(stg0);
-    stage_sync<(NST - 2) * GPW>();
-    fill(stg0, min((kt + 4) * BK, klast));
-    consume(stg1);
-    stage_sync<(NST - 2) * GPW>();
-    fill(stg1, min((kt + 5) * BK, klast));
-    consume(stg2);
-    stage_sync<(NST - 2) * GPW>();
-    fill(stg2, min((kt + 6) * BK, klast));
-    consume(stg3);
+#pragma unroll
+    for (int si = 0; si < NST; ++si) {
+      if (kt + si < nk) {  // uniform; only the last group can be partial
+        stage_sync<(NST - 2) * GPW>();
+        fill((si + NST - 1) % NST, min((kt + si + NST - 1) * BK, klast));
+        consume(si);
+      }
+    }
   }
   wait_vmcnt<0>();
   __syncthreads();
@@ -243,20 +241,33 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   }
 }
 
+template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST>
+void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  constexpr size_t pipe = (size_t)NST * (2 * BM + BN) * 2 * BK, epi = (size_t)64 * (BN + 4) * 4;
+  constexpr size_t lds = pipe > epi ? pipe : epi;
+  // gfx950: 160 KB of LDS per workgroup, the row scales (BM floats) included
+  static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)k_gemm<EPI, BM, BN, NWM, NWN, BK, NST>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr = true;
+  }
+  const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
+  hipLaunchKernelGGL((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST>), g, dim3(64 * NWM * NWN), lds, s,
+                     a, d_pos);
+}
+
 template <int EPI>
 void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   const int bn = gemm_tile_n(a.M, a.N);
-  const int64_t mt128 = (a.M + 127) / 128, mt64 = (a.M + 63) / 64;
-  if (bn == 128 && mt128 * (a.N / 128) >= 256) {
-    dim3 g(a.N / 128, (unsigned)mt128);
-    hipLaunchKernelGGL((k_gemm<EPI, 128, 128, 4, 2>), g, dim3(512), 0, s, a, d_pos);
-  } else if (bn == 128) {
-    dim3 g(a.N / 128, (unsigned)mt64);
-    hipLaunchKernelGGL((k_gemm<EPI, 64, 128, 2, 2>), g, dim3(256), 0, s, a, d_pos);
-  } else {
-    dim3 g(a.N / 64, (unsigned)mt64);
-    hipLaunchKernelGGL((k_gemm<EPI, 64, 64, 2, 2>), g, dim3(256), 0, s, a, d_pos);
-  }
+  const int64_t mt128 = (a.M + 127) / 128;
+  if (bn == 128 && mt128 * (a.N / 128) >= 256)
+    launch_cfg<EPI, 128, 128, 4, 2, 32, 3>(s, a, d_pos);  // 72 KB: two blocks per CU
+  else if (bn == 128)
+    launch_cfg<EPI, 64, 128, 2, 2, 32, 4>(s, a, d_pos);
+  else
+    launch_cfg<EPI, 64, 64, 2, 2, 32, 4>(s, a, d_pos);
 }
 
 }  // namespace
