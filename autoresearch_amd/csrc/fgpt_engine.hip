@@ -372,7 +372,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   const double at_bytes = (double)B * (2.0 * T * d.qd() + 2.0 * (pos_host + T) * d.kvd()) * 4;
   const int64_t xplane = (int64_t)rows * d.D, aplane = (int64_t)rows * d.qd();
   const int64_t hplane = (int64_t)rows * d.dff;
-  const int nt_resid = d.D / gemm_tile_n(rows, d.D);  // ssq partials per row after a RESID
+  const int nt_resid = gemm_ssq_parts(rows, d.D);  // ssq partials per row after a RESID
 
   timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
     launch_embed_norm(s, d, m->w.wte, ids, rows, ws.x, gm ? ws.xs : nullptr, xplane,

@@ -124,9 +124,8 @@ void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 // MFMA GEMM, C[M][N] = epi(rowscale * (A[M][K] . W[N][K]^T)), A in the
 // split format (xs), W bf16, fp32 accumulation. K must be a multiple of 128.
 void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a);
-// Width of the N tile the GEMM uses for an M x N problem (the number of
-// ssq_out partials per row is N / gemm_tile_n(M, N)).
-int gemm_tile_n(int64_t M, int N);
+// Number of ssq_out partials per row that a RESID GEMM of M x N writes.
+int gemm_ssq_parts(int64_t M, int N);
 
 // Causal chunk attention of T queries at positions pos0..pos0+T-1 against
 // keys 0..pos0+t, on MFMA from the bf16 hi/lo planes (layouts of

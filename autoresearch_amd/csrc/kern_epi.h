@@ -72,4 +72,41 @@ __device__ __forceinline__ void qkv_pair_epilogue(const GemvArgs& a, int m, int 
   }
 }
 
+// One element of a rotation pair, for producers that hold one column per
+// lane: stored column r of the pair-interleaved QKV matrix (r even: head
+// dim j, r odd: dim j + hd/2, j = (r % hd) / 2), `own` its value and `other`
+// the value of the pair's other column. Same arithmetic and destinations as
+// qkv_pair_epilogue.
+__device__ __forceinline__ void qkv_elem_epilogue(const GemvArgs& a, int m, int pos0, int r,
+                                                  float own, float other) {
+  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
+  const int b = m / a.T, t = m % a.T, pos = pos0 + t;
+  const bool odd = r & 1;
+  if (r < qd + kd) {
+    const bool isq = r < qd;
+    const int base = isq ? r : r - qd;
+    const int head = base / hd, j = (base % hd) >> 1, dim = odd ? j + hd / 2 : j;
+    const float cs = a.cosb[(int64_t)pos * (hd / 2) + j];
+    const float sn = a.sinb[(int64_t)pos * (hd / 2) + j];
+    const float x1 = odd ? other : own, x2 = odd ? own : other;
+    const float yv = odd ? x1 * (-sn) + x2 * cs : x1 * cs + x2 * sn;
+    if (isq) {
+      if (a.qs)
+        split_bf16(yv, a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd + dim, a.q_plane);
+      else
+        a.y[(int64_t)m * qd + head * hd + dim] = yv;
+    } else {
+      if (a.kc) a.kc[((int64_t)b * a.maxT + pos) * kd + head * hd + dim] = yv;
+      if (a.ks)
+        split_bf16(yv, a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd + dim, a.kv_plane);
+    }
+  } else {
+    const int base = r - qd - kd;
+    const int head = base / hd, j = (base % hd) >> 1, dim = odd ? j + hd / 2 : j;
+    if (a.vc) a.vc[((int64_t)b * a.maxT + pos) * kd + head * hd + dim] = own;
+    if (a.vt)
+      split_bf16(own, a.vt + (((int64_t)b * a.KH + head) * hd + dim) * a.npos + pos, a.kv_plane);
+  }
+}
+
 }  // namespace fgpt

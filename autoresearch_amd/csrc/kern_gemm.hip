@@ -241,6 +241,230 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   }
 }
 
+// ------------------------------------------------------------------ v2
+// Wave tile (WM x 32) x (WN x 32). The operand fragments of the next
+// 16-deep half slice are read from LDS into a second register set while
+// the MFMAs of the current one run, so LDS latency hides behind MFMA work
+// even at one wavefront per SIMD. The epilogue works straight from the
+// accumulators: lane l of a 32x32 block holds column l % 32 of rows
+// 8(r/4) + 4(l/32) + r%4, r = 0..15, so 32 lanes store 32 consecutive
+// columns of one row.
+template <int WM, int WN>
+struct Frag {
+  bf16x8_t h[WM], l[WM], w[WN];
+};
+
+template <int BM, int WM, int WN>
+__device__ __forceinline__ void frag_load(Frag<WM, WN>& f, const uint8_t* stg, int kk, int wm,
+                                          int wn, int lane) {
+  const int c = 2 * kk + (lane >> 5);  // logical chunk of this half-wave
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int r = (wm * WM + i) * 32 + (lane & 31);
+    f.h[i] = *(const bf16x8_t*)(stg + r * 64 + swz<32>(r, c) * 16);
+    f.l[i] = *(const bf16x8_t*)(stg + (BM + r) * 64 + swz<32>(BM + r, c) * 16);
+  }
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int r = 2 * BM + (wn * WN + j) * 32 + (lane & 31);
+    f.w[j] = *(const bf16x8_t*)(stg + r * 64 + swz<32>(r, c) * 16);
+  }
+}
+
+template <int WM, int WN>
+__device__ __forceinline__ void frag_mma(const Frag<WM, WN>& f, f32x16_t (&acc)[WM][WN]) {
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.h[i], f.w[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.l[i], f.w[j], acc[i][j], 0, 0, 0);
+}
+
+template <int EPI, int NWM, int NWN, int WM, int WN, int NST>
+__global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
+                                                         const int32_t* __restrict__ d_pos) {
+  constexpr int BK = 32, RPG = 16;
+  constexpr int BM = NWM * WM * 32, BN = NWN * WN * 32;
+  constexpr int NW = NWM * NWN, NT = 64 * NW;
+  constexpr int ROWS = 2 * BM + BN, GROUPS = ROWS / RPG, GPW = GROUPS / NW;
+  static_assert(GROUPS % NW == 0, "tile / wave grid mismatch");
+  constexpr int STAGE_BYTES = ROWS * 64;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  __shared__ float sinv[BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid / NWN, wn = wid % NWN;
+  // XCD x runs a contiguous run of tiles in row-major order (see k_gemm)
+  const int nbn = gridDim.x, ntile = gridDim.x * gridDim.y;
+  int lin = blockIdx.x + nbn * blockIdx.y;
+  if ((ntile & 7) == 0) lin = (lin & 7) * (ntile >> 3) + (lin >> 3);
+  const int m0 = (lin / nbn) * BM, n0 = (lin % nbn) * BN;
+  const int M = a.M, K = a.K;
+
+  const uint16_t* src[GPW];
+#pragma unroll
+  for (int q = 0; q < GPW; ++q) {
+    const int g = wid + NW * q;
+    const int r = RPG * g + (lane >> 2), slot = lane & 3;
+    const int c = swz<32>(r, slot);
+    if (r < 2 * BM) {
+      const int ar = r < BM ? r : r - BM;
+      const int row = min(m0 + ar, M - 1);  // rows past M are never stored
+      src[q] = a.xs + (r < BM ? 0 : a.xs_plane) + (int64_t)row * K + c * 8;
+    } else {
+      src[q] = a.w + (int64_t)(n0 + r - 2 * BM) * K + c * 8;
+    }
+  }
+
+  f32x16_t acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = K / BK, klast = K - BK;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_off(smem) + wid * 1024);
+  auto fill = [&](int stg, int k0) {
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) dma16(src[q] + k0, lds0 + stg * STAGE_BYTES + NW * q * 1024);
+  };
+#pragma unroll
+  for (int si = 0; si < NST - 1; ++si) fill(si, min(si * BK, klast));
+  Frag<WM, WN> f0, f1;
+  for (int kt = 0; kt < nk; kt += NST) {
+#pragma unroll
+    for (int si = 0; si < NST; ++si) {
+      if (kt + si < nk) {
+        stage_sync<(NST - 2) * GPW>();
+        fill((si + NST - 1) % NST, min((kt + si + NST - 1) * BK, klast));
+        const uint8_t* stg = smem + si * STAGE_BYTES;
+        frag_load<BM>(f0, stg, 0, wm, wn, lane);
+        if (kt + si > 0) frag_mma(f1, acc);  // second half of the previous slice
+        frag_load<BM>(f1, stg, 1, wm, wn, lane);
+        frag_mma(f0, acc);
+      }
+    }
+  }
+  frag_mma(f1, acc);
+  wait_vmcnt<0>();
+
+  if (a.norm) {
+    for (int r = tid; r < BM; r += NT) {
+      float ssum = 0.f;
+      if (m0 + r < M)
+        for (int t = 0; t < a.ssq_n; ++t) ssum += a.ssq_in[(int64_t)(m0 + r) * a.ssq_n + t];
+      sinv[r] = 1.0f / sqrtf(ssum / (float)K + a.eps);
+    }
+    __syncthreads();
+  }
+
+  const int pos0 = d_pos ? *d_pos : a.pos0;
+  const int half = lane >> 5, cl = lane & 31;
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int rb = (wm * WM + i) * 32 + 4 * half;  // tile row of r = 0
+    float ssq[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ssq[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int cb = n0 + (wn * WN + j) * 32, n = cb + cl;
+      float v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rl = rb + 8 * (r >> 2) + (r & 3);
+        v[r] = a.norm ? acc[i][j][r] * sinv[rl] : acc[i][j][r];
+      }
+      if (EPI == GV_QKV) {
+        const bool vblock = cb >= (a.H + a.KH) * a.hd;  // a 32-column block never straddles
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int m = m0 + rb + 8 * rq;  // rows m .. m+3
+          const int t = m % a.T;
+          const int pos = pos0 + t;
+          if (vblock && a.vt && !a.vc && m + 3 < M && t + 3 < a.T && (pos & 3) == 0) {
+            // four consecutive positions of one dim: one 8-byte store per plane
+            const int base = n - (a.H + a.KH) * a.hd;
+            const int head = base / a.hd, j2 = (base % a.hd) >> 1;
+            const int dim = (n & 1) ? j2 + a.hd / 2 : j2;
+            const int b = m / a.T;
+            uint16_t hb[4], lb[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              hb[e] = f32_to_bf16_rne(v[4 * rq + e]);
+              lb[e] = f32_to_bf16_rne(v[4 * rq + e] - bf16_to_f32(hb[e]));
+            }
+            uint16_t* p = a.vt + (((int64_t)b * a.KH + head) * a.hd + dim) * a.npos + pos;
+            *(uint2*)p = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
+            *(uint2*)(p + a.kv_plane) =
+                make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float own = v[4 * rq + e];
+              const float other = __shfl_xor(own, 1, 64);
+              if (m + e < M) qkv_elem_epilogue(a, m + e, pos0, n, own, other);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + rb + 8 * (r >> 2) + (r & 3);
+          if (m >= M) continue;
+          const int64_t o = (int64_t)m * a.N + n;
+          if (EPI == GV_RESID) {
+            const float x = a.y[o] + v[r];
+            a.y[o] = x;
+            split_bf16(x, a.ys + o, a.ys_plane);
+            ssq[r] += x * x;
+          } else if (EPI == GV_RELU2) {
+            const float t = v[r] < 0.f ? 0.f : v[r];
+            split_bf16(t * t, a.ys + o, a.ys_plane);
+          } else {
+            a.y[o] = v[r];
+          }
+        }
+      }
+    }
+    if (EPI == GV_RESID) {
+      // per-row partial over this wavefront's WN*32 columns
+      const int nparts = a.N / (WN * 32), part = (n0 + wn * WN * 32) / (WN * 32);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float sq = ssq[r];
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+        const int m = m0 + rb + 8 * (r >> 2) + (r & 3);
+        if (cl == 0 && m < M) a.ssq_out[(int64_t)m * nparts + part] = sq;
+      }
+    }
+  }
+}
+
+template <int EPI, int NWM, int NWN, int WM, int WN, int NST>
+void launch_cfg2(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  constexpr int BM = NWM * WM * 32, BN = NWN * WN * 32;
+  constexpr size_t lds = (size_t)NST * (2 * BM + BN) * 64;
+  static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute((const void*)k_gemm2<EPI, NWM, NWN, WM, WN, NST>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    attr = true;
+  }
+  const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
+  hipLaunchKernelGGL((k_gemm2<EPI, NWM, NWN, WM, WN, NST>), g, dim3(64 * NWM * NWN), lds, s, a,
+                     d_pos);
+}
+
 template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST>
 void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr size_t pipe = (size_t)NST * (2 * BM + BN) * 2 * BK, epi = (size_t)64 * (BN + 4) * 4;
@@ -258,11 +482,31 @@ void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
                      a, d_pos);
 }
 
+// 128 wide while that still leaves half the CUs a block (the wider tile
+// reads the A panel half as often), else 64 wide
+int tile_n(int64_t M, int N) {
+  const int64_t mt64 = (M + 63) / 64;
+  return (N % 128 == 0 && mt64 * (N / 128) >= 128) ? 128 : 64;
+}
+
+// Tile choice. The LDS-staged epilogue (k_gemm) serves QKV and RESID,
+// whose outputs are scattered or need per-row reductions; the register
+// epilogue (k_gemm2) serves the plain stores of RELU2 and lm_head, with
+// 128x256 tiles (wave 64x128) when there are >= 1.5 blocks per CU.
 template <int EPI>
 void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
-  const int bn = gemm_tile_n(a.M, a.N);
   const int64_t mt128 = (a.M + 127) / 128;
-  if (bn == 128 && mt128 * (a.N / 128) >= 256)
+  if (EPI == GV_STORE && a.N % 256 == 0 && mt128 * (a.N / 256) >= 384) {
+    launch_cfg2<EPI, 2, 2, 2, 4, 2>(s, a, d_pos);
+    return;
+  }
+  const bool big = a.N % 128 == 0 && mt128 * (a.N / 128) >= 256;
+  if (big && (EPI == GV_RELU2 || EPI == GV_STORE)) {
+    launch_cfg2<EPI, 4, 2, 1, 2, 3>(s, a, d_pos);
+    return;
+  }
+  const int bn = tile_n(a.M, a.N);
+  if (bn == 128 && big)
     launch_cfg<EPI, 128, 128, 4, 2, 32, 3>(s, a, d_pos);  // 72 KB: two blocks per CU
   else if (bn == 128)
     launch_cfg<EPI, 64, 128, 2, 2, 32, 4>(s, a, d_pos);
@@ -272,12 +516,8 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 
 }  // namespace
 
-// 128 wide while that still leaves half the CUs a block (the wider tile
-// reads the A panel half as often), else 64 wide
-int gemm_tile_n(int64_t M, int N) {
-  const int64_t mt64 = (M + 63) / 64;
-  return (N % 128 == 0 && mt64 * (N / 128) >= 128) ? 128 : 64;
-}
+// RESID runs on k_gemm: one sum-of-squares partial per row and N tile.
+int gemm_ssq_parts(int64_t M, int N) { return N / tile_n(M, N); }
 
 void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
   switch (epi) {
