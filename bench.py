@@ -13,10 +13,15 @@ this host's cores on a bounded sample.
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -138,6 +143,82 @@ def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, with_roofline=True)
     return out
 
 
+# --- HBM traffic of the dominant prefill kernel kind, from PMC counters ---
+PMC_KIND = "gemm"                 # kernel kind the prefill roofline is quoted on
+PMC_MATCH = ("k_gemm",)           # kernel-name fragments of that kind
+CALIB_BYTES = 256 << 20           # plain copy of known size: reads and writes this much
+
+
+def pmc_probe():
+    """Child of a `rocprofv3 --pmc` run: one warm-up and one measured T=2048
+    prefill, then a 256 MiB device copy whose counter reading calibrates the
+    counter against known bytes."""
+    import torch
+    from autoresearch_amd import engine
+    from autoresearch_amd.weights import D12, seeded_weights, rope_tables, uniform_ids
+    d = D12
+    m = engine.Model(d, stacks=seeded_weights(d, SEED))
+    c, s = rope_tables(2048, d.head_dim)
+    m.set_rope(c.reshape(-1), s.reshape(-1))
+    T = 2048
+    ids = uniform_ids(2, T + 1, d.vocab)
+    dev = torch.device("cuda:0")
+    d_ids = torch.from_numpy(ids[:T].copy()).to(dev)
+    d_lg = torch.empty(T * d.vocab, dtype=torch.float32, device=dev)
+    for _ in range(2):
+        m.forward_dev(d_ids.data_ptr(), 1, T, d_lg.data_ptr(), 0, 0, 0)
+        m.sync()
+    a = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    print("pmc probe done", flush=True)
+
+
+def pmc_counter(counter: str, launches_per_forward: int):
+    """Mean `counter` (KiB per dispatch) over the dominant kind's launches of
+    the probe's last forward, and the reading for the calibration copy."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    with tempfile.TemporaryDirectory(dir="/tmp") as td:
+        cmd = ["timeout", "-s", "KILL", "180", exe, "--pmc", counter, "--output-format", "csv",
+               "-d", td, "-o", "run", "--", sys.executable, os.path.abspath(__file__),
+               "--pmc-probe"]
+        env = dict(os.environ, TMPDIR="/tmp")
+        r = subprocess.run(cmd, cwd=ROOT, env=env, stdout=subprocess.PIPE,
+                           stderr=subprocess.STDOUT, text=True)
+        files = glob.glob(os.path.join(td, "**", "*counter_collection.csv"), recursive=True)
+        if not files or "pmc probe done" not in r.stdout:
+            log(f"bench: rocprofv3 --pmc {counter} gave no result (rc {r.returncode})")
+            return None
+        rows = sorted(csv.DictReader(open(files[0])), key=lambda x: int(x["Dispatch_Id"]))
+    rows = [x for x in rows if x["Counter_Name"] == counter]
+    kern = [float(x["Counter_Value"]) for x in rows
+            if any(f in x["Kernel_Name"] for f in PMC_MATCH)][-launches_per_forward:]
+    copy = [float(x["Counter_Value"]) for x in rows if "copy" in x["Kernel_Name"].lower()]
+    if len(kern) < launches_per_forward or not copy:
+        return None
+    return sum(kern) / len(kern), copy[-1]
+
+
+def pmc_traffic(launches_per_forward: int):
+    """HBM bytes per launch of the dominant kind: FETCH_SIZE and WRITE_SIZE
+    (two runs), each scaled by bytes / reading of the calibration copy."""
+    out = {}
+    for counter, key in (("FETCH_SIZE", "read"), ("WRITE_SIZE", "write")):
+        got = pmc_counter(counter, launches_per_forward)
+        if got is None:
+            return None
+        kib, calib_kib = got
+        factor = CALIB_BYTES / (calib_kib * 1024.0)
+        out[key + "_bytes"] = kib * 1024.0 * factor
+        out[key + "_calibration"] = factor
+    out["bytes"] = out["read_bytes"] + out["write_bytes"]
+    return out
+
+
 def cpu_baseline(d, w, budget_s: float = 12.0) -> dict:
     """The CPU oracle (a restatement of the reference loops) on this host's
     cores: T=2048 prefill forwards until the budget is spent."""
@@ -180,11 +261,24 @@ def main():
     ap.add_argument("--no-b64", action="store_true")
     ap.add_argument("--only", choices=("prefill", "decode_b1", "decode_b64"),
                     help="run one workload and print its record (for profiling runs)")
+    ap.add_argument("--no-pmc", action="store_true", help="skip the PMC traffic runs")
+    ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.pmc_probe:
+        pmc_probe()
+        return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "
               "(data-parallel sharding is described in DESIGN.md, not built)", file=sys.stderr)
         sys.exit(2)
+
+    # the counter runs go first, before this process touches the GPU
+    traffic = None
+    if not args.only and not args.no_pmc:
+        log("bench: PMC traffic runs (FETCH_SIZE, WRITE_SIZE)")
+        from autoresearch_amd.weights import D12 as _d
+        traffic = pmc_traffic(4 * _d.n_layer + 1)
+        log("bench: traffic", json.dumps(traffic))
 
     import torch
     from autoresearch_amd import engine
@@ -224,6 +318,9 @@ def main():
         cpu["decode_b1"] = cpu_decode_baseline(d, w, c.reshape(-1), s.reshape(-1))
         log("bench: cpu", json.dumps(cpu))
 
+    if traffic is not None and pre["roofline"]["kernel_kind"] == PMC_KIND:
+        pre["roofline"]["traffic"] = traffic["bytes"]
+        pre["roofline"]["traffic_detail"] = traffic
     line = {
         "metric": METRIC, "value": pre["tok_s"], "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": pre["ms_per_step"],
