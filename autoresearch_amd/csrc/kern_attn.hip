@@ -341,25 +341,42 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
   const int b = bh / p.H, h = bh % p.H;
   const int64_t yrow = (int64_t)p.H * HD;
   const float* P0 = p.part + ((int64_t)bh * p.iph + base) * PSTR;
+  // chunks are read 8 at a time, all loads of a group in flight together
 #pragma unroll
   for (int u = 0; u < 32 * D4 / 256; ++u) {
     const int e = threadIdx.x + 256 * u;
     const int q = quarter * 32 + e / D4, d = 4 * (e % D4), tt = j * QB + q;
     if (tt >= p.T) continue;
     float m = -FLT_MAX;
-    for (int k = 0; k < nch; ++k) m = fmaxf(m, P0[k * PSTR + QB * HD + 2 * q]);
+    for (int k0 = 0; k0 < nch; k0 += 8) {
+      float mk[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        mk[k] = k0 + k < nch ? P0[(k0 + k) * PSTR + QB * HD + 2 * q] : -FLT_MAX;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m = fmaxf(m, mk[k]);
+    }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float l = 0.f;
-#pragma unroll 4
-    for (int k = 0; k < nch; ++k) {
-      const float2 ml = *(const float2*)(P0 + k * PSTR + QB * HD + 2 * q);
-      const float4 ov = *(const float4*)(P0 + k * PSTR + q * HD + d);
-      const float w = exp2f(ml.x - m);
-      l += w * ml.y;
-      acc.x += w * ov.x;
-      acc.y += w * ov.y;
-      acc.z += w * ov.z;
-      acc.w += w * ov.w;
+    for (int k0 = 0; k0 < nch; k0 += 8) {
+      float2 ml[8];
+      float4 ov[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const bool ok = k0 + k < nch;
+        ml[k] = ok ? *(const float2*)(P0 + (k0 + k) * PSTR + QB * HD + 2 * q) : make_float2(-FLT_MAX, 0.f);
+        ov[k] = ok ? *(const float4*)(P0 + (k0 + k) * PSTR + q * HD + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (k0 + k >= nch) break;
+        const float w = exp2f(ml[k].x - m);
+        l += w * ml[k].y;
+        acc.x += w * ov[k].x;
+        acc.y += w * ov[k].y;
+        acc.z += w * ov[k].z;
+        acc.w += w * ov[k].w;
+      }
     }
     const float inv = 1.0f / l;
     const float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};

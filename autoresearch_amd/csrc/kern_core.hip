@@ -446,18 +446,35 @@ void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int3
   launch_argmax_step(s, logits, rows, V, out, nullptr, nullptr, nullptr, nullptr);
 }
 
+// One block per row. Rows of up to 256*4*NV4 logits are read once, as
+// float4s held in registers (all loads in flight together); longer rows take
+// the two-pass loop.
+template <int NV4>
 __global__ __launch_bounds__(256) void k_nll(const float* __restrict__ logits,
                                              const int32_t* __restrict__ tgt, int V,
                                              float* __restrict__ out) {
-  __shared__ float red[4];
+  __shared__ float red[8];
   const int64_t row = blockIdx.x;
   const float* l = logits + row * V;
-  float m = -FLT_MAX;
-  for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, l[j]);
-  m = block_max<4>(m, red);
-  float s = 0.f;
-  for (int j = threadIdx.x; j < V; j += 256) s += expf(l[j] - m);
-  s = block_sum<4>(s, red);
+  float m = -FLT_MAX, s = 0.f;
+  if (NV4 > 0) {
+    float4 v[NV4 > 0 ? NV4 : 1];
+#pragma unroll
+    for (int i = 0; i < NV4; ++i) {
+      const int j = 4 * (threadIdx.x + 256 * i);
+      v[i] = j < V ? *(const float4*)(l + j) : make_float4(-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX);
+      m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    }
+    m = block_max<4>(m, red);
+#pragma unroll
+    for (int i = 0; i < NV4; ++i)
+      s += expf(v[i].x - m) + expf(v[i].y - m) + expf(v[i].z - m) + expf(v[i].w - m);
+  } else {
+    for (int j = threadIdx.x; j < V; j += 256) m = fmaxf(m, l[j]);
+    m = block_max<4>(m, red);
+    for (int j = threadIdx.x; j < V; j += 256) s += expf(l[j] - m);
+  }
+  s = block_sum<4>(s, red + 4);
   const int t = tgt[row];
   if (threadIdx.x == 0) out[row] = (t >= 0 && t < V) ? (m + logf(s)) - l[t] : __builtin_nanf("");
 }
@@ -465,7 +482,13 @@ __global__ __launch_bounds__(256) void k_nll(const float* __restrict__ logits,
 void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
                 float* out) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_nll, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
+  // V % 64 == 0, so a row is whole float4s
+  if (V <= 256 * 4 * 8)
+    hipLaunchKernelGGL(k_nll<8>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
+  else if (V <= 256 * 4 * 16)
+    hipLaunchKernelGGL(k_nll<16>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
+  else
+    hipLaunchKernelGGL(k_nll<0>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
 }
 
 }  // namespace fgpt

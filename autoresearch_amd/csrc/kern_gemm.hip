@@ -100,6 +100,24 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
     }
   }
 
+  // epilogue items (column pairs of a 64-row pass) per thread
+  constexpr int EPT = 64 * (BN / 2) / NT;
+  static_assert(EPT * NT == 64 * (BN / 2), "epilogue pass / block size mismatch");
+  // RESID: the residual tile is read now, so its latency hides behind the
+  // K loop instead of stalling the epilogue
+  float2 xres[EPI == GV_RESID ? (BM / 64) * EPT : 1];
+  if (EPI == GV_RESID) {
+#pragma unroll
+    for (int q = 0; q < BM / 64; ++q)
+#pragma unroll
+      for (int k = 0; k < EPT; ++k) {
+        const int e = tid + k * NT, m = m0 + q * 64 + e / (BN / 2);
+        xres[q * EPT + k] = m < M ? *reinterpret_cast<const float2*>(
+                                        a.y + (int64_t)m * a.N + n0 + 2 * (e % (BN / 2)))
+                                  : make_float2(0.f, 0.f);
+      }
+  }
+
   f32x16_t acc[WM][WN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
@@ -197,7 +215,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
     __syncthreads();
     // BN/2 consecutive e cover one row; with BN = 128 that is one
     // wavefront, with BN = 64 half of one (reductions stay in the wave)
-    for (int e = tid; e < 64 * (BN / 2); e += NT) {
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+      const int e = tid + k * NT;
       const int srow = rows_fast ? e % 64 : e / (BN / 2);
       const int pc = rows_fast ? 2 * (e / 64) : 2 * (e % (BN / 2));
       const int ml = q * 64 + srow;
@@ -214,7 +234,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
         float2 o = make_float2(0.f, 0.f);
         float* y = a.y + (int64_t)(live ? m : 0) * a.N + n;
         if (live) {
-          o = *reinterpret_cast<float2*>(y);
+          o = xres[q * EPT + k];
           o.x += v0;
           o.y += v1;
           *reinterpret_cast<float2*>(y) = o;
