@@ -206,16 +206,21 @@ def gpt_step_multi(ids, cosb, sinb, w: dict, d, kv: KVCache) -> np.ndarray:
     return out.reshape(TB, d.vocab)
 
 
-def greedy_decode(prompt, w: dict, d, n_gen: int, cosb, sinb, maxT: int):
+def greedy_decode(prompt, w: dict, d, n_gen: int, cosb, sinb, maxT: int,
+                  prefill_multi: bool = False):
     """The ids-in/ids-out loop of src/app/chat_text.f90:257-278,423-462 with
-    plain argmax: prompt[:-1] through gpt_step, then n_gen steps each fed the
-    previous id. Returns (generated ids, per-step logits)."""
+    plain argmax: prompt[:-1] through gpt_step (or, with prefill_multi, one
+    gpt_step_multi call, as a chunked prefill does), then n_gen steps each fed
+    the previous id. Returns (generated ids, per-step logits)."""
     prompt = i32(prompt)
     hd2 = d.head_dim // 2
     kv = KVCache(d, maxT)
     cosb, sinb = f32(cosb).reshape(-1), f32(sinb).reshape(-1)
-    for t in range(prompt.size - 1):
-        gpt_step(prompt[t:t + 1], cosb[t * hd2:], sinb[t * hd2:], w, d, kv)
+    if prefill_multi and prompt.size > 1:
+        gpt_step_multi(prompt[:-1], cosb, sinb, w, d, kv)
+    else:
+        for t in range(prompt.size - 1):
+            gpt_step(prompt[t:t + 1], cosb[t * hd2:], sinb[t * hd2:], w, d, kv)
     ids = list(prompt)
     logits = []
     for step in range(n_gen):

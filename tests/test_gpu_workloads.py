@@ -1,0 +1,98 @@
+"""The full-size workloads on the GPU against the oracle's committed results.
+
+tests/golden/make_fixtures.py ran the CPU oracle once on the same seeded
+weights and ids (regenerated here bit for bit by the repository's own
+generators) and stored: the per-row NLL sums of the B=8 x 2048 Zipf eval
+rows, the greedy ids of two of the 64 batched-decode sequences (1024-id
+prompt, 512 steps), and the depth-20 GQA model's last prefill row and 256
+greedy ids. Bars: logits within 2e-3 x max|logit|, NLL sums within
+2 x max|d logit| per token, greedy ids identical.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from autoresearch_amd import engine
+from autoresearch_amd.weights import D12, GQA20, rope_tables, seeded_weights, uniform_ids, zipf_ids
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = os.path.join(HERE, "golden")
+TOL = 2e-3
+
+
+def fixture(name):
+    with open(os.path.join(GOLD, name + ".json")) as f:
+        return json.load(f)
+
+
+def model(d, seed, n_pos):
+    m = engine.Model(d, stacks=seeded_weights(d, seed))
+    c, s = rope_tables(n_pos, d.head_dim)
+    m.set_rope(c.reshape(-1), s.reshape(-1))
+    return m
+
+
+def test_eval_rows_b8_t2048():
+    """bpb-style evaluation, B=8 independent rows of T=2048 in one batch."""
+    g = fixture("eval_rows_d12")
+    d, B, T = D12, g["B"], g["T"]
+    rows = zipf_ids(g["seed"], B * (T + 1), d.vocab).reshape(B, T + 1)
+    rows[:, 0] = g["bos"]
+    m = model(d, g["weights_seed"], T)
+    lg, nll = m.forward(rows[:, :T], B, T, targets=rows[:, 1:])
+    maxlogit = float(np.abs(lg).max())
+    got = nll.astype(np.float64).sum(axis=1)
+    ref = np.array(g["nats"])
+    print("eval rows: max |d nats| per row", np.abs(got - ref).max(), "max|logit|", maxlogit)
+    # |d nll| <= 2 max|d logit| per token, max|d logit| <= TOL * max|logit|
+    assert np.all(np.abs(got - ref) <= 2 * TOL * maxlogit * T)
+    # and far inside that bar: below 1e-4 nats per token on average
+    assert np.all(np.abs(got - ref) <= 1e-4 * T)
+    # one row alone gives the same sums as inside the batch
+    _, nll1 = m.forward(rows[B - 1:, :T], 1, T, targets=rows[B - 1:, 1:])
+    assert abs(float(nll1.astype(np.float64).sum()) - got[B - 1]) <= 1e-6 * T
+    m.close()
+
+
+def test_decode_b64_prompt1024_steps512():
+    """Batched greedy decode: 64 sequences, 1024-id prompts, 512 steps."""
+    g = fixture("decode_b64_d12")
+    d, B, P, n = D12, g["B"], g["P"], g["steps"]
+    prompts = uniform_ids(g["seed"], B * P, d.vocab).reshape(B, P)
+    m = model(d, g["weights_seed"], P + n)
+    kv = m.kv(B, P + n)
+    kv.step_multi(prompts[:, :-1], want_logits=False)
+    ids = kv.decode_greedy(prompts[:, -1], n)[0]
+    for b, rec in g["sequences"].items():
+        got = ids[:, int(b)]
+        first = int(np.argmax(got != np.array(rec["ids"]))) if not np.array_equal(got, rec["ids"]) else -1
+        print(f"sequence {b}: first mismatch {first}, oracle min top-2 margin {rec['min_top2_margin']:.3g}")
+        assert np.array_equal(got, np.array(rec["ids"], dtype=np.int32))
+    kv.close()
+    m.close()
+
+
+def test_gqa20_prefill2048_decode256():
+    """Depth-20 GQA (10 query heads over 2 KV heads): prefill and 256 steps."""
+    g = fixture("gqa20_decode")
+    d, P, n = GQA20, g["P"], g["steps"]
+    prompt = uniform_ids(g["seed"], P, d.vocab)
+    m = model(d, g["weights_seed"], P + n)
+    lg, _ = m.forward(prompt, 1, P)
+    last = np.load(os.path.join(GOLD, "gqa20_prefill_last.npy"))
+    rel = float(np.abs(lg.reshape(P, d.vocab)[-1].astype(np.float64) - last).max() / np.abs(last).max())
+    print("gqa20 last prefill row rel err", rel)
+    assert rel < TOL
+    kv = m.kv(1, P + n)
+    kv.step_multi(prompt[None, :-1], want_logits=False)
+    ids = kv.decode_greedy(prompt[None, -1:], n)[0][:, 0]
+    ref = np.array(g["ids"], dtype=np.int32)
+    first = int(np.argmax(ids != ref)) if not np.array_equal(ids, ref) else -1
+    print(f"gqa20 decode: first mismatch {first}, oracle min top-2 margin {g['min_top2_margin']:.3g}")
+    assert np.array_equal(ids, ref)
+    kv.close()
+    m.close()
