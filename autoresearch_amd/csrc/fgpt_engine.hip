@@ -245,7 +245,7 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
 void free_work(fg_model* m) {
   Work& ws = m->ws;
   void* ptrs[] = {ws.x, ws.q, ws.ao, ws.h, ws.logits, ws.ids, ws.tgt, ws.nll, ws.stat, ws.amax,
-                  ws.xs, ws.aos, ws.hs, ws.ssq, m->qs};
+                  ws.xs, ws.aos, ws.hs, ws.ssq, ws.part, m->qs};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   ws = Work();
@@ -280,6 +280,16 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
   RCCHK(alloc((void**)&ws.aos, rows * d.qd() * 2 * 2));
   RCCHK(alloc((void**)&ws.hs, rows * d.dff * 2 * 2));
   RCCHK(alloc((void**)&ws.ssq, rows * (d.D / 64) * 4));
+  // split-K partials of the small-M GEMMs: the largest any row count up to
+  // `rows` needs over the five GEMM shapes
+  int64_t part = 0;
+  for (int64_t r = 1; r <= rows && r <= 128; ++r) {
+    const int64_t shapes[5][2] = {{d.nqkv(), d.D}, {d.D, d.qd()}, {d.dff, d.D}, {d.D, d.dff},
+                                  {d.V, d.D}};
+    for (auto& sh : shapes)
+      part = std::max(part, gemm_splitk_floats(r, (int)sh[0], (int)sh[1]));
+  }
+  if (part > 0) RCCHK(alloc((void**)&ws.part, part * 4));
   ws.rows = rows;
   m->work_bytes = total;
   m->gen++;
@@ -343,6 +353,7 @@ void linear(fg_model* m, hipStream_t s, GemvEpi epi, const GemvArgs& a, const in
 GemvArgs base_args(fg_model* m) {
   GemvArgs a;
   memset(&a, 0, sizeof a);
+  a.part = m->ws.part;
   a.eps = m->d.eps;
   a.cosb = m->d_cos;
   a.sinb = m->d_sin;
@@ -372,7 +383,8 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   const double at_bytes = (double)B * (2.0 * T * d.qd() + 2.0 * (pos_host + T) * d.kvd()) * 4;
   const int64_t xplane = (int64_t)rows * d.D, aplane = (int64_t)rows * d.qd();
   const int64_t hplane = (int64_t)rows * d.dff;
-  const int nt_resid = gemm_ssq_parts(rows, d.D);  // ssq partials per row after a RESID
+  // ssq partials per row after the attention-output RESID
+  const int nt_resid = gemm_ssq_parts(rows, d.D, d.qd());
 
   timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
     launch_embed_norm(s, d, m->w.wte, ids, rows, ws.x, gm ? ws.xs : nullptr, xplane,
@@ -439,7 +451,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     a.w = m->w.proj2(l); a.N = d.D; a.K = d.dff; a.norm = 0; a.y = ws.x;
     a.ys = ws.xs; a.ys_plane = xplane; a.ssq_out = ws.ssq;
     linear(m, s, GV_RESID, a, d_pos, gm);
-    nt = nt_resid;
+    nt = gemm_ssq_parts(rows, d.D, d.dff);
   }
   GemvArgs a = base_args(m);
   a.M = rows; a.T = T;

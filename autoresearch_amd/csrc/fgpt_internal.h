@@ -63,6 +63,7 @@ struct Work {
   uint16_t* aos = nullptr;  // attention output [rows][H*hd]
   uint16_t* hs = nullptr;   // relu2(fc) [rows][4D]
   float* ssq = nullptr;
+  float* part = nullptr;    // split-K partial sums of the small-M GEMMs
 };
 
 struct KVCacheDev {
@@ -118,14 +119,22 @@ struct GemvArgs {
   uint16_t* ys;
   int64_t ys_plane;
   float* ssq_out;
+  // split-K scratch for small-M GEMMs (nullable): the K-split partial sums,
+  // [splits][M][N] fp32, reduced in split order by a second kernel that
+  // applies the norm and the epilogue (RESID then writes one ssq partial per
+  // row). Sized by gemm_splitk_floats.
+  float* part;
 };
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 
 // MFMA GEMM, C[M][N] = epi(rowscale * (A[M][K] . W[N][K]^T)), A in the
 // split format (xs), W bf16, fp32 accumulation. K must be a multiple of 128.
 void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a);
-// Number of ssq_out partials per row that a RESID GEMM of M x N writes.
-int gemm_ssq_parts(int64_t M, int N);
+// Number of ssq_out partials per row that a RESID GEMM of M x N x K
+// writes (when it is given split-K scratch, if it splits).
+int gemm_ssq_parts(int64_t M, int N, int K);
+// Floats of split-K scratch an M x N x K GEMM needs (0: it does not split).
+int64_t gemm_splitk_floats(int64_t M, int N, int K);
 
 // Causal chunk attention of T queries at positions pos0..pos0+T-1 against
 // keys 0..pos0+t, on MFMA from the bf16 hi/lo planes (layouts of

@@ -81,6 +81,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   if ((ntile & 7) == 0) lin = (lin & 7) * (ntile >> 3) + (lin >> 3);
   const int m0 = (lin / nbn) * BM, n0 = (lin % nbn) * BN;
   const int M = a.M, K = a.K;
+  // split-K (a.part set): this block sums K range [kz*klen, kz*klen + klen)
+  const int kz = blockIdx.z, klen = K / (int)gridDim.z, kbeg = kz * klen;
 
   // This lane's source rows for each of its load groups (fixed for the whole
   // K loop): group g covers stage rows RPG*g .. RPG*g+RPG-1; lane -> row
@@ -94,9 +96,9 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
     if (r < 2 * BM) {  // A hi (r < BM) or A lo
       const int ar = r < BM ? r : r - BM;
       const int row = min(m0 + ar, M - 1);  // rows past M are never stored
-      src[q] = a.xs + (r < BM ? 0 : a.xs_plane) + (int64_t)row * K + c * 8;
+      src[q] = a.xs + (r < BM ? 0 : a.xs_plane) + (int64_t)row * K + kbeg + c * 8;
     } else {
-      src[q] = a.w + (int64_t)(n0 + r - 2 * BM) * K + c * 8;
+      src[q] = a.w + (int64_t)(n0 + r - 2 * BM) * K + kbeg + c * 8;
     }
   }
 
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   // RESID: the residual tile is read now, so its latency hides behind the
   // K loop instead of stalling the epilogue
   float2 xres[EPI == GV_RESID ? (BM / 64) * EPT : 1];
-  if (EPI == GV_RESID) {
+  if (EPI == GV_RESID && !a.part) {
 #pragma unroll
     for (int q = 0; q < BM / 64; ++q)
 #pragma unroll
@@ -126,8 +128,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = K / BK;  // K % BK == 0 (checked by the host)
-  const int klast = K - BK;
+  const int nk = klen / BK;  // klen % BK == 0 (checked by the host)
+  const int klast = klen - BK;
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_off(smem) + wid * 1024);
   auto fill = [&](int stg, int k0) {
 #pragma unroll
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   __syncthreads();
 
   // row scale from the producer's partial sums of squares
-  if (a.norm) {
+  if (a.norm && !a.part) {
     for (int r = tid; r < BM; r += NT) {
       float ssum = 0.f;
       if (m0 + r < M)
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   // Tiles holding v columns that go to the transposed bf16 layout
   // ([..][hd][npos]: positions contiguous) walk the staged tile row-fastest,
   // so a wavefront's stores cover 64 consecutive positions of one dim.
-  const bool rows_fast = EPI == GV_QKV && a.vt && n0 + BN > (a.H + a.KH) * a.hd;
+  const bool rows_fast = EPI == GV_QKV && a.vt && !a.part && n0 + BN > (a.H + a.KH) * a.hd;
 #pragma unroll
   for (int q = 0; q < BM / 64; ++q) {
 #pragma unroll
@@ -224,6 +226,11 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
       const int m = m0 + ml, n = n0 + pc;
       const bool live = m < M;
       float v0 = stage[srow * SSTR + pc], v1 = stage[srow * SSTR + pc + 1];
+      if (a.part) {  // raw partial; the reduce kernel applies norm and epilogue
+        if (live)
+          *reinterpret_cast<float2*>(a.part + ((int64_t)kz * M + m) * a.N + n) = make_float2(v0, v1);
+        continue;
+      }
       if (a.norm) {
         v0 *= sinv[ml];
         v1 *= sinv[ml];
@@ -509,35 +516,122 @@ int tile_n(int64_t M, int N) {
   return (N % 128 == 0 && mt64 * (N / 128) >= 128) ? 128 : 64;
 }
 
+// Small M (batched decode, short chunks): too few output tiles to fill the
+// chip, so K is split over blockIdx.z as well: 64x64 tiles, enough splits
+// for ~256 blocks, each split a whole number of 32-wide slices.
+constexpr int64_t SPLITK_MAX_M = 128;
+
+int splitk_count(int64_t M, int N, int K) {
+  if (M > SPLITK_MAX_M || N % 64 != 0) return 1;
+  const int nb = (int)((M + 63) / 64) * (N / 64), nsl = K / 32;
+  int sp = (256 + nb - 1) / nb;
+  if (sp > nsl) sp = nsl;
+  while (sp > 1 && nsl % sp != 0) --sp;
+  return sp;
+}
+
+// Sum of the K-split partials in split order, then the row norm and the
+// epilogue; one block per row. RESID leaves one sum-of-squares partial per
+// row (the whole row).
+template <int EPI>
+__global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
+                                                       const int32_t* __restrict__ d_pos) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x, N = a.N;
+  float inv = 1.f;
+  if (a.norm) {
+    float ssum = 0.f;
+    for (int t = 0; t < a.ssq_n; ++t) ssum += a.ssq_in[(int64_t)m * a.ssq_n + t];
+    inv = 1.0f / sqrtf(ssum / (float)a.K + a.eps);
+  }
+  const int pos0 = d_pos ? *d_pos : a.pos0;
+  float sq = 0.f;
+  for (int n = 2 * tid; n < N; n += 512) {
+    float v0 = 0.f, v1 = 0.f;
+    for (int sp = 0; sp < splits; ++sp) {
+      const float2 p = *reinterpret_cast<const float2*>(a.part + ((int64_t)sp * a.M + m) * N + n);
+      v0 += p.x;
+      v1 += p.y;
+    }
+    v0 *= inv;
+    v1 *= inv;
+    const int64_t o = (int64_t)m * N + n;
+    if (EPI == GV_QKV) {
+      qkv_pair_epilogue(a, m, pos0, n, v0, v1);
+    } else if (EPI == GV_RESID) {
+      float2 x = *reinterpret_cast<const float2*>(a.y + o);
+      x.x += v0;
+      x.y += v1;
+      *reinterpret_cast<float2*>(a.y + o) = x;
+      if (a.ys) {
+        split_bf16(x.x, a.ys + o, a.ys_plane);
+        split_bf16(x.y, a.ys + o + 1, a.ys_plane);
+      }
+      sq += x.x * x.x + x.y * x.y;
+    } else if (EPI == GV_RELU2) {
+      const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
+      split_bf16(t0 * t0, a.ys + o, a.ys_plane);
+      split_bf16(t1 * t1, a.ys + o + 1, a.ys_plane);
+    } else {
+      *reinterpret_cast<float2*>(a.y + o) = make_float2(v0, v1);
+    }
+  }
+  if (EPI == GV_RESID && a.ssq_out) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = sq;
+    __syncthreads();
+    if (tid == 0) a.ssq_out[m] = red[0] + red[1] + red[2] + red[3];
+  }
+}
+
 // Tile choice. The LDS-staged epilogue (k_gemm) serves QKV and RESID,
 // whose outputs are scattered or need per-row reductions; the register
 // epilogue (k_gemm2) serves the plain stores of RELU2 and lm_head, with
 // 128x256 tiles (wave 64x128) when there are >= 1.5 blocks per CU.
 template <int EPI>
 void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  const int sp = a.part ? splitk_count(a.M, a.N, a.K) : 1;
+  if (sp > 1) {
+    constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
+    const dim3 g(a.N / 64, (unsigned)((a.M + 63) / 64), (unsigned)sp);
+    hipLaunchKernelGGL((k_gemm<EPI, 64, 64, 2, 2, 32, 4>), g, dim3(256), lds, s, a, d_pos);
+    hipLaunchKernelGGL((k_splitk_reduce<EPI>), dim3((unsigned)a.M), dim3(256), 0, s, a, sp, d_pos);
+    return;
+  }
+  GemvArgs b = a;
+  b.part = nullptr;  // the kernels below write the epilogue themselves
   const int64_t mt128 = (a.M + 127) / 128;
   if (EPI == GV_STORE && a.N % 256 == 0 && mt128 * (a.N / 256) >= 384) {
-    launch_cfg2<EPI, 2, 2, 2, 4, 2>(s, a, d_pos);
+    launch_cfg2<EPI, 2, 2, 2, 4, 2>(s, b, d_pos);
     return;
   }
   const bool big = a.N % 128 == 0 && mt128 * (a.N / 128) >= 256;
   if (big && (EPI == GV_RELU2 || EPI == GV_STORE)) {
-    launch_cfg2<EPI, 4, 2, 1, 2, 3>(s, a, d_pos);
+    launch_cfg2<EPI, 4, 2, 1, 2, 3>(s, b, d_pos);
     return;
   }
   const int bn = tile_n(a.M, a.N);
   if (bn == 128 && big)
-    launch_cfg<EPI, 128, 128, 4, 2, 32, 3>(s, a, d_pos);  // 72 KB: two blocks per CU
+    launch_cfg<EPI, 128, 128, 4, 2, 32, 3>(s, b, d_pos);  // 72 KB: two blocks per CU
   else if (bn == 128)
-    launch_cfg<EPI, 64, 128, 2, 2, 32, 4>(s, a, d_pos);
+    launch_cfg<EPI, 64, 128, 2, 2, 32, 4>(s, b, d_pos);
   else
-    launch_cfg<EPI, 64, 64, 2, 2, 32, 4>(s, a, d_pos);
+    launch_cfg<EPI, 64, 64, 2, 2, 32, 4>(s, b, d_pos);
 }
 
 }  // namespace
 
-// RESID runs on k_gemm: one sum-of-squares partial per row and N tile.
-int gemm_ssq_parts(int64_t M, int N) { return N / tile_n(M, N); }
+// RESID on k_gemm: one sum-of-squares partial per row and N tile; split-K
+// RESID (given split-K scratch): one per row.
+int gemm_ssq_parts(int64_t M, int N, int K) {
+  return splitk_count(M, N, K) > 1 ? 1 : N / tile_n(M, N);
+}
+
+int64_t gemm_splitk_floats(int64_t M, int N, int K) {
+  const int sp = splitk_count(M, N, K);
+  return sp > 1 ? (int64_t)sp * M * N : 0;
+}
 
 void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
   switch (epi) {
