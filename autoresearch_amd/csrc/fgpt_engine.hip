@@ -936,8 +936,9 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
   if (m->timing) {  // eager launches so every kernel can be bracketed by events
     for (int st = 0; st < n_steps; ++st) greedy_step_launches(m, kv, s, with_logits, lens[0] + st);
   } else {
-    // runs of up to kGraphSteps captured steps, replayed back to back
-    const int kGraphSteps = 32;
+    // runs of captured steps replayed back to back; ~2k kernel nodes per
+    // graph (a GEMM-path step has about twice the launches of a GEMV step)
+    const int kGraphSteps = use_gemm(m->d, B) ? 16 : 32;
     int done = 0;
     while (done < n_steps) {
       const int run = n_steps - done < kGraphSteps ? n_steps - done : kGraphSteps;

@@ -122,7 +122,7 @@ struct GemvArgs {
   // split-K scratch for small-M GEMMs (nullable): the K-split partial sums,
   // [splits][M][N] fp32, reduced in split order by a second kernel that
   // applies the norm and the epilogue (RESID then writes one ssq partial per
-  // row). Sized by gemm_splitk_floats.
+  // row and 512 columns). Sized by gemm_splitk_floats.
   float* part;
 };
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);

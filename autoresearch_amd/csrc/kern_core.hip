@@ -323,19 +323,37 @@ __global__ __launch_bounds__(64) void k_attn_dec_merge(DecArgs a) {
   const int nch = (len + DPC - 1) / DPC;
   if (nch == 1 || tid >= HD / 4) return;
   const float* P = a.part + (int64_t)bh * a.nchunk * (HD + 2);
+  // eight chunks' loads in flight at a time; chunk order is kept
   float m = -FLT_MAX;
-  for (int c = 0; c < nch; ++c) m = fmaxf(m, P[c * (HD + 2) + HD]);
+  for (int c0 = 0; c0 < nch; c0 += 8) {
+    float mk[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mk[k] = c0 + k < nch ? P[(c0 + k) * (HD + 2) + HD] : -FLT_MAX;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m = fmaxf(m, mk[k]);
+  }
   float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
   float l = 0.f;
-  for (int c = 0; c < nch; ++c) {
-    const float2 ml = *(const float2*)(P + c * (HD + 2) + HD);
-    const float4 ov = *(const float4*)(P + c * (HD + 2) + 4 * tid);
-    const float w = expf(ml.x - m);
-    l += w * ml.y;
-    t.x += w * ov.x;
-    t.y += w * ov.y;
-    t.z += w * ov.z;
-    t.w += w * ov.w;
+  for (int c0 = 0; c0 < nch; c0 += 8) {
+    float2 ml[8];
+    float4 ov[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool ok = c0 + k < nch;
+      ml[k] = ok ? *(const float2*)(P + (c0 + k) * (HD + 2) + HD) : make_float2(-FLT_MAX, 0.f);
+      ov[k] = ok ? *(const float4*)(P + (c0 + k) * (HD + 2) + 4 * tid)
+                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (c0 + k >= nch) break;
+      const float w = expf(ml[k].x - m);
+      l += w * ml[k].y;
+      t.x += w * ov[k].x;
+      t.y += w * ov[k].y;
+      t.z += w * ov[k].z;
+      t.w += w * ov[k].w;
+    }
   }
   const float inv = 1.0f / l;
   dec_store<HD>(a, (int64_t)bh * HD, 4 * tid, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));

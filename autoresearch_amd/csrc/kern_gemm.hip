@@ -531,13 +531,17 @@ int splitk_count(int64_t M, int N, int K) {
 }
 
 // Sum of the K-split partials in split order, then the row norm and the
-// epilogue; one block per row. RESID leaves one sum-of-squares partial per
-// row (the whole row).
+// epilogue. Block = (row, 512 columns), a thread a column pair; the splits'
+// loads go out eight at a time. RESID leaves one sum-of-squares partial per
+// row and 512-column group.
+constexpr int RED_COLS = 512;
+
 template <int EPI>
 __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
                                                        const int32_t* __restrict__ d_pos) {
   __shared__ float red[4];
   const int m = blockIdx.x, tid = threadIdx.x, N = a.N;
+  const int n = blockIdx.y * RED_COLS + 2 * tid;
   float inv = 1.f;
   if (a.norm) {
     float ssum = 0.f;
@@ -546,12 +550,21 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
   }
   const int pos0 = d_pos ? *d_pos : a.pos0;
   float sq = 0.f;
-  for (int n = 2 * tid; n < N; n += 512) {
+  if (n < N) {
     float v0 = 0.f, v1 = 0.f;
-    for (int sp = 0; sp < splits; ++sp) {
-      const float2 p = *reinterpret_cast<const float2*>(a.part + ((int64_t)sp * a.M + m) * N + n);
-      v0 += p.x;
-      v1 += p.y;
+    const float* P = a.part + (int64_t)m * N + n;
+    const int64_t stride = (int64_t)a.M * N;
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+      float2 p[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        p[k] = s0 + k < splits ? *reinterpret_cast<const float2*>(P + (s0 + k) * stride)
+                               : make_float2(0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {  // split order (a zero adds nothing)
+        v0 += p[k].x;
+        v1 += p[k].y;
+      }
     }
     v0 *= inv;
     v1 *= inv;
@@ -567,7 +580,7 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
         split_bf16(x.x, a.ys + o, a.ys_plane);
         split_bf16(x.y, a.ys + o + 1, a.ys_plane);
       }
-      sq += x.x * x.x + x.y * x.y;
+      sq = x.x * x.x + x.y * x.y;
     } else if (EPI == GV_RELU2) {
       const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
       split_bf16(t0 * t0, a.ys + o, a.ys_plane);
@@ -581,7 +594,8 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
     for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
     if ((tid & 63) == 0) red[tid >> 6] = sq;
     __syncthreads();
-    if (tid == 0) a.ssq_out[m] = red[0] + red[1] + red[2] + red[3];
+    if (tid == 0)
+      a.ssq_out[(int64_t)m * gridDim.y + blockIdx.y] = red[0] + red[1] + red[2] + red[3];
   }
 }
 
@@ -596,7 +610,8 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
     constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
     const dim3 g(a.N / 64, (unsigned)((a.M + 63) / 64), (unsigned)sp);
     hipLaunchKernelGGL((k_gemm<EPI, 64, 64, 2, 2, 32, 4>), g, dim3(256), lds, s, a, d_pos);
-    hipLaunchKernelGGL((k_splitk_reduce<EPI>), dim3((unsigned)a.M), dim3(256), 0, s, a, sp, d_pos);
+    const dim3 rg((unsigned)a.M, (unsigned)((a.N + RED_COLS - 1) / RED_COLS));
+    hipLaunchKernelGGL((k_splitk_reduce<EPI>), rg, dim3(256), 0, s, a, sp, d_pos);
     return;
   }
   GemvArgs b = a;
@@ -623,9 +638,9 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 }  // namespace
 
 // RESID on k_gemm: one sum-of-squares partial per row and N tile; split-K
-// RESID (given split-K scratch): one per row.
+// RESID (given split-K scratch): one per row and 512 columns.
 int gemm_ssq_parts(int64_t M, int N, int K) {
-  return splitk_count(M, N, K) > 1 ? 1 : N / tile_n(M, N);
+  return splitk_count(M, N, K) > 1 ? (N + RED_COLS - 1) / RED_COLS : N / tile_n(M, N);
 }
 
 int64_t gemm_splitk_floats(int64_t M, int N, int K) {
