@@ -371,7 +371,7 @@ GemvArgs base_args(fg_model* m) {
 // chunk kernel (causal_attn / attn_chunk).
 void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, int pos0,
                  const int32_t* d_pos, float* kc, float* vc, int maxT, int64_t lstride,
-                 float* dec_part, float* logits, int pos_host = -1) {
+                 float* dec_part, float* logits, int pos_host = -1, bool embed = true) {
   const Dims& d = m->d;
   Work& ws = m->ws;
   const int rows = B * T;
@@ -386,10 +386,11 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   // ssq partials per row after the attention-output RESID
   const int nt_resid = gemm_ssq_parts(rows, d.D, d.qd());
 
-  timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
-    launch_embed_norm(s, d, m->w.wte, ids, rows, ws.x, gm ? ws.xs : nullptr, xplane,
-                      gm ? ws.ssq : nullptr);
-  });
+  if (embed)  // (else x already holds the embedded rows)
+    timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
+      launch_embed_norm(s, d, m->w.wte, ids, rows, ws.x, gm ? ws.xs : nullptr, xplane,
+                        gm ? ws.ssq : nullptr);
+    });
   int nt = 1;  // partial sums of squares per row of the current residual
   for (int l = 0; l < d.L; ++l) {
     float* lk = kc ? kc + l * lstride : nullptr;  // null: no persistent cache (gpt_forward)
@@ -848,12 +849,26 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
                           int pos_host) {
   const int B = kv->B;
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
-  layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride, kv->d_part,
-              m->ws.logits, pos_host);
-  timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
-    launch_argmax_step(s, m->ws.logits, B, m->d.V, kv->d_ids, kv->d_out, kv->d_len,
-                       kv->d_len + 1, with_logits ? kv->d_lgs : nullptr);
-  });
+  if (use_gemm(m->d, B)) {
+    layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
+                kv->d_part, m->ws.logits, pos_host);
+    timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
+      launch_argmax_step(s, m->ws.logits, B, m->d.V, kv->d_ids, kv->d_out, kv->d_len,
+                         kv->d_len + 1, with_logits ? kv->d_lgs : nullptr);
+    });
+  } else {
+    // GEMV path: x of this step was embedded by the previous step's tail (or
+    // before the first step); the tail does argmax, the next embedding and
+    // the length update in one launch
+    layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
+                kv->d_part, m->ws.logits, pos_host, false);
+    timed(m, s, FG_K_OTHER, 0, (double)B * (m->d.V * 4 * (with_logits ? 2 : 1) + 6 * m->d.D),
+          [&] {
+            launch_greedy_tail(s, m->d, m->ws.logits, B, m->w.wte, kv->d_ids, kv->d_out,
+                               kv->d_len, kv->d_len + 1, with_logits ? kv->d_lgs : nullptr,
+                               m->ws.x);
+          });
+  }
 }
 
 // Replay (capturing on first use) a graph of `steps` greedy steps.
@@ -932,6 +947,8 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
   const int32_t lens[2] = {kv->len, kv->len};
   HIPCHK(hipMemcpyAsync(kv->d_ids, ids, (size_t)B * 4, hipMemcpyHostToDevice, s));
   HIPCHK(hipMemcpyAsync(kv->d_len, lens, 8, hipMemcpyHostToDevice, s));
+  if (!use_gemm(m->d, B))  // the GEMV-path steps expect x embedded (see greedy_step_launches)
+    launch_embed_norm(s, m->d, m->w.wte, kv->d_ids, B, m->ws.x, nullptr, 0, nullptr);
   HIPCHK(hipStreamSynchronize(s));
   if (m->timing) {  // eager launches so every kernel can be bracketed by events
     for (int st = 0; st < n_steps; ++st) greedy_step_launches(m, kv, s, with_logits, lens[0] + st);

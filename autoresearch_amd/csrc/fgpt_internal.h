@@ -173,6 +173,13 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
 void launch_argmax_step(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out,
                         int32_t* out2, int32_t* d_len, const int32_t* d_len0, float* lgs_out);
 
+// GEMV-path greedy step end (rows <= 4, one block): argmax of each row into
+// ids and out2 (and the logits row into lgs_out) as launch_argmax_step does,
+// then x[row] = rmsnorm0(wte[id]) for the next step, then *d_len += 1.
+void launch_greedy_tail(hipStream_t s, const Dims& d, const float* logits, int rows,
+                        const bf16_t* wte, int32_t* ids, int32_t* out2, int32_t* d_len,
+                        const int32_t* d_len0, float* lgs_out, float* x);
+
 // Per-row argmax (first max) of logits [rows][V] -> out [rows].
 void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out);
 // Per-row nll = logsumexp - logit[tgt].

@@ -107,64 +107,58 @@ __device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, fl
 }
 
 // ------------------------------------------------------------ GEMV
-// M <= 4 token rows. x rows are staged in LDS (normalised there when
-// a.norm, so each product uses the rounded xn as the reference does). A
-// wavefront owns a pair of weight rows at a time; lanes stride the row in
-// 16-byte chunks (8 bf16), so each row is read as whole, coalesced lines.
-template <int M, int EPI>
+// M <= 4 token rows. A wavefront owns R weight rows at a time (R = 2 for
+// QKV, so a rotation pair stays in one wavefront; else 1, for twice the
+// wavefronts): lanes stride the rows in 16-byte chunks (8 bf16), so each row
+// is read as whole, coalesced lines, and x comes straight from global memory
+// (L2) in matching float4 pairs. No LDS and no barrier: the weight loads go
+// out at once. The row norm (a.norm) is a scale of the dot products, from
+// sum(x^2) the same lanes accumulate over the chunks they read.
+template <int M, int EPI, int R>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restrict__ d_pos) {
-  extern __shared__ float sx[];  // [M][K]
-  __shared__ float sinv[4];
-  const int K = a.K, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  for (int i = tid; i < M * K; i += 256) sx[i] = a.x[i];
-  __syncthreads();
-  if (a.norm) {
-    if (wid < M) {
-      float ss = 0.f;
-      for (int k = lane; k < K; k += 64) ss += sx[wid * K + k] * sx[wid * K + k];
-      ss = wave_sum(ss);
-      if (lane == 0) sinv[wid] = 1.0f / sqrtf(ss / (float)K + a.eps);
-    }
-    __syncthreads();
-    for (int i = tid; i < M * K; i += 256) sx[i] = sx[i] * sinv[i / K];
-    __syncthreads();
-  }
+  const int K = a.K, lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int pos0 = d_pos ? *d_pos : a.pos0;
-  const int nunits = a.N >> 1, nch = K >> 3;
+  const int nunits = a.N / R, nch = K >> 3;
   for (int u = blockIdx.x * 4 + wid; u < nunits; u += gridDim.x * 4) {
-    const bf16_t* w0 = a.w + (int64_t)(2 * u) * K;
-    float acc0[M], acc1[M];
+    const bf16_t* w0 = a.w + (int64_t)(R * u) * K;
+    float acc[R][M], ss[M];
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc0[m] = acc1[m] = 0.f;
+    for (int m = 0; m < M; ++m) {
+      ss[m] = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][m] = 0.f;
+    }
+#pragma unroll 2
     for (int c = lane; c < nch; c += 64) {
-      const uint4 p0 = *(const uint4*)(w0 + c * 8);
-      const uint4 p1 = *(const uint4*)(w0 + K + c * 8);
-      float f0[8], f1[8];
-      unpack8(p0, f0);
-      unpack8(p1, f1);
+      float f[R][8];
+#pragma unroll
+      for (int r = 0; r < R; ++r) unpack8(*(const uint4*)(w0 + (int64_t)r * K + c * 8), f[r]);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const float4 xa = *(const float4*)(sx + m * K + c * 8);
-        const float4 xb = *(const float4*)(sx + m * K + c * 8 + 4);
-        acc0[m] += f0[0] * xa.x + f0[1] * xa.y + f0[2] * xa.z + f0[3] * xa.w +
-                   f0[4] * xb.x + f0[5] * xb.y + f0[6] * xb.z + f0[7] * xb.w;
-        acc1[m] += f1[0] * xa.x + f1[1] * xa.y + f1[2] * xa.z + f1[3] * xa.w +
-                   f1[4] * xb.x + f1[5] * xb.y + f1[6] * xb.z + f1[7] * xb.w;
+        const float4 xa = *(const float4*)(a.x + (int64_t)m * K + c * 8);
+        const float4 xb = *(const float4*)(a.x + (int64_t)m * K + c * 8 + 4);
+        ss[m] += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x +
+                 xb.y * xb.y + xb.z * xb.z + xb.w * xb.w;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          acc[r][m] += f[r][0] * xa.x + f[r][1] * xa.y + f[r][2] * xa.z + f[r][3] * xa.w +
+                       f[r][4] * xb.x + f[r][5] * xb.y + f[r][6] * xb.z + f[r][7] * xb.w;
       }
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      acc0[m] = wave_sum(acc0[m]);
-      acc1[m] = wave_sum(acc1[m]);
+      const float inv = a.norm ? 1.0f / sqrtf(wave_sum(ss[m]) / (float)K + a.eps) : 1.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r][m] = wave_sum(acc[r][m]) * inv;
     }
     if (lane == 0) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         if (EPI == GV_QKV) {
-          qkv_pair_epilogue(a, m, pos0, 2 * u, acc0[m], acc1[m]);
+          qkv_pair_epilogue(a, m, pos0, 2 * u, acc[0][m], acc[R - 1][m]);
         } else {
-          single_store<EPI>(a, m, 2 * u, acc0[m]);
-          single_store<EPI>(a, m, 2 * u + 1, acc1[m]);
+#pragma unroll
+          for (int r = 0; r < R; ++r) single_store<EPI>(a, m, R * u + r, acc[r][m]);
         }
       }
     }
@@ -173,15 +167,15 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restr
 
 template <int EPI>
 static void gemv_m(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
-  const int nunits = a.N / 2;
+  constexpr int R = EPI == GV_QKV ? 2 : 1;
+  const int nunits = a.N / R;
   int grid = (nunits + 3) / 4;
   if (grid > 2048) grid = 2048;
-  const size_t lds = sizeof(float) * (size_t)a.M * a.K;
   switch (a.M) {
-    case 1: hipLaunchKernelGGL((k_gemv<1, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
-    case 2: hipLaunchKernelGGL((k_gemv<2, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
-    case 3: hipLaunchKernelGGL((k_gemv<3, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
-    default: hipLaunchKernelGGL((k_gemv<4, EPI>), dim3(grid), dim3(256), lds, s, a, d_pos); break;
+    case 1: hipLaunchKernelGGL((k_gemv<1, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
+    case 2: hipLaunchKernelGGL((k_gemv<2, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
+    case 3: hipLaunchKernelGGL((k_gemv<3, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
+    default: hipLaunchKernelGGL((k_gemv<4, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
   }
 }
 
@@ -458,6 +452,81 @@ void launch_argmax_step(hipStream_t s, const float* logits, int64_t rows, int V,
   hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(256), 0, s, logits, V, out, out2, d_len,
                      d_len0, lgs_out);
   if (d_len) hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, d_len);
+}
+
+// The end of a GEMV-path greedy step in one single-block launch: for each of
+// the (<= 4) rows, the first-max argmax of its logits (sample_token's
+// strict > scan), the id into ids[row] and out2[(len-len0)*rows + row],
+// the logits row into lgs_out at that slot (when set), then the next
+// step's input x[row] = rmsnorm0(wte[id]); finally len += 1. One block, so
+// every read of len precedes the increment.
+__global__ __launch_bounds__(1024) void k_greedy_tail(const float* __restrict__ logits, int rows,
+                                                      int V, int D, float eps,
+                                                      const bf16_t* __restrict__ wte,
+                                                      int32_t* __restrict__ ids,
+                                                      int32_t* __restrict__ out2,
+                                                      int32_t* __restrict__ d_len,
+                                                      const int32_t* __restrict__ d_len0,
+                                                      float* __restrict__ lgs_out,
+                                                      float* __restrict__ x) {
+  __shared__ float rv[16];
+  __shared__ int ri[16];
+  __shared__ float red[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t slot = (int64_t)(*d_len - *d_len0);
+  for (int r = 0; r < rows; ++r) {
+    const float* l = logits + (int64_t)r * V;
+    float* cp = lgs_out ? lgs_out + (slot * rows + r) * V : nullptr;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = tid; j < V; j += 1024) {
+      const float v = l[j];
+      if (cp) cp[j] = v;
+      if (v > bv) {
+        bv = v;
+        bi = j;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax_merge(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    if (lane == 0) {
+      rv[w] = bv;
+      ri[w] = bi;
+    }
+    __syncthreads();
+    bv = rv[0];
+    bi = ri[0];
+    for (int k = 1; k < 16; ++k) amax_merge(bv, bi, rv[k], ri[k]);
+    if (bi == 0x7fffffff) bi = 0;  // all -inf / NaN: position 1, as the scan starts there
+    if (tid == 0) {
+      ids[r] = bi;
+      out2[slot * rows + r] = bi;
+    }
+    // next input row
+    const bf16_t* row = wte + (int64_t)bi * D;
+    float ss = 0.f;
+    for (int k = tid; k < D; k += 1024) {
+      const float v = bf16_to_f32(row[k]);
+      ss += v * v;
+    }
+    ss = wave_sum(ss);
+    __syncthreads();  // rv/ri reads above are done before red is reused
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    float t = 0.f;
+    for (int k = 0; k < 16; ++k) t += red[k];
+    const float inv = 1.0f / sqrtf(t / (float)D + eps);
+    for (int k = tid; k < D; k += 1024) x[(int64_t)r * D + k] = bf16_to_f32(row[k]) * inv;
+    __syncthreads();
+  }
+  if (tid == 0) *d_len = *d_len + 1;
+}
+
+void launch_greedy_tail(hipStream_t s, const Dims& d, const float* logits, int rows,
+                        const bf16_t* wte, int32_t* ids, int32_t* out2, int32_t* d_len,
+                        const int32_t* d_len0, float* lgs_out, float* x) {
+  hipLaunchKernelGGL(k_greedy_tail, dim3(1), dim3(1024), 0, s, logits, rows, d.V, d.D, d.eps, wte,
+                     ids, out2, d_len, d_len0, lgs_out, x);
 }
 
 void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out) {
