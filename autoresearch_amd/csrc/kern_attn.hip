@@ -139,6 +139,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
   const int t = tq0 + qg * 32 + qi;  // this lane's query (column)
   const bool tok = t < p.T;
   const int qpos = p.pos0 + t;
+  const int klim = min(qpos + 1, p.nvalid);  // keys below this are visible
   const bool wact = tq0 + qg * 32 < p.T;  // the wavefront has queries
   const int wq0 = p.pos0 + tq0 + qg * 32;
   const int wq1 = p.pos0 + min(tq0 + qg * 32 + 32, p.T) - 1;
@@ -217,36 +218,34 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
         sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[s], sc, 0, 0, 0);
       }
     }
-    // scores in the log2 domain; accumulator r of this lane is key
-    // kt0 + 16(r/8) + 8g + (r%8); mask only tiles that reach the diagonal or
-    // the end of the valid keys
-    const bool need_mask = (kt0 + 31 > wq0) || (kt0 + 32 > p.nvalid);
+    // accumulator r of this lane is key kt0 + 16(r/8) + 8g + (r%8); mask
+    // (select, no branch) only tiles that reach the diagonal or the end of
+    // the valid keys
+    if ((kt0 + 31 > wq0) || (kt0 + 32 > p.nvalid)) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        sc[r] = kt0 + 16 * (r >> 3) + 8 * g + (r & 7) < klim ? sc[r] : -INFINITY;
+    }
     float mx = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = sc[r] * cs;
-      if (need_mask) {
-        const int key = kt0 + 16 * (r >> 3) + 8 * g + (r & 7);
-        if (key > qpos || key >= p.nvalid) v = -INFINITY;
-      }
-      sc[r] = v;
-      mx = fmaxf(mx, v);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    if (__any(m_new > m_run)) {
-      const float alpha = exp2f(m_run - m_new);
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * cs;  // log2 domain (cs > 0)
+    // lazy rescale: the running max moves only when a score passes it by
+    // 2^8, so most tiles skip rescaling O; probabilities stay below 2^8
+    if (__any(mx > m_run + 8.f)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
       for (int i = 0; i < ND; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[i][r] *= alpha;
+      m_run = m_new;
     }
-    m_run = m_new;
     float ps = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float pr = exp2f(sc[r] - m_new);
+      const float pr = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], cs, -m_run));
       sc[r] = pr;
       ps += pr;
     }
