@@ -30,6 +30,8 @@ static int32_t seterr(int32_t code, const char* fmt, ...) {
   return code;
 }
 
+int32_t fgpt::set_error(int32_t code, const char* msg) { return seterr(code, "%s", msg); }
+
 #define HIPCHK(x)                                                                   \
   do {                                                                              \
     hipError_t e_ = (x);                                                            \
@@ -162,7 +164,9 @@ int32_t check_device(int* dev_out) {
   return FG_OK;
 }
 
-int32_t check_dims(const fg_dims* in, Dims* d) {
+}  // namespace
+
+int32_t fgpt::check_dims(const fg_dims* in, Dims* d) {
   if (!in) return seterr(FG_EARG, "dims is NULL");
   d->L = in->n_layer;
   d->D = in->d_model;
@@ -184,6 +188,8 @@ int32_t check_dims(const fg_dims* in, Dims* d) {
   if (!(d->eps > 0.f)) return seterr(FG_EDIMS, "eps must be > 0");
   return FG_OK;
 }
+
+namespace {
 
 // fp32 -> bf16 bits, refusing values that are not exactly representable.
 int32_t to_bf16_exact(const float* src, size_t n, bf16_t* dst, const char* name) {
@@ -524,107 +530,15 @@ extern "C" int32_t fg_model_create(const fg_dims* dims, const float* wte, const 
   return FG_OK;
 }
 
-namespace {
-
-// Minimal .npy reader: version 1/2/3 header, dtype '<f4', C order, 1-D.
-int32_t read_npy_f32(const std::string& path, size_t want, float* dst) {
-  FILE* f = fopen(path.c_str(), "rb");
-  if (!f) return seterr(FG_EWEIGHT, "load failed (missing file): %s", path.c_str());
-  unsigned char mg[8];
-  int32_t rc = FG_OK;
-  std::string hdr;
-  uint32_t hlen = 0;
-  if (fread(mg, 1, 8, f) != 8 || memcmp(mg, "\x93NUMPY", 6) != 0) {
-    rc = seterr(FG_EWEIGHT, "not a .npy file (missing or empty): %s", path.c_str());
-  } else {
-    if (mg[6] == 1) {
-      unsigned char b[2];
-      if (fread(b, 1, 2, f) != 2) rc = seterr(FG_EWEIGHT, "truncated header: %s", path.c_str());
-      hlen = b[0] | (b[1] << 8);
-    } else {
-      unsigned char b[4];
-      if (fread(b, 1, 4, f) != 4) rc = seterr(FG_EWEIGHT, "truncated header: %s", path.c_str());
-      hlen = b[0] | (b[1] << 8) | (b[2] << 16) | ((uint32_t)b[3] << 24);
-    }
-    if (rc == FG_OK) {
-      hdr.resize(hlen);
-      if (hlen > 65536 || fread(&hdr[0], 1, hlen, f) != hlen)
-        rc = seterr(FG_EWEIGHT, "truncated header: %s", path.c_str());
-    }
-  }
-  if (rc == FG_OK) {
-    auto has = [&](const char* s) { return hdr.find(s) != std::string::npos; };
-    if (!has("'descr': '<f4'"))
-      rc = seterr(FG_EWEIGHT, "%s: dtype is not '<f4'", path.c_str());
-    else if (!has("'fortran_order': False"))
-      rc = seterr(FG_EWEIGHT, "%s: fortran_order arrays are not supported", path.c_str());
-    else {
-      size_t p = hdr.find("'shape': (");
-      unsigned long long n = 0;
-      char tail = 0;
-      if (p == std::string::npos ||
-          sscanf(hdr.c_str() + p + 10, "%llu%c", &n, &tail) != 2 || tail != ',')
-        rc = seterr(FG_EWEIGHT, "%s: shape is not 1-D", path.c_str());
-      else if (hdr.find(')', p) < hdr.find(',', p) || hdr.find(',', hdr.find(',', p) + 1) < hdr.find(')', p))
-        rc = seterr(FG_EWEIGHT, "%s: shape is not 1-D", path.c_str());
-      else if (n != want)
-        rc = seterr(FG_EWEIGHT, "%s: %llu values, expected %zu", path.c_str(), n, want);
-      else if (fread(dst, 4, want, f) != want)
-        rc = seterr(FG_EWEIGHT, "%s: truncated payload", path.c_str());
-    }
-  }
-  fclose(f);
-  return rc;
-}
-
-int32_t check_arch_txt(const std::string& dir, const Dims& d) {
-  FILE* f = fopen((dir + "/arch.txt").c_str(), "r");
-  if (!f) return FG_OK;  // absent = accepted, as read_arch_txt does
-  char line[256];
-  int32_t rc = FG_OK;
-  while (fgets(line, sizeof line, f)) {
-    if (line[0] == '#') continue;
-    char key[64];
-    long val;
-    if (sscanf(line, " %63[a-z_] = %ld", key, &val) != 2) continue;
-    long want = -1;
-    if (!strcmp(key, "d_model")) want = d.D;
-    else if (!strcmp(key, "n_head")) want = d.H;
-    else if (!strcmp(key, "n_kv")) want = d.KH;
-    else if (!strcmp(key, "n_layer")) want = d.L;
-    else if (!strcmp(key, "vocab")) want = d.V;
-    else if (!strcmp(key, "head_dim")) want = d.hd;
-    if (want >= 0 && want != val) {
-      rc = seterr(FG_EARCH, "arch.txt %s = %ld but the dims say %ld", key, val, want);
-      break;
-    }
-  }
-  fclose(f);
-  return rc;
-}
-
-}  // namespace
-
 extern "C" int32_t fg_model_load(const fg_dims* dims, const char* weights_dir, fg_model** out) {
   if (!weights_dir) return seterr(FG_EARG, "weights_dir is NULL");
   Dims d;
   RCCHK(check_dims(dims, &d));
-  const std::string dir(weights_dir);
-  RCCHK(check_arch_txt(dir, d));
   const size_t D = d.D, qd = d.qd(), kd = d.kvd(), dff = d.dff, V = d.V, L = d.L;
   std::vector<float> wte(V * D), lm(V * D), cq(L * qd * D), ck(L * kd * D), cv(L * kd * D),
       cp(L * D * qd), cf(L * dff * D), cp2(L * D * dff);
-  RCCHK(read_npy_f32(dir + "/transformer_wte_weight.npy", V * D, wte.data()));
-  RCCHK(read_npy_f32(dir + "/lm_head_weight.npy", V * D, lm.data()));
-  for (size_t l = 0; l < L; ++l) {
-    const std::string p = dir + "/transformer_h_" + std::to_string(l) + "_";
-    RCCHK(read_npy_f32(p + "attn_c_q_weight.npy", qd * D, cq.data() + l * qd * D));
-    RCCHK(read_npy_f32(p + "attn_c_k_weight.npy", kd * D, ck.data() + l * kd * D));
-    RCCHK(read_npy_f32(p + "attn_c_v_weight.npy", kd * D, cv.data() + l * kd * D));
-    RCCHK(read_npy_f32(p + "attn_c_proj_weight.npy", D * qd, cp.data() + l * D * qd));
-    RCCHK(read_npy_f32(p + "mlp_c_fc_weight.npy", dff * D, cf.data() + l * dff * D));
-    RCCHK(read_npy_f32(p + "mlp_c_proj_weight.npy", D * dff, cp2.data() + l * D * dff));
-  }
+  RCCHK(fg_weights_read(dims, weights_dir, wte.data(), cq.data(), ck.data(), cv.data(), cp.data(),
+                        cf.data(), cp2.data(), lm.data()));
   return fg_model_create(dims, wte.data(), cq.data(), ck.data(), cv.data(), cp.data(), cf.data(),
                          cp2.data(), lm.data(), out);
 }

@@ -6,7 +6,12 @@
 
 #include <string>
 
+#include "../../include/fgpt.h"
+
 namespace fgpt {
+
+// Set the calling thread's error (code + message, see fg_last_error); returns code.
+int32_t set_error(int32_t code, const char* msg);
 
 typedef uint16_t bf16_t;  // raw bf16 bits in HBM
 
@@ -17,6 +22,9 @@ struct Dims {
   int kvd() const { return KH * hd; }
   int nqkv() const { return (H + 2 * KH) * hd; }
 };
+
+// Validate the public dims against what the kernels support and fill Dims.
+int32_t check_dims(const fg_dims* in, Dims* d);
 
 // Weight arena in HBM (bf16), one allocation:
 //   per layer l: Wqkv[(H+2KH)*hd][D]  rows permuted, see qkv_row_of()

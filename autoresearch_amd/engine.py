@@ -28,7 +28,8 @@ FG_ERRORS = {
 
 # every symbol include/fgpt.h declares
 EXPORTS = (
-    "fg_version", "fg_last_error", "fg_model_create", "fg_model_load", "fg_model_destroy",
+    "fg_version", "fg_last_error", "fg_model_create", "fg_weights_read", "fg_model_load",
+    "fg_model_destroy",
     "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_destroy",
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
@@ -72,6 +73,7 @@ def load_library(path: str = LIB_PATH):
         "fg_version": (i32, []),
         "fg_last_error": (i32, [C.c_char_p, i32]),
         "fg_model_create": (i32, [C.POINTER(_FgDims)] + [_f] * 8 + [C.POINTER(_vp)]),
+        "fg_weights_read": (i32, [C.POINTER(_FgDims), C.c_char_p] + [_f] * 8),
         "fg_model_load": (i32, [C.POINTER(_FgDims), C.c_char_p, C.POINTER(_vp)]),
         "fg_model_destroy": (i32, [_vp]),
         "fg_set_rope": (i32, [_vp, i32, i32, _f, _f]),
@@ -263,6 +265,21 @@ class KV:
 
 
 # ------------------------------------------------------- reference-shaped API
+
+def weights_read(wdir: str, d: Dims) -> dict:
+    """fg_weights_read: the eight fp32 stacks of a checkpoint directory
+    (model.safetensors when present, else the .npy files), host only."""
+    load_library()
+    D, qd, kd, ff, V, L = d.d_model, d.n_head * d.head_dim, d.n_kv_head * d.head_dim, \
+        d.d_ff, d.vocab, d.n_layer
+    out = {"wte": np.empty(V * D, np.float32), "c_q": np.empty(L * qd * D, np.float32),
+           "c_k": np.empty(L * kd * D, np.float32), "c_v": np.empty(L * kd * D, np.float32),
+           "c_proj": np.empty(L * D * qd, np.float32), "c_fc": np.empty(L * ff * D, np.float32),
+           "c_proj2": np.empty(L * D * ff, np.float32), "lm_head": np.empty(V * D, np.float32)}
+    dims = _cdims(d)
+    _check(_LIB.fg_weights_read(C.byref(dims), wdir.encode(), *[_fp(out[k]) for k in STACK_NAMES]))
+    return out
+
 
 def load_gpt_weights(wdir: str, d: Dims) -> Model:
     """load_gpt_weights + require_arch (src/lib/load_weights.f90:830-874,

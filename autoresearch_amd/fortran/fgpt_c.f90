@@ -18,7 +18,8 @@ module fgpt_c
     real(c_float) :: eps
   end type fg_dims
 
-  public :: fg_version, fg_last_error, fg_model_create, fg_model_load, fg_model_destroy, &
+  public :: fg_version, fg_last_error, fg_model_create, fg_weights_read, fg_model_load, &
+      fg_model_destroy, &
       fg_set_rope, fg_forward, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
       fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_error_message
 
@@ -40,6 +41,15 @@ module fgpt_c
       real(c_float), intent(in) :: wte(*), c_q(*), c_k(*), c_v(*), c_proj(*), c_fc(*), &
           c_proj2(*), lm_head(*)
       type(c_ptr), intent(out) :: out
+    end function
+
+    integer(c_int32_t) function fg_weights_read(dims, weights_dir, wte, c_q, c_k, c_v, &
+        c_proj, c_fc, c_proj2, lm_head) bind(C, name="fg_weights_read")
+      import :: c_int32_t, c_char, c_float, fg_dims
+      type(fg_dims), intent(in) :: dims
+      character(kind=c_char), intent(in) :: weights_dir(*)
+      real(c_float), intent(out) :: wte(*), c_q(*), c_k(*), c_v(*), c_proj(*), c_fc(*), &
+          c_proj2(*), lm_head(*)
     end function
 
     integer(c_int32_t) function fg_model_load(dims, weights_dir, out) &

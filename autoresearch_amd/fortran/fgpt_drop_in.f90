@@ -20,7 +20,7 @@
 !    loud-failure convention (print + exit, or error stop).
 module fgpt_drop_in_mod
   use, intrinsic :: iso_c_binding
-  use, intrinsic :: iso_fortran_env, only: int8, error_unit
+  use, intrinsic :: iso_fortran_env, only: error_unit
   use fgpt_c
   implicit none
   private
@@ -222,104 +222,21 @@ contains
   end subroutine gpt_step_multi
 
   ! ------------------------------------------------------------ weights
-  ! One 1-D '<f4' C-order .npy file of exactly n values (the exporter's
-  ! format, scripts/export_weights.py:22-24,151-166); missing, empty or
-  ! malformed files stop the program, as load1 does (load_weights.f90:139-159).
-  subroutine load1(path, a, at, n)
-    character(*), intent(in) :: path
-    real(c_float), intent(inout) :: a(:)
-    integer, intent(in) :: at, n
-    integer :: u, ios, sz, hlen, hstart
-    character(len=6) :: magic
-    integer(int8) :: ver(2), hl(2)
-    character(len=:), allocatable :: hdr
-    logical :: ex
-
-    inquire (file=path, exist=ex, size=sz)
-    if (.not. ex .or. sz <= 0) then
-      print '(2A)', "load failed (missing or empty file): ", trim(path)
-      error stop 1
-    end if
-    open (newunit=u, file=path, access='stream', form='unformatted', status='old', &
-        action='read', iostat=ios)
-    if (ios /= 0) then
-      print '(2A)', "load failed: ", trim(path)
-      error stop 1
-    end if
-    read (u, iostat=ios) magic, ver, hl
-    if (ios /= 0 .or. magic(2:6) /= 'NUMPY' .or. ver(1) /= 1) then
-      print '(2A)', "load failed (not a version-1 .npy): ", trim(path)
-      error stop 1
-    end if
-    hlen = iand(int(hl(1)), 255) + 256*iand(int(hl(2)), 255)
-    allocate (character(len=hlen) :: hdr)
-    read (u, iostat=ios) hdr
-    hstart = 10 + hlen
-    if (ios /= 0 .or. index(hdr, "'descr': '<f4'") == 0 .or. &
-        index(hdr, "'fortran_order': False") == 0) then
-      print '(2A)', "load failed (need a '<f4' C-order array): ", trim(path)
-      error stop 1
-    end if
-    if (sz /= hstart + 4*n) then
-      print '(2A,I0,A)', "load failed (size mismatch, expected ", trim(path), n, " values)"
-      error stop 1
-    end if
-    read (u, pos=hstart + 1, iostat=ios) a(at:at + n - 1)
-    if (ios /= 0) then
-      print '(2A)', "load failed (short read): ", trim(path)
-      error stop 1
-    end if
-    close (u)
-  end subroutine load1
-
-  ! arch.txt, when present, must agree with the dims (read_arch_txt /
-  ! require_arch, src/lib/fortran_arch.f90:121-159,238-246).
-  subroutine require_arch(wdir, dims)
-    character(*), intent(in) :: wdir
-    integer, intent(in) :: dims(6)   ! n_layer, d_model, n_head, n_kv_head, head_dim, vocab
-    character(len=128) :: line
-    character(len=64) :: key
-    integer :: u, ios, eq, val, want
-    open (newunit=u, file=trim(wdir)//'/arch.txt', status='old', action='read', iostat=ios)
-    if (ios /= 0) return
-    do
-      read (u, '(A)', iostat=ios) line
-      if (ios /= 0) exit
-      eq = index(line, '=')
-      if (eq == 0 .or. line(1:1) == '#') cycle
-      key = trim(adjustl(line(:eq - 1)))
-      read (line(eq + 1:), *, iostat=ios) val
-      if (ios /= 0) cycle
-      select case (key)
-      case ('n_layer'); want = dims(1)
-      case ('d_model'); want = dims(2)
-      case ('n_head'); want = dims(3)
-      case ('n_kv'); want = dims(4)
-      case ('head_dim'); want = dims(5)
-      case ('vocab'); want = dims(6)
-      case default; cycle
-      end select
-      if (want /= val) then
-        print '(A,A,A,I0,A,I0)', 'FATAL: shape mismatch in arch.txt ', trim(key), &
-            ': expected ', want, ', checkpoint has ', val
-        error stop 1
-      end if
-    end do
-    close (u)
-  end subroutine require_arch
-
-  ! src/lib/load_weights.f90:830-874 (.npy branch) plus require_arch.
+  ! load_gpt_weights (src/lib/load_weights.f90:830-874): model.safetensors
+  ! when the directory has one (canonical names, arch.* metadata checked),
+  ! else the 1-D '<f4' .npy files with arch.txt checked when present. The
+  ! engine's host reader does both; any failure stops the program with its
+  ! message, as the reference's die/error stop do.
   subroutine load_gpt_weights(wdir, n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size, &
       wte, lm_head, c_q, c_k, c_v, c_pr, c_fc, c_pr2)
     character(*), intent(in) :: wdir
     integer, intent(in) :: n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size
     real(c_float), allocatable, intent(out) :: wte(:), lm_head(:)
     real(c_float), allocatable, intent(out) :: c_q(:), c_k(:), c_v(:), c_pr(:), c_fc(:), c_pr2(:)
-    integer :: ll, qsz, ksz, psz, fsz
-    character(len=16) :: ls
-    character(len=:), allocatable :: p
+    integer :: qsz, ksz, psz, fsz
+    integer(c_int32_t) :: rc
+    type(fg_dims) :: fd
 
-    call require_arch(wdir, [n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size])
     qsz = n_head*head_dim*d_model
     ksz = n_kv_head*head_dim*d_model
     psz = d_model*n_head*head_dim
@@ -327,18 +244,10 @@ contains
     allocate (wte(vocab_size*d_model), lm_head(vocab_size*d_model))
     allocate (c_q(n_layer*qsz), c_k(n_layer*ksz), c_v(n_layer*ksz), c_pr(n_layer*psz))
     allocate (c_fc(n_layer*fsz), c_pr2(n_layer*fsz))
-    call load1(trim(wdir)//"/transformer_wte_weight.npy", wte, 1, vocab_size*d_model)
-    call load1(trim(wdir)//"/lm_head_weight.npy", lm_head, 1, vocab_size*d_model)
-    do ll = 0, n_layer - 1
-      write (ls, '(I0)') ll
-      p = trim(wdir)//"/transformer_h_"//trim(ls)//"_"
-      call load1(p//"attn_c_q_weight.npy", c_q, ll*qsz + 1, qsz)
-      call load1(p//"attn_c_k_weight.npy", c_k, ll*ksz + 1, ksz)
-      call load1(p//"attn_c_v_weight.npy", c_v, ll*ksz + 1, ksz)
-      call load1(p//"attn_c_proj_weight.npy", c_pr, ll*psz + 1, psz)
-      call load1(p//"mlp_c_fc_weight.npy", c_fc, ll*fsz + 1, fsz)
-      call load1(p//"mlp_c_proj_weight.npy", c_pr2, ll*fsz + 1, fsz)
-    end do
+    fd = fg_dims(n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size, 1.0e-5_c_float)
+    rc = fg_weights_read(fd, trim(wdir)//c_null_char, wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, &
+        lm_head)
+    if (rc /= FG_OK) call die('load_gpt_weights', rc)
   end subroutine load_gpt_weights
 
 end module fgpt_drop_in_mod

@@ -189,3 +189,61 @@ def write_npy_dir(path: str, d: Dims, w: dict, ctx: int = 2048, bos: int = BOS_I
         f.write(f"d_model = {d.d_model}\nn_head = {d.n_head}\nn_kv = {d.n_kv_head}\n"
                 f"n_layer = {d.n_layer}\nvocab = {d.vocab}\nctx = {ctx}\nbos = {bos}\n"
                 f"head_dim = {d.head_dim}\n")
+
+
+# ---------------------------------------------------------------- safetensors
+def arch_canonical_of(d_model, n_head, n_kv, head_dim, n_layer, vocab, ctx, bos) -> str:
+    """The canonical arch string checkpoints carry as arch.canonical
+    (src/lib/fortran_arch.f90:200-210): fixed key order, no spaces."""
+    return ('{"schema":"fortran_gpt/arch/1"' + f',"d_model":{d_model},"n_head":{n_head}'
+            f',"n_kv":{n_kv},"head_dim":{head_dim},"n_layer":{n_layer},"vocab":{vocab}'
+            f',"ctx":{ctx},"bos":{bos}' + "}")
+
+
+def arch_id_of(s: str) -> str:
+    """arch.id: 16 hex digits of a 64-bit rotate-left-17 / xor-shift-29 digest
+    of the canonical string's bytes from seed 0x0123456789abcdef
+    (src/lib/fortran_arch.f90:217-236)."""
+    acc, mask = 0x0123456789ABCDEF, (1 << 64) - 1
+    for b in s.encode():
+        acc ^= b
+        acc = ((acc << 17) | (acc >> 47)) & mask
+        acc ^= acc >> 29
+    return f"{acc:016x}"
+
+
+def safetensors_tensors(d: Dims, w: dict) -> dict:
+    """Canonical names and 2-D shapes of a checkpoint (load_weights.f90:469-489)."""
+    D, qd, kd, ff = d.d_model, d.n_head * d.head_dim, d.n_kv_head * d.head_dim, d.d_ff
+    out = {"wte": w["wte"].reshape(d.vocab, D), "lm": w["lm_head"].reshape(d.vocab, D)}
+    per = {"q": ("c_q", qd, D), "k": ("c_k", kd, D), "v": ("c_v", kd, D),
+           "p": ("c_proj", D, qd), "fc": ("c_fc", ff, D), "p2": ("c_proj2", D, ff)}
+    for L in range(d.n_layer):
+        for short, (name, r, c) in per.items():
+            out[f"l{L}.{short}"] = w[name][L * r * c:(L + 1) * r * c].reshape(r, c)
+    return {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in out.items()}
+
+
+def write_safetensors(path: str, d: Dims, w: dict, ctx: int = 2048, bos: int = BOS_ID,
+                      metadata: dict | None = None) -> str:
+    """model.safetensors in `path` with the arch.* metadata a trained
+    checkpoint carries (fields, arch.canonical, arch.id); `metadata` entries
+    override or add keys (None values remove them)."""
+    from safetensors.numpy import save_file
+    os.makedirs(path, exist_ok=True)
+    meta = {"arch.d_model": d.d_model, "arch.n_head": d.n_head, "arch.n_kv": d.n_kv_head,
+            "arch.head_dim": d.head_dim, "arch.n_layer": d.n_layer, "arch.vocab": d.vocab,
+            "arch.ctx": ctx, "arch.bos": bos}
+    canon = arch_canonical_of(d.d_model, d.n_head, d.n_kv_head, d.head_dim, d.n_layer, d.vocab,
+                              ctx, bos)
+    meta = {k: str(v) for k, v in meta.items()}
+    meta["arch.canonical"] = canon
+    meta["arch.id"] = arch_id_of(canon)
+    for k, v in (metadata or {}).items():
+        if v is None:
+            meta.pop(k, None)
+        else:
+            meta[k] = str(v)
+    out = os.path.join(path, "model.safetensors")
+    save_file(safetensors_tensors(d, w), out, metadata=meta)
+    return out

@@ -39,7 +39,9 @@ enum {
   FG_EROPE = -6,    /* RoPE table row not set for a position in use        */
   FG_ENODEV = -7,   /* no usable gfx950 device                             */
   FG_EBUSY = -8,    /* handle in use by another thread                     */
-  FG_EARCH = -9     /* arch.txt disagrees with the dims (fortran_arch.f90:238-246) */
+  FG_EARCH = -9     /* arch.txt or safetensors arch.* metadata disagrees with the
+                       dims or with itself (fortran_arch.f90:238-246,
+                       load_weights.f90:533-590,799-821) */
 };
 
 typedef struct fg_model fg_model;
@@ -68,9 +70,20 @@ int32_t fg_model_create(const fg_dims *dims, const float *wte, const float *c_q,
                         const float *c_fc, const float *c_proj2,
                         const float *lm_head, fg_model **out);
 
-/* Load a reference weight directory (.npy flats with the file names of
- * src/lib/load_weights.f90:7-9, :853-873) and check arch.txt against dims
- * when present (require_arch, src/lib/fortran_arch.f90:238-246). */
+/* Read a reference weight directory into caller-owned fp32 stacks (the
+ * layout fg_model_create takes). As load_gpt_weights does
+ * (src/lib/load_weights.f90:830-874), model.safetensors is used when the
+ * directory has one: canonical tensor names wte, lm, l{L}.q/.k/.v/.p/.fc/.p2,
+ * F32 payloads, declared arch.* metadata checked against dims and for
+ * self-consistency (arch.canonical, arch.id; :446-592,
+ * src/lib/fortran_arch.f90:200-236). Otherwise the 1-D <f4 .npy files
+ * (:853-873), with arch.txt checked when present (require_arch,
+ * src/lib/fortran_arch.f90:238-246). Host only: needs no device. */
+int32_t fg_weights_read(const fg_dims *dims, const char *weights_dir, float *wte, float *c_q,
+                        float *c_k, float *c_v, float *c_proj, float *c_fc, float *c_proj2,
+                        float *lm_head);
+
+/* fg_weights_read + fg_model_create. */
 int32_t fg_model_load(const fg_dims *dims, const char *weights_dir, fg_model **out);
 
 int32_t fg_model_destroy(fg_model *m);

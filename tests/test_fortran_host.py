@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from autoresearch_amd.weights import (D12, Dims, seeded_weights, uniform_ids, write_npy_dir,
-                                      zipf_ids, BOS_ID)
+                                      write_safetensors, zipf_ids, BOS_ID)
 from oracle import oracle as O
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -68,6 +68,28 @@ def test_fortran_greedy_small(tmp_path, loop, pchunk):
 
 
 @pytest.mark.gpu
+def test_fortran_greedy_from_safetensors(tmp_path):
+    """A checkpoint directory holding only model.safetensors (the trainer's
+    default output) drives the same greedy run as the .npy export."""
+    d = SMALL
+    w = seeded_weights(d, 21)
+    write_safetensors(str(tmp_path / "w"), d, w, ctx=64)
+    prompt = uniform_ids(31, 11, d.vocab)
+    np.savetxt(tmp_path / "ids.txt", prompt, fmt="%d")
+    r = run(["greedy", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "ids.txt"), "20",
+             str(tmp_path / "out.txt"), "64", "device"])
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0
+    got = np.loadtxt(tmp_path / "out.txt", dtype=np.int32)
+    assert np.array_equal(got, oracle_greedy(d, w, prompt, 20))
+    # declared arch that disagrees with the dims stops the program
+    write_safetensors(str(tmp_path / "bad"), d, w, ctx=64, metadata={"arch.n_layer": 3})
+    r = run(["greedy", str(tmp_path / "bad"), *dims_args(d), str(tmp_path / "ids.txt"), "2",
+             str(tmp_path / "o2.txt")])
+    assert r.returncode != 0 and "architecture mismatch" in r.stderr
+
+
+@pytest.mark.gpu
 def test_fortran_greedy_depth12(tmp_path):
     """The B=1 decode workload through the Fortran drop-in: 16 prompt ids,
     32 greedy steps, host argmax per step as chat_text does."""
@@ -118,4 +140,4 @@ def test_fortran_arch_mismatch_stops(tmp_path):
     wrong[3] = "2"  # n_kv_head 2 vs arch.txt n_kv = 1
     r = run(["greedy", str(tmp_path / "w"), *wrong, str(tmp_path / "ids.txt"), "2",
              str(tmp_path / "o.txt")])
-    assert r.returncode != 0 and "arch.txt" in r.stdout
+    assert r.returncode != 0 and "arch.txt" in r.stdout + r.stderr

@@ -13,7 +13,7 @@ import pytest
 
 from autoresearch_amd import engine
 from autoresearch_amd.weights import (D12, Dims, rope_tables, seeded_weights, uniform_ids,
-                                      write_npy_dir, zipf_ids, BOS_ID)
+                                      write_npy_dir, write_safetensors, zipf_ids, BOS_ID)
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -260,5 +260,12 @@ def test_load_npy_dir_equals_create(tmp_path):
     with pytest.raises(engine.FgptError) as e:
         engine.load_gpt_weights(str(tmp_path), d)
     assert e.value.code == -3 and "missing" in str(e.value)
+    # a model.safetensors beside them is read instead, and loads the same model
+    write_safetensors(str(tmp_path), d, w, ctx=64)
+    st = engine.load_gpt_weights(str(tmp_path), d)
+    st.set_rope(c, s)
+    ls, _ = st.forward(ids, 1, 16)
+    assert np.array_equal(la, ls)
+    st.close()
     a.close()
     b.close()
