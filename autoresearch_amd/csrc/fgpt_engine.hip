@@ -628,6 +628,81 @@ extern "C" int32_t fg_forward(fg_model* m, const int32_t* ids, int32_t B, int32_
   return FG_OK;
 }
 
+extern "C" int32_t fg_eval_bpb(fg_model* m, const int32_t* rows, int32_t n_rows, int32_t T,
+                               int32_t batch, const int32_t* token_bytes, int32_t n_token_bytes,
+                               float* nll, double* row_nats, int64_t* row_bytes,
+                               double* total_nats, int64_t* total_bytes) {
+  if (!m || !rows || !token_bytes || !total_nats || !total_bytes)
+    return seterr(FG_EARG, "NULL argument");
+  if (n_rows < 1 || T < 1) return seterr(FG_EARG, "n_rows and T must be >= 1");
+  if (batch < 1 || batch > 64) return seterr(FG_EARG, "require 1 <= batch <= 64");
+  if (n_token_bytes < 1) return seterr(FG_EARG, "empty token_bytes");
+  const int64_t W = (int64_t)T + 1;
+  for (int64_t r = 0; r < n_rows; ++r)
+    for (int64_t t = 0; t < W; ++t) {
+      const int32_t id = rows[r * W + t];
+      if (t < T && (id < 0 || id >= m->d.V))
+        return seterr(FG_EARG, "row %lld: id %d at %lld outside [0, %d)", (long long)r, id,
+                      (long long)t, m->d.V);
+      if (t > 0 && (id < 0 || id >= m->d.V || id >= n_token_bytes))
+        return seterr(FG_EARG, "row %lld: token id %d at %lld out of token_bytes range (%d)",
+                      (long long)r, id, (long long)t, n_token_bytes);
+    }
+  GUARD(m);
+  const int64_t cap = (int64_t)batch * T;
+  RCCHK(ensure_work(m, cap));
+  hipStream_t s = m->stream;
+  int32_t* d_tb = nullptr;
+  double* d_rn = nullptr;
+  long long* d_rb = nullptr;
+  HIPCHK(hipMalloc((void**)&d_tb, (size_t)n_token_bytes * 4));
+  int32_t rc = FG_OK;
+  auto run = [&]() -> int32_t {
+    HIPCHK(hipMalloc((void**)&d_rn, (size_t)batch * sizeof(double)));
+    HIPCHK(hipMalloc((void**)&d_rb, (size_t)batch * sizeof(long long)));
+    HIPCHK(hipMemcpyAsync(d_tb, token_bytes, (size_t)n_token_bytes * 4, hipMemcpyHostToDevice, s));
+    std::vector<int32_t> ids(cap), tgt(cap);
+    std::vector<double> rn(batch);
+    std::vector<long long> rb(batch);
+    double tn = 0.0;
+    int64_t tbt = 0;
+    for (int64_t r0 = 0; r0 < n_rows; r0 += batch) {
+      const int nb = (int)std::min<int64_t>(batch, n_rows - r0);
+      for (int b = 0; b < nb; ++b) {
+        const int32_t* row = rows + (r0 + b) * W;
+        std::copy(row, row + T, ids.data() + (int64_t)b * T);          // inputs ids[0:T]
+        std::copy(row + 1, row + W, tgt.data() + (int64_t)b * T);      // targets ids[1:T+1]
+      }
+      const int64_t n = (int64_t)nb * T;
+      HIPCHK(hipMemcpyAsync(m->ws.ids, ids.data(), n * 4, hipMemcpyHostToDevice, s));
+      HIPCHK(hipMemcpyAsync(m->ws.tgt, tgt.data(), n * 4, hipMemcpyHostToDevice, s));
+      RCCHK(forward_core(m, m->ws.ids, nb, T, m->ws.logits, m->ws.tgt, m->ws.nll, s));
+      timed(m, s, FG_K_OTHER, 0, (double)n * 12, [&] {
+        launch_bpb_rows(s, m->ws.nll, m->ws.tgt, nb, T, d_tb, d_rn, d_rb);
+      });
+      if (nll) HIPCHK(hipMemcpyAsync(nll + r0 * T, m->ws.nll, n * 4, hipMemcpyDeviceToHost, s));
+      HIPCHK(hipMemcpyAsync(rn.data(), d_rn, nb * sizeof(double), hipMemcpyDeviceToHost, s));
+      HIPCHK(hipMemcpyAsync(rb.data(), d_rb, nb * sizeof(long long), hipMemcpyDeviceToHost, s));
+      HIPCHK(hipStreamSynchronize(s));
+      for (int b = 0; b < nb; ++b) {  // rows in order, as bpb_agg adds them
+        if (row_nats) row_nats[r0 + b] = rn[b];
+        if (row_bytes) row_bytes[r0 + b] = rb[b];
+        tn += rn[b];
+        tbt += rb[b];
+      }
+    }
+    *total_nats = tn;
+    *total_bytes = tbt;
+    return FG_OK;
+  };
+  rc = run();
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(d_tb);
+  if (d_rn) (void)hipFree(d_rn);
+  if (d_rb) (void)hipFree(d_rb);
+  return rc;
+}
+
 extern "C" int32_t fg_forward_dev(fg_model* m, const int32_t* d_ids, int32_t B, int32_t T,
                                   float* d_logits, const int32_t* d_targets, float* d_nll,
                                   void* stream) {

@@ -190,6 +190,10 @@ void launch_greedy_tail(hipStream_t s, const Dims& d, const float* logits, int r
 
 // Per-row argmax (first max) of logits [rows][V] -> out [rows].
 void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out);
+// Per eval row (rows of T positions): byte-weighted nats and byte count
+// with the token byte-length table tbytes (targets already range-checked).
+void launch_bpb_rows(hipStream_t s, const float* nll, const int32_t* tgt, int rows, int T,
+                     const int32_t* tbytes, double* row_nats, long long* row_bytes);
 // Per-row nll = logsumexp - logit[tgt].
 void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
                 float* out);

@@ -1,4 +1,5 @@
-// fgpt_weights.hip -- host-side checkpoint reading for fg_weights_read:
+// fgpt_weights.hip -- host-side file reading: checkpoints for
+// fg_weights_read, and eval rows for fg_rows_npy. Checkpoints are
 // the two on-disk formats load_gpt_weights accepts
 // (src/lib/load_weights.f90:830-874): model.safetensors with canonical names
 // and arch.* metadata (:446-592), or one 1-D <f4 .npy file per tensor
@@ -449,4 +450,65 @@ extern "C" int32_t fg_weights_read(const fg_dims* dims, const char* weights_dir,
     TRY(read_npy_f32(p + "mlp_c_proj_weight.npy", D * dff, c_proj2 + l * D * dff));
   }
   return FG_OK;
+}
+
+// eval_bpb's rows file (src/app/eval_bpb.f90:51-57,97-115): one int32 .npy
+// of logical shape (N, T+1), written with fortran_order True by numpy from a
+// Fortran-order array or False from a C-order one; either way row i is
+// element (i, :). rows == NULL: only the shape.
+extern "C" int32_t fg_rows_npy(const char* path, int32_t* n_rows, int32_t* width, int32_t* rows) {
+  if (!path || !n_rows || !width) return set_error(FG_EARG, "NULL argument");
+  FILE* f = fopen(path, "rb");
+  if (!f) return fail(FG_EARG, "rows npy missing or empty: %s", path);
+  unsigned char mg[10];
+  int32_t rc = FG_OK;
+  std::string hdr;
+  if (fread(mg, 1, 8, f) != 8 || memcmp(mg, "\x93NUMPY", 6) != 0) {
+    rc = fail(FG_EARG, "rows npy unreadable: %s", path);
+  } else {
+    uint32_t hlen = 0;
+    if (mg[6] == 1) {
+      if (fread(mg, 1, 2, f) != 2) rc = fail(FG_EARG, "rows npy unreadable: %s", path);
+      hlen = mg[0] | (mg[1] << 8);
+    } else {
+      if (fread(mg, 1, 4, f) != 4) rc = fail(FG_EARG, "rows npy unreadable: %s", path);
+      hlen = mg[0] | (mg[1] << 8) | (mg[2] << 16) | ((uint32_t)mg[3] << 24);
+    }
+    if (rc == FG_OK) {
+      hdr.resize(hlen);
+      if (hlen > 65536 || fread(&hdr[0], 1, hlen, f) != hlen)
+        rc = fail(FG_EARG, "rows npy unreadable: %s", path);
+    }
+  }
+  long long n = 0, w = 0;
+  bool forder = false;
+  if (rc == FG_OK) {
+    const size_t p = hdr.find("'shape': (");
+    if (hdr.find("'descr': '<i4'") == std::string::npos)
+      rc = fail(FG_EARG, "rows npy %s: dtype is not '<i4' (int32)", path);
+    else if (p == std::string::npos || sscanf(hdr.c_str() + p + 10, "%lld, %lld)", &n, &w) != 2 ||
+             n < 1 || w < 2)
+      rc = fail(FG_EARG, "rows npy %s: need a 2-D (N, T+1) array", path);
+    else
+      forder = hdr.find("'fortran_order': True") != std::string::npos;
+  }
+  if (rc == FG_OK && (n > INT32_MAX || w > INT32_MAX))
+    rc = fail(FG_EARG, "rows npy %s: too large", path);
+  if (rc == FG_OK) {
+    *n_rows = (int32_t)n;
+    *width = (int32_t)w;
+    if (rows) {
+      std::vector<int32_t> buf((size_t)(n * w));
+      if (fread(buf.data(), 4, buf.size(), f) != buf.size()) {
+        rc = fail(FG_EARG, "rows npy %s: truncated payload", path);
+      } else if (forder) {  // column-major: element (i, j) at j*N + i
+        for (long long i = 0; i < n; ++i)
+          for (long long j = 0; j < w; ++j) rows[i * w + j] = buf[(size_t)(j * n + i)];
+      } else {
+        memcpy(rows, buf.data(), buf.size() * 4);
+      }
+    }
+  }
+  fclose(f);
+  return rc;
 }

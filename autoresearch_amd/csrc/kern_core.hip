@@ -566,6 +566,53 @@ __global__ __launch_bounds__(256) void k_nll(const float* __restrict__ logits,
   if (threadIdx.x == 0) out[row] = (t >= 0 && t < V) ? (m + logf(s)) - l[t] : __builtin_nanf("");
 }
 
+// Byte-weighted sums of one eval row (scripts/eval_driver.py:174-190,
+// src/app/bpb_agg.f90:130-152): nats = sum of nll[t] over positions whose
+// target has a nonzero byte length, bytes = sum of those lengths. One block
+// per row; double accumulation in a fixed order (strided partial sums, then
+// a tree), so repeated runs give identical sums. Targets were range-checked
+// against the table on the host.
+__global__ __launch_bounds__(256) void k_bpb_rows(const float* __restrict__ nll,
+                                                  const int32_t* __restrict__ tgt, int T,
+                                                  const int32_t* __restrict__ tbytes,
+                                                  double* __restrict__ row_nats,
+                                                  long long* __restrict__ row_bytes) {
+  __shared__ double sn[256];
+  __shared__ long long sb[256];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  double n = 0.0;
+  long long b = 0;
+  for (int t = tid; t < T; t += 256) {
+    const int64_t i = (int64_t)r * T + t;
+    const int tb = tbytes[tgt[i]];
+    if (tb > 0) {
+      n += (double)nll[i];
+      b += tb;
+    }
+  }
+  sn[tid] = n;
+  sb[tid] = b;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (tid < off) {
+      sn[tid] += sn[tid + off];
+      sb[tid] += sb[tid + off];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    row_nats[r] = sn[0];
+    row_bytes[r] = sb[0];
+  }
+}
+
+void launch_bpb_rows(hipStream_t s, const float* nll, const int32_t* tgt, int rows, int T,
+                     const int32_t* tbytes, double* row_nats, long long* row_bytes) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(k_bpb_rows, dim3((unsigned)rows), dim3(256), 0, s, nll, tgt, T, tbytes,
+                     row_nats, row_bytes);
+}
+
 void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
                 float* out) {
   if (rows <= 0) return;

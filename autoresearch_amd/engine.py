@@ -33,6 +33,7 @@ EXPORTS = (
     "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_destroy",
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
+    "fg_eval_bpb", "fg_rows_npy",
 )
 
 KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other"}
@@ -90,6 +91,9 @@ def load_library(path: str = LIB_PATH):
         "fg_sync": (i32, [_vp]),
         "fg_model_bytes": (i32, [_vp, C.POINTER(i64), C.POINTER(i64)]),
         "fg_timing": (i32, [_vp, i32]),
+        "fg_eval_bpb": (i32, [_vp, _i, i32, i32, i32, _i, i32, _f, C.POINTER(C.c_double),
+                              C.POINTER(i64), C.POINTER(C.c_double), C.POINTER(i64)]),
+        "fg_rows_npy": (i32, [C.c_char_p, _i, _i, _i]),
         "fg_timing_read": (i32, [_vp, i32, C.POINTER(i64), C.POINTER(C.c_double),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
@@ -191,6 +195,27 @@ class Model:
     def timing(self, enable: bool):
         _check(_LIB.fg_timing(self._h, 1 if enable else 0))
 
+    def eval_bpb(self, rows, token_bytes, batch: int = 8, want_nll: bool = False) -> dict:
+        """fg_eval_bpb over rows (N, T+1): per-row and total byte-weighted nats
+        and bytes, bpb = nats / bytes / ln 2 (and the per-position NLL)."""
+        rows = _i32(rows)
+        n, w = rows.shape
+        T = w - 1
+        tb = _i32(token_bytes)
+        nll = np.empty(n * T, np.float32) if want_nll else None
+        rn = np.empty(n, np.float64)
+        rb = np.empty(n, np.int64)
+        tn, tbt = C.c_double(), C.c_int64()
+        _check(_LIB.fg_eval_bpb(self._h, _ip(rows), n, T, batch, _ip(tb), tb.size, _fp(nll),
+                                rn.ctypes.data_as(C.POINTER(C.c_double)),
+                                rb.ctypes.data_as(C.POINTER(C.c_int64)), C.byref(tn),
+                                C.byref(tbt)))
+        out = {"row_nats": rn, "row_bytes": rb, "nats": tn.value, "bytes": tbt.value,
+               "bpb": tn.value / tbt.value / np.log(2) if tbt.value else float("nan")}
+        if want_nll:
+            out["nll"] = nll.reshape(n, T)
+        return out
+
     def timing_read(self) -> dict:
         """{kind: (launches, ms, flops, bytes)} of the launches recorded so far."""
         out = {}
@@ -265,6 +290,16 @@ class KV:
 
 
 # ------------------------------------------------------- reference-shaped API
+
+def rows_npy(path: str) -> np.ndarray:
+    """fg_rows_npy: eval_bpb's (N, T+1) int32 rows file, C or Fortran order."""
+    load_library()
+    n, w = C.c_int32(), C.c_int32()
+    _check(_LIB.fg_rows_npy(path.encode(), C.byref(n), C.byref(w), None))
+    out = np.empty((n.value, w.value), np.int32)
+    _check(_LIB.fg_rows_npy(path.encode(), C.byref(n), C.byref(w), _ip(out)))
+    return out
+
 
 def weights_read(wdir: str, d: Dims) -> dict:
     """fg_weights_read: the eight fp32 stacks of a checkpoint directory

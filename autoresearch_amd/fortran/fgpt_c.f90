@@ -21,7 +21,8 @@ module fgpt_c
   public :: fg_version, fg_last_error, fg_model_create, fg_weights_read, fg_model_load, &
       fg_model_destroy, &
       fg_set_rope, fg_forward, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
-      fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_error_message
+      fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_eval_bpb, fg_rows_npy, &
+      fg_error_message
 
   interface
     integer(c_int32_t) function fg_version() bind(C, name="fg_version")
@@ -50,6 +51,25 @@ module fgpt_c
       character(kind=c_char), intent(in) :: weights_dir(*)
       real(c_float), intent(out) :: wte(*), c_q(*), c_k(*), c_v(*), c_proj(*), c_fc(*), &
           c_proj2(*), lm_head(*)
+    end function
+
+    integer(c_int32_t) function fg_eval_bpb(m, rows, n_rows, T, batch, token_bytes, &
+        n_token_bytes, nll, row_nats, row_bytes, total_nats, total_bytes) &
+        bind(C, name="fg_eval_bpb")
+      import :: c_int32_t, c_int64_t, c_float, c_double, c_ptr
+      type(c_ptr), value :: m
+      integer(c_int32_t), intent(in) :: rows(*), token_bytes(*)
+      integer(c_int32_t), value :: n_rows, T, batch, n_token_bytes
+      real(c_float), intent(out) :: nll(*)
+      real(c_double), intent(out) :: row_nats(*), total_nats
+      integer(c_int64_t), intent(out) :: row_bytes(*), total_bytes
+    end function
+
+    integer(c_int32_t) function fg_rows_npy(path, n_rows, width, rows) bind(C, name="fg_rows_npy")
+      import :: c_int32_t, c_char, c_ptr
+      character(kind=c_char), intent(in) :: path(*)
+      integer(c_int32_t), intent(out) :: n_rows, width
+      type(c_ptr), value :: rows
     end function
 
     integer(c_int32_t) function fg_model_load(dims, weights_dir, out) &

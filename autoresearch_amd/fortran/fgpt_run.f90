@@ -11,12 +11,18 @@
 !   eval     the per-position NLL of src/app/eval_bpb.f90:117-126,156-181:
 !            B rows of T+1 ids, gpt_forward on the first T, nats per
 !            position = logsumexp - logit[target].
+!   bpb      eval_bpb + bpb_agg on the device (src/app/eval_bpb.f90:97-181,
+!            src/app/bpb_agg.f90): an int32 (N, T+1) rows .npy, batch rows
+!            per forward, nats weighted by a token byte-length table (one
+!            int per line, token id order); prints bpb_agg's summary line,
+!            and eval_bpb's per-position NLL lines to NLL_OUT when given.
 !   selftest cached steps == full forward (src/test/test_kernels.f90:720-779)
 !            through the drop-in subroutines on frand-filled weights.
 !
 ! Usage:
 !   fgpt_run greedy WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [PCHUNK] [host|device]
 !   fgpt_run eval   WDIR L D H KH HD V ROWS_FILE B T OUT_FILE
+!   fgpt_run bpb    WDIR L D H KH HD V ROWS_NPY TOKEN_BYTES [BATCH] [NLL_OUT]
 !   fgpt_run selftest
 ! Ids files are whitespace-separated 0-based integers. Timing goes to stderr.
 program fgpt_run
@@ -37,6 +43,8 @@ program fgpt_run
     call run_greedy()
   case ('eval')
     call run_eval()
+  case ('bpb')
+    call run_bpb()
   case ('selftest')
     call run_selftest()
   case default
@@ -48,6 +56,7 @@ contains
   subroutine usage()
     write (error_unit, '(A)') 'usage: fgpt_run greedy WDIR L D H KH HD V IDS NGEN OUT [PCHUNK] [host|device]'
     write (error_unit, '(A)') '       fgpt_run eval WDIR L D H KH HD V ROWS B T OUT'
+    write (error_unit, '(A)') '       fgpt_run bpb WDIR L D H KH HD V ROWS_NPY TOKEN_BYTES [BATCH] [NLL_OUT]'
     write (error_unit, '(A)') '       fgpt_run selftest'
     stop 2
   end subroutine usage
@@ -296,6 +305,100 @@ contains
         ' tok_s=', real(B*T, 8)/max(t1-t0, 1d-9)
     call fgpt_release()
   end subroutine run_eval
+
+  subroutine stop_rc(what, rc)
+    character(*), intent(in) :: what
+    integer(c_int32_t), intent(in) :: rc
+    write (error_unit, '(4A,I0,A)') what, ': ', fg_error_message(), ' (rc ', rc, ')'
+    stop 1
+  end subroutine stop_rc
+
+  subroutine run_bpb()
+    character(len=512) :: wdir, rows_file, tb_file, nll_file
+    integer :: L, D, H, KH, HD, V, batch, u, ios, ntb, r, tc
+    integer(c_int32_t) :: rc, nrows, width, T
+    integer(c_int32_t), allocatable, target :: rows(:)
+    integer(c_int32_t), allocatable :: tb(:), tmp(:)
+    real(c_float), allocatable :: cos_b(:), sin_b(:), nll(:)
+    real(c_double), allocatable :: rn(:)
+    integer(c_int64_t), allocatable :: rb(:)
+    real(c_double) :: tn
+    integer(c_int64_t) :: tbt
+    type(c_ptr) :: model
+    type(fg_dims) :: fd
+    real(8) :: t0, t1
+
+    if (command_argument_count() < 10) call usage()
+    wdir = sarg(2); L = iarg(3); D = iarg(4); H = iarg(5); KH = iarg(6); HD = iarg(7); V = iarg(8)
+    rows_file = sarg(9); tb_file = sarg(10)
+    batch = 8
+    if (command_argument_count() >= 11) batch = iarg(11)
+    nll_file = ''
+    if (command_argument_count() >= 12) nll_file = sarg(12)
+
+    rc = fg_rows_npy(trim(rows_file)//c_null_char, nrows, width, c_null_ptr)
+    if (rc /= FG_OK) call stop_rc('rows', rc)
+    T = width - 1
+    allocate (rows(int(nrows)*int(width)))
+    rc = fg_rows_npy(trim(rows_file)//c_null_char, nrows, width, c_loc(rows))
+    if (rc /= FG_OK) call stop_rc('rows', rc)
+
+    ! token byte lengths: one integer per line, id order (bpb_agg.f90:63-84)
+    allocate (tmp(1048576))
+    ntb = 0
+    open (newunit=u, file=trim(tb_file), status='old', action='read', iostat=ios)
+    if (ios /= 0) then
+      write (error_unit, '(2A)') 'cannot open ', trim(tb_file)
+      stop 2
+    end if
+    do
+      if (ntb >= size(tmp)) exit
+      read (u, *, iostat=ios) tmp(ntb + 1)
+      if (ios /= 0) exit
+      ntb = ntb + 1
+    end do
+    close (u)
+    if (ntb == 0) then
+      write (error_unit, '(A)') 'empty token_bytes'
+      stop 2
+    end if
+    tb = tmp(1:ntb)
+
+    fd = fg_dims(L, D, H, KH, HD, V, 1.0e-5_c_float)
+    rc = fg_model_load(fd, trim(wdir)//c_null_char, model)
+    if (rc /= FG_OK) call stop_rc('fg_model_load', rc)
+    call rope_tables(int(T), HD, cos_b, sin_b)
+    call set_rope_rows(model, 0, int(T), HD, cos_b, sin_b)
+    allocate (nll(int(nrows)*int(T)), rn(nrows), rb(nrows))
+    t0 = now()
+    rc = fg_eval_bpb(model, rows, nrows, T, int(batch, c_int32_t), tb, int(ntb, c_int32_t), nll, &
+        rn, rb, tn, tbt)
+    t1 = now()
+    if (rc /= FG_OK) call stop_rc('fg_eval_bpb', rc)
+    if (len_trim(nll_file) > 0) then
+      open (newunit=u, file=trim(nll_file), status='replace', action='write')
+      do r = 1, nrows
+        do tc = 1, T
+          if (tc > 1) write (u, '(A)', advance='no') ' '
+          write (u, '(ES14.7)', advance='no') nll((r - 1)*T + tc)
+        end do
+        write (u, *)
+      end do
+      close (u)
+    end if
+    do r = 1, nrows
+      if (rb(r) > 0) write (*, '(A,I0,A,F0.4)') 'row ', r - 1, ': bpb=', rn(r)/(log(2.0d0)*rb(r))
+    end do
+    if (tbt == 0) then
+      write (error_unit, '(A)') 'no counted bytes'
+      stop 1
+    end if
+    write (*, '(A,I0,A,I0,A,F0.2,A,F0.5)') 'rows=', nrows, ' bytes=', tbt, ' nll_sum=', tn, &
+        ' bpb=', tn / real(tbt, 8) / log(2.0d0)
+    write (error_unit, '(A,F10.3,A,F14.1)') 'stats: eval_ms=', 1000*(t1 - t0), &
+        ' tok_s=', real(nrows, 8)*T/max(t1 - t0, 1d-9)
+    rc = fg_model_destroy(model)
+  end subroutine run_bpb
 
   ! frand of src/test/test_kernels.f90:115-119, explicit 32-bit wrap
   real(c_float) function frand(seed)

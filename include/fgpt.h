@@ -101,6 +101,26 @@ int32_t fg_set_rope(fg_model *m, int32_t pos0, int32_t n_pos, const float *cos_b
 int32_t fg_forward(fg_model *m, const int32_t *ids, int32_t B, int32_t T, float *logits,
                    const int32_t *targets, float *nll);
 
+/* eval_bpb on the device (src/app/eval_bpb.f90:97-181 with the byte
+ * weighting of scripts/eval_driver.py:174-190 / src/app/bpb_agg.f90:130-155):
+ * rows holds n_rows rows of T+1 ids (row-major); each row runs inputs
+ * ids[0:T] against targets ids[1:T+1], `batch` rows per forward (1..64, as
+ * --batch). nll (nullable, n_rows*T): the per-position NLL in nats that
+ * eval_bpb prints. Per row (nullable) and in total: nats summed over the
+ * positions whose target has token_bytes > 0, and those byte counts; bpb =
+ * total_nats / total_bytes / ln 2. Ids outside [0, vocab) or targets outside
+ * token_bytes fail with FG_EARG before any work, as bpb_agg aborts. */
+int32_t fg_eval_bpb(fg_model *m, const int32_t *rows, int32_t n_rows, int32_t T, int32_t batch,
+                    const int32_t *token_bytes, int32_t n_token_bytes, float *nll,
+                    double *row_nats, int64_t *row_bytes, double *total_nats,
+                    int64_t *total_bytes);
+
+/* Read eval_bpb's rows file: an int32 .npy of logical shape (N, T+1), C or
+ * Fortran order (src/app/eval_bpb.f90:51-57,97-115). rows == NULL returns
+ * only n_rows and width (= T+1); else rows receives N*width ids, row-major.
+ * Host only. */
+int32_t fg_rows_npy(const char *path, int32_t *n_rows, int32_t *width, int32_t *rows);
+
 /* fg_forward on device buffers, enqueued on `stream` (a hipStream_t, NULL =
  * the handle's stream) without host synchronisation. d_logits may be NULL
  * (the handle keeps them in its workspace); d_targets/d_nll as above. */

@@ -141,3 +141,41 @@ def test_fortran_arch_mismatch_stops(tmp_path):
     r = run(["greedy", str(tmp_path / "w"), *wrong, str(tmp_path / "ids.txt"), "2",
              str(tmp_path / "o.txt")])
     assert r.returncode != 0 and "arch.txt" in r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+def test_fortran_bpb_rows_npy(tmp_path):
+    """eval_bpb + bpb_agg through the harness: a Fortran-order (N, T+1) int32
+    rows .npy, a token byte-length table, the summary line of bpb_agg and the
+    per-position NLL lines of eval_bpb, against the oracle weighted on the
+    host (scripts/eval_driver.py:174-190)."""
+    d = SMALL
+    w = seeded_weights(d, 29)
+    write_safetensors(str(tmp_path / "w"), d, w, ctx=64)
+    N, T = 3, 40
+    rows = zipf_ids(3, N * (T + 1), d.vocab).reshape(N, T + 1)
+    rows[:, 0] = 7
+    np.save(tmp_path / "rows.npy", np.asfortranarray(rows))
+    tb = uniform_ids(8, d.vocab, 4)      # 0..3 bytes per token
+    np.savetxt(tmp_path / "tb.txt", tb, fmt="%d")
+    r = run(["bpb", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.npy"),
+             str(tmp_path / "tb.txt"), "2", str(tmp_path / "nll.txt")])
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0
+    c, s = O.rope_tables(T, d.head_dim)
+    nats, nbytes, maxlg = 0.0, 0, 0.0
+    lines = open(tmp_path / "nll.txt").read().split("\n")
+    for b in range(N):
+        lg = O.gpt_forward(rows[b, :T], c, s, w, d, 1, T).reshape(T, d.vocab)
+        nl = O.nll(lg, rows[b, 1:], d.vocab).astype(np.float64)
+        got = np.array(lines[b].split(), dtype=np.float64)
+        assert got.size == T and np.abs(got - nl).max() < 2 * 2e-3 * np.abs(lg).max()
+        keep = tb[rows[b, 1:]] > 0
+        nats += nl[keep].sum()
+        nbytes += int(tb[rows[b, 1:]][keep].sum())
+        maxlg = max(maxlg, float(np.abs(lg).max()))
+    summary = [x for x in r.stdout.split("\n") if x.startswith("rows=")][0]
+    kv = dict(p.split("=") for p in summary.split())
+    assert int(kv["rows"]) == N and int(kv["bytes"]) == nbytes
+    bpb = nats / nbytes / np.log(2)
+    assert abs(float(kv["bpb"]) - bpb) < 1e-4 * bpb + 1e-5

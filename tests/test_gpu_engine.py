@@ -269,3 +269,45 @@ def test_load_npy_dir_equals_create(tmp_path):
     st.close()
     a.close()
     b.close()
+
+
+def test_eval_bpb_small_vs_oracle():
+    """fg_eval_bpb: per-position NLL and the byte-weighted sums of
+    scripts/eval_driver.py:174-190 (positions whose target has 0 bytes are
+    left out) against the oracle's NLL weighted in float64 on the host."""
+    d = SMALL
+    w = seeded_weights(d, 17)
+    N, T = 5, 130
+    rows = uniform_ids(5, N * (T + 1), d.vocab).reshape(N, T + 1)
+    tb = (uniform_ids(6, d.vocab, 5)).astype(np.int32)   # 0..4 bytes, zeros included
+    assert (tb == 0).any()
+    c, s = tables(d, T)
+    m = engine.Model(d, stacks=w)
+    m.set_rope(c, s)
+    got = m.eval_bpb(rows, tb, batch=2, want_nll=True)       # batches of 2, 2, 1
+    tot_n, tot_b = 0.0, 0
+    for r in range(N):
+        lg = O.gpt_forward(rows[r, :T], c, s, w, d, 1, T).reshape(T, d.vocab)
+        nl = O.nll(lg, rows[r, 1:], d.vocab).astype(np.float64)
+        keep = tb[rows[r, 1:]] > 0
+        rn, rb = float(nl[keep].sum()), int(tb[rows[r, 1:]][keep].sum())
+        assert got["row_bytes"][r] == rb
+        assert abs(got["row_nats"][r] - rn) <= 2 * TOL * np.abs(lg).max() * T
+        assert abs(got["row_nats"][r] - rn) <= 1e-4 * T
+        assert np.abs(got["nll"][r] - nl).max() <= 2 * TOL * np.abs(lg).max()
+        tot_n += rn
+        tot_b += rb
+    assert got["bytes"] == tot_b
+    bpb_ref = tot_n / tot_b / np.log(2)
+    record("eval_bpb_small", bpb=got["bpb"], ref=bpb_ref)
+    assert abs(got["bpb"] - bpb_ref) <= 1e-4 * bpb_ref
+    # the sums do not depend on how rows are batched
+    again = m.eval_bpb(rows, tb, batch=5)
+    assert np.allclose(again["row_nats"], got["row_nats"], rtol=1e-6, atol=0)
+    # a target outside the table stops before any work
+    with pytest.raises(engine.FgptError) as e:
+        m.eval_bpb(rows, tb[:100], batch=2)
+    assert e.value.code == -1 and "token_bytes" in str(e.value)
+    with pytest.raises(engine.FgptError):
+        m.eval_bpb(rows, tb, batch=65)
+    m.close()

@@ -55,6 +55,11 @@ def test_eval_rows_b8_t2048():
     # one row alone gives the same sums as inside the batch
     _, nll1 = m.forward(rows[B - 1:, :T], 1, T, targets=rows[B - 1:, 1:])
     assert abs(float(nll1.astype(np.float64).sum()) - got[B - 1]) <= 1e-6 * T
+    # the device bpb path with every token one byte long: bytes = T per row
+    # and nats = the row sums
+    bp = m.eval_bpb(rows, np.ones(d.vocab, np.int32), batch=B)
+    assert np.all(bp["row_bytes"] == T)
+    assert np.all(np.abs(bp["row_nats"] - ref) <= 1e-4 * T)
     m.close()
 
 

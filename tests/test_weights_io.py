@@ -133,3 +133,25 @@ def test_malformed_safetensors_stop(tmp_path, w, case):
     with pytest.raises(engine.FgptError) as e:
         engine.weights_read(str(tmp_path), SMALL)
     assert e.value.code == -3
+
+
+@pytest.mark.parametrize("order", ["C", "F"])
+def test_rows_npy_either_order(tmp_path, order):
+    """eval_bpb's rows file: (N, T+1) int32; numpy writes a Fortran-order
+    array with fortran_order True (what the reference's exporter produces)."""
+    rows = np.arange(5 * 9, dtype=np.int32).reshape(5, 9) * 7 % 8192
+    p = str(tmp_path / "rows.npy")
+    np.save(p, np.asfortranarray(rows) if order == "F" else rows)
+    assert np.array_equal(engine.rows_npy(p), rows)
+
+
+def test_rows_npy_rejects_bad_files(tmp_path):
+    p = str(tmp_path / "r.npy")
+    np.save(p, np.zeros((3, 4), np.int64))
+    with pytest.raises(engine.FgptError, match="int32"):
+        engine.rows_npy(p)
+    np.save(p, np.zeros(5, np.int32))
+    with pytest.raises(engine.FgptError, match="2-D"):
+        engine.rows_npy(p)
+    with pytest.raises(engine.FgptError, match="missing"):
+        engine.rows_npy(str(tmp_path / "nope.npy"))
