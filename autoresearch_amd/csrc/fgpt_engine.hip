@@ -87,6 +87,9 @@ struct fg_model {
   std::vector<hipEvent_t> evpool;
 };
 
+// layout of fg_kv::d_spec / h_spec (int32): [0] length, [1..16] ids, argmax
+constexpr int SPEC_TARG = 32, SPEC_INTS = 48;
+
 struct fg_kv {
   fg_model* m = nullptr;
   int B = 0, maxT = 0, len = 0;
@@ -100,7 +103,15 @@ struct fg_kv {
   float* d_lgs = nullptr;    // [cap_lgs] per-step logits of fg_decode_greedy
   float* d_part = nullptr;   // per-chunk partials of the single-query attention
   int64_t cap_lgs = 0;
-  // captured runs of greedy steps keyed by (steps, with_logits), valid for gen
+  // greedy speculative decoding (fg_decode_spec): d_spec[0] = cache length
+  // before a verification pass, d_spec[1..TB] its ids, d_spec[SPEC_TARG..]
+  // the per-row argmax; h_spec is its pinned host mirror; d_spart holds the
+  // single-query attention partials of up to GEMV_MAX_ROWS rows
+  int32_t* d_spec = nullptr;
+  int32_t* h_spec = nullptr;
+  float* d_spart = nullptr;
+  // captured runs of greedy steps keyed by (steps, with_logits), and
+  // verification passes keyed by (rows, 2); valid for gen
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
   int64_t graphs_gen = -1;
 };
@@ -369,20 +380,30 @@ GemvArgs base_args(fg_model* m) {
   return a;
 }
 
+struct PassOpts {
+  int pos_host = -1;      // host value of the first position (timing model), -1: pos0
+  bool embed = true;      // false: x already holds the embedded rows
+  bool rows_single = false;  // every row as a single cached step (see layer_stack)
+};
+
 // One pass over rows = B*T token rows: embedding of ids, the layer stack,
 // lm_head into logits. Positions: pos0 (+ *d_pos if given) + row % T. K/V
 // go to kc/vc with [L][B][maxT][KH*hd] layout (layer stride lstride floats),
 // or only to the split planes when kc is null (gpt_forward). Attention: the
 // single-query kernel for a cached step (T == 1, attn_step), else the causal
-// chunk kernel (causal_attn / attn_chunk).
+// chunk kernel (causal_attn / attn_chunk). With o.rows_single the T rows
+// of a sequence are T consecutive single steps in one pass: fp32 GEMV and
+// the single-query kernel per row, each row's arithmetic that of the step
+// it stands for (a speculative verification pass).
 void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, int pos0,
                  const int32_t* d_pos, float* kc, float* vc, int maxT, int64_t lstride,
-                 float* dec_part, float* logits, int pos_host = -1, bool embed = true) {
+                 float* dec_part, float* logits, const PassOpts& o = PassOpts()) {
   const Dims& d = m->d;
   Work& ws = m->ws;
   const int rows = B * T;
-  const bool gm = use_gemm(d, rows);
-  if (pos_host < 0) pos_host = pos0;
+  const bool gm = !o.rows_single && use_gemm(d, rows);
+  const int pos_host = o.pos_host < 0 ? pos0 : o.pos_host;
+  const bool embed = o.embed;
   // causal (query, key) pairs per (sequence, head) and the attention traffic
   const double pairs = (double)T * pos_host + 0.5 * (double)T * (T + 1);
   const double at_flops = 4.0 * d.hd * d.H * B * pairs;
@@ -410,7 +431,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     a.maxT = maxT;
     // q, k, v = rmsnorm(x) Wqkv^T, RoPE on q and k, k/v appended to the cache
     // (and, for a chunk, written as bf16 hi/lo planes for the MFMA attention)
-    const bool one = (T == 1 && lk != nullptr);
+    const bool one = (T == 1 || o.rows_single) && lk != nullptr;
     const int npos = npos_pad(pos0 + T);
     if (!one) {
       a.qs = m->qs;
@@ -429,7 +450,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     if (one) {
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
         launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, dec_part, ws.ao, aos,
-                               aplane);
+                               aplane, T);
       });
     } else {
       if (pos0 > 0)  // earlier cache positions enter the chunk's key planes
@@ -751,9 +772,11 @@ extern "C" int32_t fg_kv_destroy(fg_kv* kv) {
   (void)hipSetDevice(kv->m->device);
   (void)hipStreamSynchronize(kv->m->stream);
   for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
-  void* ptrs[] = {kv->k, kv->v, kv->d_len, kv->d_ids, kv->d_out, kv->d_lgs, kv->d_part};
+  void* ptrs[] = {kv->k,     kv->v,    kv->d_len,  kv->d_ids, kv->d_out,
+                  kv->d_lgs, kv->d_part, kv->d_spec, kv->d_spart};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
+  if (kv->h_spec) (void)hipHostFree(kv->h_spec);
   delete kv;
   return FG_OK;
 }
@@ -839,8 +862,10 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
   const int B = kv->B;
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
   if (use_gemm(m->d, B)) {
+    PassOpts o;
+    o.pos_host = pos_host;
     layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
-                kv->d_part, m->ws.logits, pos_host);
+                kv->d_part, m->ws.logits, o);
     timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
       launch_argmax_step(s, m->ws.logits, B, m->d.V, kv->d_ids, kv->d_out, kv->d_len,
                          kv->d_len + 1, with_logits ? kv->d_lgs : nullptr);
@@ -849,8 +874,11 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
     // GEMV path: x of this step was embedded by the previous step's tail (or
     // before the first step); the tail does argmax, the next embedding and
     // the length update in one launch
+    PassOpts o;
+    o.pos_host = pos_host;
+    o.embed = false;
     layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
-                kv->d_part, m->ws.logits, pos_host, false);
+                kv->d_part, m->ws.logits, o);
     timed(m, s, FG_K_OTHER, 0, (double)B * (m->d.V * 4 * (with_logits ? 2 : 1) + 6 * m->d.D),
           [&] {
             launch_greedy_tail(s, m->d, m->ws.logits, B, m->w.wte, kv->d_ids, kv->d_out,
@@ -957,6 +985,142 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
     HIPCHK(hipMemcpyAsync(logits_out, kv->d_lgs, nout * m->d.V * 4, hipMemcpyDeviceToHost, s));
   HIPCHK(hipStreamSynchronize(s));
   kv->len += n_steps;
+  return FG_OK;
+}
+
+namespace {
+
+// A verification pass of TB rows (the pending id and TB-1 drafts) at the
+// device-held cache length d_spec[0]: TB single steps in one pass
+// (gpt_step_multi, src/lib/fortran_kv.f90:160-289, with every row computed
+// as gpt_step computes it), then the argmax of each row into d_spec.
+void spec_verify_launches(fg_model* m, fg_kv* kv, hipStream_t s, int TB, int pos_host) {
+  const int64_t lstride = (int64_t)kv->maxT * m->d.kvd();
+  PassOpts o;
+  o.pos_host = pos_host;
+  o.rows_single = true;
+  layer_stack(m, s, kv->d_spec + 1, 1, TB, 0, kv->d_spec, kv->k, kv->v, kv->maxT, lstride,
+              kv->d_spart, m->ws.logits, o);
+  timed(m, s, FG_K_OTHER, 0, (double)TB * m->d.V * 4, [&] {
+    launch_argmax(s, m->ws.logits, TB, m->d.V, kv->d_spec + SPEC_TARG);
+  });
+}
+
+// One verification pass: ids[0:TB] at cache length len, per-row argmax
+// into targ. Replays a captured pass (captured on first use of TB).
+int32_t spec_verify(fg_model* m, fg_kv* kv, const int32_t* ids, int TB, int len, int32_t* targ) {
+  hipStream_t s = m->stream;
+  kv->h_spec[0] = len;
+  for (int j = 0; j < TB; ++j) kv->h_spec[1 + j] = ids[j];
+  HIPCHK(hipMemcpyAsync(kv->d_spec, kv->h_spec, (size_t)(1 + TB) * 4, hipMemcpyHostToDevice, s));
+  if (m->timing) {  // eager, so each launch is bracketed by events
+    spec_verify_launches(m, kv, s, TB, len);
+  } else {
+    const auto key = std::make_pair(TB, 2);
+    auto it = kv->graphs.find(key);
+    if (it == kv->graphs.end()) {
+      hipGraph_t g = nullptr;
+      HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+      spec_verify_launches(m, kv, s, TB, -1);
+      HIPCHK(hipStreamEndCapture(s, &g));
+      hipGraphExec_t ge = nullptr;
+      hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (e != hipSuccess)
+        return seterr(FG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+      it = kv->graphs.emplace(key, ge).first;
+    }
+    HIPCHK(hipGraphLaunch(it->second, s));
+  }
+  HIPCHK(hipMemcpyAsync(kv->h_spec + SPEC_TARG, kv->d_spec + SPEC_TARG, (size_t)TB * 4,
+                        hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  for (int j = 0; j < TB; ++j) targ[j] = kv->h_spec[SPEC_TARG + j];
+  return FG_OK;
+}
+
+}  // namespace
+
+// The draft/verify/commit loop of src/app/chat_text.f90:293-422 at
+// temperature 0 with the prompt-lookup drafter and the sliding-window
+// controller. Invariant per round (as the reference's): ids[0:pp] known,
+// the cache holds pp-1 positions, ids[pp-1] pending.
+extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t n_known,
+                                  int32_t n_total, const fg_spec_cfg* cfg,
+                                  fg_spec_stats* stats) {
+  if (!m || !kv || !ids || !cfg || kv->m != m) return seterr(FG_EARG, "bad argument");
+  if (kv->B != 1) return seterr(FG_EARG, "speculative decoding runs one sequence (B=1), not %d",
+                                kv->B);
+  if (cfg->k < 1 || cfg->k > GEMV_MAX_ROWS - 1)
+    return seterr(FG_EARG, "k = %d outside [1, %d]", cfg->k, GEMV_MAX_ROWS - 1);
+  if (cfg->match < 1) return seterr(FG_EARG, "match = %d must be >= 1", cfg->match);
+  if (cfg->probe < 1) return seterr(FG_EARG, "probe = %d must be >= 1", cfg->probe);
+  if (n_known < 1 || n_total < n_known)
+    return seterr(FG_EARG, "need 1 <= n_known (%d) <= n_total (%d)", n_known, n_total);
+  if (kv->len != n_known - 1)
+    return seterr(FG_EARG, "cache holds %d positions, expected n_known-1 = %d", kv->len,
+                  n_known - 1);
+  if (n_total > kv->maxT)
+    return seterr(FG_EFULL, "cache full (raise maxT): n_total %d > %d", n_total, kv->maxT);
+  RCCHK(check_ids(m, ids, n_known));
+  GUARD(m);
+  RCCHK(check_rope(m, n_total));
+  RCCHK(ensure_work(m, cfg->k + 1));
+  if (!kv->d_spec) {
+    HIPCHK(hipMalloc((void**)&kv->d_spec, SPEC_INTS * 4));
+    HIPCHK(hipHostMalloc((void**)&kv->h_spec, SPEC_INTS * 4, hipHostMallocDefault));
+    HIPCHK(hipMalloc((void**)&kv->d_spart,
+                     (size_t)attn_decode_scratch_floats(m->d, GEMV_MAX_ROWS, kv->maxT) * 4));
+  }
+  if (kv->graphs_gen != m->gen) {
+    for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
+    kv->graphs.clear();
+    kv->graphs_gen = m->gen;
+  }
+  fg_spec_stats st = {0, 0, 0, 0, 0};
+  fgpt::SpecWindow win;
+  win.probe = cfg->probe;
+  win.min_acc = cfg->min_acc;
+  int32_t inp[GEMV_MAX_ROWS], targ[GEMV_MAX_ROWS];
+  int pp = n_known;
+  while (pp < n_total) {
+    int keff = 0;
+    bool spec_round = false;
+    if (win.spec) {
+      keff = fgpt::spec_lookup_draft(ids, pp, cfg->match, cfg->k, inp + 1);
+      spec_round = keff > 0;  // no context match: a plain step is cheaper
+    }
+    if (spec_round && pp + keff > n_total) keff = n_total - pp > 0 ? n_total - pp : 0;
+    inp[0] = ids[pp - 1];
+    const int TB = spec_round ? keff + 1 : 1;
+    const int32_t rc = spec_verify(m, kv, inp, TB, pp - 1, targ);
+    if (rc != FG_OK) {
+      kv->len = pp - 1;
+      return rc;
+    }
+    int na = 0;
+    if (spec_round) {
+      int32_t corr = 0;
+      na = fgpt::spec_accept_prefix(inp + 1, targ, keff, &corr);
+      if (pp + na + 1 > n_total) {
+        na = n_total - pp - 1;
+        corr = targ[na];
+      }
+      for (int j = 0; j < na; ++j) ids[pp + j] = inp[1 + j];
+      ids[pp + na] = corr;
+      ++st.passes;
+      st.accepted += na;
+      st.proposed += keff;
+    } else {
+      ids[pp] = targ[0];
+      ++st.plain;
+    }
+    pp += na + 1;  // the cache keeps pp-1 positions: rows past it are rolled back
+    win.after_round(spec_round, na);
+  }
+  kv->len = n_total - 1;
+  st.pauses = win.pauses;
+  if (stats) *stats = st;
   return FG_OK;
 }
 

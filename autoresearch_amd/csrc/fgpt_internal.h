@@ -89,7 +89,9 @@ void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const in
                        int64_t rows, float* x, uint16_t* xs = nullptr, int64_t plane = 0,
                        float* ssq = nullptr);
 
-// GEMV family for M <= 4 token rows, fp32 activations x bf16 weights.
+// GEMV family for M <= GEMV_MAX_ROWS token rows, fp32 activations x bf16
+// weights (the MFMA GEMM shares the argument block).
+constexpr int GEMV_MAX_ROWS = 16;
 enum GemvEpi { GV_QKV = 0, GV_RESID = 1, GV_RELU2 = 2, GV_STORE = 3 };
 struct GemvArgs {
   const float* x;   // [M][K] input rows
@@ -165,16 +167,18 @@ void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const flo
 // captured decode step replays at successive positions).
 void launch_gemv_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
 void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
-// Single-query attention over the cache: q [B][H][hd] at position len-1
-// -> y [B][H*hd] (or its split format in ys). d_len (nullable) holds the
-// cache length before the step (the query is at *d_len), else len is the
-// length including the query. scratch: attn_decode_scratch_floats(d, B,
-// maxT) floats (a multi-chunk step also launches a merge kernel).
+// Single-query attention over the cache: q [B*qpr][H][hd] -> y [B*qpr][H*hd]
+// (or its split format in ys). Query row j of sequence b (row b*qpr + j)
+// sits at position len-1+j of cache b and sees positions 0..len-1+j: qpr
+// consecutive single steps in one launch. d_len (nullable) holds the cache
+// length before the step (the first query is at *d_len), else len is the
+// length including the first query. scratch: attn_decode_scratch_floats(d,
+// B*qpr, maxT) floats (a multi-chunk step also launches a merge kernel).
 int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT);
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
                             float* scratch, float* y, uint16_t* ys = nullptr,
-                            int64_t ys_plane = 0);
+                            int64_t ys_plane = 0, int qpr = 1);
 // argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +
 // row] (and the logits row into lgs_out at that slot, when set), then
 // *d_len += 1.
@@ -197,5 +201,19 @@ void launch_bpb_rows(hipStream_t s, const float* nll, const int32_t* tgt, int ro
 // Per-row nll = logsumexp - logit[tgt].
 void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
                 float* out);
+
+// ---- greedy speculative decoding, host side (fgpt_spec.hip)
+int spec_accept_prefix(const int32_t* draft, const int32_t* targ, int k, int32_t* correction);
+int spec_lookup_draft(const int32_t* ids, int p, int m, int k, int32_t* d);
+// Sliding-window controller of the draft/verify loop: spec is true while
+// verification passes run, false during a plain pause.
+struct SpecWindow {
+  int probe = 8;
+  float min_acc = 0.5f;
+  bool spec = true;
+  int plain_left = 0, npass = 0, nacc = 0;
+  int64_t pauses = 0;
+  void after_round(bool was_spec_pass, int n_accept);
+};
 
 }  // namespace fgpt

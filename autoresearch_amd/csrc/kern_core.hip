@@ -107,20 +107,28 @@ __device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, fl
 }
 
 // ------------------------------------------------------------ GEMV
-// M <= 4 token rows. A wavefront owns R weight rows at a time (R = 2 for
+// Up to 16 token rows. A wavefront owns R weight rows at a time (R = 2 for
 // QKV, so a rotation pair stays in one wavefront; else 1, for twice the
-// wavefronts): lanes stride the rows in 16-byte chunks (8 bf16), so each row
-// is read as whole, coalesced lines, and x comes straight from global memory
+// wavefronts; 4 above four token rows, so each x load serves more weight
+// rows): lanes stride the rows in 16-byte chunks (8 bf16), so each row is
+// read as whole, coalesced lines, and x comes straight from global memory
 // (L2) in matching float4 pairs. No LDS and no barrier: the weight loads go
 // out at once. The row norm (a.norm) is a scale of the dot products, from
-// sum(x^2) the same lanes accumulate over the chunks they read.
+// sum(x^2) the same lanes accumulate over the chunks they read. Each
+// (token row, weight row) result is the same sequence of operations
+// whatever M and R are, so a row's value does not depend on how many rows
+// share the launch.
 template <int M, int EPI, int R>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restrict__ d_pos) {
+  // M > 4 serves a.M <= M rows: the spare ones re-read row a.M-1 and store nothing
+  constexpr bool PART = M > 4;
   const int K = a.K, lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int pos0 = d_pos ? *d_pos : a.pos0;
-  const int nunits = a.N / R, nch = K >> 3;
+  const int nunits = (a.N + R - 1) / R, nch = K >> 3;
   for (int u = blockIdx.x * 4 + wid; u < nunits; u += gridDim.x * 4) {
-    const bf16_t* w0 = a.w + (int64_t)(R * u) * K;
+    const bf16_t* wr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wr[r] = a.w + (int64_t)min(R * u + r, a.N - 1) * K;
     float acc[R][M], ss[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
@@ -132,11 +140,12 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restr
     for (int c = lane; c < nch; c += 64) {
       float f[R][8];
 #pragma unroll
-      for (int r = 0; r < R; ++r) unpack8(*(const uint4*)(w0 + (int64_t)r * K + c * 8), f[r]);
+      for (int r = 0; r < R; ++r) unpack8(*(const uint4*)(wr[r] + c * 8), f[r]);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const float4 xa = *(const float4*)(a.x + (int64_t)m * K + c * 8);
-        const float4 xb = *(const float4*)(a.x + (int64_t)m * K + c * 8 + 4);
+        const int mr = PART ? min(m, a.M - 1) : m;
+        const float4 xa = *(const float4*)(a.x + (int64_t)mr * K + c * 8);
+        const float4 xb = *(const float4*)(a.x + (int64_t)mr * K + c * 8 + 4);
         ss[m] += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x +
                  xb.y * xb.y + xb.z * xb.z + xb.w * xb.w;
 #pragma unroll
@@ -154,29 +163,40 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restr
     if (lane == 0) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
+        if (PART && m >= a.M) break;
         if (EPI == GV_QKV) {
-          qkv_pair_epilogue(a, m, pos0, 2 * u, acc[0][m], acc[R - 1][m]);
+#pragma unroll
+          for (int pr = 0; pr < R; pr += 2)
+            if (R * u + pr < a.N)
+              qkv_pair_epilogue(a, m, pos0, R * u + pr, acc[pr][m], acc[pr + 1][m]);
         } else {
 #pragma unroll
-          for (int r = 0; r < R; ++r) single_store<EPI>(a, m, R * u + r, acc[r][m]);
+          for (int r = 0; r < R; ++r)
+            if (R * u + r < a.N) single_store<EPI>(a, m, R * u + r, acc[r][m]);
         }
       }
     }
   }
 }
 
+template <int M, int EPI, int R>
+static void gemv_grid(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  const int nunits = (a.N + R - 1) / R;
+  int grid = (nunits + 3) / 4;
+  if (grid > 2048) grid = 2048;
+  hipLaunchKernelGGL((k_gemv<M, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos);
+}
+
 template <int EPI>
 static void gemv_m(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr int R = EPI == GV_QKV ? 2 : 1;
-  const int nunits = a.N / R;
-  int grid = (nunits + 3) / 4;
-  if (grid > 2048) grid = 2048;
-  switch (a.M) {
-    case 1: hipLaunchKernelGGL((k_gemv<1, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
-    case 2: hipLaunchKernelGGL((k_gemv<2, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
-    case 3: hipLaunchKernelGGL((k_gemv<3, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
-    default: hipLaunchKernelGGL((k_gemv<4, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos); break;
-  }
+  if (a.M <= 1) gemv_grid<1, EPI, R>(s, a, d_pos);
+  else if (a.M == 2) gemv_grid<2, EPI, R>(s, a, d_pos);
+  else if (a.M == 3) gemv_grid<3, EPI, R>(s, a, d_pos);
+  else if (a.M == 4) gemv_grid<4, EPI, R>(s, a, d_pos);
+  else if (a.M <= 8) gemv_grid<8, EPI, 4>(s, a, d_pos);
+  else if (a.M <= 12) gemv_grid<12, EPI, 4>(s, a, d_pos);
+  else gemv_grid<16, EPI, 4>(s, a, d_pos);
 }
 
 void launch_gemv_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
@@ -210,8 +230,9 @@ struct DecArgs {
   const float* kc;  // [B][maxT][KH*hd]
   const float* vc;
   int H, KH, maxT, nchunk;
-  const int32_t* d_len;  // cache length before the step (query at *d_len), or null
-  int len_imm;           // cache length including the query's position, if d_len is null
+  const int32_t* d_len;  // cache length before the step (first query at *d_len), or null
+  int len_imm;           // cache length including the first query, if d_len is null
+  int qpr;               // query rows per sequence: row j sees one position more than j-1
   float* y;
   uint16_t* ys;
   int64_t ys_plane;
@@ -238,11 +259,11 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
   __shared__ float red[8];
   __shared__ float4 so[4][LPP];
   const int bh = blockIdx.x, c = blockIdx.y;
-  const int len = a.d_len ? *a.d_len + 1 : a.len_imm;
+  const int row = bh / a.H, b = row / a.qpr, h = bh % a.H, kvh = h / (a.H / a.KH);
+  const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + row % a.qpr;
   const int p0 = c * DPC;
   if (p0 >= len) return;
   const int nch = (len + DPC - 1) / DPC;
-  const int b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.KH);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int sub = lane / LPP, dl = lane % LPP;
   const int64_t kd = (int64_t)a.KH * HD;
@@ -313,7 +334,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
 template <int HD>
 __global__ __launch_bounds__(64) void k_attn_dec_merge(DecArgs a) {
   const int bh = blockIdx.x, tid = threadIdx.x;
-  const int len = a.d_len ? *a.d_len + 1 : a.len_imm;
+  const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + (bh / a.H) % a.qpr;
   const int nch = (len + DPC - 1) / DPC;
   if (nch == 1 || tid >= HD / 4) return;
   const float* P = a.part + (int64_t)bh * a.nchunk * (HD + 2);
@@ -361,7 +382,7 @@ int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT) {
 
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* scratch, float* y, uint16_t* ys, int64_t ys_plane) {
+                            float* scratch, float* y, uint16_t* ys, int64_t ys_plane, int qpr) {
   DecArgs a;
   a.q = q;
   a.kc = kc;
@@ -369,21 +390,24 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.H = d.H;
   a.KH = d.KH;
   a.maxT = maxT;
-  // chunks that can be live: all of maxT for a replayed step, else those of len
-  a.nchunk = attn_decode_chunks(d_len ? maxT : len);
+  // chunks that can be live: all of maxT for a replayed step, else those of
+  // the last query row
+  a.nchunk = attn_decode_chunks(d_len ? maxT : len + qpr - 1);
   a.d_len = d_len;
   a.len_imm = len;
+  a.qpr = qpr;
   a.y = y;
   a.ys = ys;
   a.ys_plane = ys_plane;
   a.part = scratch;
-  const dim3 grid((unsigned)(B * d.H), (unsigned)a.nchunk);
+  const int rows = B * qpr;
+  const dim3 grid((unsigned)(rows * d.H), (unsigned)a.nchunk);
   if (d.hd == 128) {
     hipLaunchKernelGGL(k_attn_dec<128>, grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<128>, dim3(B * d.H), dim3(64), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<128>, dim3(rows * d.H), dim3(64), 0, s, a);
   } else {
     hipLaunchKernelGGL(k_attn_dec<64>, grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<64>, dim3(B * d.H), dim3(64), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<64>, dim3(rows * d.H), dim3(64), 0, s, a);
   }
 }
 
@@ -502,19 +526,23 @@ __global__ __launch_bounds__(1024) void k_greedy_tail(const float* __restrict__ 
       ids[r] = bi;
       out2[slot * rows + r] = bi;
     }
-    // next input row
+    // next input row, its sum of squares in k_embed_norm's order (four
+    // waves of 256-strided partials), so an id embeds to the same bits here
+    // as in any other pass
     const bf16_t* row = wte + (int64_t)bi * D;
     float ss = 0.f;
-    for (int k = tid; k < D; k += 1024) {
-      const float v = bf16_to_f32(row[k]);
-      ss += v * v;
-    }
+    if (tid < 256)
+      for (int k = tid; k < D; k += 256) {
+        const float v = bf16_to_f32(row[k]);
+        ss += v * v;
+      }
     ss = wave_sum(ss);
     __syncthreads();  // rv/ri reads above are done before red is reused
     if (lane == 0) red[w] = ss;
     __syncthreads();
     float t = 0.f;
-    for (int k = 0; k < 16; ++k) t += red[k];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) t += red[k];
     const float inv = 1.0f / sqrtf(t / (float)D + eps);
     for (int k = tid; k < D; k += 1024) x[(int64_t)r * D + k] = bf16_to_f32(row[k]) * inv;
     __syncthreads();

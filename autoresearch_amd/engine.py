@@ -33,7 +33,7 @@ EXPORTS = (
     "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_destroy",
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
-    "fg_eval_bpb", "fg_rows_npy",
+    "fg_eval_bpb", "fg_rows_npy", "fg_decode_spec", "fg_spec_accept", "fg_spec_draft",
 )
 
 KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other"}
@@ -53,6 +53,16 @@ class _FgDims(C.Structure):
     _fields_ = [("n_layer", C.c_int32), ("d_model", C.c_int32), ("n_head", C.c_int32),
                 ("n_kv_head", C.c_int32), ("head_dim", C.c_int32), ("vocab_size", C.c_int32),
                 ("eps", C.c_float)]
+
+
+class _SpecCfg(C.Structure):
+    _fields_ = [("k", C.c_int32), ("match", C.c_int32), ("probe", C.c_int32),
+                ("min_acc", C.c_float)]
+
+
+class _SpecStats(C.Structure):
+    _fields_ = [("passes", C.c_int64), ("accepted", C.c_int64), ("proposed", C.c_int64),
+                ("plain", C.c_int64), ("pauses", C.c_int64)]
 
 
 _f = C.POINTER(C.c_float)
@@ -94,6 +104,10 @@ def load_library(path: str = LIB_PATH):
         "fg_eval_bpb": (i32, [_vp, _i, i32, i32, i32, _i, i32, _f, C.POINTER(C.c_double),
                               C.POINTER(i64), C.POINTER(C.c_double), C.POINTER(i64)]),
         "fg_rows_npy": (i32, [C.c_char_p, _i, _i, _i]),
+        "fg_decode_spec": (i32, [_vp, _vp, _i, i32, i32, C.POINTER(_SpecCfg),
+                                 C.POINTER(_SpecStats)]),
+        "fg_spec_accept": (i32, [_i, _i, i32, _i, _i]),
+        "fg_spec_draft": (i32, [_i, i32, i32, i32, _i, _i]),
         "fg_timing_read": (i32, [_vp, i32, C.POINTER(i64), C.POINTER(C.c_double),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
@@ -287,6 +301,46 @@ class KV:
         _check(_LIB.fg_decode_greedy(self.m.handle, self._h, _ip(ids), n_steps, _ip(out), _fp(lg)))
         out = out.reshape(n_steps, self.B)
         return out, (lg.reshape(n_steps, self.B, -1) if lg is not None else None)
+
+
+    def decode_spec(self, prompt, n_gen: int, k: int = 8, match: int = 2, probe: int = 8,
+                    min_acc: float = 0.5):
+        """fg_decode_spec: greedy speculative continuation of `prompt`, whose
+        first len-1 ids must already be cached (B = 1). Returns the n_gen
+        generated ids and the loop's counters."""
+        prompt = _i32(prompt).reshape(-1)
+        ids = np.zeros(prompt.size + n_gen, np.int32)
+        ids[:prompt.size] = prompt
+        cfg = _SpecCfg(k, match, probe, min_acc)
+        st = _SpecStats()
+        _check(_LIB.fg_decode_spec(self.m.handle, self._h, _ip(ids), prompt.size, ids.size,
+                                   C.byref(cfg), C.byref(st)))
+        stats = {f: getattr(st, f) for f, _ in _SpecStats._fields_}
+        return ids[prompt.size:], stats
+
+
+def spec_accept(draft, targmax):
+    """fg_spec_accept (accept_prefix): (n_accept, correction)."""
+    load_library()
+    d, t = _i32(draft).reshape(-1), _i32(targmax).reshape(-1)
+    if t.size < d.size + 1:
+        raise ValueError("targmax needs k+1 ids")
+    na, corr = C.c_int32(), C.c_int32()
+    _check(_LIB.fg_spec_accept(_ip(d) if d.size else None, _ip(t), d.size, C.byref(na),
+                               C.byref(corr)))
+    return na.value, corr.value
+
+
+def spec_draft(ids, p: int, m: int, k: int):
+    """fg_spec_draft (lookup_draft) over ids[0:p]: the proposed ids."""
+    load_library()
+    ids = _i32(ids).reshape(-1)
+    if p > ids.size:
+        raise ValueError("p exceeds the ids given")
+    d = np.zeros(max(k, 1), np.int32)
+    n = C.c_int32()
+    _check(_LIB.fg_spec_draft(_ip(ids) if ids.size else None, p, m, k, _ip(d), C.byref(n)))
+    return d[:n.value].tolist()
 
 
 # ------------------------------------------------------- reference-shaped API

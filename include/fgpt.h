@@ -157,6 +157,50 @@ int32_t fg_step_multi(fg_model *m, fg_kv *kv, const int32_t *ids, int32_t TB, fl
 int32_t fg_decode_greedy(fg_model *m, fg_kv *kv, const int32_t *ids, int32_t n_steps,
                          int32_t *ids_out, float *logits_out);
 
+/* Greedy speculative decoding (temperature 0), the --spec loop of
+ * src/app/chat_text.f90:293-422: prompt-lookup drafts (lookup_draft,
+ * src/lib/fortran_spec.f90:62-92), one verification pass over the pending
+ * id and k_eff drafts (gpt_step_multi), the accept rule (accept_prefix,
+ * fortran_spec.f90:41-52), and the sliding-window controller that pauses
+ * drafting for `probe` plain steps when a window of `probe` passes accepted
+ * fewer than min_acc drafts per pass. */
+typedef struct fg_spec_cfg {
+  int32_t k;     /* drafts per verification pass, 1..15 (--spec)           */
+  int32_t match; /* lookup match length in ids, >= 1 (--match)             */
+  int32_t probe; /* controller window, passes, >= 1 (--spec-probe)         */
+  float min_acc; /* pause threshold, mean accepted drafts (--spec-min-acc) */
+} fg_spec_cfg;
+
+typedef struct fg_spec_stats {
+  int64_t passes;   /* verification passes                                  */
+  int64_t accepted; /* drafts accepted, summed over passes                  */
+  int64_t proposed; /* drafts verified (k_eff), summed over passes          */
+  int64_t plain;    /* single plain steps (no lookup match, or paused)      */
+  int64_t pauses;   /* times the controller paused drafting                 */
+} fg_spec_stats;
+
+/* ids holds n_total slots; ids[0:n_known] are known and the cache (B = 1)
+ * holds n_known-1 positions (the prompt minus its last id, which is
+ * pending). Fills ids[n_known:n_total] with the target's greedy stream,
+ * leaves n_total-1 positions cached. Every verification row is computed as
+ * fg_step computes that position, so the stream equals fg_decode_greedy's
+ * bit for bit. stats is nullable. */
+int32_t fg_decode_spec(fg_model *m, fg_kv *kv, int32_t *ids, int32_t n_known, int32_t n_total,
+                       const fg_spec_cfg *cfg, fg_spec_stats *stats);
+
+/* accept_prefix (src/lib/fortran_spec.f90:41-52): n_accept = length of the
+ * longest prefix of draft[0:k] equal to targmax, correction =
+ * targmax[n_accept] (targmax holds k+1 ids). Host only. */
+int32_t fg_spec_accept(const int32_t *draft, const int32_t *targmax, int32_t k,
+                       int32_t *n_accept, int32_t *correction);
+
+/* lookup_draft (src/lib/fortran_spec.f90:62-92) over the p known ids:
+ * the continuation (at most k ids, never past ids[p-1]) of the most recent
+ * earlier occurrence of the last min(m, p-1) ids; n_draft = 0 on a miss.
+ * Host only. */
+int32_t fg_spec_draft(const int32_t *ids, int32_t p, int32_t m, int32_t k, int32_t *draft,
+                      int32_t *n_draft);
+
 /* Block until the handle's queued work is done. */
 int32_t fg_sync(fg_model *m);
 
