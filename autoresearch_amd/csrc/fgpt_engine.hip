@@ -87,9 +87,6 @@ struct fg_model {
   std::vector<hipEvent_t> evpool;
 };
 
-// layout of fg_kv::d_spec / h_spec (int32): [0] length, [1..16] ids, argmax
-constexpr int SPEC_TARG = 32, SPEC_INTS = 48;
-
 struct fg_kv {
   fg_model* m = nullptr;
   int B = 0, maxT = 0, len = 0;
@@ -103,15 +100,15 @@ struct fg_kv {
   float* d_lgs = nullptr;    // [cap_lgs] per-step logits of fg_decode_greedy
   float* d_part = nullptr;   // per-chunk partials of the single-query attention
   int64_t cap_lgs = 0;
-  // greedy speculative decoding (fg_decode_spec): d_spec[0] = cache length
-  // before a verification pass, d_spec[1..TB] its ids, d_spec[SPEC_TARG..]
-  // the per-row argmax; h_spec is its pinned host mirror; d_spart holds the
+  // greedy speculative decoding (fg_decode_spec): the loop's device state
+  // and its pinned host mirror, the sequence's ids [maxT], and the
   // single-query attention partials of up to GEMV_MAX_ROWS rows
-  int32_t* d_spec = nullptr;
-  int32_t* h_spec = nullptr;
+  SpecDev* d_sst = nullptr;
+  SpecDev* h_sst = nullptr;
+  int32_t* d_sids = nullptr;
   float* d_spart = nullptr;
-  // captured runs of greedy steps keyed by (steps, with_logits), and
-  // verification passes keyed by (rows, 2); valid for gen
+  // captured runs of greedy steps keyed by (steps, with_logits), and runs
+  // of speculative rounds keyed by (rounds, 100 + rows per pass); valid for gen
   std::map<std::pair<int, int>, hipGraphExec_t> graphs;
   int64_t graphs_gen = -1;
 };
@@ -384,6 +381,7 @@ struct PassOpts {
   int pos_host = -1;      // host value of the first position (timing model), -1: pos0
   bool embed = true;      // false: x already holds the embedded rows
   bool rows_single = false;  // every row as a single cached step (see layer_stack)
+  const int32_t* d_rows = nullptr;  // rows_single: rows live, read on the device
 };
 
 // One pass over rows = B*T token rows: embedding of ids, the layer stack,
@@ -416,7 +414,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   if (embed)  // (else x already holds the embedded rows)
     timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
       launch_embed_norm(s, d, m->w.wte, ids, rows, ws.x, gm ? ws.xs : nullptr, xplane,
-                        gm ? ws.ssq : nullptr);
+                        gm ? ws.ssq : nullptr, o.d_rows);
     });
   int nt = 1;  // partial sums of squares per row of the current residual
   for (int l = 0; l < d.L; ++l) {
@@ -424,6 +422,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     float* lv = vc ? vc + l * lstride : nullptr;
     GemvArgs a = base_args(m);
     a.M = rows;
+    a.d_M = o.d_rows;
     a.T = T;
     a.pos0 = pos0;
     a.kc = lk;
@@ -450,7 +449,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     if (one) {
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
         launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, dec_part, ws.ao, aos,
-                               aplane, T);
+                               aplane, T, o.d_rows);
       });
     } else {
       if (pos0 > 0)  // earlier cache positions enter the chunk's key planes
@@ -482,7 +481,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     nt = gemm_ssq_parts(rows, d.D, d.dff);
   }
   GemvArgs a = base_args(m);
-  a.M = rows; a.T = T;
+  a.M = rows; a.T = T; a.d_M = o.d_rows;
   a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
   a.w = m->w.lm; a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
   linear(m, s, GV_STORE, a, d_pos, gm);
@@ -772,11 +771,11 @@ extern "C" int32_t fg_kv_destroy(fg_kv* kv) {
   (void)hipSetDevice(kv->m->device);
   (void)hipStreamSynchronize(kv->m->stream);
   for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
-  void* ptrs[] = {kv->k,     kv->v,    kv->d_len,  kv->d_ids, kv->d_out,
-                  kv->d_lgs, kv->d_part, kv->d_spec, kv->d_spart};
+  void* ptrs[] = {kv->k,     kv->v,      kv->d_len, kv->d_ids,  kv->d_out,
+                  kv->d_lgs, kv->d_part, kv->d_sst, kv->d_sids, kv->d_spart};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  if (kv->h_spec) (void)hipHostFree(kv->h_spec);
+  if (kv->h_sst) (void)hipHostFree(kv->h_sst);
   delete kv;
   return FG_OK;
 }
@@ -990,52 +989,46 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
 
 namespace {
 
-// A verification pass of TB rows (the pending id and TB-1 drafts) at the
-// device-held cache length d_spec[0]: TB single steps in one pass
-// (gpt_step_multi, src/lib/fortran_kv.f90:160-289, with every row computed
-// as gpt_step computes it), then the argmax of each row into d_spec.
-void spec_verify_launches(fg_model* m, fg_kv* kv, hipStream_t s, int TB, int pos_host) {
-  const int64_t lstride = (int64_t)kv->maxT * m->d.kvd();
+// One round of the speculative loop, all on the device: draft (lookup and
+// the pass's ids), the verification pass over up to `maxr` rows (the live
+// count and the cache length come from the state: every row a single step,
+// as gpt_step computes it), commit (argmax, accept, controller).
+void spec_round_launches(fg_model* m, fg_kv* kv, hipStream_t s, int maxr, int pos_host) {
+  SpecDev* st = kv->d_sst;
+  timed(m, s, FG_K_OTHER, 0, 0, [&] { launch_spec_draft(s, st, kv->d_sids); });
   PassOpts o;
   o.pos_host = pos_host;
   o.rows_single = true;
-  layer_stack(m, s, kv->d_spec + 1, 1, TB, 0, kv->d_spec, kv->k, kv->v, kv->maxT, lstride,
-              kv->d_spart, m->ws.logits, o);
-  timed(m, s, FG_K_OTHER, 0, (double)TB * m->d.V * 4, [&] {
-    launch_argmax(s, m->ws.logits, TB, m->d.V, kv->d_spec + SPEC_TARG);
+  o.d_rows = &st->rows;
+  layer_stack(m, s, st->inp, 1, maxr, 0, &st->len, kv->k, kv->v, kv->maxT,
+              (int64_t)kv->maxT * m->d.kvd(), kv->d_spart, m->ws.logits, o);
+  timed(m, s, FG_K_OTHER, 0, (double)maxr * m->d.V * 4, [&] {
+    launch_spec_commit(s, st, m->ws.logits, m->d.V, kv->d_sids);
   });
 }
 
-// One verification pass: ids[0:TB] at cache length len, per-row argmax
-// into targ. Replays a captured pass (captured on first use of TB).
-int32_t spec_verify(fg_model* m, fg_kv* kv, const int32_t* ids, int TB, int len, int32_t* targ) {
+// `rounds` rounds, replayed from a graph captured on first use (eager when
+// timing is on).
+int32_t spec_rounds(fg_model* m, fg_kv* kv, int rounds, int maxr, int pos_host) {
   hipStream_t s = m->stream;
-  kv->h_spec[0] = len;
-  for (int j = 0; j < TB; ++j) kv->h_spec[1 + j] = ids[j];
-  HIPCHK(hipMemcpyAsync(kv->d_spec, kv->h_spec, (size_t)(1 + TB) * 4, hipMemcpyHostToDevice, s));
-  if (m->timing) {  // eager, so each launch is bracketed by events
-    spec_verify_launches(m, kv, s, TB, len);
-  } else {
-    const auto key = std::make_pair(TB, 2);
-    auto it = kv->graphs.find(key);
-    if (it == kv->graphs.end()) {
-      hipGraph_t g = nullptr;
-      HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-      spec_verify_launches(m, kv, s, TB, -1);
-      HIPCHK(hipStreamEndCapture(s, &g));
-      hipGraphExec_t ge = nullptr;
-      hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-      (void)hipGraphDestroy(g);
-      if (e != hipSuccess)
-        return seterr(FG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
-      it = kv->graphs.emplace(key, ge).first;
-    }
-    HIPCHK(hipGraphLaunch(it->second, s));
+  if (m->timing) {
+    for (int r = 0; r < rounds; ++r) spec_round_launches(m, kv, s, maxr, pos_host);
+    return FG_OK;
   }
-  HIPCHK(hipMemcpyAsync(kv->h_spec + SPEC_TARG, kv->d_spec + SPEC_TARG, (size_t)TB * 4,
-                        hipMemcpyDeviceToHost, s));
-  HIPCHK(hipStreamSynchronize(s));
-  for (int j = 0; j < TB; ++j) targ[j] = kv->h_spec[SPEC_TARG + j];
+  const auto key = std::make_pair(rounds, 100 + maxr);
+  auto it = kv->graphs.find(key);
+  if (it == kv->graphs.end()) {
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    for (int r = 0; r < rounds; ++r) spec_round_launches(m, kv, s, maxr, -1);
+    HIPCHK(hipStreamEndCapture(s, &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return seterr(FG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    it = kv->graphs.emplace(key, ge).first;
+  }
+  HIPCHK(hipGraphLaunch(it->second, s));
   return FG_OK;
 }
 
@@ -1043,8 +1036,10 @@ int32_t spec_verify(fg_model* m, fg_kv* kv, const int32_t* ids, int TB, int len,
 
 // The draft/verify/commit loop of src/app/chat_text.f90:293-422 at
 // temperature 0 with the prompt-lookup drafter and the sliding-window
-// controller. Invariant per round (as the reference's): ids[0:pp] known,
-// the cache holds pp-1 positions, ids[pp-1] pending.
+// controller, resident on the device: the host replays runs of captured
+// rounds and reads the state back once per run. Every round commits at
+// least one id, so a run never holds more rounds than ids remain and no
+// round is spent past n_total.
 extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t n_known,
                                   int32_t n_total, const fg_spec_cfg* cfg,
                                   fg_spec_stats* stats) {
@@ -1064,11 +1059,15 @@ extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t 
     return seterr(FG_EFULL, "cache full (raise maxT): n_total %d > %d", n_total, kv->maxT);
   RCCHK(check_ids(m, ids, n_known));
   GUARD(m);
+  if (stats) *stats = fg_spec_stats{0, 0, 0, 0, 0};
+  if (n_total == n_known) return FG_OK;
+  const int maxr = cfg->k + 1;
   RCCHK(check_rope(m, n_total));
-  RCCHK(ensure_work(m, cfg->k + 1));
-  if (!kv->d_spec) {
-    HIPCHK(hipMalloc((void**)&kv->d_spec, SPEC_INTS * 4));
-    HIPCHK(hipHostMalloc((void**)&kv->h_spec, SPEC_INTS * 4, hipHostMallocDefault));
+  RCCHK(ensure_work(m, maxr));
+  if (!kv->d_sst) {
+    HIPCHK(hipMalloc((void**)&kv->d_sst, sizeof(SpecDev)));
+    HIPCHK(hipHostMalloc((void**)&kv->h_sst, sizeof(SpecDev), hipHostMallocDefault));
+    HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
     HIPCHK(hipMalloc((void**)&kv->d_spart,
                      (size_t)attn_decode_scratch_floats(m->d, GEMV_MAX_ROWS, kv->maxT) * 4));
   }
@@ -1077,50 +1076,40 @@ extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t 
     kv->graphs.clear();
     kv->graphs_gen = m->gen;
   }
-  fg_spec_stats st = {0, 0, 0, 0, 0};
-  fgpt::SpecWindow win;
-  win.probe = cfg->probe;
-  win.min_acc = cfg->min_acc;
-  int32_t inp[GEMV_MAX_ROWS], targ[GEMV_MAX_ROWS];
+  SpecDev* h = kv->h_sst;
+  memset(h, 0, sizeof *h);
+  h->pp = n_known;
+  h->n_total = n_total;
+  h->len = n_known - 1;
+  h->mode_spec = 1;
+  h->k = cfg->k;
+  h->match = cfg->match;
+  h->probe = cfg->probe;
+  h->min_acc = cfg->min_acc;
+  hipStream_t s = m->stream;
+  HIPCHK(hipMemcpyAsync(kv->d_sids, ids, (size_t)n_known * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(kv->d_sst, h, sizeof *h, hipMemcpyHostToDevice, s));
+  HIPCHK(hipStreamSynchronize(s));
   int pp = n_known;
   while (pp < n_total) {
-    int keff = 0;
-    bool spec_round = false;
-    if (win.spec) {
-      keff = fgpt::spec_lookup_draft(ids, pp, cfg->match, cfg->k, inp + 1);
-      spec_round = keff > 0;  // no context match: a plain step is cheaper
+    int rounds = 16;
+    while (rounds > n_total - pp) rounds >>= 1;
+    const int32_t rc = spec_rounds(m, kv, rounds, maxr, pp - 1);
+    if (rc == FG_OK) {
+      HIPCHK(hipMemcpyAsync(h, kv->d_sst, sizeof *h, hipMemcpyDeviceToHost, s));
+      HIPCHK(hipStreamSynchronize(s));
     }
-    if (spec_round && pp + keff > n_total) keff = n_total - pp > 0 ? n_total - pp : 0;
-    inp[0] = ids[pp - 1];
-    const int TB = spec_round ? keff + 1 : 1;
-    const int32_t rc = spec_verify(m, kv, inp, TB, pp - 1, targ);
-    if (rc != FG_OK) {
+    if (rc != FG_OK || h->pp <= pp) {  // (every round commits at least one id)
       kv->len = pp - 1;
-      return rc;
+      return rc != FG_OK ? rc : seterr(FG_EHIP, "speculative rounds made no progress");
     }
-    int na = 0;
-    if (spec_round) {
-      int32_t corr = 0;
-      na = fgpt::spec_accept_prefix(inp + 1, targ, keff, &corr);
-      if (pp + na + 1 > n_total) {
-        na = n_total - pp - 1;
-        corr = targ[na];
-      }
-      for (int j = 0; j < na; ++j) ids[pp + j] = inp[1 + j];
-      ids[pp + na] = corr;
-      ++st.passes;
-      st.accepted += na;
-      st.proposed += keff;
-    } else {
-      ids[pp] = targ[0];
-      ++st.plain;
-    }
-    pp += na + 1;  // the cache keeps pp-1 positions: rows past it are rolled back
-    win.after_round(spec_round, na);
+    pp = h->pp;
   }
+  HIPCHK(hipMemcpyAsync(ids + n_known, kv->d_sids + n_known, (size_t)(n_total - n_known) * 4,
+                        hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
   kv->len = n_total - 1;
-  st.pauses = win.pauses;
-  if (stats) *stats = st;
+  if (stats) *stats = fg_spec_stats{h->passes, h->accepted, h->proposed, h->plain, h->pauses};
   return FG_OK;
 }
 

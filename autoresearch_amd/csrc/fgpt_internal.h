@@ -85,9 +85,10 @@ struct KVCacheDev {
 
 // x[r] = rmsnorm(wte[ids[r]]); when xs is set, also the split copy of x
 // (hi plane, lo plane `plane` elements later) and ssq[r] = sum_k x[r][k]^2.
+// d_rows (nullable): rows live this launch, read on the device.
 void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
                        int64_t rows, float* x, uint16_t* xs = nullptr, int64_t plane = 0,
-                       float* ssq = nullptr);
+                       float* ssq = nullptr, const int32_t* d_rows = nullptr);
 
 // GEMV family for M <= GEMV_MAX_ROWS token rows, fp32 activations x bf16
 // weights (the MFMA GEMM shares the argument block).
@@ -97,6 +98,8 @@ struct GemvArgs {
   const float* x;   // [M][K] input rows
   const bf16_t* w;  // [N][K]
   int M, N, K;
+  const int32_t* d_M;  // GEMV only (nullable): rows live this launch, <= M, read on
+                       // the device (rows past it are neither read nor written)
   int norm;         // apply rmsnorm(x) (scale by inv-rms of each x row)
   float eps;
   float* y;         // output [M][N] (RESID: y += ..., in place)
@@ -174,11 +177,13 @@ void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_
 // length before the step (the first query is at *d_len), else len is the
 // length including the first query. scratch: attn_decode_scratch_floats(d,
 // B*qpr, maxT) floats (a multi-chunk step also launches a merge kernel).
+// d_rows (nullable): query rows live this launch (of B*qpr), on the device.
 int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT);
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
                             float* scratch, float* y, uint16_t* ys = nullptr,
-                            int64_t ys_plane = 0, int qpr = 1);
+                            int64_t ys_plane = 0, int qpr = 1,
+                            const int32_t* d_rows = nullptr);
 // argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +
 // row] (and the logits row into lgs_out at that slot, when set), then
 // *d_len += 1.
@@ -202,18 +207,30 @@ void launch_bpb_rows(hipStream_t s, const float* nll, const int32_t* tgt, int ro
 void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
                 float* out);
 
-// ---- greedy speculative decoding, host side (fgpt_spec.hip)
+// ---- greedy speculative decoding
+// host side (fgpt_spec.hip)
 int spec_accept_prefix(const int32_t* draft, const int32_t* targ, int k, int32_t* correction);
 int spec_lookup_draft(const int32_t* ids, int p, int m, int k, int32_t* d);
-// Sliding-window controller of the draft/verify loop: spec is true while
-// verification passes run, false during a plain pause.
-struct SpecWindow {
-  int probe = 8;
-  float min_acc = 0.5f;
-  bool spec = true;
-  int plain_left = 0, npass = 0, nacc = 0;
-  int64_t pauses = 0;
-  void after_round(bool was_spec_pass, int n_accept);
+
+// Device-resident state of the draft/verify loop for one sequence whose ids
+// live in a device array. A round is k_spec_draft (lookup, the pass's ids
+// and live row count), the verification pass (rows single steps at cache
+// length `len`), then k_spec_commit (argmax of each row, the accept rule,
+// the commit, the controller). Rounds after pp reaches n_total do nothing.
+struct SpecDev {
+  int32_t pp;          // known ids (ids[pp-1] pending, pp-1 positions cached)
+  int32_t n_total;     // stop when pp reaches it
+  int32_t len;         // cache length before this round's pass (pp-1)
+  int32_t rows;        // live rows of this round's pass; 0 once done
+  int32_t keff;        // drafts verified this round
+  int32_t spec_round;  // this round verifies drafts (else a plain step)
+  int32_t mode_spec, plain_left, npass_w, nacc_w;  // the controller window
+  int32_t k, match, probe;
+  float min_acc;
+  int32_t passes, accepted, proposed, plain, pauses;
+  int32_t inp[GEMV_MAX_ROWS];  // the pass's ids: pending id, then drafts
 };
+void launch_spec_draft(hipStream_t s, SpecDev* st, const int32_t* ids);
+void launch_spec_commit(hipStream_t s, SpecDev* st, const float* logits, int V, int32_t* ids);
 
 }  // namespace fgpt

@@ -1,7 +1,7 @@
 // fgpt_spec.hip -- host side of greedy speculative decoding: the accept
-// rule, the prompt-lookup drafter and the sliding-window controller of the
-// draft/verify loop. No device code; fg_decode_spec (fgpt_engine.hip) runs
-// the verification passes.
+// rule and the prompt-lookup drafter, as C-ABI functions. No device code;
+// the device-resident loop (kern_core.hip k_spec_draft / k_spec_commit,
+// fgpt_engine.hip fg_decode_spec) follows the same rules.
 //
 // The rule is temperature 0 only, as in the reference: the committed
 // stream is exactly the target's greedy stream.
@@ -39,31 +39,6 @@ int spec_lookup_draft(const int32_t* ids, int p, int m, int k, int32_t* d) {
     return kk;
   }
   return 0;
-}
-
-// The controller at src/app/chat_text.f90:400-420: every `probe` passes of
-// spec mode the window's accepted drafts are compared (in single precision)
-// with min_acc * passes; below it, the next `probe` rounds run plain.
-void SpecWindow::after_round(bool was_spec_pass, int n_accept) {
-  if (spec) {
-    if (was_spec_pass) {
-      ++npass;
-      nacc += n_accept;
-    }
-    if (npass >= probe) {
-      if ((float)nacc < min_acc * (float)npass) {
-        spec = false;
-        plain_left = probe;
-        ++pauses;
-      }
-      npass = 0;
-      nacc = 0;
-    }
-  } else if (--plain_left <= 0) {
-    spec = true;
-    npass = 0;
-    nacc = 0;
-  }
 }
 
 }  // namespace fgpt

@@ -59,17 +59,44 @@ __device__ __forceinline__ void stage_sync() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// Sum across the 64 lanes of a wavefront (result valid in every lane).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+// v from the lane that a DPP pattern names (all lanes are valid sources).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// Sum across the 64 lanes of a wavefront (result valid in every lane): the
+// butterfly over lane strides 1, 2, 4, 8, 16, 32. Strides 1 and 2 are quad
+// permutes; once quads (then groups of 8) hold equal values, the half-row
+// and row mirrors pair the same values that strides 4 and 8 would; once
+// rows of 16 are uniform, strides 16 and 32 are (row0 + row1) + (row2 +
+// row3) from four lane reads. All VALU/DPP: no LDS-crossbar permutes.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  const int iv = __builtin_bit_cast(int, v);
+  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+  return (a + b) + (c + d);
+}
+
+// Maximum across the 64 lanes, in wave_sum's pattern.
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  const int iv = __builtin_bit_cast(int, v);
+  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 }  // namespace fgpt

@@ -55,9 +55,11 @@ __global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ w
                                                     const int32_t* __restrict__ ids, int D, int V,
                                                     float eps, float* __restrict__ x,
                                                     uint16_t* __restrict__ xs, int64_t plane,
-                                                    float* __restrict__ ssq) {
+                                                    float* __restrict__ ssq,
+                                                    const int32_t* __restrict__ d_rows) {
   __shared__ float red[4];
   const int64_t r = blockIdx.x;
+  if (d_rows && r >= *d_rows) return;
   const int id = ids[r];
   if (id < 0 || id >= V) {
     for (int k = threadIdx.x; k < D; k += 256) x[r * D + k] = __builtin_nanf("");
@@ -86,10 +88,11 @@ __global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ w
 }
 
 void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
-                       int64_t rows, float* x, uint16_t* xs, int64_t plane, float* ssq) {
+                       int64_t rows, float* x, uint16_t* xs, int64_t plane, float* ssq,
+                       const int32_t* d_rows) {
   if (rows <= 0) return;
   hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V, d.eps,
-                     x, xs, plane, ssq);
+                     x, xs, plane, ssq, d_rows);
 }
 
 // ------------------------------------------------------------ epilogues
@@ -107,23 +110,20 @@ __device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, fl
 }
 
 // ------------------------------------------------------------ GEMV
-// Up to 16 token rows. A wavefront owns R weight rows at a time (R = 2 for
-// QKV, so a rotation pair stays in one wavefront; else 1, for twice the
-// wavefronts; 4 above four token rows, so each x load serves more weight
-// rows): lanes stride the rows in 16-byte chunks (8 bf16), so each row is
-// read as whole, coalesced lines, and x comes straight from global memory
-// (L2) in matching float4 pairs. No LDS and no barrier: the weight loads go
-// out at once. The row norm (a.norm) is a scale of the dot products, from
-// sum(x^2) the same lanes accumulate over the chunks they read. Each
-// (token row, weight row) result is the same sequence of operations
-// whatever M and R are, so a row's value does not depend on how many rows
-// share the launch.
+// M <= 4 token rows per wavefront (k_gemv: one group of rows; k_gemv_live:
+// up to 16 live rows read on the device, in groups of four). A wavefront
+// owns R weight rows at a time (R = 2 for QKV, so a rotation pair stays in
+// one wavefront; else 1, for twice the wavefronts): lanes stride the rows in
+// 16-byte chunks (8 bf16), so each row is read as whole, coalesced lines,
+// and x comes straight from global memory (L2) in matching float4 pairs. No
+// LDS and no barrier: the weight loads go out at once. The row norm (a.norm)
+// is a scale of the dot products, from sum(x^2) the same lanes accumulate
+// over the chunks they read. Each (token row, weight row) result is the same
+// sequence of operations whatever M is, so a row's value does not depend on
+// how many rows share the launch.
 template <int M, int EPI, int R>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restrict__ d_pos) {
-  // M > 4 serves a.M <= M rows: the spare ones re-read row a.M-1 and store nothing
-  constexpr bool PART = M > 4;
+__device__ __forceinline__ void gemv_rows(const GemvArgs& a, int pos0) {
   const int K = a.K, lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int pos0 = d_pos ? *d_pos : a.pos0;
   const int nunits = (a.N + R - 1) / R, nch = K >> 3;
   for (int u = blockIdx.x * 4 + wid; u < nunits; u += gridDim.x * 4) {
     const bf16_t* wr[R];
@@ -143,9 +143,8 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restr
       for (int r = 0; r < R; ++r) unpack8(*(const uint4*)(wr[r] + c * 8), f[r]);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const int mr = PART ? min(m, a.M - 1) : m;
-        const float4 xa = *(const float4*)(a.x + (int64_t)mr * K + c * 8);
-        const float4 xb = *(const float4*)(a.x + (int64_t)mr * K + c * 8 + 4);
+        const float4 xa = *(const float4*)(a.x + (int64_t)m * K + c * 8);
+        const float4 xb = *(const float4*)(a.x + (int64_t)m * K + c * 8 + 4);
         ss[m] += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x +
                  xb.y * xb.y + xb.z * xb.z + xb.w * xb.w;
 #pragma unroll
@@ -163,7 +162,6 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restr
     if (lane == 0) {
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        if (PART && m >= a.M) break;
         if (EPI == GV_QKV) {
 #pragma unroll
           for (int pr = 0; pr < R; pr += 2)
@@ -180,6 +178,29 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restr
 }
 
 template <int M, int EPI, int R>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restrict__ d_pos) {
+  gemv_rows<M, EPI, R>(a, d_pos ? *d_pos : a.pos0);
+}
+
+// Up to 16 rows, the live count *a.d_M read on the device (a captured pass
+// whose row count changes between replays). blockIdx.y picks a group of up
+// to four rows; each group runs the exact 1-4 row body of k_gemv on its
+// rows (offset x, y and positions), groups past the live count exit.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemv_live(GemvArgs a, const int32_t* __restrict__ d_pos) {
+  constexpr int R = EPI == GV_QKV ? 2 : 1;
+  const int g0 = blockIdx.y * 4, ml = *a.d_M - g0;
+  if (ml <= 0) return;
+  const int pos0 = (d_pos ? *d_pos : a.pos0) + g0;
+  a.x += (int64_t)g0 * a.K;
+  a.y += (int64_t)g0 * (EPI == GV_QKV ? a.H * a.hd : a.N);
+  if (ml == 1) gemv_rows<1, EPI, R>(a, pos0);
+  else if (ml == 2) gemv_rows<2, EPI, R>(a, pos0);
+  else if (ml == 3) gemv_rows<3, EPI, R>(a, pos0);
+  else gemv_rows<4, EPI, R>(a, pos0);
+}
+
+template <int M, int EPI, int R>
 static void gemv_grid(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   const int nunits = (a.N + R - 1) / R;
   int grid = (nunits + 3) / 4;
@@ -190,13 +211,19 @@ static void gemv_grid(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 template <int EPI>
 static void gemv_m(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr int R = EPI == GV_QKV ? 2 : 1;
-  if (a.M <= 1) gemv_grid<1, EPI, R>(s, a, d_pos);
-  else if (a.M == 2) gemv_grid<2, EPI, R>(s, a, d_pos);
-  else if (a.M == 3) gemv_grid<3, EPI, R>(s, a, d_pos);
-  else if (a.M == 4) gemv_grid<4, EPI, R>(s, a, d_pos);
-  else if (a.M <= 8) gemv_grid<8, EPI, 4>(s, a, d_pos);
-  else if (a.M <= 12) gemv_grid<12, EPI, 4>(s, a, d_pos);
-  else gemv_grid<16, EPI, 4>(s, a, d_pos);
+  if (a.d_M) {  // a.M = the most rows the launch can be given
+    int grid = (a.N / R + 3) / 4;
+    if (grid > 2048) grid = 2048;
+    hipLaunchKernelGGL((k_gemv_live<EPI>), dim3(grid, (a.M + 3) / 4), dim3(256), 0, s, a, d_pos);
+  } else if (a.M <= 1) {
+    gemv_grid<1, EPI, R>(s, a, d_pos);
+  } else if (a.M == 2) {
+    gemv_grid<2, EPI, R>(s, a, d_pos);
+  } else if (a.M == 3) {
+    gemv_grid<3, EPI, R>(s, a, d_pos);
+  } else {
+    gemv_grid<4, EPI, R>(s, a, d_pos);
+  }
 }
 
 void launch_gemv_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
@@ -233,6 +260,7 @@ struct DecArgs {
   const int32_t* d_len;  // cache length before the step (first query at *d_len), or null
   int len_imm;           // cache length including the first query, if d_len is null
   int qpr;               // query rows per sequence: row j sees one position more than j-1
+  const int32_t* d_rows; // query rows live (nullable): later rows' blocks exit at once
   float* y;
   uint16_t* ys;
   int64_t ys_plane;
@@ -260,6 +288,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
   __shared__ float4 so[4][LPP];
   const int bh = blockIdx.x, c = blockIdx.y;
   const int row = bh / a.H, b = row / a.qpr, h = bh % a.H, kvh = h / (a.H / a.KH);
+  if (a.d_rows && row >= *a.d_rows) return;
   const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + row % a.qpr;
   const int p0 = c * DPC;
   if (p0 >= len) return;
@@ -334,6 +363,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
 template <int HD>
 __global__ __launch_bounds__(64) void k_attn_dec_merge(DecArgs a) {
   const int bh = blockIdx.x, tid = threadIdx.x;
+  if (a.d_rows && bh / a.H >= *a.d_rows) return;
   const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + (bh / a.H) % a.qpr;
   const int nch = (len + DPC - 1) / DPC;
   if (nch == 1 || tid >= HD / 4) return;
@@ -382,7 +412,8 @@ int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT) {
 
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
                             const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* scratch, float* y, uint16_t* ys, int64_t ys_plane, int qpr) {
+                            float* scratch, float* y, uint16_t* ys, int64_t ys_plane, int qpr,
+                            const int32_t* d_rows) {
   DecArgs a;
   a.q = q;
   a.kc = kc;
@@ -396,6 +427,7 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.d_len = d_len;
   a.len_imm = len;
   a.qpr = qpr;
+  a.d_rows = d_rows;
   a.y = y;
   a.ys = ys;
   a.ys_plane = ys_plane;
@@ -555,6 +587,148 @@ void launch_greedy_tail(hipStream_t s, const Dims& d, const float* logits, int r
                         const int32_t* d_len0, float* lgs_out, float* x) {
   hipLaunchKernelGGL(k_greedy_tail, dim3(1), dim3(1024), 0, s, logits, rows, d.V, d.D, d.eps, wte,
                      ids, out2, d_len, d_len0, lgs_out, x);
+}
+
+// ------------------------------------------------------------ speculative loop
+// Start of a round of the draft/verify loop (src/app/chat_text.f90:
+// 297-318): when the controller is in spec mode, the prompt-lookup drafter
+// (lookup_draft, src/lib/fortran_spec.f90:62-92) searches the ids for the
+// most recent earlier window equal to the last mm = min(match, pp-1) ids
+// (1-based window ends s from pp-mm down to mm; each thread scans its own
+// stride from the top, so its first hit is its largest, and the block keeps
+// the largest) and proposes what followed it; then the pass's ids (pending
+// id + drafts), its cache length and its live row count. No match, or plain
+// mode: a one-row pass (a plain step).
+__global__ __launch_bounds__(256) void k_spec_draft(SpecDev* __restrict__ st,
+                                                    const int32_t* __restrict__ ids) {
+  __shared__ int best;
+  const int tid = threadIdx.x;
+  const int pp = st->pp, nt = st->n_total;
+  if (pp >= nt) {
+    if (tid == 0) st->rows = 0;
+    return;
+  }
+  const bool spec = st->mode_spec != 0;
+  const int mm = min(st->match, pp - 1);
+  if (tid == 0) best = 0;
+  __syncthreads();
+  if (spec && mm >= 1) {
+    int mine = 0;
+    for (int s = pp - mm - tid; s >= mm; s -= 256) {
+      int j = 0;
+      while (j < mm && ids[s - mm + j] == ids[pp - mm + j]) ++j;
+      if (j == mm) {
+        mine = s;
+        break;
+      }
+    }
+    if (mine) atomicMax(&best, mine);
+  }
+  __syncthreads();
+  const int s = best;
+  int keff = s > 0 ? min(st->k, pp - s) : 0;
+  const bool round_spec = keff > 0;
+  if (round_spec && pp + keff > nt) keff = nt - pp;
+  if (round_spec && tid < keff) st->inp[1 + tid] = ids[s + tid];
+  if (tid == 0) {
+    st->inp[0] = ids[pp - 1];
+    st->keff = round_spec ? keff : 0;
+    st->spec_round = round_spec ? 1 : 0;
+    st->len = pp - 1;
+    st->rows = round_spec ? keff + 1 : 1;
+  }
+}
+
+// End of a round (src/app/chat_text.f90:319-420): the first-max argmax of
+// each live row of the pass's logits (sample_token's strict > scan), the
+// accept rule (accept_prefix, src/lib/fortran_spec.f90:41-52) with the
+// clamp at n_total, the commit into ids, and the sliding-window controller:
+// every `probe` passes in spec mode, fewer than min_acc accepted drafts per
+// pass (compared in single precision) pauses drafting for `probe` rounds.
+__global__ __launch_bounds__(1024) void k_spec_commit(SpecDev* __restrict__ st,
+                                                      const float* __restrict__ logits, int V,
+                                                      int32_t* __restrict__ ids) {
+  __shared__ float rv[16];
+  __shared__ int ri[16];
+  __shared__ int targ[GEMV_MAX_ROWS];
+  const int rows = st->rows;
+  if (rows == 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int r = 0; r < rows; ++r) {
+    const float* l = logits + (int64_t)r * V;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = tid; j < V; j += 1024) {
+      const float v = l[j];
+      if (v > bv) {
+        bv = v;
+        bi = j;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax_merge(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+    if (lane == 0) {
+      rv[w] = bv;
+      ri[w] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int k = 1; k < 16; ++k) amax_merge(bv, bi, rv[k], ri[k]);
+      targ[r] = bi == 0x7fffffff ? 0 : bi;  // all -inf / NaN: position 1
+    }
+    __syncthreads();
+  }
+  if (tid != 0) return;
+  const int pp = st->pp, nt = st->n_total;
+  int na = 0;
+  if (st->spec_round) {
+    const int keff = st->keff;
+    while (na < keff && st->inp[1 + na] == targ[na]) ++na;
+    int corr = targ[na];
+    if (pp + na + 1 > nt) {
+      na = nt - pp - 1;
+      corr = targ[na];
+    }
+    for (int j = 0; j < na; ++j) ids[pp + j] = st->inp[1 + j];
+    ids[pp + na] = corr;
+    st->passes += 1;
+    st->accepted += na;
+    st->proposed += keff;
+  } else {
+    ids[pp] = targ[0];
+    st->plain += 1;
+  }
+  st->pp = pp + na + 1;
+  if (st->mode_spec) {
+    if (st->spec_round) {
+      st->npass_w += 1;
+      st->nacc_w += na;
+    }
+    if (st->npass_w >= st->probe) {
+      if ((float)st->nacc_w < st->min_acc * (float)st->npass_w) {
+        st->mode_spec = 0;
+        st->plain_left = st->probe;
+        st->pauses += 1;
+      }
+      st->npass_w = 0;
+      st->nacc_w = 0;
+    }
+  } else {
+    st->plain_left -= 1;
+    if (st->plain_left <= 0) {
+      st->mode_spec = 1;
+      st->npass_w = 0;
+      st->nacc_w = 0;
+    }
+  }
+}
+
+void launch_spec_draft(hipStream_t s, SpecDev* st, const int32_t* ids) {
+  hipLaunchKernelGGL(k_spec_draft, dim3(1), dim3(256), 0, s, st, ids);
+}
+
+void launch_spec_commit(hipStream_t s, SpecDev* st, const float* logits, int V, int32_t* ids) {
+  hipLaunchKernelGGL(k_spec_commit, dim3(1), dim3(1024), 0, s, st, logits, V, ids);
 }
 
 void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out) {
