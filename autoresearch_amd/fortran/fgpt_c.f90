@@ -18,11 +18,21 @@ module fgpt_c
     real(c_float) :: eps
   end type fg_dims
 
+  ! --spec, --match, --spec-probe, --spec-min-acc (src/app/chat_text.f90:117-120)
+  type, bind(C), public :: fg_spec_cfg
+    integer(c_int32_t) :: k, match, probe
+    real(c_float) :: min_acc
+  end type fg_spec_cfg
+
+  type, bind(C), public :: fg_spec_stats
+    integer(c_int64_t) :: passes, accepted, proposed, plain, pauses
+  end type fg_spec_stats
+
   public :: fg_version, fg_last_error, fg_model_create, fg_weights_read, fg_model_load, &
       fg_model_destroy, &
       fg_set_rope, fg_forward, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
       fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_eval_bpb, fg_rows_npy, &
-      fg_error_message
+      fg_decode_spec, fg_spec_accept, fg_spec_draft, fg_error_message
 
   interface
     integer(c_int32_t) function fg_version() bind(C, name="fg_version")
@@ -143,6 +153,32 @@ module fgpt_c
       integer(c_int32_t), value :: TB
       real(c_float), intent(out) :: logits(*)
       type(c_ptr), value :: next_ids
+    end function
+
+    integer(c_int32_t) function fg_decode_spec(m, kv, ids, n_known, n_total, cfg, stats) &
+        bind(C, name="fg_decode_spec")
+      import :: c_int32_t, c_ptr, fg_spec_cfg, fg_spec_stats
+      type(c_ptr), value :: m, kv
+      integer(c_int32_t), intent(inout) :: ids(*)
+      integer(c_int32_t), value :: n_known, n_total
+      type(fg_spec_cfg), intent(in) :: cfg
+      type(fg_spec_stats), intent(out) :: stats
+    end function
+
+    integer(c_int32_t) function fg_spec_accept(draft, targmax, k, n_accept, correction) &
+        bind(C, name="fg_spec_accept")
+      import :: c_int32_t
+      integer(c_int32_t), intent(in) :: draft(*), targmax(*)
+      integer(c_int32_t), value :: k
+      integer(c_int32_t), intent(out) :: n_accept, correction
+    end function
+
+    integer(c_int32_t) function fg_spec_draft(ids, p, m, k, draft, n_draft) &
+        bind(C, name="fg_spec_draft")
+      import :: c_int32_t
+      integer(c_int32_t), intent(in) :: ids(*)
+      integer(c_int32_t), value :: p, m, k
+      integer(c_int32_t), intent(out) :: draft(*), n_draft
     end function
 
     integer(c_int32_t) function fg_decode_greedy(m, kv, ids, n_steps, ids_out, logits_out) &

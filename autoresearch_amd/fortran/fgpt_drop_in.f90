@@ -25,7 +25,7 @@ module fgpt_drop_in_mod
   implicit none
   private
   public :: gpt_forward, gpt_step, gpt_step_multi, load_gpt_weights, fgpt_release, &
-      fgpt_handles
+      fgpt_handles, accept_prefix, lookup_draft
 
   type(c_ptr), save :: g_model = c_null_ptr
   type(c_ptr), save :: g_kv = c_null_ptr
@@ -249,5 +249,34 @@ contains
         lm_head)
     if (rc /= FG_OK) call die('load_gpt_weights', rc)
   end subroutine load_gpt_weights
+
+  ! accept_prefix (src/lib/fortran_spec.f90:41-52): the greedy accept rule,
+  ! on the engine's host implementation. targmax holds k+1 ids.
+  subroutine accept_prefix(draft, targmax, k, n_accept, correction)
+    integer, intent(in) :: draft(:), targmax(:), k
+    integer, intent(out) :: n_accept, correction
+    integer(c_int32_t) :: d(max(k, 1)), t(k + 1), na, corr, rc
+
+    if (k > 0) d(1:k) = int(draft(1:k), c_int32_t)
+    t = int(targmax(1:k + 1), c_int32_t)
+    rc = fg_spec_accept(d, t, int(k, c_int32_t), na, corr)
+    if (rc /= FG_OK) call die('fg_spec_accept', rc)
+    n_accept = na
+    correction = corr
+  end subroutine accept_prefix
+
+  ! lookup_draft (src/lib/fortran_spec.f90:62-92): prompt-lookup proposals
+  ! over ids(1:p), on the engine's host implementation.
+  subroutine lookup_draft(ids, p, m, k, d, kk)
+    integer, intent(in) :: ids(:), p, m, k
+    integer, intent(out) :: d(:), kk
+    integer(c_int32_t) :: x(max(p, 1)), o(max(k, 1)), n, rc
+
+    if (p > 0) x(1:p) = int(ids(1:p), c_int32_t)
+    rc = fg_spec_draft(x, int(p, c_int32_t), int(m, c_int32_t), int(k, c_int32_t), o, n)
+    if (rc /= FG_OK) call die('fg_spec_draft', rc)
+    kk = n
+    if (kk > 0) d(1:kk) = o(1:kk)
+  end subroutine lookup_draft
 
 end module fgpt_drop_in_mod

@@ -18,12 +18,22 @@
 !            and eval_bpb's per-position NLL lines to NLL_OUT when given.
 !   selftest cached steps == full forward (src/test/test_kernels.f90:720-779)
 !            through the drop-in subroutines on frand-filled weights.
+!   spec     greedy speculative decoding as chat_text --spec runs it
+!            (src/app/chat_text.f90:293-422: prompt-lookup drafts, one
+!            verification pass per round, the sliding-window controller),
+!            checked against a plain greedy run on a second cache as
+!            src/app/spec_bench.f90 does; prints its summary lines.
+!   spectest the accept rule and the drafter through the drop-in names, on
+!            the known answers of src/test/test_kernels.f90:1556-1650 (host
+!            only).
 !
 ! Usage:
 !   fgpt_run greedy WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [PCHUNK] [host|device]
 !   fgpt_run eval   WDIR L D H KH HD V ROWS_FILE B T OUT_FILE
 !   fgpt_run bpb    WDIR L D H KH HD V ROWS_NPY TOKEN_BYTES [BATCH] [NLL_OUT]
 !   fgpt_run selftest
+!   fgpt_run spec   WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [K] [MATCH] [PROBE] [MIN_ACC]
+!   fgpt_run spectest
 ! Ids files are whitespace-separated 0-based integers. Timing goes to stderr.
 program fgpt_run
   use, intrinsic :: iso_c_binding
@@ -47,6 +57,10 @@ program fgpt_run
     call run_bpb()
   case ('selftest')
     call run_selftest()
+  case ('spec')
+    call run_spec()
+  case ('spectest')
+    call run_spectest()
   case default
     call usage()
   end select
@@ -58,6 +72,8 @@ contains
     write (error_unit, '(A)') '       fgpt_run eval WDIR L D H KH HD V ROWS B T OUT'
     write (error_unit, '(A)') '       fgpt_run bpb WDIR L D H KH HD V ROWS_NPY TOKEN_BYTES [BATCH] [NLL_OUT]'
     write (error_unit, '(A)') '       fgpt_run selftest'
+    write (error_unit, '(A)') '       fgpt_run spec WDIR L D H KH HD V IDS NGEN OUT [K] [MATCH] [PROBE] [MIN_ACC]'
+    write (error_unit, '(A)') '       fgpt_run spectest'
     stop 2
   end subroutine usage
 
@@ -73,17 +89,33 @@ contains
     end if
   end function iarg
 
+  real(8) function rarg(i)
+    integer, intent(in) :: i
+    character(len=64) :: s
+    integer :: ios
+    call get_command_argument(i, s)
+    read (s, *, iostat=ios) rarg
+    if (ios /= 0) then
+      write (error_unit, '(A,I0,2A)') 'bad real argument ', i, ': ', trim(s)
+      stop 2
+    end if
+  end function rarg
+
   character(len=512) function sarg(i)
     integer, intent(in) :: i
     call get_command_argument(i, sarg)
   end function sarg
 
+  ! Every whitespace-separated integer of the file, in order (any number per
+  ! line).
   subroutine read_ids(path, ids, n)
     character(*), intent(in) :: path
     integer(c_int), allocatable, intent(out) :: ids(:)
     integer, intent(out) :: n
-    integer :: u, ios, v
+    integer :: u, ios, j, nt
     integer(c_int), allocatable :: tmp(:)
+    character(len=65536) :: line
+    logical :: intok
     allocate (ids(1024))
     n = 0
     open (newunit=u, file=path, status='old', action='read', iostat=ios)
@@ -92,15 +124,30 @@ contains
       stop 1
     end if
     do
-      read (u, *, iostat=ios) v
+      read (u, '(A)', iostat=ios) line
       if (ios /= 0) exit
-      n = n + 1
-      if (n > size(ids)) then
+      nt = 0
+      intok = .false.
+      do j = 1, len_trim(line)
+        if (line(j:j) == ' ' .or. line(j:j) == char(9) .or. line(j:j) == ',') then
+          intok = .false.
+        else if (.not. intok) then
+          intok = .true.
+          nt = nt + 1
+        end if
+      end do
+      if (nt == 0) cycle
+      do while (n + nt > size(ids))
         allocate (tmp(2*size(ids)))
         tmp(1:size(ids)) = ids
         call move_alloc(tmp, ids)
+      end do
+      read (line, *, iostat=ios) ids(n+1:n+nt)
+      if (ios /= 0) then
+        write (error_unit, '(2A)') 'bad ids line in ', trim(path)
+        stop 1
       end if
-      ids(n) = v
+      n = n + nt
     end do
     close (u)
   end subroutine read_ids
@@ -399,6 +446,177 @@ contains
         ' tok_s=', real(nrows, 8)*T/max(t1 - t0, 1d-9)
     rc = fg_model_destroy(model)
   end subroutine run_bpb
+
+  subroutine run_spec()
+    character(len=512) :: wdir, ids_file, out_file
+    integer :: L, D, H, KH, HD, V, ngen, nprompt, ntot, srow, tb, u, i
+    integer(c_int32_t) :: rc
+    integer(c_int), allocatable :: prompt(:)
+    integer(c_int32_t), allocatable :: ids(:), plain(:)
+    real(c_float), allocatable :: cos_b(:), sin_b(:), lg(:)
+    type(c_ptr) :: model, kv, kv2
+    type(fg_dims) :: fd
+    type(fg_spec_cfg) :: cfg
+    type(fg_spec_stats) :: st
+    real(8) :: t0, t1, t2
+
+    if (command_argument_count() < 11) call usage()
+    wdir = sarg(2); L = iarg(3); D = iarg(4); H = iarg(5); KH = iarg(6); HD = iarg(7); V = iarg(8)
+    ids_file = sarg(9); ngen = iarg(10); out_file = sarg(11)
+    ! chat_text's defaults for --match / --spec-probe / --spec-min-acc
+    cfg = fg_spec_cfg(8, 2, 8, 0.5_c_float)
+    if (command_argument_count() >= 12) cfg%k = iarg(12)
+    if (command_argument_count() >= 13) cfg%match = iarg(13)
+    if (command_argument_count() >= 14) cfg%probe = iarg(14)
+    if (command_argument_count() >= 15) cfg%min_acc = real(rarg(15), c_float)
+    call read_ids(trim(ids_file), prompt, nprompt)
+    if (nprompt < 1) then
+      write (error_unit, '(A)') 'empty prompt'
+      stop 1
+    end if
+    ntot = nprompt + ngen
+    fd = fg_dims(L, D, H, KH, HD, V, 1.0e-5_c_float)
+    rc = fg_model_load(fd, trim(wdir)//c_null_char, model)
+    if (rc /= FG_OK) call stop_rc('fg_model_load', rc)
+    call rope_tables(ntot, HD, cos_b, sin_b)
+    call set_rope_rows(model, 0, ntot, HD, cos_b, sin_b)
+    allocate (ids(ntot), plain(max(ngen, 1)), lg(64*V))
+    ids(1:nprompt) = prompt(1:nprompt)
+
+    ! plain greedy on its own cache (spec_bench's run_plain)
+    call prefill(kv2)
+    t0 = now()
+    if (ngen > 0) then
+      rc = fg_decode_greedy(model, kv2, ids(nprompt:nprompt), ngen, plain, c_null_ptr)
+      if (rc /= FG_OK) call stop_rc('fg_decode_greedy', rc)
+    end if
+    t1 = now()
+    ! speculative (spec_bench's run_spec with the lookup drafter)
+    call prefill(kv)
+    t2 = now()
+    rc = fg_decode_spec(model, kv, ids, int(nprompt, c_int32_t), int(ntot, c_int32_t), cfg, st)
+    if (rc /= FG_OK) call stop_rc('fg_decode_spec', rc)
+    t2 = now() - t2
+
+    open (newunit=u, file=trim(out_file), status='replace', action='write')
+    do i = nprompt + 1, ntot
+      write (u, '(I0)') ids(i)
+    end do
+    close (u)
+    write (*, '(A,F10.1,A,F10.2)') 'plain : ', 1000*(t1 - t0), ' ms   ', &
+        real(ngen, 8)/max(t1 - t0, 1d-9), ' tok/s'
+    write (*, '(A,F10.1,A,F10.2)') 'spec  : ', 1000*t2, ' ms   ', real(ngen, 8)/max(t2, 1d-9), ' tok/s'
+    write (*, '(A,F8.2,A)') 'speedup: ', (t1 - t0)/max(t2, 1d-9), 'x'
+    write (*, '(A,I0,A,F8.2,A,F8.2,A,I0,A,I0)') 'passes=', st%passes, ' tokens/pass=', &
+        real(ngen - st%plain, 8)/max(1d0, real(st%passes, 8)), ' mean n_accept=', &
+        real(st%accepted, 8)/max(1d0, real(st%passes, 8)), ' plain=', st%plain, &
+        ' pauses=', st%pauses
+    write (*, '(A,F8.2)') 'mean acceptance rate (nacc/k_eff) = ', &
+        real(st%accepted, 8)/max(1d0, real(st%proposed, 8))
+    if (ngen == 0) then
+      write (*, '(A)') 'EQUIVALENCE ok: spec stream == plain greedy stream'
+    else if (all(ids(nprompt+1:ntot) == plain(1:ngen))) then
+      write (*, '(A)') 'EQUIVALENCE ok: spec stream == plain greedy stream'
+    else
+      write (*, '(A)') 'EQUIVALENCE FAILED: spec stream differs from plain greedy'
+      stop 1
+    end if
+    rc = fg_kv_destroy(kv)
+    rc = fg_kv_destroy(kv2)
+    rc = fg_model_destroy(model)
+
+  contains
+
+    ! a fresh cache holding the prompt minus its last id, in chunks of 64
+    subroutine prefill(c)
+      type(c_ptr), intent(out) :: c
+      rc = fg_kv_create(model, 1_c_int32_t, int(ntot, c_int32_t), c)
+      if (rc /= FG_OK) call stop_rc('fg_kv_create', rc)
+      srow = 1
+      do while (srow <= nprompt - 1)
+        tb = min(64, nprompt - srow)
+        rc = fg_step_multi(model, c, ids(srow:srow+tb-1), int(tb, c_int32_t), lg, c_null_ptr)
+        if (rc /= FG_OK) call stop_rc('fg_step_multi', rc)
+        srow = srow + tb
+      end do
+    end subroutine prefill
+  end subroutine run_spec
+
+  ! The reference's accept_prefix and lookup_draft known answers, through
+  ! the drop-in subroutines of the same names (host only).
+  subroutine run_spectest()
+    integer, parameter :: K = 5, NT = 40
+    integer :: draft(K), targ(K+1), tg(NT+K+1), buf(NT+K+1), ids(9), d(6)
+    integer :: na, corr, p, j, ncomm, npass, ncorr, kk, nfail, nchk
+
+    nfail = 0
+    nchk = 0
+    draft(1:4) = [1, 2, 3, 4]
+    targ(1:5) = [1, 2, 9, 9, 7]
+    call accept_prefix(draft, targ, 4, na, corr)
+    call chk(na == 2 .and. corr == 9, 'partial match')
+    draft(1:3) = [1, 2, 3]
+    targ(1:4) = [1, 2, 3, 5]
+    call accept_prefix(draft, targ, 3, na, corr)
+    call chk(na == 3 .and. corr == 5, 'all match: bonus row')
+    draft(1:2) = [1, 2]
+    targ(1:3) = [7, 8, 9]
+    call accept_prefix(draft, targ, 2, na, corr)
+    call chk(na == 0 .and. corr == 7, 'first rejected')
+    targ(1) = 4
+    call accept_prefix(draft, targ, 0, na, corr)
+    call chk(na == 0 .and. corr == 4, 'k=0 is a plain step')
+    do j = 1, NT + K + 1
+      tg(j) = mod(j*7 + 3, 11)
+    end do
+    p = 1
+    ncomm = 0
+    npass = 0
+    ncorr = 0
+    do while (ncomm < NT .and. p <= NT)
+      draft(1:K) = tg(p:p+K-1)
+      if (mod(p, 7) == 0) draft(3) = mod(draft(3) + 1, 11)
+      targ(1:K+1) = tg(p:p+K)
+      call accept_prefix(draft, targ, K, na, corr)
+      buf(ncomm+1:ncomm+na) = draft(1:na)
+      buf(ncomm+na+1) = corr
+      if (na < K) ncorr = ncorr + 1
+      ncomm = ncomm + na + 1
+      p = p + na + 1
+      npass = npass + 1
+    end do
+    call chk(ncomm >= NT, 'simulation commits the span')
+    call chk(all(buf(1:ncomm) == tg(1:ncomm)), 'committed stream == target stream')
+    call chk(ncorr > 0, 'reject path exercised')
+    ids = [5, 1, 2, 3, 9, 1, 2, 3, 7]
+    call lookup_draft(ids, 8, 3, 6, d, kk)
+    call chk(kk == 4 .and. all(d(1:4) == [9, 1, 2, 3]), 'continuation capped at known ids')
+    call lookup_draft(ids, 8, 3, 2, d, kk)
+    call chk(kk == 2 .and. all(d(1:2) == [9, 1]), 'k truncates')
+    ids(1:3) = [5, 1, 2]
+    call lookup_draft(ids, 3, 5, 4, d, kk)
+    call chk(kk == 0, 'm > p-1 is a miss')
+    ids(1:6) = [1, 2, 3, 4, 5, 6]
+    call lookup_draft(ids, 6, 2, 3, d, kk)
+    call chk(kk == 0, 'no earlier occurrence')
+    ids(1:6) = [7, 8, 9, 7, 8, 9]
+    call lookup_draft(ids, 6, 3, 5, d, kk)
+    call chk(kk == 3 .and. all(d(1:3) == [7, 8, 9]), 'match at position 1')
+    write (*, '(A,I0,A,I0,A)') 'spectest: ', nchk - nfail, ' of ', nchk, ' checks passed'
+    if (nfail > 0) stop 1
+
+  contains
+
+    subroutine chk(ok, what)
+      logical, intent(in) :: ok
+      character(*), intent(in) :: what
+      nchk = nchk + 1
+      if (.not. ok) then
+        nfail = nfail + 1
+        write (*, '(2A)') 'FAIL: ', what
+      end if
+    end subroutine chk
+  end subroutine run_spectest
 
   ! frand of src/test/test_kernels.f90:115-119, explicit 32-bit wrap
   real(c_float) function frand(seed)

@@ -143,6 +143,40 @@ def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, with_roofline=True)
     return out
 
 
+def bench_spec(m, d, reps, warmup, k=8, match=2, probe=8, min_acc=0.5):
+    """Greedy speculative decoding (fg_decode_spec, prompt-lookup drafts) next
+    to plain greedy decoding on the same prompt and weights: 256 ids after an
+    88-id prompt that repeats a 24-id span (the context prompt lookup feeds
+    on). Both streams must be equal; tok/s of each, and the loop's counters."""
+    from autoresearch_amd.weights import uniform_ids
+    base = uniform_ids(77, 24, d.vocab)
+    prompt = np.concatenate([np.tile(base, 3), base[:16]]).astype(np.int32)
+    n_gen = 256
+    kv = m.kv(1, prompt.size + n_gen)
+    kv.step_multi(prompt[:-1], want_logits=False)
+    L0 = prompt.size - 1
+
+    def timed(fn):
+        for _ in range(warmup):
+            kv.len = L0
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            kv.len = L0
+            out = fn()
+        return out, (time.perf_counter() - t0) / reps
+
+    g, t_g = timed(lambda: kv.decode_greedy(prompt[-1:], n_gen)[0][:, 0])
+    (sp, st), t_s = timed(lambda: kv.decode_spec(prompt, n_gen, k=k, match=match, probe=probe,
+                                                 min_acc=min_acc))
+    kv.close()
+    if not np.array_equal(g, sp):
+        raise RuntimeError("speculative stream differs from the greedy stream")
+    return {"prompt": int(prompt.size), "gen": n_gen, "k": k, "match": match,
+            "greedy_tok_s": n_gen / t_g, "spec_tok_s": n_gen / t_s, "speedup": t_g / t_s,
+            "stats": st, "streams_equal": True}
+
+
 # --- HBM traffic of the dominant prefill kernel kind, from PMC counters ---
 PMC_KIND = "gemm"                 # kernel kind the prefill roofline is quoted on
 PMC_MATCH = ("k_gemm",)           # kernel-name fragments of that kind
@@ -259,7 +293,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b64", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "decode_b1", "decode_b64"),
+    ap.add_argument("--only", choices=("prefill", "decode_b1", "decode_b64", "decode_spec"),
                     help="run one workload and print its record (for profiling runs)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the PMC traffic runs")
     ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
@@ -295,8 +329,8 @@ def main():
         rec = {"prefill": lambda: bench_prefill(m, d, args.steps, args.warmup, torch),
                "decode_b1": lambda: bench_decode(m, d, 1, 16, 32, reps=max(args.steps, 5),
                                                  warmup=args.warmup),
-               "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0)}[
-            args.only]()
+               "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0),
+               "decode_spec": lambda: bench_spec(m, d, reps=3, warmup=1)}[args.only]()
         print(json.dumps({"only": args.only, **rec}), flush=True)
         return
 
@@ -311,6 +345,9 @@ def main():
         log("bench: decode B=64")
         dec64 = bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0)
         log("bench: decode B=64", json.dumps(dec64))
+    log("bench: speculative decode B=1")
+    spec = bench_spec(m, d, reps=3, warmup=1)
+    log("bench: decode spec", json.dumps(spec))
     cpu = None
     if not args.no_cpu:
         log("bench: CPU oracle baseline")
@@ -334,6 +371,7 @@ def main():
         "prefill": pre,
         "decode_b1": dec1,
         "decode_b64": dec64,
+        "decode_spec": spec,
     }
     print(json.dumps(line), flush=True)
 

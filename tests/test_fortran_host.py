@@ -179,3 +179,33 @@ def test_fortran_bpb_rows_npy(tmp_path):
     assert int(kv["rows"]) == N and int(kv["bytes"]) == nbytes
     bpb = nats / nbytes / np.log(2)
     assert abs(float(kv["bpb"]) - bpb) < 1e-4 * bpb + 1e-5
+
+
+def test_fortran_spectest_reference_kats():
+    """accept_prefix / lookup_draft through the drop-in names on the
+    reference's known answers (host functions: no device needed)."""
+    r = run(["spectest"], timeout=60)
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0 and "spectest: 12 of 12 checks passed" in r.stdout
+
+
+@pytest.mark.gpu
+def test_fortran_spec_equals_greedy(tmp_path):
+    """chat_text --spec semantics through the harness: the speculative stream
+    equals the plain greedy stream (printed EQUIVALENCE line) and the oracle's
+    greedy ids."""
+    d = SMALL
+    w = seeded_weights(d, 23)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=160)
+    base = uniform_ids(41, 10, d.vocab)
+    prompt = np.concatenate([base, base, base[:4]]).astype(np.int32)
+    np.savetxt(tmp_path / "p.txt", prompt[None, :], fmt="%d")
+    ngen = 60
+    r = run(["spec", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "p.txt"), str(ngen),
+             str(tmp_path / "o.txt"), "6", "2", "4", "0.5"])
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stderr
+    assert "EQUIVALENCE ok" in r.stdout
+    assert "passes=" in r.stdout
+    got = np.loadtxt(tmp_path / "o.txt", dtype=np.int32).reshape(-1)
+    assert np.array_equal(got, oracle_greedy(d, w, prompt, ngen))
