@@ -73,6 +73,9 @@ struct fg_model {
   // partial results of the chunk attention
   float* attn_part = nullptr;
   int64_t attn_floats = 0;
+  // fg_sample's device copies (logits row, history, state, id), grown on use
+  char* samp = nullptr;
+  int64_t samp_bytes = 0;
   int64_t work_bytes = 0;
   int64_t gen = 0;      // bumped whenever a buffer a captured graph uses moves
   std::atomic<int> busy{0};
@@ -105,7 +108,10 @@ struct fg_kv {
   // single-query attention partials of up to GEMV_MAX_ROWS rows
   SpecDev* d_sst = nullptr;
   SpecDev* h_sst = nullptr;
-  int32_t* d_sids = nullptr;
+  // the sampling loop's device state and pinned mirror (fg_decode_sample)
+  SampleDev* d_smp = nullptr;
+  SampleDev* h_smp = nullptr;
+  int32_t* d_sids = nullptr;  // [maxT] the sequence's ids (speculative and sampling loops)
   float* d_spart = nullptr;
   // captured runs of greedy steps keyed by (steps, with_logits), and runs
   // of speculative rounds keyed by (rounds, 100 + rows per pass); valid for gen
@@ -571,6 +577,7 @@ extern "C" int32_t fg_model_destroy(fg_model* m) {
   if (m->ks) (void)hipFree(m->ks);
   if (m->vt) (void)hipFree(m->vt);
   if (m->attn_part) (void)hipFree(m->attn_part);
+  if (m->samp) (void)hipFree(m->samp);
   if (m->w.base) (void)hipFree(m->w.base);
   if (m->d_cos) (void)hipFree(m->d_cos);
   if (m->d_sin) (void)hipFree(m->d_sin);
@@ -771,11 +778,12 @@ extern "C" int32_t fg_kv_destroy(fg_kv* kv) {
   (void)hipSetDevice(kv->m->device);
   (void)hipStreamSynchronize(kv->m->stream);
   for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
-  void* ptrs[] = {kv->k,     kv->v,      kv->d_len, kv->d_ids,  kv->d_out,
-                  kv->d_lgs, kv->d_part, kv->d_sst, kv->d_sids, kv->d_spart};
+  void* ptrs[] = {kv->k,     kv->v,      kv->d_len, kv->d_ids,   kv->d_out,  kv->d_lgs,
+                  kv->d_part, kv->d_sst, kv->d_sids, kv->d_spart, kv->d_smp};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   if (kv->h_sst) (void)hipHostFree(kv->h_sst);
+  if (kv->h_smp) (void)hipHostFree(kv->h_smp);
   delete kv;
   return FG_OK;
 }
@@ -1064,10 +1072,10 @@ extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t 
   const int maxr = cfg->k + 1;
   RCCHK(check_rope(m, n_total));
   RCCHK(ensure_work(m, maxr));
+  if (!kv->d_sids) HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
   if (!kv->d_sst) {
     HIPCHK(hipMalloc((void**)&kv->d_sst, sizeof(SpecDev)));
     HIPCHK(hipHostMalloc((void**)&kv->h_sst, sizeof(SpecDev), hipHostMallocDefault));
-    HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
     HIPCHK(hipMalloc((void**)&kv->d_spart,
                      (size_t)attn_decode_scratch_floats(m->d, GEMV_MAX_ROWS, kv->maxT) * 4));
   }
@@ -1110,6 +1118,170 @@ extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t 
   HIPCHK(hipStreamSynchronize(s));
   kv->len = n_total - 1;
   if (stats) *stats = fg_spec_stats{h->passes, h->accepted, h->proposed, h->plain, h->pauses};
+  return FG_OK;
+}
+
+// ------------------------------------------------------------------ sampling
+namespace {
+
+int32_t check_sample_cfg(const fg_sample_cfg* c, int V, SampleCfg* out) {
+  if (!c) return seterr(FG_EARG, "NULL sampling config");
+  if (V < 1 || V > SAMPLE_MAX_V)
+    return seterr(FG_EDIMS, "sampling takes 1 <= V <= %d ids, not %d", SAMPLE_MAX_V, V);
+  if (c->nblock < 0 || c->pwin < 0) return seterr(FG_EARG, "nblock and pwin must be >= 0");
+  out->temp = c->temp;
+  out->topp = c->topp;
+  out->pres = c->pres;
+  out->freq = c->freq;
+  out->rep = c->rep;
+  out->plen = c->plen;
+  out->pwin = c->pwin;
+  out->nblock = c->nblock;
+  out->byte_space = c->byte_space != 0;
+  return FG_OK;
+}
+
+}  // namespace
+
+// sample_next (src/lib/sample.f90:153-233) over one host row of V logits on
+// the device: history gen[0:ngen], the generator state advanced in place.
+extern "C" int32_t fg_sample(fg_model* m, const float* logits, int32_t V, const int32_t* gen,
+                             int32_t ngen, const fg_sample_cfg* cfg, int64_t* state,
+                             int32_t* id) {
+  if (!m || !logits || !state || !id || ngen < 0 || (ngen > 0 && !gen))
+    return seterr(FG_EARG, "bad argument");
+  SampleCfg c;
+  RCCHK(check_sample_cfg(cfg, V, &c));
+  GUARD(m);
+  const int64_t need = (int64_t)V * 4 + (int64_t)ngen * 4 + 64;
+  if (need > m->samp_bytes) {
+    if (m->samp) HIPCHK(hipFree(m->samp));
+    m->samp = nullptr;
+    m->samp_bytes = 0;
+    HIPCHK(hipMalloc((void**)&m->samp, need));
+    m->samp_bytes = need;
+  }
+  int64_t* d_state = (int64_t*)m->samp;
+  int32_t* d_id = (int32_t*)(m->samp + 8);
+  float* d_lg = (float*)(m->samp + 64);
+  int32_t* d_gen = (int32_t*)(m->samp + 64 + (int64_t)V * 4);
+  hipStream_t s = m->stream;
+  HIPCHK(hipMemcpyAsync(d_state, state, 8, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(d_lg, logits, (size_t)V * 4, hipMemcpyHostToDevice, s));
+  if (ngen > 0) HIPCHK(hipMemcpyAsync(d_gen, gen, (size_t)ngen * 4, hipMemcpyHostToDevice, s));
+  launch_sample_one(s, d_lg, V, d_gen, ngen, c, d_state, d_id);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(state, d_state, 8, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipMemcpyAsync(id, d_id, 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return FG_OK;
+}
+
+namespace {
+
+// One step of the sampling loop: the pass over inp[0] at the device-held
+// cache length, then the sampled id (history = the ids generated so far).
+void sample_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, int pos_host) {
+  SampleDev* sd = kv->d_smp;
+  PassOpts o;
+  o.pos_host = pos_host;
+  layer_stack(m, s, sd->inp, 1, 1, 0, &sd->len, kv->k, kv->v, kv->maxT,
+              (int64_t)kv->maxT * m->d.kvd(), kv->d_part, m->ws.logits, o);
+  timed(m, s, FG_K_OTHER, 0, (double)m->d.V * 4, [&] {
+    launch_sample_step(s, sd, m->ws.logits, m->d.V, kv->d_sids);
+  });
+}
+
+int32_t sample_steps(fg_model* m, fg_kv* kv, int steps, int pos_host) {
+  hipStream_t s = m->stream;
+  if (m->timing) {
+    for (int r = 0; r < steps; ++r) sample_step_launches(m, kv, s, pos_host + r);
+    return FG_OK;
+  }
+  const auto key = std::make_pair(steps, 200);
+  auto it = kv->graphs.find(key);
+  if (it == kv->graphs.end()) {
+    hipGraph_t g = nullptr;
+    HIPCHK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    for (int r = 0; r < steps; ++r) sample_step_launches(m, kv, s, -1);
+    HIPCHK(hipStreamEndCapture(s, &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return seterr(FG_EHIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    it = kv->graphs.emplace(key, ge).first;
+  }
+  HIPCHK(hipGraphLaunch(it->second, s));
+  return FG_OK;
+}
+
+}  // namespace
+
+// The plain decode loop of src/app/chat_text.f90:423-462 with sample_next:
+// one cached step per id, each id drawn from that step's logits with the
+// ids generated so far as the penalty history, on the device. Captured runs
+// of steps are replayed; every step commits one id, so the runs add up to
+// exactly n_total - n_known steps.
+extern "C" int32_t fg_decode_sample(fg_model* m, fg_kv* kv, int32_t* ids, int32_t n_known,
+                                    int32_t n_total, const fg_sample_cfg* cfg, int64_t* state) {
+  if (!m || !kv || !ids || !state || kv->m != m) return seterr(FG_EARG, "bad argument");
+  if (kv->B != 1) return seterr(FG_EARG, "sampled decoding runs one sequence (B=1), not %d", kv->B);
+  SampleCfg c;
+  RCCHK(check_sample_cfg(cfg, m->d.V, &c));
+  if (n_known < 1 || n_total < n_known)
+    return seterr(FG_EARG, "need 1 <= n_known (%d) <= n_total (%d)", n_known, n_total);
+  if (kv->len != n_known - 1)
+    return seterr(FG_EARG, "cache holds %d positions, expected n_known-1 = %d", kv->len,
+                  n_known - 1);
+  if (n_total > kv->maxT)
+    return seterr(FG_EFULL, "cache full (raise maxT): n_total %d > %d", n_total, kv->maxT);
+  RCCHK(check_ids(m, ids, n_known));
+  GUARD(m);
+  if (n_total == n_known) return FG_OK;
+  RCCHK(check_rope(m, n_total));
+  RCCHK(ensure_work(m, 1));
+  if (!kv->d_sids) HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
+  if (!kv->d_smp) {
+    HIPCHK(hipMalloc((void**)&kv->d_smp, sizeof(SampleDev)));
+    HIPCHK(hipHostMalloc((void**)&kv->h_smp, sizeof(SampleDev), hipHostMallocDefault));
+  }
+  if (kv->graphs_gen != m->gen) {
+    for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
+    kv->graphs.clear();
+    kv->graphs_gen = m->gen;
+  }
+  SampleDev* h = kv->h_smp;
+  memset(h, 0, sizeof *h);
+  h->pp = n_known;
+  h->n_total = n_total;
+  h->len = n_known - 1;
+  h->n_known = n_known;
+  h->rng = *state;
+  h->inp[0] = ids[n_known - 1];
+  h->cfg = c;
+  hipStream_t s = m->stream;
+  HIPCHK(hipMemcpyAsync(kv->d_sids, ids, (size_t)n_known * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(kv->d_smp, h, sizeof *h, hipMemcpyHostToDevice, s));
+  int done = 0;
+  const int total = n_total - n_known;
+  while (done < total) {
+    int run = 32;
+    while (run > total - done) run >>= 1;
+    const int32_t rc = sample_steps(m, kv, run, n_known - 1 + done);
+    if (rc != FG_OK) {
+      (void)hipStreamSynchronize(s);
+      kv->len = n_known - 1;
+      return rc;
+    }
+    done += run;
+  }
+  HIPCHK(hipMemcpyAsync(h, kv->d_smp, sizeof *h, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipMemcpyAsync(ids + n_known, kv->d_sids + n_known, (size_t)total * 4,
+                        hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  if (h->pp != n_total) return seterr(FG_EHIP, "sampling loop ended at %d of %d", h->pp, n_total);
+  *state = h->rng;
+  kv->len = n_total - 1;
   return FG_OK;
 }
 

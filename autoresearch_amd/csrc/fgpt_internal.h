@@ -233,4 +233,22 @@ struct SpecDev {
 void launch_spec_draft(hipStream_t s, SpecDev* st, const int32_t* ids);
 void launch_spec_commit(hipStream_t s, SpecDev* st, const float* logits, int V, int32_t* ids);
 
+// ---- token sampling (kern_sample.hip): sample_next of src/lib/sample.f90
+struct SampleCfg {
+  float temp, topp, pres, freq, rep, plen;
+  int32_t pwin, nblock, byte_space;
+};
+constexpr int SAMPLE_MAX_V = 8192;  // the row, its sort keys and sums sit in LDS
+// Device state of the sampling loop for one sequence (ids in a device array):
+// each step samples ids[pp] from the pass over ids[pp-1] = inp[0].
+struct SampleDev {
+  int32_t pp, n_total, len, n_known;
+  int64_t rng;
+  int32_t inp[2];
+  SampleCfg cfg;
+};
+void launch_sample_one(hipStream_t s, const float* logits, int V, const int32_t* gen, int ngen,
+                       const SampleCfg& c, int64_t* state, int32_t* out);
+void launch_sample_step(hipStream_t s, SampleDev* sd, const float* logits, int V, int32_t* ids);
+
 }  // namespace fgpt

@@ -34,6 +34,7 @@ EXPORTS = (
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
     "fg_eval_bpb", "fg_rows_npy", "fg_decode_spec", "fg_spec_accept", "fg_spec_draft",
+    "fg_sample", "fg_decode_sample",
 )
 
 KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other"}
@@ -63,6 +64,18 @@ class _SpecCfg(C.Structure):
 class _SpecStats(C.Structure):
     _fields_ = [("passes", C.c_int64), ("accepted", C.c_int64), ("proposed", C.c_int64),
                 ("plain", C.c_int64), ("pauses", C.c_int64)]
+
+
+class _SampleCfg(C.Structure):
+    _fields_ = [("temp", C.c_float), ("topp", C.c_float), ("pres", C.c_float),
+                ("freq", C.c_float), ("rep", C.c_float), ("plen", C.c_float),
+                ("pwin", C.c_int32), ("nblock", C.c_int32), ("byte_space", C.c_int32)]
+
+
+def sample_cfg(temp=0.0, topp=1.0, pres=0.0, freq=0.0, rep=1.0, plen=0.0, pwin=0, nblock=0,
+               byte_space=False) -> _SampleCfg:
+    """chat_text's sampling options (defaults as its command line has them)."""
+    return _SampleCfg(temp, topp, pres, freq, rep, plen, pwin, nblock, 1 if byte_space else 0)
 
 
 _f = C.POINTER(C.c_float)
@@ -108,6 +121,9 @@ def load_library(path: str = LIB_PATH):
                                  C.POINTER(_SpecStats)]),
         "fg_spec_accept": (i32, [_i, _i, i32, _i, _i]),
         "fg_spec_draft": (i32, [_i, i32, i32, i32, _i, _i]),
+        "fg_sample": (i32, [_vp, _f, i32, _i, i32, C.POINTER(_SampleCfg), C.POINTER(i64), _i]),
+        "fg_decode_sample": (i32, [_vp, _vp, _i, i32, i32, C.POINTER(_SampleCfg),
+                                   C.POINTER(i64)]),
         "fg_timing_read": (i32, [_vp, i32, C.POINTER(i64), C.POINTER(C.c_double),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
@@ -239,6 +255,17 @@ class Model:
             out[name] = (n.value, ms.value, fl.value, by.value)
         return out
 
+    def sample(self, logits, gen=(), state: int = 12345, **cfg):
+        """fg_sample (sample_next) on one row of logits: (id, new state)."""
+        lg = _f32(logits).reshape(-1)
+        g = _i32(np.asarray(gen, dtype=np.int32)).reshape(-1)
+        st = C.c_int64(state)
+        out = C.c_int32()
+        c = sample_cfg(**cfg)
+        _check(_LIB.fg_sample(self._h, _fp(lg), lg.size, _ip(g) if g.size else None, g.size,
+                              C.byref(c), C.byref(st), C.byref(out)))
+        return out.value, st.value
+
     def kv(self, B: int, maxT: int) -> "KV":
         return KV(self, B, maxT)
 
@@ -317,6 +344,23 @@ class KV:
                                    C.byref(cfg), C.byref(st)))
         stats = {f: getattr(st, f) for f, _ in _SpecStats._fields_}
         return ids[prompt.size:], stats
+
+    def decode_sample(self, prompt, n_gen: int, seed: int = 12345, **cfg):
+        """fg_decode_sample: chat_text's plain loop with sample_next after
+        `prompt` (its first len-1 ids already cached, B = 1). Returns the
+        n_gen ids and the generator state after them."""
+        return _decode_sample(self, prompt, n_gen, seed, cfg)
+
+
+def _decode_sample(kv, prompt, n_gen, seed, cfg):
+    prompt = _i32(prompt).reshape(-1)
+    ids = np.zeros(prompt.size + n_gen, np.int32)
+    ids[:prompt.size] = prompt
+    st = C.c_int64(seed)
+    c = sample_cfg(**cfg)
+    _check(_LIB.fg_decode_sample(kv.m.handle, kv._h, _ip(ids), prompt.size, ids.size,
+                                 C.byref(c), C.byref(st)))
+    return ids[prompt.size:], st.value
 
 
 def spec_accept(draft, targmax):

@@ -201,6 +201,39 @@ int32_t fg_spec_accept(const int32_t *draft, const int32_t *targmax, int32_t k,
 int32_t fg_spec_draft(const int32_t *ids, int32_t p, int32_t m, int32_t k, int32_t *draft,
                       int32_t *n_draft);
 
+/* Token sampling, sample_next of src/lib/sample.f90:153-233 with
+ * chat_text's options (src/app/chat_text.f90:118-128): presence/frequency
+ * penalties over the ids generated so far, or over the last pwin of them
+ * with a length penalty on id 0; the repetition penalty; the no-repeat
+ * n-gram ban; the byte-level mask; then argmax (temp <= 0) or a nucleus draw
+ * from softmax(logits / temp) with the xorshift64* generator
+ * (sample.f90:15-28). Vocabularies up to 8192 ids. */
+typedef struct fg_sample_cfg {
+  float temp;         /* <= 0: first-max argmax, no draw (--temp)             */
+  float topp;         /* nucleus mass; >= 1 keeps every id (--topp)           */
+  float pres, freq;   /* presence and frequency penalties (--pres, --freq)    */
+  float rep;          /* repetition penalty, active above 1 (--rep)           */
+  float plen;         /* length penalty on id 0 within the window (--plen)    */
+  int32_t pwin;       /* > 0: penalties over the last pwin ids only (--pwin)  */
+  int32_t nblock;     /* >= 2: ban ids completing a seen n-gram (--nblock)    */
+  int32_t byte_space; /* nonzero: only ids 0..127 and 256..511 (--space byte) */
+} fg_sample_cfg;
+
+/* sample_next on the device for one host row logits[0:V]: gen[0:ngen] the
+ * ids generated so far, *state the generator state (int64, advanced in
+ * place only when a draw is made), *id the 0-based id. */
+int32_t fg_sample(fg_model *m, const float *logits, int32_t V, const int32_t *gen, int32_t ngen,
+                  const fg_sample_cfg *cfg, int64_t *state, int32_t *id);
+
+/* The plain decode loop of src/app/chat_text.f90:423-462 with sample_next,
+ * on the device: ids holds n_total slots, ids[0:n_known] known, the cache
+ * (B = 1) holds n_known-1 positions; fills ids[n_known:n_total] (history
+ * for the penalties = the ids generated in this call), advances *state,
+ * leaves n_total-1 positions cached. With temp <= 0 and no penalties it is
+ * fg_decode_greedy's stream. */
+int32_t fg_decode_sample(fg_model *m, fg_kv *kv, int32_t *ids, int32_t n_known, int32_t n_total,
+                         const fg_sample_cfg *cfg, int64_t *state);
+
 /* Block until the handle's queued work is done. */
 int32_t fg_sync(fg_model *m);
 
