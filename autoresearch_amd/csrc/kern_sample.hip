@@ -198,22 +198,36 @@ __device__ int sample_row(const float* __restrict__ logits, int V, int np2,
     }
   }
   __syncthreads();
-  // descending probability, ties by id: bitonic network over np2 entries
+  // descending probability, ties by id: bitonic network over np2 entries.
+  // A stage's np2/2 compare-exchange pairs are disjoint; each thread loads
+  // all of its pairs before it writes any (one LDS round trip per stage).
+  constexpr int PPT = SAMPLE_MAX_V / 2 / ST;  // pairs per thread, at most
+  const int npairs = np2 >> 1;
   for (int k = 2; k <= np2; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = tid; i < np2; i += ST) {
-        const int p = i ^ j;
-        if (p > i) {
-          const float a = pr[i], b = pr[p];
-          const int ia = ox[i], ib = ox[p];
-          const bool b_first = b > a || (b == a && ib < ia);
-          const bool a_first = a > b || (a == b && ia < ib);
-          if ((i & k) == 0 ? b_first : a_first) {
-            pr[i] = b;
-            pr[p] = a;
-            ox[i] = ib;
-            ox[p] = ia;
-          }
+      float a[PPT], b[PPT];
+      int ia[PPT], ib[PPT], lo[PPT];
+#pragma unroll
+      for (int r = 0; r < PPT; ++r) {
+        const int q = tid + r * ST;
+        lo[r] = q < npairs ? (q / j) * 2 * j + q % j : -1;
+        if (lo[r] >= 0) {
+          a[r] = pr[lo[r]];
+          b[r] = pr[lo[r] + j];
+          ia[r] = ox[lo[r]];
+          ib[r] = ox[lo[r] + j];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < PPT; ++r) {
+        if (lo[r] < 0) continue;
+        const bool b_first = b[r] > a[r] || (b[r] == a[r] && ib[r] < ia[r]);
+        const bool a_first = a[r] > b[r] || (a[r] == b[r] && ia[r] < ib[r]);
+        if ((lo[r] & k) == 0 ? b_first : a_first) {
+          pr[lo[r]] = b[r];
+          pr[lo[r] + j] = a[r];
+          ox[lo[r]] = ib[r];
+          ox[lo[r] + j] = ia[r];
         }
       }
       __syncthreads();

@@ -28,11 +28,19 @@ module fgpt_c
     integer(c_int64_t) :: passes, accepted, proposed, plain, pauses
   end type fg_spec_stats
 
+  ! --temp --topp --pres --freq --rep --plen --pwin --nblock --space byte
+  ! (src/app/chat_text.f90:118-128)
+  type, bind(C), public :: fg_sample_cfg
+    real(c_float) :: temp, topp, pres, freq, rep, plen
+    integer(c_int32_t) :: pwin, nblock, byte_space
+  end type fg_sample_cfg
+
   public :: fg_version, fg_last_error, fg_model_create, fg_weights_read, fg_model_load, &
       fg_model_destroy, &
       fg_set_rope, fg_forward, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
       fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_eval_bpb, fg_rows_npy, &
-      fg_decode_spec, fg_spec_accept, fg_spec_draft, fg_error_message
+      fg_decode_spec, fg_spec_accept, fg_spec_draft, fg_sample, fg_decode_sample, &
+      fg_error_message
 
   interface
     integer(c_int32_t) function fg_version() bind(C, name="fg_version")
@@ -163,6 +171,28 @@ module fgpt_c
       integer(c_int32_t), value :: n_known, n_total
       type(fg_spec_cfg), intent(in) :: cfg
       type(fg_spec_stats), intent(out) :: stats
+    end function
+
+    integer(c_int32_t) function fg_sample(m, logits, V, gen, ngen, cfg, state, id) &
+        bind(C, name="fg_sample")
+      import :: c_int32_t, c_int64_t, c_float, c_ptr, fg_sample_cfg
+      type(c_ptr), value :: m
+      real(c_float), intent(in) :: logits(*)
+      integer(c_int32_t), value :: V, ngen
+      integer(c_int32_t), intent(in) :: gen(*)
+      type(fg_sample_cfg), intent(in) :: cfg
+      integer(c_int64_t), intent(inout) :: state
+      integer(c_int32_t), intent(out) :: id
+    end function
+
+    integer(c_int32_t) function fg_decode_sample(m, kv, ids, n_known, n_total, cfg, state) &
+        bind(C, name="fg_decode_sample")
+      import :: c_int32_t, c_int64_t, c_ptr, fg_sample_cfg
+      type(c_ptr), value :: m, kv
+      integer(c_int32_t), intent(inout) :: ids(*)
+      integer(c_int32_t), value :: n_known, n_total
+      type(fg_sample_cfg), intent(in) :: cfg
+      integer(c_int64_t), intent(inout) :: state
     end function
 
     integer(c_int32_t) function fg_spec_accept(draft, targmax, k, n_accept, correction) &

@@ -25,7 +25,7 @@ module fgpt_drop_in_mod
   implicit none
   private
   public :: gpt_forward, gpt_step, gpt_step_multi, load_gpt_weights, fgpt_release, &
-      fgpt_handles, accept_prefix, lookup_draft
+      fgpt_handles, accept_prefix, lookup_draft, sample_next
 
   type(c_ptr), save :: g_model = c_null_ptr
   type(c_ptr), save :: g_kv = c_null_ptr
@@ -278,5 +278,34 @@ contains
     kk = n
     if (kk > 0) d(1:kk) = o(1:kk)
   end subroutine lookup_draft
+
+  ! sample_next (src/lib/sample.f90:153-177): the 1-based position of the
+  ! sampled token, drawn on the device of the bound model (the model a
+  ! gpt_forward / gpt_step / gpt_step_multi call has bound). state is the
+  ! caller's xorshift64* state, advanced as the reference advances it.
+  integer function sample_next(logits, V, temp, topp, pres, freq, rep, pwin, plen, gen, ngen, &
+      nblock, state, byte_space)
+    integer, intent(in) :: V, ngen, nblock, pwin
+    real(c_float), intent(in) :: logits(:), temp, topp, pres, freq, rep, plen
+    integer, intent(in) :: gen(:)
+    integer(c_int64_t), intent(inout) :: state
+    logical, intent(in), optional :: byte_space
+    type(fg_sample_cfg) :: cfg
+    integer(c_int32_t) :: g(max(ngen, 1)), id, rc
+
+    if (.not. c_associated(g_model)) then
+      write (error_unit, '(A)') 'sample_next: no model bound (call gpt_step or gpt_forward first)'
+      error stop 1
+    end if
+    cfg = fg_sample_cfg(temp, topp, pres, freq, rep, plen, int(pwin, c_int32_t), &
+        int(nblock, c_int32_t), 0_c_int32_t)
+    if (present(byte_space)) then
+      if (byte_space) cfg%byte_space = 1
+    end if
+    if (ngen > 0) g(1:ngen) = int(gen(1:ngen), c_int32_t)
+    rc = fg_sample(g_model, logits, int(V, c_int32_t), g, int(ngen, c_int32_t), cfg, state, id)
+    if (rc /= FG_OK) call die('fg_sample', rc)
+    sample_next = id + 1
+  end function sample_next
 
 end module fgpt_drop_in_mod

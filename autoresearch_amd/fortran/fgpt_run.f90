@@ -23,6 +23,10 @@
 !            verification pass per round, the sliding-window controller),
 !            checked against a plain greedy run on a second cache as
 !            src/app/spec_bench.f90 does; prints its summary lines.
+!   sample   chat_text's plain loop with sample_next (src/app/chat_text.f90:
+!            423-462, src/lib/sample.f90:153-233): loop=host steps through the
+!            drop-in gpt_step and sample_next, loop=device is one
+!            fg_decode_sample call; the history is the ids generated so far.
 !   spectest the accept rule and the drafter through the drop-in names, on
 !            the known answers of src/test/test_kernels.f90:1556-1650 (host
 !            only).
@@ -34,6 +38,8 @@
 !   fgpt_run selftest
 !   fgpt_run spec   WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [K] [MATCH] [PROBE] [MIN_ACC]
 !   fgpt_run spectest
+!   fgpt_run sample WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE TEMP TOPP SEED
+!                   [PRES FREQ REP PWIN PLEN NBLOCK BYTE(0|1) [host|device]]
 ! Ids files are whitespace-separated 0-based integers. Timing goes to stderr.
 program fgpt_run
   use, intrinsic :: iso_c_binding
@@ -61,6 +67,8 @@ program fgpt_run
     call run_spec()
   case ('spectest')
     call run_spectest()
+  case ('sample')
+    call run_sample()
   case default
     call usage()
   end select
@@ -74,6 +82,8 @@ contains
     write (error_unit, '(A)') '       fgpt_run selftest'
     write (error_unit, '(A)') '       fgpt_run spec WDIR L D H KH HD V IDS NGEN OUT [K] [MATCH] [PROBE] [MIN_ACC]'
     write (error_unit, '(A)') '       fgpt_run spectest'
+    write (error_unit, '(A)') '       fgpt_run sample WDIR L D H KH HD V IDS NGEN OUT TEMP TOPP SEED ' // &
+        '[PRES FREQ REP PWIN PLEN NBLOCK BYTE [host|device]]'
     stop 2
   end subroutine usage
 
@@ -541,6 +551,89 @@ contains
       end do
     end subroutine prefill
   end subroutine run_spec
+
+  subroutine run_sample()
+    character(len=512) :: wdir, ids_file, out_file, loop
+    integer :: L, D, H, KH, HD, V, ngen, nprompt, ntot, srow, tb, u, i, pwin, nblock, tc
+    integer(c_int) :: clen
+    integer(c_int32_t) :: rc
+    integer(c_int64_t) :: rng
+    real(c_float) :: temp, topp, pres, freq, rep, plen
+    logical :: bytes
+    real(c_float), allocatable :: wte(:), lm(:), c_q(:), c_k(:), c_v(:), c_pr(:), c_fc(:), c_pr2(:)
+    real(c_float), allocatable :: cos_b(:), sin_b(:), out1(:), outc(:), ck(:), cv(:)
+    integer(c_int), allocatable :: prompt(:), idx(:)
+    type(c_ptr) :: model, kv
+    type(fg_sample_cfg) :: cfg
+    real(8) :: t0, t1
+
+    if (command_argument_count() < 14) call usage()
+    wdir = sarg(2); L = iarg(3); D = iarg(4); H = iarg(5); KH = iarg(6); HD = iarg(7); V = iarg(8)
+    ids_file = sarg(9); ngen = iarg(10); out_file = sarg(11)
+    temp = real(rarg(12), c_float); topp = real(rarg(13), c_float)
+    rng = int(iarg(14), c_int64_t)
+    pres = 0; freq = 0; rep = 1; pwin = 0; plen = 0; nblock = 0; bytes = .false.; loop = 'host'
+    if (command_argument_count() >= 20) then
+      pres = real(rarg(15), c_float); freq = real(rarg(16), c_float); rep = real(rarg(17), c_float)
+      pwin = iarg(18); plen = real(rarg(19), c_float); nblock = iarg(20)
+    end if
+    if (command_argument_count() >= 21) bytes = iarg(21) /= 0
+    if (command_argument_count() >= 22) loop = sarg(22)
+
+    call load_gpt_weights(trim(wdir), L, D, H, KH, HD, V, wte, lm, c_q, c_k, c_v, c_pr, c_fc, c_pr2)
+    call read_ids(trim(ids_file), prompt, nprompt)
+    if (nprompt < 1) then
+      write (error_unit, '(A)') 'empty prompt'
+      stop 1
+    end if
+    ntot = nprompt + ngen
+    allocate (idx(ntot), out1(V), ck(1), cv(1))
+    idx(1:nprompt) = prompt(1:nprompt)
+    call rope_tables(ntot, HD, cos_b, sin_b)
+    clen = 0
+    if (nprompt > 1) then
+      allocate (outc(max(1, min(64, nprompt - 1))*V))
+      srow = 1
+      do while (srow <= nprompt - 1)
+        tb = min(64, nprompt - srow)
+        call gpt_step_multi(idx(srow:srow+tb-1), cos_b((srow-1)*(HD/2)+1:), &
+            sin_b((srow-1)*(HD/2)+1:), wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, &
+            ck, cv, clen, ntot, outc, 1, V, D, H, KH, HD, L, tb, 1.0e-5_c_float)
+        srow = srow + tb
+      end do
+    end if
+    t0 = now()
+    if (trim(loop) == 'device') then
+      if (nprompt < 2) then
+        write (error_unit, '(A)') 'loop=device needs a prompt of two ids or more'
+        stop 2
+      end if
+      call fgpt_handles(model, kv)
+      call set_rope_rows(model, 0, ntot, HD, cos_b, sin_b)
+      cfg = fg_sample_cfg(temp, topp, pres, freq, rep, plen, int(pwin, c_int32_t), &
+          int(nblock, c_int32_t), merge(1_c_int32_t, 0_c_int32_t, bytes))
+      rc = fg_decode_sample(model, kv, idx, int(nprompt, c_int32_t), int(ntot, c_int32_t), cfg, rng)
+      if (rc /= FG_OK) call stop_rc('fg_decode_sample', rc)
+    else
+      do tc = nprompt, ntot - 1
+        call gpt_step(idx(tc:tc), cos_b((tc-1)*(HD/2)+1:), sin_b((tc-1)*(HD/2)+1:), &
+            wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, ck, cv, clen, ntot, out1, &
+            1, V, D, H, KH, HD, L, 1.0e-5_c_float)
+        idx(tc + 1) = sample_next(out1, V, temp, topp, pres, freq, rep, pwin, plen, &
+            idx(nprompt+1:), tc - nprompt, nblock, rng, byte_space=bytes) - 1
+      end do
+    end if
+    t1 = now()
+    open (newunit=u, file=trim(out_file), status='replace', action='write')
+    do i = nprompt + 1, ntot
+      write (u, '(I0)') idx(i)
+    end do
+    close (u)
+    write (*, '(A,I0)') 'rng_state=', rng
+    write (error_unit, '(A,F10.3,A,F12.1,2A)') 'stats: decode_ms=', 1000*(t1 - t0), &
+        ' tok_s=', real(ngen, 8)/max(t1 - t0, 1d-9), ' loop=', trim(loop)
+    call fgpt_release()
+  end subroutine run_sample
 
   ! The reference's accept_prefix and lookup_draft known answers, through
   ! the drop-in subroutines of the same names (host only).

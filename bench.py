@@ -177,6 +177,41 @@ def bench_spec(m, d, reps, warmup, k=8, match=2, probe=8, min_acc=0.5):
             "stats": st, "streams_equal": True}
 
 
+def bench_sample(m, d, reps, warmup, n_gen=256):
+    """chat_text's plain loop with sample_next on the device (fg_decode_sample:
+    temp 0.8, top-p 0.9, presence 0.2, frequency 0.1, repetition 1.1, no-repeat
+    3-grams) after a 16-id prompt, beside plain greedy decoding; tok/s of
+    each and the sampling kernel's share from an eager timing pass."""
+    from autoresearch_amd.weights import uniform_ids
+    cfg = dict(temp=0.8, topp=0.9, pres=0.2, freq=0.1, rep=1.1, nblock=3)
+    prompt = uniform_ids(91, 16, d.vocab)
+    kv = m.kv(1, prompt.size + n_gen)
+    kv.step_multi(prompt[:-1], want_logits=False)
+    L0 = prompt.size - 1
+
+    def timed(fn):
+        for _ in range(warmup):
+            kv.len = L0
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            kv.len = L0
+            out = fn()
+        return out, (time.perf_counter() - t0) / reps
+
+    _, t_g = timed(lambda: kv.decode_greedy(prompt[-1:], n_gen))
+    (ids, _), t_s = timed(lambda: kv.decode_sample(prompt, n_gen, seed=12345, **cfg))
+    m.timing(True)
+    kv.len = L0
+    kv.decode_sample(prompt, n_gen, seed=12345, **cfg)
+    tm = m.timing_read()
+    m.timing(False)
+    kv.close()
+    return {"prompt": int(prompt.size), "gen": n_gen, "cfg": cfg, "greedy_tok_s": n_gen / t_g,
+            "sample_tok_s": n_gen / t_s, "first_ids": ids[:8].tolist(),
+            "kernel_ms_per_step": {k: v[1] / n_gen for k, v in tm.items()}}
+
+
 # --- HBM traffic of the dominant prefill kernel kind, from PMC counters ---
 PMC_KIND = "gemm"                 # kernel kind the prefill roofline is quoted on
 PMC_MATCH = ("k_gemm",)           # kernel-name fragments of that kind
@@ -293,7 +328,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b64", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "decode_b1", "decode_b64", "decode_spec"),
+    ap.add_argument("--only", choices=("prefill", "decode_b1", "decode_b64", "decode_spec",
+                                       "decode_sample"),
                     help="run one workload and print its record (for profiling runs)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the PMC traffic runs")
     ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
@@ -330,7 +366,8 @@ def main():
                "decode_b1": lambda: bench_decode(m, d, 1, 16, 32, reps=max(args.steps, 5),
                                                  warmup=args.warmup),
                "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0),
-               "decode_spec": lambda: bench_spec(m, d, reps=3, warmup=1)}[args.only]()
+               "decode_spec": lambda: bench_spec(m, d, reps=3, warmup=1),
+               "decode_sample": lambda: bench_sample(m, d, reps=3, warmup=1)}[args.only]()
         print(json.dumps({"only": args.only, **rec}), flush=True)
         return
 
@@ -348,6 +385,9 @@ def main():
     log("bench: speculative decode B=1")
     spec = bench_spec(m, d, reps=3, warmup=1)
     log("bench: decode spec", json.dumps(spec))
+    log("bench: sampled decode B=1")
+    samp = bench_sample(m, d, reps=3, warmup=1)
+    log("bench: decode sample", json.dumps(samp))
     cpu = None
     if not args.no_cpu:
         log("bench: CPU oracle baseline")
@@ -372,6 +412,7 @@ def main():
         "decode_b1": dec1,
         "decode_b64": dec64,
         "decode_spec": spec,
+        "decode_sample": samp,
     }
     print(json.dumps(line), flush=True)
 

@@ -209,3 +209,32 @@ def test_fortran_spec_equals_greedy(tmp_path):
     assert "passes=" in r.stdout
     got = np.loadtxt(tmp_path / "o.txt", dtype=np.int32).reshape(-1)
     assert np.array_equal(got, oracle_greedy(d, w, prompt, ngen))
+
+
+@pytest.mark.gpu
+def test_fortran_sample_host_loop_equals_device_loop(tmp_path):
+    """chat_text's plain loop with sample_next: stepping through the drop-in
+    gpt_step + sample_next gives the same ids and generator state as one
+    fg_decode_sample call; temp 0 gives the oracle's greedy ids."""
+    d = SMALL
+    w = seeded_weights(d, 29)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=96)
+    prompt = uniform_ids(43, 9, d.vocab)
+    np.savetxt(tmp_path / "p.txt", prompt, fmt="%d")
+    ngen = 40
+    outs = {}
+    for loop in ("host", "device"):
+        r = run(["sample", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "p.txt"), str(ngen),
+                 str(tmp_path / f"o_{loop}.txt"), "0.9", "0.92", "777", "0.3", "0.1", "1.15", "12",
+                 "0.5", "3", "0", loop])
+        print(r.stdout, r.stderr)
+        assert r.returncode == 0, r.stderr
+        outs[loop] = (np.loadtxt(tmp_path / f"o_{loop}.txt", dtype=np.int32),
+                      r.stdout.strip().splitlines()[-1])
+    assert np.array_equal(outs["host"][0], outs["device"][0])
+    assert outs["host"][1] == outs["device"][1]  # rng_state=...
+    r = run(["sample", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "p.txt"), str(ngen),
+             str(tmp_path / "g.txt"), "0", "1", "1", "0", "0", "1", "0", "0", "0", "0", "device"])
+    assert r.returncode == 0, r.stderr
+    got = np.loadtxt(tmp_path / "g.txt", dtype=np.int32)
+    assert np.array_equal(got, oracle_greedy(d, w, prompt, ngen))
