@@ -22,16 +22,51 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t* p, int64_t plane) 
   p[plane] = f32_to_bf16_rne(v - bf16_to_f32(h));
 }
 
-__device__ __forceinline__ void qkv_pair_epilogue(const GemvArgs& a, int m, int pos0, int r,
-                                                  float x1, float x2) {
+// The same for two adjacent values as one 32-bit store per plane (p even).
+__device__ __forceinline__ void split_bf16x2(float v0, float v1, uint16_t* p, int64_t plane) {
+  const uint16_t h0 = f32_to_bf16_rne(v0), h1 = f32_to_bf16_rne(v1);
+  const uint16_t l0 = f32_to_bf16_rne(v0 - bf16_to_f32(h0));
+  const uint16_t l1 = f32_to_bf16_rne(v1 - bf16_to_f32(h1));
+  *reinterpret_cast<uint32_t*>(p) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+  *reinterpret_cast<uint32_t*>(p + plane) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+}
+
+// The same for four adjacent values as one 64-bit store per plane (p a
+// multiple of 4 elements).
+__device__ __forceinline__ void split_bf16x4(const float (&v)[4], uint16_t* p, int64_t plane) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t hb = f32_to_bf16_rne(v[i]);
+    h[i] = hb;
+    l[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(hb));
+  }
+  *reinterpret_cast<uint2*>(p) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  *reinterpret_cast<uint2*>(p + plane) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+}
+
+// RoPE coefficients of stored column pair r for token row m (q and k
+// columns; v columns take none).
+__device__ __forceinline__ void qkv_pair_coeffs(const GemvArgs& a, int m, int pos0, int r,
+                                                float& cs, float& sn) {
+  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
+  if (r < qd + kd) {
+    const int base = r < qd ? r : r - qd;
+    const int64_t at = (int64_t)(pos0 + m % a.T) * (hd / 2) + ((base % hd) >> 1);
+    cs = a.cosb[at];
+    sn = a.sinb[at];
+  }
+}
+
+// qkv_pair_epilogue with the pair's RoPE coefficients already loaded.
+__device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos0, int r,
+                                               float x1, float x2, float cs, float sn) {
   const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
   const int b = m / a.T, t = m % a.T, pos = pos0 + t;
   if (r < qd + kd) {
     const bool isq = r < qd;
     const int base = isq ? r : r - qd;
     const int head = base / hd, j = (base % hd) >> 1;
-    const float cs = a.cosb[(int64_t)pos * (hd / 2) + j];
-    const float sn = a.sinb[(int64_t)pos * (hd / 2) + j];
     const float y1 = x1 * cs + x2 * sn;
     const float y2 = x1 * (-sn) + x2 * cs;
     if (isq) {
@@ -70,6 +105,75 @@ __device__ __forceinline__ void qkv_pair_epilogue(const GemvArgs& a, int m, int 
       split_bf16(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
     }
   }
+}
+
+// Four rotation pairs at stored columns r8 .. r8+7 (r8 % 8 == 0, so one
+// head and dims j .. j+3 with j % 4 == 0) of token row m, x the eight
+// values, cs/sn the four pairs' RoPE coefficients: the arithmetic of
+// qkv_pair_store, with each plane's four dims written by one wide store.
+__device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos0, int r8,
+                                               const float (&x)[8], const float4& cs,
+                                               const float4& sn) {
+  const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
+  const int b = m / a.T, t = m % a.T, pos = pos0 + t;
+  const float c[4] = {cs.x, cs.y, cs.z, cs.w}, s[4] = {sn.x, sn.y, sn.z, sn.w};
+  float y1[4], y2[4];
+  if (r8 < qd + kd) {
+    const bool isq = r8 < qd;
+    const int base = isq ? r8 : r8 - qd;
+    const int head = base / hd, j = (base % hd) >> 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x1 = x[2 * i], x2 = x[2 * i + 1];
+      y1[i] = x1 * c[i] + x2 * s[i];
+      y2[i] = x1 * (-s[i]) + x2 * c[i];
+    }
+    if (isq) {
+      if (a.qs) {
+        uint16_t* p = a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd;
+        split_bf16x4(y1, p + j, a.q_plane);
+        split_bf16x4(y2, p + j + hd / 2, a.q_plane);
+      } else {
+        float* q = a.y + (int64_t)m * qd + head * hd;
+        *reinterpret_cast<float4*>(q + j) = make_float4(y1[0], y1[1], y1[2], y1[3]);
+        *reinterpret_cast<float4*>(q + j + hd / 2) = make_float4(y2[0], y2[1], y2[2], y2[3]);
+      }
+    } else {
+      if (a.kc) {
+        float* k = a.kc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
+        *reinterpret_cast<float4*>(k + j) = make_float4(y1[0], y1[1], y1[2], y1[3]);
+        *reinterpret_cast<float4*>(k + j + hd / 2) = make_float4(y2[0], y2[1], y2[2], y2[3]);
+      }
+      if (a.ks) {
+        uint16_t* p = a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd;
+        split_bf16x4(y1, p + j, a.kv_plane);
+        split_bf16x4(y2, p + j + hd / 2, a.kv_plane);
+      }
+    }
+  } else {
+    const int base = r8 - qd - kd;
+    const int head = base / hd, j = (base % hd) >> 1;
+    if (a.vc) {
+      float* v = a.vc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
+      *reinterpret_cast<float4*>(v + j) = make_float4(x[0], x[2], x[4], x[6]);
+      *reinterpret_cast<float4*>(v + j + hd / 2) = make_float4(x[1], x[3], x[5], x[7]);
+    }
+    if (a.vt) {  // (tiles holding v columns normally take the row-fast path)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
+        split_bf16(x[2 * i], p + (int64_t)(j + i) * a.npos, a.kv_plane);
+        split_bf16(x[2 * i + 1], p + (int64_t)(j + i + hd / 2) * a.npos, a.kv_plane);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void qkv_pair_epilogue(const GemvArgs& a, int m, int pos0, int r,
+                                                  float x1, float x2) {
+  float cs = 0.f, sn = 0.f;
+  qkv_pair_coeffs(a, m, pos0, r, cs, sn);
+  qkv_pair_store(a, m, pos0, r, x1, x2, cs, sn);
 }
 
 // One element of a rotation pair, for producers that hold one column per

@@ -38,16 +38,98 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 namespace {
 
 // 16-byte chunk slot of logical chunk c in row r of a stage whose rows hold
-// BK bf16 (BK/8 chunks): rows r and r+1 share a slot pattern, so 16 rows
-// read at one logical chunk spread over the banks
+// BK bf16 (BK/8 chunks). gfx950's LDS has 64 banks (256 bytes a cycle), and
+// a 16-byte read is served 16 lanes at a time: the 16 rows an MFMA operand
+// read touches at one logical chunk must land on 16 different 16-byte bank
+// groups. 128 / BK rows fill 256 bytes, so the XOR pattern changes every
+// 128 / BK rows (every 4 rows of 64 bytes, every 2 rows of 128 bytes).
 template <int BK>
 __device__ __forceinline__ int swz(int r, int c) {
-  return c ^ ((r >> 1) & (BK / 8 - 1));
+  constexpr int S = BK == 32 ? 2 : BK == 64 ? 1 : 0;
+  static_assert(BK == 32 || BK == 64 || BK == 128, "stage row width");
+  return c ^ ((r >> S) & (BK / 8 - 1));
 }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// One 64-row pass of the QKV epilogue from the staged tile (fp32 [64][SSTR],
+// rows m0 + 64 q ..): q/k/v columns in items of four rotation pairs of one
+// row (one wide store per plane and four dims); for tiles holding v columns
+// that go to the transposed layout, items of one pair over four consecutive
+// rows (positions), so v^T gets one wide store per dim. Rows that do not
+// form an aligned run of four positions of one sequence take the per-pair
+// path. Every item's RoPE coefficients are loaded before any item stores.
+template <int BN, int NT>
+__device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* stage,
+                                              const float* sinv, int m0, int n0, int q,
+                                              bool rows_fast, int pos0) {
+  constexpr int SSTR = BN + 4, NI = 8 * BN / NT;  // items per thread (64 * BN / 8 in all)
+  static_assert(NI * NT == 8 * BN, "epilogue items / block size mismatch");
+  const int tid = threadIdx.x, M = a.M, hd = a.hd, qdk = (a.H + a.KH) * hd;
+  if (!rows_fast) {
+    float4 c4[NI], s4[NI];
+#pragma unroll
+    for (int k = 0; k < NI; ++k) {
+      const int e = tid + k * NT, srow = e / (BN / 8), pc = 8 * (e % (BN / 8));
+      const int m = m0 + q * 64 + srow, n = n0 + pc;
+      c4[k] = s4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (m < M && n < qdk) {
+        const int base = n < a.H * hd ? n : n - a.H * hd;
+        const int64_t at = (int64_t)(pos0 + m % a.T) * (hd / 2) + ((base % hd) >> 1);
+        c4[k] = *reinterpret_cast<const float4*>(a.cosb + at);
+        s4[k] = *reinterpret_cast<const float4*>(a.sinb + at);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NI; ++k) {
+      const int e = tid + k * NT, srow = e / (BN / 8), pc = 8 * (e % (BN / 8));
+      const int ml = q * 64 + srow, m = m0 + ml;
+      if (m >= M) continue;
+      const float4 lo = *reinterpret_cast<const float4*>(stage + srow * SSTR + pc);
+      const float4 hi = *reinterpret_cast<const float4*>(stage + srow * SSTR + pc + 4);
+      const float sc = a.norm ? sinv[ml] : 1.f;
+      const float x[8] = {lo.x * sc, lo.y * sc, lo.z * sc, lo.w * sc,
+                          hi.x * sc, hi.y * sc, hi.z * sc, hi.w * sc};
+      qkv_quad_store(a, m, pos0, n0 + pc, x, c4[k], s4[k]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < NI; ++k) {
+    const int e = tid + k * NT, g = e % 16, pc = 2 * (e / 16);
+    const int r0 = 4 * g, n = n0 + pc, mb = m0 + q * 64 + r0;
+    float x1[4], x2[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float sc = a.norm ? sinv[q * 64 + r0 + i] : 1.f;
+      x1[i] = stage[(r0 + i) * SSTR + pc] * sc;
+      x2[i] = stage[(r0 + i) * SSTR + pc + 1] * sc;
+    }
+    const int t0 = mb % a.T, pos = pos0 + t0;
+    const bool run4 = n >= qdk && a.vt && mb + 3 < M && t0 + 3 < a.T && (pos & 3) == 0;
+    if (run4) {
+      const int base = n - qdk, head = base / hd, j = (base % hd) >> 1, b = mb / a.T;
+      uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
+      split_bf16x4(x1, p + (int64_t)j * a.npos, a.kv_plane);
+      split_bf16x4(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
+      if (a.vc) {
+        const int kd = a.KH * hd;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float* v = a.vc + ((int64_t)b * a.maxT + pos + i) * kd + head * hd;
+          v[j] = x1[i];
+          v[j + hd / 2] = x2[i];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (mb + i < M) qkv_pair_epilogue(a, mb + i, pos0, n, x1[i], x2[i]);
+    }
+  }
 }
 
 template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST>
@@ -104,6 +186,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
 
   // epilogue items (column pairs of a 64-row pass) per thread
   constexpr int EPT = 64 * (BN / 2) / NT;
+  static_assert(EPI != GV_RESID || BN == 64 || BN == 128,
+                "the residual epilogue's row sums cover a half or a whole wavefront");
   static_assert(EPT * NT == 64 * (BN / 2), "epilogue pass / block size mismatch");
   // RESID: the residual tile is read now, so its latency hides behind the
   // K loop instead of stalling the epilogue
@@ -217,6 +301,11 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
     __syncthreads();
     // BN/2 consecutive e cover one row; with BN = 128 that is one
     // wavefront, with BN = 64 half of one (reductions stay in the wave)
+    if (EPI == GV_QKV && !a.part) {
+      qkv_tile_pass<BN, NT>(a, stage, sinv, m0, n0, q, rows_fast, pos0);
+      __syncthreads();
+      continue;
+    }
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
       const int e = tid + k * NT;
@@ -245,20 +334,17 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
           o.x += v0;
           o.y += v1;
           *reinterpret_cast<float2*>(y) = o;
-          uint16_t* ys = a.ys + (int64_t)m * a.N + n;
-          split_bf16(o.x, ys, a.ys_plane);
-          split_bf16(o.y, ys + 1, a.ys_plane);
+          split_bf16x2(o.x, o.y, a.ys + (int64_t)m * a.N + n, a.ys_plane);
         }
-        float sq = o.x * o.x + o.y * o.y;
-#pragma unroll
-        for (int off = BN / 4; off > 0; off >>= 1) sq += __shfl_xor(sq, off, 64);
+        // the row's sum of squares over this tile: the row spans the whole
+        // wavefront (BN = 128) or half of it (BN = 64)
+        const float sq0 = o.x * o.x + o.y * o.y;
+        const float sq = BN == 128 ? wave_sum(sq0) : half_sum(sq0);
         if (live && pc == 0) a.ssq_out[(int64_t)m * (a.N / BN) + n0 / BN] = sq;
       } else if (EPI == GV_RELU2) {
         if (live) {
           const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
-          uint16_t* ys = a.ys + (int64_t)m * a.N + n;
-          split_bf16(t0 * t0, ys, a.ys_plane);
-          split_bf16(t1 * t1, ys + 1, a.ys_plane);
+          split_bf16x2(t0 * t0, t1 * t1, a.ys + (int64_t)m * a.N + n, a.ys_plane);
         }
       } else {
         if (live) *reinterpret_cast<float2*>(a.y + (int64_t)m * a.N + n) = make_float2(v0, v1);
@@ -576,15 +662,11 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
       x.x += v0;
       x.y += v1;
       *reinterpret_cast<float2*>(a.y + o) = x;
-      if (a.ys) {
-        split_bf16(x.x, a.ys + o, a.ys_plane);
-        split_bf16(x.y, a.ys + o + 1, a.ys_plane);
-      }
+      if (a.ys) split_bf16x2(x.x, x.y, a.ys + o, a.ys_plane);
       sq = x.x * x.x + x.y * x.y;
     } else if (EPI == GV_RELU2) {
       const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
-      split_bf16(t0 * t0, a.ys + o, a.ys_plane);
-      split_bf16(t1 * t1, a.ys + o + 1, a.ys_plane);
+      split_bf16x2(t0 * t0, t1 * t1, a.ys + o, a.ys_plane);
     } else {
       *reinterpret_cast<float2*>(a.y + o) = make_float2(v0, v1);
     }
@@ -603,6 +685,21 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
 // whose outputs are scattered or need per-row reductions; the register
 // epilogue (k_gemm2) serves the plain stores of RELU2 and lm_head, with
 // 128x256 tiles (wave 64x128) when there are >= 1.5 blocks per CU.
+// Compute units of the current device (tile counts are weighed against it).
+int cu_count() {
+  static int n[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (n[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    n[dev] = v;
+  }
+  return n[dev];
+}
+
 template <int EPI>
 void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   const int sp = a.part ? splitk_count(a.M, a.N, a.K) : 1;
@@ -617,7 +714,19 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   GemvArgs b = a;
   b.part = nullptr;  // the kernels below write the epilogue themselves
   const int64_t mt128 = (a.M + 127) / 128;
-  if (EPI == GV_STORE && a.N % 256 == 0 && mt128 * (a.N / 256) >= 384) {
+  // fc at prefill sizes: where 128x128 tiles spill into a second, mostly
+  // empty round over the CUs, 128x192 tiles fit in one (QKV stays on
+  // 128x128: its epilogue costs more per column in the wider tile)
+  if constexpr (EPI == GV_RELU2) {
+    const int64_t ncu = cu_count();
+    if (a.N % 192 == 0 && a.K % 64 == 0 && mt128 * (a.N / 128) > ncu &&
+        mt128 * (a.N / 192) <= ncu) {
+      launch_cfg<EPI, 128, 192, 4, 2, 64, 2>(s, b, d_pos);
+      return;
+    }
+  }
+  if (a.N % 256 == 0 && ((EPI == GV_STORE && mt128 * (a.N / 256) >= 384) ||
+                         (EPI == GV_RELU2 && mt128 * (a.N / 256) >= 768))) {
     launch_cfg2<EPI, 2, 2, 2, 4, 2>(s, b, d_pos);
     return;
   }
