@@ -91,11 +91,12 @@ __device__ __forceinline__ void split8(const float* v, bf16x8_t& h, bf16x8_t& l)
   }
 }
 
+// four consecutive output dims (d % 4 == 0): fp32, or the bf16 hi/lo planes
+// the next GEMM reads, one 8-byte store per plane
 template <int HD>
-__device__ __forceinline__ void store_out(const AttnArgs& p, int64_t yo, int d, const float* v) {
+__device__ __forceinline__ void store_out(const AttnArgs& p, int64_t yo, int d, const float (&v)[4]) {
   if (p.ys) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) split_bf16(v[e], p.ys + yo + d + e, p.ys_plane);
+    split_bf16x4(v, p.ys + yo + d, p.ys_plane);
   } else {
     *(float4*)(p.y + yo + d) = make_float4(v[0], v[1], v[2], v[3]);
   }

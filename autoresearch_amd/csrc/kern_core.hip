@@ -269,11 +269,9 @@ struct DecArgs {
 
 template <int HD>
 __device__ __forceinline__ void dec_store(const DecArgs& a, int64_t o, int d, float4 v) {
-  if (a.ys) {
-    split_bf16(v.x, a.ys + o + d, a.ys_plane);
-    split_bf16(v.y, a.ys + o + d + 1, a.ys_plane);
-    split_bf16(v.z, a.ys + o + d + 2, a.ys_plane);
-    split_bf16(v.w, a.ys + o + d + 3, a.ys_plane);
+  if (a.ys) {  // d % 4 == 0: one 8-byte store per plane
+    const float w[4] = {v.x, v.y, v.z, v.w};
+    split_bf16x4(w, a.ys + o + d, a.ys_plane);
   } else {
     *(float4*)(a.y + o + d) = v;
   }
