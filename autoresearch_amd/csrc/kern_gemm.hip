@@ -132,18 +132,26 @@ __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* st
   }
 }
 
-template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST>
-__global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
-                                                        const int32_t* __restrict__ d_pos) {
-  constexpr int NW = NWM * NWN, NT = 64 * NW;
+// KG > 1 splits each stage's 16-deep K steps over KG groups of NWM x NWN
+// wavefronts (group g takes steps g, g + KG, ..): a tile too small to give
+// every SIMD two wavefronts of its own still keeps them all busy. The
+// groups' partial sums meet in the LDS staging buffer in a fixed order
+// (KG - 1 first, 0 last), so the result does not depend on timing.
+template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST, int KG = 1>
+__global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
+                                                             const int32_t* __restrict__ d_pos) {
+  constexpr int NWT = NWM * NWN, NW = NWT * KG, NT = 64 * NW;
   constexpr int WM = BM / (32 * NWM), WN = BN / (32 * NWN);  // 32x32 blocks per wave
   // a stage: A hi rows, A lo rows, W rows of RB bytes each, loaded 1 KB
   // (1024 / RB rows) per wavefront instruction
   constexpr int RB = 2 * BK, CPR = BK / 8, RPG = 1024 / RB;
   constexpr int ROWS = 2 * BM + BN;
   constexpr int GROUPS = ROWS / RPG;         // 1 KB load groups per stage
-  constexpr int GPW = GROUPS / NW;           // groups per wavefront per stage
-  static_assert(GROUPS % NW == 0 && WM >= 1 && WN >= 1, "tile / wave grid mismatch");
+  // groups per wavefront per stage; when NW does not divide GROUPS, the
+  // spare slots repeat the last group (the same bytes to the same place)
+  constexpr int GPW = (GROUPS + NW - 1) / NW;
+  static_assert(ROWS % RPG == 0 && WM >= 1 && WN >= 1, "tile / wave grid mismatch");
+  static_assert(KG == 1 || (BM == 64 && (BK / 16) % KG == 0), "K groups: one 64-row pass");
   constexpr int STAGE_BYTES = ROWS * RB;
   constexpr int SSTR = BN + 4;  // epilogue staging row stride (floats)
   // NST stages of STAGE_BYTES; after the K loop the same memory (sized for
@@ -154,7 +162,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   __shared__ float sinv[BM];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int wm = wid / NWN, wn = wid % NWN;
+  const int kg = wid / NWT, wm = (wid % NWT) / NWN, wn = wid % NWN;
   // Blocks go to the 8 XCDs round-robin by linear id. Remap so that XCD x
   // runs a contiguous run of tiles in row-major order: tiles sharing an A
   // row-block (and the weight panel sweep) stay in one XCD's L2.
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   const uint16_t* src[GPW];
 #pragma unroll
   for (int q = 0; q < GPW; ++q) {
-    const int g = wid + NW * q;
+    const int g = min(wid + NW * q, GROUPS - 1);
     const int r = RPG * g + lane / CPR, slot = lane % CPR;
     const int c = swz<BK>(r, slot);
     if (r < 2 * BM) {  // A hi (r < BM) or A lo
@@ -186,9 +194,13 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
 
   // epilogue items (column pairs of a 64-row pass) per thread
   constexpr int EPT = 64 * (BN / 2) / NT;
-  static_assert(EPI != GV_RESID || BN == 64 || BN == 128,
-                "the residual epilogue's row sums cover a half or a whole wavefront");
   static_assert(EPT * NT == 64 * (BN / 2), "epilogue pass / block size mismatch");
+  // RESID row sums of squares: within the wavefront when a row's BN / 2
+  // column pairs are exactly one wavefront (BN = 128) or half of one
+  // (BN = 64), else through LDS (sqs, a padded [64][BN / 2] after the
+  // staged tile), each row summed in column order by one thread
+  constexpr bool SQ_LDS = EPI == GV_RESID && BN != 64 && BN != 128;
+  constexpr int SQS = BN / 2 + 1;
   // RESID: the residual tile is read now, so its latency hides behind the
   // K loop instead of stalling the epilogue
   float2 xres[EPI == GV_RESID ? (BM / 64) * EPT : 1];
@@ -214,15 +226,19 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
 
   const int nk = klen / BK;  // klen % BK == 0 (checked by the host)
   const int klast = klen - BK;
-  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_off(smem) + wid * 1024);
+  uint32_t ldsq[GPW];  // LDS byte offset of each of this wavefront's groups
+#pragma unroll
+  for (int q = 0; q < GPW; ++q)
+    ldsq[q] = __builtin_amdgcn_readfirstlane(lds_off(smem) + min(wid + NW * q, GROUPS - 1) * 1024);
   auto fill = [&](int stg, int k0) {
 #pragma unroll
-    for (int q = 0; q < GPW; ++q) dma16(src[q] + k0, lds0 + stg * STAGE_BYTES + NW * q * 1024);
+    for (int q = 0; q < GPW; ++q) dma16(src[q] + k0, ldsq[q] + stg * STAGE_BYTES);
   };
   auto consume = [&](int si) {
     const uint8_t* stg = smem + si * STAGE_BYTES;
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
+    for (int k2 = 0; k2 < BK / 16 / KG; ++k2) {
+      const int kk = k2 * KG + kg;         // this group's 16-deep step of the stage
       const int c = 2 * kk + (lane >> 5);  // logical chunk of this half-wave
       bf16x8_t ah[WM], al[WM], bw[WN];
 #pragma unroll
@@ -284,27 +300,37 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
   // ([..][hd][npos]: positions contiguous) walk the staged tile row-fastest,
   // so a wavefront's stores cover 64 consecutive positions of one dim.
   const bool rows_fast = EPI == GV_QKV && a.vt && !a.part && n0 + BN > (a.H + a.KH) * a.hd;
+  float* sqs = stage + 64 * SSTR;
 #pragma unroll
   for (int q = 0; q < BM / 64; ++q) {
+    // K groups add into the staged tile one after another, KG - 1 first
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-      const int rb = wm * WM + i;  // 32-row block of the tile
-      if (rb / 2 != q) continue;
+    for (int g = KG - 1; g >= 0; --g) {
+      if (kg == g) {
 #pragma unroll
-      for (int j = 0; j < WN; ++j)
+        for (int i = 0; i < WM; ++i) {
+          const int rb = wm * WM + i;  // 32-row block of the tile
+          if (rb / 2 != q) continue;
 #pragma unroll
-        for (int rg = 0; rg < 16; ++rg) {
-          const int r = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
-          stage[((rb & 1) * 32 + r) * SSTR + (wn * WN + j) * 32 + (lane & 31)] = acc[i][j][rg];
+          for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int rg = 0; rg < 16; ++rg) {
+              const int r = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
+              float& st = stage[((rb & 1) * 32 + r) * SSTR + (wn * WN + j) * 32 + (lane & 31)];
+              st = g == KG - 1 ? acc[i][j][rg] : st + acc[i][j][rg];
+            }
         }
+      }
+      __syncthreads();
     }
-    __syncthreads();
     // BN/2 consecutive e cover one row; with BN = 128 that is one
     // wavefront, with BN = 64 half of one (reductions stay in the wave)
-    if (EPI == GV_QKV && !a.part) {
-      qkv_tile_pass<BN, NT>(a, stage, sinv, m0, n0, q, rows_fast, pos0);
-      __syncthreads();
-      continue;
+    if constexpr (EPI == GV_QKV) {
+      if (!a.part) {
+        qkv_tile_pass<BN, NT>(a, stage, sinv, m0, n0, q, rows_fast, pos0);
+        __syncthreads();
+        continue;
+      }
     }
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
@@ -336,11 +362,14 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
           *reinterpret_cast<float2*>(y) = o;
           split_bf16x2(o.x, o.y, a.ys + (int64_t)m * a.N + n, a.ys_plane);
         }
-        // the row's sum of squares over this tile: the row spans the whole
-        // wavefront (BN = 128) or half of it (BN = 64)
+        // the row's sum of squares over this tile
         const float sq0 = o.x * o.x + o.y * o.y;
-        const float sq = BN == 128 ? wave_sum(sq0) : half_sum(sq0);
-        if (live && pc == 0) a.ssq_out[(int64_t)m * (a.N / BN) + n0 / BN] = sq;
+        if constexpr (SQ_LDS) {
+          sqs[srow * SQS + pc / 2] = sq0;
+        } else {
+          const float sq = BN == 128 ? wave_sum(sq0) : half_sum(sq0);
+          if (live && pc == 0) a.ssq_out[(int64_t)m * (a.N / BN) + n0 / BN] = sq;
+        }
       } else if (EPI == GV_RELU2) {
         if (live) {
           const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
@@ -351,6 +380,14 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm(GemvArgs a,
       }
     }
     __syncthreads();
+    if constexpr (SQ_LDS) {
+      if (!a.part && tid < 64 && m0 + q * 64 + tid < M) {
+        float sum = 0.f;
+        for (int p = 0; p < BN / 2; ++p) sum += sqs[tid * SQS + p];
+        a.ssq_out[(int64_t)(m0 + q * 64 + tid) * (a.N / BN) + n0 / BN] = sum;
+      }
+      __syncthreads();
+    }
   }
 }
 
@@ -578,21 +615,38 @@ void launch_cfg2(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
                      d_pos);
 }
 
-template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST>
+template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST, int KG = 1>
 void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
-  constexpr size_t pipe = (size_t)NST * (2 * BM + BN) * 2 * BK, epi = (size_t)64 * (BN + 4) * 4;
+  constexpr bool sq_lds = EPI == GV_RESID && BN != 64 && BN != 128;
+  constexpr size_t pipe = (size_t)NST * (2 * BM + BN) * 2 * BK;
+  constexpr size_t epi = (size_t)64 * (BN + 4) * 4 + (sq_lds ? (size_t)64 * (BN / 2 + 1) * 4 : 0);
   constexpr size_t lds = pipe > epi ? pipe : epi;
   // gfx950: 160 KB of LDS per workgroup, the row scales (BM floats) included
   static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)k_gemm<EPI, BM, BN, NWM, NWN, BK, NST>,
+    (void)hipFuncSetAttribute((const void*)k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr = true;
   }
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST>), g, dim3(64 * NWM * NWN), lds, s,
-                     a, d_pos);
+  hipLaunchKernelGGL((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG>), g, dim3(64 * NWM * NWN * KG),
+                     lds, s, a, d_pos);
+}
+
+// Compute units of the current device (tile counts are weighed against it).
+int cu_count() {
+  static int n[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (n[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    n[dev] = v;
+  }
+  return n[dev];
 }
 
 // 128 wide while that still leaves half the CUs a block (the wider tile
@@ -600,6 +654,16 @@ void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 int tile_n(int64_t M, int N) {
   const int64_t mt64 = (M + 63) / 64;
   return (N % 128 == 0 && mt64 * (N / 128) >= 128) ? 128 : 64;
+}
+
+// The residual GEMMs (proj, proj2) at prefill sizes, where 64x128 tiles
+// leave CUs idle and 64x96 tiles give more than half of them one each
+// (M = 2048, N = 768: 256 tiles): 64x96 tiles with K split over 4
+// wavefront groups, two wavefronts per SIMD (measured 2-4 us a launch
+// faster than 64x128 tiles at one wavefront per SIMD).
+bool resid_k4(int64_t M, int N, int K) {
+  const int64_t mt64 = (M + 63) / 64, ncu = cu_count(), t96 = mt64 * (N / 96);
+  return K % 64 == 0 && N % 96 == 0 && mt64 * (N / 128) < ncu && t96 <= ncu && 2 * t96 > ncu;
 }
 
 // Small M (batched decode, short chunks): too few output tiles to fill the
@@ -685,20 +749,6 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
 // whose outputs are scattered or need per-row reductions; the register
 // epilogue (k_gemm2) serves the plain stores of RELU2 and lm_head, with
 // 128x256 tiles (wave 64x128) when there are >= 1.5 blocks per CU.
-// Compute units of the current device (tile counts are weighed against it).
-int cu_count() {
-  static int n[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (n[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        v <= 0)
-      v = 256;
-    n[dev] = v;
-  }
-  return n[dev];
-}
 
 template <int EPI>
 void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
@@ -735,6 +785,12 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
     launch_cfg2<EPI, 4, 2, 1, 2, 3>(s, b, d_pos);
     return;
   }
+  if constexpr (EPI == GV_RESID) {
+    if (resid_k4(a.M, a.N, a.K)) {
+      launch_cfg<EPI, 64, 96, 2, 1, 64, 3, 4>(s, b, d_pos);
+      return;
+    }
+  }
   const int bn = tile_n(a.M, a.N);
   if (bn == 128 && big)
     launch_cfg<EPI, 128, 128, 4, 2, 32, 3>(s, b, d_pos);  // 72 KB: two blocks per CU
@@ -754,6 +810,7 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 // RESID on k_gemm: one sum-of-squares partial per row and N tile; split-K
 // RESID (given split-K scratch): one per row and 512 columns.
 int gemm_ssq_parts(int64_t M, int N, int K) {
+  if (splitk_count(M, N, K) == 1 && resid_k4(M, N, K)) return N / 96;
   return splitk_count(M, N, K) > 1 ? (N + RED_COLS - 1) / RED_COLS : N / tile_n(M, N);
 }
 
