@@ -117,6 +117,132 @@ __device__ void count_ids(const int32_t* gen, int lo, int hi, int V, int* cnt) {
   __syncthreads();
 }
 
+// Sort keys: the probability's bits (p >= 0, so they order as p does) above,
+// 0x7fffffff - id below: descending key order is descending probability
+// with ties in ascending id; key 0 (padding past V) sorts last.
+__device__ __forceinline__ uint64_t prob_key(float p, int id) {
+  return ((uint64_t)__float_as_uint(p) << 32) | (uint32_t)(0x7fffffff - id);
+}
+
+// v of lane (lane ^ D), D a power of two below 64: DPP within quads, a
+// swizzle within 32-lane halves, a permute across them
+template <int D>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (D == 1)
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (D == 2)
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (D < 32)
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (D << 10) | 0x1F);
+  else
+    return (uint32_t)__shfl_xor((int)v, 32, 64);
+}
+
+// Bitonic network, descending, over np2 = EPT * ST keys; thread t holds
+// elements EPT t .. EPT t + EPT - 1 in registers. A compare-exchange
+// (k, j) of elements i and i ^ j orders them descending when i & k == 0,
+// ascending otherwise. Partners j < EPT apart are in the same thread, up to
+// 64 EPT apart in the same wavefront (lane ^ j / EPT); farther ones meet
+// through LDS (kb, element e of thread t at e * ST + t).
+template <int EPT, int J>
+__device__ __forceinline__ void cx_regs(uint64_t (&key)[EPT], int k) {
+  if constexpr (J < EPT) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      if (e & J) continue;
+      const uint64_t a = key[e], b = key[e | J];
+      const bool sw = ((EPT * tid + e) & k) == 0 ? a < b : a > b;
+      key[e] = sw ? b : a;
+      key[e | J] = sw ? a : b;
+    }
+  }
+}
+
+template <int EPT, int D>
+__device__ __forceinline__ void cx_lanes(uint64_t (&key)[EPT], int k) {
+  const int tid = threadIdx.x;
+  const bool lower = (tid & D) == 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const uint32_t lo = lane_xor<D>((uint32_t)key[e]);
+    const uint32_t hi = lane_xor<D>((uint32_t)(key[e] >> 32));
+    const uint64_t other = ((uint64_t)hi << 32) | lo;
+    const bool keep_max = lower == (((EPT * tid + e) & k) == 0);
+    key[e] = (key[e] > other) == keep_max ? key[e] : other;
+  }
+}
+
+template <int EPT>
+__device__ __forceinline__ void cx_lds(uint64_t (&key)[EPT], uint64_t* kb, int k, int j) {
+  const int tid = threadIdx.x, dt = j / EPT;  // partner thread tid ^ dt
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) kb[e * ST + tid] = key[e];
+  __syncthreads();
+  uint64_t other[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) other[e] = kb[e * ST + (tid ^ dt)];
+  __syncthreads();
+  const bool lower = (tid & dt) == 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const bool keep_max = lower == (((EPT * tid + e) & k) == 0);
+    key[e] = (key[e] > other[e]) == keep_max ? key[e] : other[e];
+  }
+}
+
+template <int EPT>
+__device__ void bitonic_desc(uint64_t (&key)[EPT], uint64_t* kb) {
+  constexpr int NP2 = EPT * ST;
+#pragma unroll
+  for (int k = 2; k <= NP2; k <<= 1)
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 64 * EPT) {
+        cx_lds<EPT>(key, kb, k, j);
+      } else if (j >= EPT) {
+        switch (j / EPT) {
+          case 1: cx_lanes<EPT, 1>(key, k); break;
+          case 2: cx_lanes<EPT, 2>(key, k); break;
+          case 4: cx_lanes<EPT, 4>(key, k); break;
+          case 8: cx_lanes<EPT, 8>(key, k); break;
+          case 16: cx_lanes<EPT, 16>(key, k); break;
+          default: cx_lanes<EPT, 32>(key, k); break;
+        }
+      } else {
+        switch (j) {
+          case 1: cx_regs<EPT, 1>(key, k); break;
+          case 2: cx_regs<EPT, 2>(key, k); break;
+          default: cx_regs<EPT, 4>(key, k); break;
+        }
+      }
+    }
+}
+
+// pr[0:V) / s sorted descending (ties by id) into pr (probabilities) and ox
+// (ids), np2 = EPT * ST entries, the tail past V padding; pr and the aux
+// array after it serve as the LDS exchange buffer meanwhile
+template <int EPT>
+__device__ void sort_probs(float* pr, int* ox, int V, float s) {
+  const int tid = threadIdx.x;
+  uint64_t key[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = EPT * tid + e;
+    key[e] = i < V ? prob_key(pr[i] / s, i) : 0ull;
+  }
+  __syncthreads();
+  bitonic_desc<EPT>(key, reinterpret_cast<uint64_t*>(pr));
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = EPT * tid + e;
+    pr[i] = __uint_as_float((uint32_t)(key[e] >> 32));
+    ox[i] = 0x7fffffff - (int)(uint32_t)key[e];
+  }
+  __syncthreads();
+}
+
 // The whole of sample_next for one row. LDS: pr, aux (floats) and ox (ints),
 // np2 entries each (np2 = V rounded up to a power of two). Every thread of
 // the workgroup calls it; the id is valid in every thread.
@@ -188,50 +314,13 @@ __device__ int sample_row(const float* __restrict__ logits, int V, int np2,
     part += e;
   }
   const float s = block_sum(part, rv);
-  for (int i = tid; i < np2; i += ST) {
-    if (i < V) {
-      pr[i] = pr[i] / s;
-      ox[i] = i;
-    } else {
-      pr[i] = -1.f;  // padding sorts last
-      ox[i] = i;
-    }
-  }
-  __syncthreads();
-  // descending probability, ties by id: bitonic network over np2 entries.
-  // A stage's np2/2 compare-exchange pairs are disjoint; each thread loads
-  // all of its pairs before it writes any (one LDS round trip per stage).
-  constexpr int PPT = SAMPLE_MAX_V / 2 / ST;  // pairs per thread, at most
-  const int npairs = np2 >> 1;
-  for (int k = 2; k <= np2; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      float a[PPT], b[PPT];
-      int ia[PPT], ib[PPT], lo[PPT];
-#pragma unroll
-      for (int r = 0; r < PPT; ++r) {
-        const int q = tid + r * ST;
-        lo[r] = q < npairs ? (q / j) * 2 * j + q % j : -1;
-        if (lo[r] >= 0) {
-          a[r] = pr[lo[r]];
-          b[r] = pr[lo[r] + j];
-          ia[r] = ox[lo[r]];
-          ib[r] = ox[lo[r] + j];
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < PPT; ++r) {
-        if (lo[r] < 0) continue;
-        const bool b_first = b[r] > a[r] || (b[r] == a[r] && ib[r] < ia[r]);
-        const bool a_first = a[r] > b[r] || (a[r] == b[r] && ia[r] < ib[r]);
-        if ((lo[r] & k) == 0 ? b_first : a_first) {
-          pr[lo[r]] = b[r];
-          pr[lo[r] + j] = a[r];
-          ox[lo[r]] = ib[r];
-          ox[lo[r] + j] = ia[r];
-        }
-      }
-      __syncthreads();
-    }
+  // descending probability, ties by id: a bitonic network with the keys in
+  // registers (the row normalised on the way in)
+  switch (np2 / ST) {
+    case 1: sort_probs<1>(pr, ox, V, s); break;
+    case 2: sort_probs<2>(pr, ox, V, s); break;
+    case 4: sort_probs<4>(pr, ox, V, s); break;
+    default: sort_probs<8>(pr, ox, V, s); break;
   }
   // inclusive cumulative sums of the sorted probabilities: each thread owns
   // np2/ST consecutive entries, then an in-order scan of the thread totals
