@@ -250,7 +250,11 @@ void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a) {
 // the chunk is loaded up front (V does not depend on the scores), so a
 // chunk costs one memory round trip. A single-chunk call writes the result;
 // otherwise each chunk leaves (max, sum, O) in scratch for k_attn_dec_merge.
-constexpr int DPC = 64;  // positions per chunk
+// DPC = 64 positions per chunk; 128 for batches of many sequences, where
+// the longer chunks halve the partial results to merge (the chunk length
+// sets the merge order, so it depends on the sequence count only: every
+// query row of one sequence, and a sequence decoded alone, sums alike)
+constexpr int DPC_MIN = 64;
 
 struct DecArgs {
   const float* q;  // [B][H][hd]
@@ -277,7 +281,7 @@ __device__ __forceinline__ void dec_store(const DecArgs& a, int64_t o, int d, fl
   }
 }
 
-template <int HD>
+template <int HD, int DPC>
 __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
   constexpr int LPP = HD / 4;         // lanes per cached row
   constexpr int PPW = 64 / LPP;       // positions per wavefront load
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
 }
 
 // Combine the chunks of a multi-chunk step in chunk order.
-template <int HD>
+template <int HD, int DPC>
 __global__ __launch_bounds__(64) void k_attn_dec_merge(DecArgs a) {
   const int bh = blockIdx.x, tid = threadIdx.x;
   if (a.d_rows && bh / a.H >= *a.d_rows) return;
@@ -402,7 +406,7 @@ __global__ __launch_bounds__(64) void k_attn_dec_merge(DecArgs a) {
   dec_store<HD>(a, (int64_t)bh * HD, 4 * tid, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
 }
 
-int attn_decode_chunks(int maxT) { return (maxT + DPC - 1) / DPC; }
+int attn_decode_chunks(int maxT) { return (maxT + DPC_MIN - 1) / DPC_MIN; }
 
 int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT) {
   return (int64_t)B * d.H * attn_decode_chunks(maxT) * (d.hd + 2);
@@ -421,7 +425,9 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.maxT = maxT;
   // chunks that can be live: all of maxT for a replayed step, else those of
   // the last query row
-  a.nchunk = attn_decode_chunks(d_len ? maxT : len + qpr - 1);
+  const int dpc = B * d.H >= 192 ? 128 : DPC_MIN;
+  const int live = d_len ? maxT : len + qpr - 1;
+  a.nchunk = (live + dpc - 1) / dpc;
   a.d_len = d_len;
   a.len_imm = len;
   a.qpr = qpr;
@@ -432,12 +438,19 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.part = scratch;
   const int rows = B * qpr;
   const dim3 grid((unsigned)(rows * d.H), (unsigned)a.nchunk);
-  if (d.hd == 128) {
-    hipLaunchKernelGGL(k_attn_dec<128>, grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<128>, dim3(rows * d.H), dim3(64), 0, s, a);
+  const dim3 mgrid((unsigned)(rows * d.H));
+  if (d.hd == 128 && dpc == 128) {
+    hipLaunchKernelGGL((k_attn_dec<128, 128>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<128, 128>), mgrid, dim3(64), 0, s, a);
+  } else if (d.hd == 128) {
+    hipLaunchKernelGGL((k_attn_dec<128, DPC_MIN>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<128, DPC_MIN>), mgrid, dim3(64), 0, s, a);
+  } else if (dpc == 128) {
+    hipLaunchKernelGGL((k_attn_dec<64, 128>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<64, 128>), mgrid, dim3(64), 0, s, a);
   } else {
-    hipLaunchKernelGGL(k_attn_dec<64>, grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL(k_attn_dec_merge<64>, dim3(rows * d.H), dim3(64), 0, s, a);
+    hipLaunchKernelGGL((k_attn_dec<64, DPC_MIN>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<64, DPC_MIN>), mgrid, dim3(64), 0, s, a);
   }
 }
 
