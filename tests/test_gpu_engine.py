@@ -84,6 +84,23 @@ def test_forward_d12_vs_oracle(d12):
     assert np.array_equal(lg[0].argmax(-1), ref[0].argmax(-1))
 
 
+@pytest.mark.parametrize("B,T", [(1, 48), (1, 1500), (2, 700)])
+def test_forward_d12_gemm_shapes(d12, B, T):
+    """Row counts that reach the other GEMM tilings: split-K partials and their
+    reduce (48 rows), and the 64x96 residual tiles whose K is split over
+    wavefront groups, with a partial last row tile (1400 and 1500 rows) and,
+    at B=2, a sequence boundary inside a tile."""
+    d, w, m, c, s = d12
+    ids = uniform_ids(40 + T, B * T, d.vocab).reshape(B, T)
+    lg, _ = m.forward(ids, B, T)
+    for b in range(B):
+        ref = O.gpt_forward(ids[b], c, s, w, d, 1, T)
+        e = relerr(lg[b], ref[0])
+        record("forward_d12_shape", B=B, T=T, row=b, relerr=e)
+        assert e < 1e-4
+        assert np.array_equal(lg[b].argmax(-1), ref[0].argmax(-1))
+
+
 def test_prefill_d12_T2048_vs_oracle(d12):
     """The prefill workload's own size: T = 2048 logits and per-token CE."""
     d, w, m, c, s = d12
