@@ -96,11 +96,13 @@ void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const in
 }
 
 // ------------------------------------------------------------ epilogues
+// res: the residual y[m][r] (RESID), loaded before the dot product
 template <int EPI>
-__device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, float v) {
+__device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, float v,
+                                             float res) {
   float* y = a.y + (int64_t)m * a.N + r;
   if (EPI == GV_RESID) {
-    *y = *y + v;
+    *y = res + v;
   } else if (EPI == GV_RELU2) {
     const float t = v < 0.f ? 0.f : v;
     *y = t * t;
@@ -116,7 +118,9 @@ __device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, fl
 // one wavefront; else 1, for twice the wavefronts): lanes stride the rows in
 // 16-byte chunks (8 bf16), so each row is read as whole, coalesced lines,
 // and x comes straight from global memory (L2) in matching float4 pairs. No
-// LDS and no barrier: the weight loads go out at once. The row norm (a.norm)
+// LDS and no barrier: the weight loads go out at once, and so do the
+// epilogue's own loads (RoPE coefficients, the residual), so none waits
+// behind the reduction. The row norm (a.norm)
 // is a scale of the dot products, from sum(x^2) the same lanes accumulate
 // over the chunks they read. Each (token row, weight row) result is the same
 // sequence of operations whatever M is, so a row's value does not depend on
@@ -130,11 +134,18 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int pos0) {
 #pragma unroll
     for (int r = 0; r < R; ++r) wr[r] = a.w + (int64_t)min(R * u + r, a.N - 1) * K;
     float acc[R][M], ss[M];
+    float e0[R][M], e1[R][M];  // RoPE cos / sin of a pair (QKV), the residual (RESID)
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       ss[m] = 0.f;
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r][m] = 0.f;
+      for (int r = 0; r < R; ++r) {
+        acc[r][m] = 0.f;
+        e0[r][m] = e1[r][m] = 0.f;
+        if (EPI == GV_QKV && (r & 1) == 0 && R * u + r < a.N)
+          qkv_pair_coeffs(a, m, pos0, R * u + r, e0[r][m], e1[r][m]);
+        if (EPI == GV_RESID && R * u + r < a.N) e0[r][m] = a.y[(int64_t)m * a.N + R * u + r];
+      }
     }
 #pragma unroll 2
     for (int c = lane; c < nch; c += 64) {
@@ -166,11 +177,12 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int pos0) {
 #pragma unroll
           for (int pr = 0; pr < R; pr += 2)
             if (R * u + pr < a.N)
-              qkv_pair_epilogue(a, m, pos0, R * u + pr, acc[pr][m], acc[pr + 1][m]);
+              qkv_pair_store(a, m, pos0, R * u + pr, acc[pr][m], acc[pr + 1][m], e0[pr][m],
+                             e1[pr][m]);
         } else {
 #pragma unroll
           for (int r = 0; r < R; ++r)
-            if (R * u + r < a.N) single_store<EPI>(a, m, R * u + r, acc[r][m]);
+            if (R * u + r < a.N) single_store<EPI>(a, m, R * u + r, acc[r][m], e0[r][m]);
         }
       }
     }
