@@ -73,7 +73,8 @@ def margin(detail, u):
     return float(np.min(np.abs(c - u))) / max(detail["total"], 1e-30)
 
 
-@pytest.mark.parametrize("V", [512, 8192])
+# 512 / 1500 / 3000 / 8192 entries: the sort's 1, 2, 4 and 8 keys per thread
+@pytest.mark.parametrize("V", [512, 1500, 3000, 8192])
 @pytest.mark.parametrize("ci", range(len(CFGS)))
 def test_device_matches_oracle(m, V, ci):
     cfg = CFGS[ci]
