@@ -16,16 +16,17 @@
 // comes from per-row sums of squares of the fp32 values, also written by
 // the producer (one partial per producer N tile, summed here in order).
 //
-// Pipeline: NST stages of 32-wide K slices in LDS, filled by
-// global_load_lds_dwordx4 (memory -> LDS without registers), NST-1 slices in
-// flight while the MFMAs consume the oldest. Each 64-byte LDS row (32 bf16)
-// holds its four 16-byte chunks XOR-swizzled by row so the MFMA operand
-// reads (32 rows x one chunk per half-wavefront) do not collide in banks.
+// Pipeline: NST stages of BK-wide K slices (BK = 32, 64 or 128) in LDS,
+// filled by global_load_lds_dwordx4 (memory -> LDS without registers),
+// NST-1 slices in flight while the MFMAs consume the oldest. Each LDS row
+// holds its 16-byte chunks XOR-swizzled by row so the MFMA operand reads
+// (32 rows x one chunk per half-wavefront) do not collide in banks.
 // Tiling: BM x BN per block of NWM x NWN 64-wide wavefronts, each owning
-// (BM/NWM) x (BN/NWN) as 32x32 MFMA blocks. The epilogue is staged through
-// LDS 64 rows at a time so each thread owns a column pair (coalesced stores;
-// a QKV rotation pair in one thread). The host picks the largest tile that
-// still gives every CU work.
+// (BM/NWM) x (BN/NWN) as 32x32 MFMA blocks, times KG groups of such
+// wavefronts that split each slice's K steps between them. The epilogue is
+// staged through LDS 64 rows at a time so each thread owns a column pair
+// (coalesced stores; a QKV rotation pair in one thread). The host picks the
+// tile per shape (launch_tile) so that one round of tiles covers the CUs.
 #include "fgpt_internal.h"
 #include "kern_common.h"
 #include "kern_epi.h"
