@@ -3,7 +3,7 @@
 hipcc compiles every .hip source for gfx950 only; amdflang builds the
 iso_c_binding module, the drop-in gpt_forward/gpt_step module and the
 ids-in/ids-out harness against the library. Outputs stay inside the package
-directory so they travel with the repository to the GPU box.
+directory, next to the sources, so a copy of the repository carries them.
 """
 from __future__ import annotations
 

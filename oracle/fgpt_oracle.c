@@ -1,8 +1,8 @@
 /* fgpt_oracle.c -- CPU restatement of the fortran_gpt forward path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker). Loaded by tests/, by
- * __graft_entry__.smoke() and by bench.py's cpu_baseline leg; never by the
- * product library.
+ * TEST INFRASTRUCTURE ONLY (the oracle results are checked against). Loaded
+ * by tests/, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg;
+ * never by the product library.
  *
  * Arithmetic is fp32 throughout, built with -ffp-contract=off so that every
  * `acc = acc + a*b` rounds the product and the sum separately, as the

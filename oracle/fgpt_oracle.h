@@ -1,8 +1,9 @@
 /* fgpt_oracle.h -- CPU restatement of the fortran_gpt forward path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP engine:
- * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load it. The product path (libfgpt.so) never links, loads or calls it.
+ * TEST INFRASTRUCTURE ONLY. The HIP engine's results are checked against this
+ * library: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it. The product path (libfgpt.so) never links, loads or calls
+ * it.
  *
  * Every routine restates one reference routine in fp32, in the reference's
  * loop and summation order, with row-major flat buffers and 0-based ids.

@@ -1,8 +1,8 @@
 """ctypes wrapper of oracle/liboracle.so, the CPU restatement of the reference path.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker. The product library never
-imports it.
+cpu_baseline leg of bench.py, which check the engine's results against it or
+time it. The product library never imports it.
 """
 from __future__ import annotations
 

@@ -21,15 +21,15 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3  # max|d logit| / max|logit|
 SMALL = Dims(n_layer=2, d_model=128, n_head=2, n_kv_head=1, head_dim=64, vocab=512)
 SMALL_MHA = Dims(n_layer=2, d_model=256, n_head=2, n_kv_head=2, head_dim=128, vocab=1024)
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def record(name, **kv):
-    """Append a parity figure to gpurun_out/parity.jsonl (when that folder exists)."""
-    out = os.path.join(ROOT, "gpurun_out")
+    """Print a parity figure; also append it as a JSON line to the file
+    $FGPT_PARITY_LOG names, when set."""
     print(name, kv, flush=True)
-    if os.path.isdir(out):
-        with open(os.path.join(out, "parity.jsonl"), "a") as f:
+    path = os.environ.get("FGPT_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
             f.write(json.dumps({"test": name, **kv}) + "\n")
 
 
