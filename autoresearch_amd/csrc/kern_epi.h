@@ -22,17 +22,33 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t* p, int64_t plane) 
   p[plane] = f32_to_bf16_rne(v - bf16_to_f32(h));
 }
 
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// A store that bypasses cache allocation (NT) or an ordinary one. Outputs
+// that only a later kernel reads, and that are too large to stay in L2 for
+// it, are written streaming.
+template <bool NT, typename V>
+__device__ __forceinline__ void store_v(V* p, V v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(v, p);
+  else
+    *p = v;
+}
+
 // The same for two adjacent values as one 32-bit store per plane (p even).
+template <bool NT = false>
 __device__ __forceinline__ void split_bf16x2(float v0, float v1, uint16_t* p, int64_t plane) {
   const uint16_t h0 = f32_to_bf16_rne(v0), h1 = f32_to_bf16_rne(v1);
   const uint16_t l0 = f32_to_bf16_rne(v0 - bf16_to_f32(h0));
   const uint16_t l1 = f32_to_bf16_rne(v1 - bf16_to_f32(h1));
-  *reinterpret_cast<uint32_t*>(p) = (uint32_t)h0 | ((uint32_t)h1 << 16);
-  *reinterpret_cast<uint32_t*>(p + plane) = (uint32_t)l0 | ((uint32_t)l1 << 16);
+  store_v<NT>(reinterpret_cast<uint32_t*>(p), (uint32_t)h0 | ((uint32_t)h1 << 16));
+  store_v<NT>(reinterpret_cast<uint32_t*>(p + plane), (uint32_t)l0 | ((uint32_t)l1 << 16));
 }
 
 // The same for four adjacent values as one 64-bit store per plane (p a
 // multiple of 4 elements).
+template <bool NT = false>
 __device__ __forceinline__ void split_bf16x4(const float (&v)[4], uint16_t* p, int64_t plane) {
   uint32_t h[4], l[4];
 #pragma unroll
@@ -41,8 +57,8 @@ __device__ __forceinline__ void split_bf16x4(const float (&v)[4], uint16_t* p, i
     h[i] = hb;
     l[i] = f32_to_bf16_rne(v[i] - bf16_to_f32(hb));
   }
-  *reinterpret_cast<uint2*>(p) = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-  *reinterpret_cast<uint2*>(p + plane) = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+  store_v<NT>(reinterpret_cast<u32x2_t*>(p), u32x2_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16)});
+  store_v<NT>(reinterpret_cast<u32x2_t*>(p + plane), u32x2_t{l[0] | (l[1] << 16), l[2] | (l[3] << 16)});
 }
 
 // RoPE coefficients of stored column pair r for token row m (q and k
@@ -111,6 +127,7 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
 // head and dims j .. j+3 with j % 4 == 0) of token row m, x the eight
 // values, cs/sn the four pairs' RoPE coefficients: the arithmetic of
 // qkv_pair_store, with each plane's four dims written by one wide store.
+template <bool NT = false>
 __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos0, int r8,
                                                const float (&x)[8], const float4& cs,
                                                const float4& sn) {
@@ -131,8 +148,8 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
     if (isq) {
       if (a.qs) {
         uint16_t* p = a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd;
-        split_bf16x4(y1, p + j, a.q_plane);
-        split_bf16x4(y2, p + j + hd / 2, a.q_plane);
+        split_bf16x4<NT>(y1, p + j, a.q_plane);
+        split_bf16x4<NT>(y2, p + j + hd / 2, a.q_plane);
       } else {
         float* q = a.y + (int64_t)m * qd + head * hd;
         *reinterpret_cast<float4*>(q + j) = make_float4(y1[0], y1[1], y1[2], y1[3]);
@@ -146,8 +163,8 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
       }
       if (a.ks) {
         uint16_t* p = a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd;
-        split_bf16x4(y1, p + j, a.kv_plane);
-        split_bf16x4(y2, p + j + hd / 2, a.kv_plane);
+        split_bf16x4<NT>(y1, p + j, a.kv_plane);
+        split_bf16x4<NT>(y2, p + j + hd / 2, a.kv_plane);
       }
     }
   } else {
