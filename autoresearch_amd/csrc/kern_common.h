@@ -9,11 +9,11 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);
 }
 
-// fp32 -> bf16 bits, round to nearest even (inputs are finite here).
+// fp32 -> bf16 bits, round to nearest even: gfx950's v_cvt_pk_bf16_f32
+// (one instruction for two values where the compiler pairs them; the same
+// bits as adding 0x7fff + the kept lsb and truncating, for finite inputs).
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
 // Unpack 8 bf16 held in a uint4 (little-endian pairs) to floats.
