@@ -307,28 +307,44 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
   // ([..][hd][npos]: positions contiguous) walk the staged tile row-fastest,
   // so a wavefront's stores cover 64 consecutive positions of one dim.
   const bool rows_fast = EPI == GV_QKV && a.vt && !a.part && n0 + BN > (a.H + a.KH) * a.hd;
-  float* sqs = stage + 64 * SSTR;
+  float* sqs = stage + KG * 64 * SSTR;
 #pragma unroll
   for (int q = 0; q < BM / 64; ++q) {
-    // K groups add into the staged tile one after another, KG - 1 first
+    // each K group stages its partial tile in a region of its own, all at
+    // once; one pass then adds the regions in a fixed order (KG - 1 first,
+    // 0 last) into region 0
+    {
+      float* reg = stage + kg * 64 * SSTR;
 #pragma unroll
-    for (int g = KG - 1; g >= 0; --g) {
-      if (kg == g) {
+      for (int i = 0; i < WM; ++i) {
+        const int rb = wm * WM + i;  // 32-row block of the tile
+        if (rb / 2 != q) continue;
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
-          const int rb = wm * WM + i;  // 32-row block of the tile
-          if (rb / 2 != q) continue;
+        for (int j = 0; j < WN; ++j)
 #pragma unroll
-          for (int j = 0; j < WN; ++j)
-#pragma unroll
-            for (int rg = 0; rg < 16; ++rg) {
-              const int r = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
-              float& st = stage[((rb & 1) * 32 + r) * SSTR + (wn * WN + j) * 32 + (lane & 31)];
-              st = g == KG - 1 ? acc[i][j][rg] : st + acc[i][j][rg];
-            }
-        }
+          for (int rg = 0; rg < 16; ++rg) {
+            const int r = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
+            reg[((rb & 1) * 32 + r) * SSTR + (wn * WN + j) * 32 + (lane & 31)] = acc[i][j][rg];
+          }
       }
       __syncthreads();
+      if constexpr (KG > 1) {
+        constexpr int NQ4 = 64 * BN / 4;  // float4s of a pass
+        for (int e = tid; e < NQ4; e += NT) {
+          const int o = (e / (BN / 4)) * SSTR + 4 * (e % (BN / 4));
+          float4 v = *reinterpret_cast<const float4*>(stage + (KG - 1) * 64 * SSTR + o);
+#pragma unroll
+          for (int g = KG - 2; g >= 0; --g) {
+            const float4 w = *reinterpret_cast<const float4*>(stage + g * 64 * SSTR + o);
+            v.x = v.x + w.x;
+            v.y = v.y + w.y;
+            v.z = v.z + w.z;
+            v.w = v.w + w.w;
+          }
+          *reinterpret_cast<float4*>(stage + o) = v;
+        }
+        __syncthreads();
+      }
     }
     // BN/2 consecutive e cover one row; with BN = 128 that is one
     // wavefront, with BN = 64 half of one (reductions stay in the wave)
@@ -388,11 +404,19 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
     }
     __syncthreads();
     if constexpr (SQ_LDS) {
-      if (!a.part && tid < 64 && m0 + q * 64 + tid < M) {
-        float sum = 0.f;
-        for (int p = 0; p < BN / 2; ++p) sum += sqs[tid * SQS + p];
-        a.ssq_out[(int64_t)(m0 + q * 64 + tid) * (a.N / BN) + n0 / BN] = sum;
-      }
+      // P = NT / 64 adjacent threads per row, each summing BN / 2 / P of
+      // its values in column order, then a fixed butterfly over the P
+      constexpr int P = NT / 64, VPP = (BN / 2) / P;
+      static_assert(P * VPP == BN / 2 && (P == 2 || P == 4 || P == 8), "row-sum split");
+      const int row = tid / P, part = tid % P;
+      float sum = 0.f;
+#pragma unroll
+      for (int v = 0; v < VPP; ++v) sum += sqs[row * SQS + part * VPP + v];
+      sum += dpp_f<0xB1>(sum);                          // lane ^ 1
+      if constexpr (P >= 4) sum += dpp_f<0x4E>(sum);    // lane ^ 2
+      if constexpr (P == 8) sum += dpp_f<0x141>(sum);   // the other quad of eight
+      if (!a.part && part == 0 && m0 + q * 64 + row < M)
+        a.ssq_out[(int64_t)(m0 + q * 64 + row) * (a.N / BN) + n0 / BN] = sum;
       __syncthreads();
     }
   }
@@ -626,7 +650,8 @@ template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST, int KG = 1
 void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr bool sq_lds = EPI == GV_RESID && BN != 64 && BN != 128;
   constexpr size_t pipe = (size_t)NST * (2 * BM + BN) * 2 * BK;
-  constexpr size_t epi = (size_t)64 * (BN + 4) * 4 + (sq_lds ? (size_t)64 * (BN / 2 + 1) * 4 : 0);
+  constexpr size_t epi =
+      (size_t)KG * 64 * (BN + 4) * 4 + (sq_lds ? (size_t)64 * (BN / 2 + 1) * 4 : 0);
   constexpr size_t lds = pipe > epi ? pipe : epi;
   // gfx950: 160 KB of LDS per workgroup, the row scales (BM floats) included
   static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
