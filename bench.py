@@ -339,7 +339,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "
-              "(data-parallel sharding is described in DESIGN.md, not built)", file=sys.stderr)
+              "(data-parallel sharding is not built)", file=sys.stderr)
         sys.exit(2)
 
     # the counter runs go first, before this process touches the GPU

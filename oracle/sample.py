@@ -1,6 +1,6 @@
 """CPU restatement of the reference's token sampling (src/lib/sample.f90).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker. The product
+TEST INFRASTRUCTURE ONLY: imported by tests/ to check the device results. The product
 library never imports it.
 
 fp32 arithmetic in the reference's order (numpy float32 scalars); ids are

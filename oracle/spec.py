@@ -1,6 +1,6 @@
 """CPU restatement of greedy speculative decoding (temperature 0).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker. The product
+TEST INFRASTRUCTURE ONLY: imported by tests/ to check the device results. The product
 library never imports it.
 
 Follows src/lib/fortran_spec.f90 (accept_prefix :41-52, lookup_draft
