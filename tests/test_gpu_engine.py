@@ -114,6 +114,10 @@ def test_prefill_d12_T2048_vs_oracle(d12):
     record("prefill_d12_T2048", relerr=e, max_dnll=dn, bits_mean=float(ref_nll.mean() / np.log(2)))
     assert e < TOL
     assert dn < 2 * TOL * np.abs(ref).max()
+    # every cross-workgroup sum (K groups, key chunks, row sums of squares)
+    # runs in a fixed order: a second forward gives the same bits
+    lg2, nll2 = m.forward(ids[:T], 1, T, targets=ids[1:])
+    assert np.array_equal(lg, lg2) and np.array_equal(nll, nll2)
 
 
 def test_eval_rows_zipf_bos(d12):
