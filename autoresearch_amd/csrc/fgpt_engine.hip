@@ -44,7 +44,7 @@ int32_t fgpt::set_error(int32_t code, const char* msg) { return seterr(code, "%s
     if (r_ != FG_OK) return r_;    \
   } while (0)
 
-extern "C" int32_t fg_version(void) { return 100; }
+extern "C" int32_t fg_version(void) { return 101; }
 
 extern "C" int32_t fg_last_error(char* buf, int32_t len) {
   if (buf && len > 0) {
@@ -88,6 +88,15 @@ struct fg_model {
   };
   std::vector<TRec> trecs;
   std::vector<hipEvent_t> evpool;
+  // the persistent B=1 greedy decode (kern_fused.hip): its weight copy,
+  // exchange slots, error flag and the next launch's first epoch
+  FusedLayout fl;
+  bf16_t* fused_w = nullptr;
+  uint64_t* fused_slots = nullptr;
+  uint32_t* fused_err = nullptr;
+  uint32_t fused_ep = 1;
+  bool fused_on = true;  // fg_set_option(FG_OPT_FUSED_DECODE)
+  std::string fused_why = "not set up";
 };
 
 struct fg_kv {
@@ -217,6 +226,40 @@ int32_t to_bf16_exact(const float* src, size_t n, bf16_t* dst, const char* name)
   return FG_OK;
 }
 
+// The persistent decode serves B=1 greedy loops when the dims fit its work
+// split and the device is the one it is laid out for: 256 CUs (8 XCDs of
+// 32) and cooperative launches. When it does not, fg_decode_greedy keeps the
+// captured per-kernel steps.
+int32_t setup_fused(fg_model* m, const bf16_t* host_main) {
+  const char* why = nullptr;
+  m->fl = fused_layout(m->d, &why);
+  if (!m->fl.ok) {
+    m->fused_why = why;
+    return FG_OK;
+  }
+  hipDeviceProp_t p;
+  HIPCHK(hipGetDeviceProperties(&p, m->device));
+  if (p.multiProcessorCount != FUSED_NWG || !p.cooperativeLaunch) {
+    m->fused_why = "device is not a 256-CU part with cooperative launch";
+    return FG_OK;
+  }
+  if (p.sharedMemPerBlock < (size_t)m->fl.lds_bytes && p.maxSharedMemoryPerMultiProcessor <
+                                                            (size_t)m->fl.lds_bytes) {
+    m->fused_why = "not enough LDS per workgroup";
+    return FG_OK;
+  }
+  std::vector<bf16_t> hf((size_t)FUSED_NWG * m->fl.cu_bytes / 2);
+  fused_pack(m->d, m->fl, m->w, host_main, hf.data());
+  HIPCHK(hipMalloc((void**)&m->fused_w, hf.size() * 2));
+  HIPCHK(hipMemcpy(m->fused_w, hf.data(), hf.size() * 2, hipMemcpyHostToDevice));
+  HIPCHK(hipMalloc((void**)&m->fused_slots, (size_t)m->fl.slots * 8));
+  HIPCHK(hipMemset(m->fused_slots, 0, (size_t)m->fl.slots * 8));
+  HIPCHK(hipMalloc((void**)&m->fused_err, 4 * (1 + FUSED_NX)));
+  m->fused_ep = 1;
+  m->fused_why = "";
+  return FG_OK;
+}
+
 int32_t upload_weights(fg_model* m, const float* const st[8]) {
   const Dims& d = m->d;
   static const char* names[8] = {"wte", "c_q", "c_k", "c_v", "c_proj", "c_fc", "c_proj2", "lm_head"};
@@ -259,7 +302,7 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
   HIPCHK(hipMemcpy(w.base, h.data(), w.bytes, hipMemcpyHostToDevice));
   w.lm = w.base + w.layer_stride * d.L;
   w.wte = w.lm + V * D;
-  return FG_OK;
+  return setup_fused(m, h.data());
 }
 
 void free_work(fg_model* m) {
@@ -579,6 +622,9 @@ extern "C" int32_t fg_model_destroy(fg_model* m) {
   if (m->attn_part) (void)hipFree(m->attn_part);
   if (m->samp) (void)hipFree(m->samp);
   if (m->w.base) (void)hipFree(m->w.base);
+  if (m->fused_w) (void)hipFree(m->fused_w);
+  if (m->fused_slots) (void)hipFree(m->fused_slots);
+  if (m->fused_err) (void)hipFree(m->fused_err);
   if (m->d_cos) (void)hipFree(m->d_cos);
   if (m->d_sin) (void)hipFree(m->d_sin);
   for (auto& r : m->trecs) {
@@ -914,6 +960,89 @@ int32_t run_greedy_graph(fg_model* m, fg_kv* kv, hipStream_t s, int steps, bool 
   return FG_OK;
 }
 
+// Per-kernel path: runs of captured steps (or eager launches under timing).
+int32_t graph_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, int with_logits) {
+  const int B = kv->B;
+  hipStream_t s = m->stream;
+  const int32_t lens[2] = {kv->len, kv->len};
+  HIPCHK(hipMemcpyAsync(kv->d_ids, ids, (size_t)B * 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemcpyAsync(kv->d_len, lens, 8, hipMemcpyHostToDevice, s));
+  if (!use_gemm(m->d, B))  // the GEMV-path steps expect x embedded (see greedy_step_launches)
+    launch_embed_norm(s, m->d, m->w.wte, kv->d_ids, B, m->ws.x, nullptr, 0, nullptr);
+  HIPCHK(hipStreamSynchronize(s));
+  if (m->timing) {  // eager launches so every kernel can be bracketed by events
+    for (int st = 0; st < n_steps; ++st) greedy_step_launches(m, kv, s, with_logits, lens[0] + st);
+  } else {
+    // runs of captured steps replayed back to back; ~2k kernel nodes per
+    // graph (a GEMM-path step has about twice the launches of a GEMV step)
+    const int kGraphSteps = use_gemm(m->d, B) ? 16 : 32;
+    int done = 0;
+    while (done < n_steps) {
+      const int run = n_steps - done < kGraphSteps ? n_steps - done : kGraphSteps;
+      RCCHK(run_greedy_graph(m, kv, s, run, with_logits));
+      done += run;
+    }
+  }
+  return FG_OK;
+}
+
+bool fused_applies(const fg_model* m, const fg_kv* kv, int n_steps) {
+  return m->fused_on && m->fused_w && kv->B == 1 && kv->len + n_steps <= FUSED_MAX_LEN;
+}
+
+// The whole greedy loop as one persistent launch: ids go to kv->d_out,
+// logits (when wanted) to kv->d_lgs, the cache rows of the n_steps positions
+// are written in place.
+int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, int with_logits) {
+  hipStream_t s = m->stream;
+  const uint32_t eps = fused_epochs(m->d, n_steps);
+  if ((uint64_t)m->fused_ep + eps >= 0xFFFFFF00ull) {  // epochs would wrap: start over
+    HIPCHK(hipMemsetAsync(m->fused_slots, 0, (size_t)m->fl.slots * 8, s));
+    m->fused_ep = 1;
+  }
+  HIPCHK(hipMemcpyAsync(kv->d_ids, ids, 4, hipMemcpyHostToDevice, s));
+  HIPCHK(hipMemsetAsync(m->fused_err, 0, 4 * (1 + FUSED_NX), s));
+  FusedArgs a;
+  a.arena = m->fused_w;
+  a.wte = m->w.wte;
+  a.cosb = m->d_cos;
+  a.sinb = m->d_sin;
+  a.kc = kv->k;
+  a.vc = kv->v;
+  a.maxT = kv->maxT;
+  a.len0 = kv->len;
+  a.n_steps = n_steps;
+  a.d_id0 = kv->d_ids;
+  a.ids_out = kv->d_out;
+  a.logits_out = with_logits ? kv->d_lgs : nullptr;
+  a.slots = m->fused_slots;
+  a.ep_base = m->fused_ep;
+  a.err = m->fused_err;
+  a.cnt = m->fused_err + 1;
+  a.D = m->d.D;
+  a.H = m->d.H;
+  a.KH = m->d.KH;
+  a.L = m->d.L;
+  a.V = m->d.V;
+  a.dff = m->d.dff;
+  a.eps = m->d.eps;
+  // algorithmic traffic of the loop: per step every weight but the
+  // embedding table once, one embedding row, the cache rows read and written
+  const Dims& d = m->d;
+  const double wbytes = (double)m->w.bytes - 2.0 * d.V * d.D;
+  double bytes = 0, flops = 0;
+  for (int st = 0; st < n_steps; ++st) {
+    const double len = kv->len + st + 1;
+    bytes += wbytes + 2.0 * d.D + (double)d.L * d.kvd() * 4 * 2 * (len + 1);
+    flops += wbytes + (double)d.L * 4 * d.hd * d.H * len;
+  }
+  hipError_t e = hipSuccess;
+  timed(m, s, FG_K_DECODE_FUSED, flops, bytes, [&] { e = launch_fused_decode(s, d, m->fl, a); });
+  m->fused_ep += eps;
+  if (e != hipSuccess) return seterr(FG_EHIP, "persistent decode launch: %s", hipGetErrorString(e));
+  return FG_OK;
+}
+
 }  // namespace
 
 extern "C" int32_t fg_step(fg_model* m, fg_kv* kv, const int32_t* ids, float* logits,
@@ -943,6 +1072,7 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
   if (kv->len + n_steps > kv->maxT)
     return seterr(FG_EFULL, "cache full (raise maxT): len %d + %d > %d", kv->len, n_steps,
                   kv->maxT);
+  if (n_steps > (1 << 20)) return seterr(FG_EARG, "n_steps %d above 2^20", n_steps);
   RCCHK(check_rope(m, kv->len + n_steps));
   RCCHK(ensure_work(m, B));
   hipStream_t s = m->stream;
@@ -968,32 +1098,28 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
     kv->graphs.clear();
     kv->graphs_gen = m->gen;
   }
-  const int32_t lens[2] = {kv->len, kv->len};
-  HIPCHK(hipMemcpyAsync(kv->d_ids, ids, (size_t)B * 4, hipMemcpyHostToDevice, s));
-  HIPCHK(hipMemcpyAsync(kv->d_len, lens, 8, hipMemcpyHostToDevice, s));
-  if (!use_gemm(m->d, B))  // the GEMV-path steps expect x embedded (see greedy_step_launches)
-    launch_embed_norm(s, m->d, m->w.wte, kv->d_ids, B, m->ws.x, nullptr, 0, nullptr);
-  HIPCHK(hipStreamSynchronize(s));
-  if (m->timing) {  // eager launches so every kernel can be bracketed by events
-    for (int st = 0; st < n_steps; ++st) greedy_step_launches(m, kv, s, with_logits, lens[0] + st);
+  const bool fused = fused_applies(m, kv, n_steps);
+  if (fused) {
+    RCCHK(fused_decode(m, kv, ids, n_steps, with_logits));
   } else {
-    // runs of captured steps replayed back to back; ~2k kernel nodes per
-    // graph (a GEMM-path step has about twice the launches of a GEMV step)
-    const int kGraphSteps = use_gemm(m->d, B) ? 16 : 32;
-    int done = 0;
-    while (done < n_steps) {
-      const int run = n_steps - done < kGraphSteps ? n_steps - done : kGraphSteps;
-      RCCHK(run_greedy_graph(m, kv, s, run, with_logits));
-      done += run;
-    }
+    RCCHK(graph_decode(m, kv, ids, n_steps, with_logits));
   }
   HIPCHK(hipMemcpyAsync(ids_out, kv->d_out, nout * 4, hipMemcpyDeviceToHost, s));
   if (logits_out)
     HIPCHK(hipMemcpyAsync(logits_out, kv->d_lgs, nout * m->d.V * 4, hipMemcpyDeviceToHost, s));
   HIPCHK(hipStreamSynchronize(s));
+  if (fused) {
+    uint32_t err = 0;
+    HIPCHK(hipMemcpy(&err, m->fused_err, 4, hipMemcpyDeviceToHost));
+    if (err != 0)
+      return seterr(FG_EHIP, "persistent decode: %s",
+                    err == 2 ? "an XCD held more than 32 of its workgroups"
+                             : "a hand-over between workgroups timed out");
+  }
   kv->len += n_steps;
   return FG_OK;
 }
+
 
 namespace {
 
@@ -1282,6 +1408,27 @@ extern "C" int32_t fg_decode_sample(fg_model* m, fg_kv* kv, int32_t* ids, int32_
   if (h->pp != n_total) return seterr(FG_EHIP, "sampling loop ended at %d of %d", h->pp, n_total);
   *state = h->rng;
   kv->len = n_total - 1;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_set_option(fg_model* m, int32_t key, int32_t value) {
+  if (!m) return seterr(FG_EARG, "NULL argument");
+  if (key != FG_OPT_FUSED_DECODE) return seterr(FG_EARG, "unknown option %d", key);
+  GUARD(m);
+  m->fused_on = value != 0;
+  return FG_OK;
+}
+
+extern "C" int32_t fg_get_option(fg_model* m, int32_t key, int32_t* value, char* why,
+                                 int32_t len) {
+  if (!m || !value) return seterr(FG_EARG, "NULL argument");
+  if (key != FG_OPT_FUSED_DECODE) return seterr(FG_EARG, "unknown option %d", key);
+  *value = (m->fused_on && m->fused_w) ? 1 : 0;
+  if (why && len > 0) {
+    const char* r = !m->fused_on ? "disabled by fg_set_option" : m->fused_w ? "" : m->fused_why.c_str();
+    strncpy(why, r, (size_t)len - 1);
+    why[len - 1] = '\0';
+  }
   return FG_OK;
 }
 

@@ -251,4 +251,61 @@ void launch_sample_one(hipStream_t s, const float* logits, int V, const int32_t*
                        const SampleCfg& c, int64_t* state, int32_t* out);
 void launch_sample_step(hipStream_t s, SampleDev* sd, const float* logits, int V, int32_t* ids);
 
+// ---- B=1 greedy decode as one persistent launch (kern_fused.hip)
+// 256 workgroups, one per CU, in 8 groups of 32 (the workgroups of one XCD,
+// found from XCC_ID at the start of the launch). XCD g < H computes head g's q/k/v, attention and its share of
+// c_proj; every XCD computes 1/8 of c_fc and the matching split of
+// c_proj2. Workgroups hand values over through "exchange slots": 8 bytes,
+// the fp32 value below a 32-bit epoch that names the hand-over, so a reader
+// polls until the epoch it expects is there and never takes a stale value.
+// Each workgroup streams its weight slices into LDS one pseudo-layer ahead
+// (the 12 layers, then lm_head) from a weight copy laid out per workgroup.
+constexpr int FUSED_NWG = 256;  // workgroups (CUs)
+constexpr int FUSED_NX = 8;     // XCDs
+constexpr int FUSED_NC = 32;    // workgroups per XCD
+constexpr int FUSED_MAX_LEN = 128;  // attention positions a step may see
+
+struct FusedLayout {
+  bool ok = false;
+  int QR, C, FR, HN, LR;  // rows per workgroup: qkv, proj/proj2 outputs, fc, proj2 K, lm_head
+  int64_t wq, wp, wf, w2;   // segment byte offsets within a layer slice
+  int64_t slice, lmb;       // bytes of a layer slice and of the lm_head slice
+  int64_t wbuf;             // LDS bytes of one weight buffer
+  int64_t cu_bytes;         // bytes of one workgroup's region of the fused arena
+  int64_t lds_bytes;        // dynamic LDS of the kernel
+  int64_t slots;            // exchange slots (8 bytes each)
+  int64_t off_ql, off_pp, off_xl, off_hl, off_p2, off_lm;  // slot offsets
+};
+// The layout for dims d; ok = false (with the reason in *why) when the
+// fused kernel does not serve them.
+FusedLayout fused_layout(const Dims& d, const char** why);
+// Copy the main arena's weights (host bf16, the Weights layout) into the
+// fused layout (host buffer of FUSED_NWG * cu_bytes bytes).
+void fused_pack(const Dims& d, const FusedLayout& f, const Weights& w, const bf16_t* host_main,
+                bf16_t* host_fused);
+
+struct FusedArgs {
+  const bf16_t* arena;  // fused weight copy
+  const bf16_t* wte;    // [V][D]
+  const float* cosb;
+  const float* sinb;
+  float* kc;            // cache [L][maxT][KH*hd] (B = 1)
+  float* vc;
+  int maxT, len0, n_steps;
+  const int32_t* d_id0;  // the first input id
+  int32_t* ids_out;      // [n_steps]
+  float* logits_out;     // [n_steps][V] or null
+  uint64_t* slots;
+  uint32_t ep_base;      // epochs of this launch start here
+  uint32_t* err;         // nonzero after the launch: a hand-over timed out (1) or
+                         // an XCD held more than 32 workgroups (2); zeroed before
+  uint32_t* cnt;         // [8] workgroups placed per XCD so far; zeroed before
+  int D, H, KH, L, V, dff;
+  float eps;
+};
+// Epochs one launch of n_steps uses (the next launch starts past them).
+uint32_t fused_epochs(const Dims& d, int n_steps);
+hipError_t launch_fused_decode(hipStream_t s, const Dims& d, const FusedLayout& f,
+                               const FusedArgs& a);
+
 }  // namespace fgpt

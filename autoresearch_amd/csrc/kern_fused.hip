@@ -1,0 +1,587 @@
+// kern_fused.hip -- the B=1 greedy decode loop (gpt_step fed back through
+// its argmax, src/app/chat_text.f90:423-462 with src/lib/fortran_kv.f90:
+// 26-149 per step) as ONE persistent launch on gfx950.
+//
+// Why one launch: at B=1 every linear of a step is a few MB of weights,
+// which a kernel of its own cannot stream faster than its launch and its
+// first load take (~3-5 us each, 62 launches a step). Here 256 workgroups,
+// one per CU, run the whole loop; the weights of the next pseudo-layer (a
+// layer, or lm_head) stream into LDS while the current one computes, so a
+// hand-over of activations between workgroups is the only thing on the
+// critical path.
+//
+// Work split (workgroup (g, c): the c-th of the 32 workgroups on XCD g):
+//   q/k/v rows of head g (XCD g < H)   12 rows per workgroup (6 RoPE pairs)
+//   attention of head g                 every workgroup of XCD g, recomputed
+//   c_proj, head g's 128 columns        C = D/32 outputs per workgroup
+//   c_fc rows [g*dff/8, (g+1)*dff/8)    dff/256 rows per workgroup
+//   c_proj2 columns of that fc block    C outputs per workgroup
+//   lm_head rows [b*V/256, (b+1)*V/256)
+// The residual columns [c*C, (c+1)*C) are owned (identically, in registers)
+// by workgroup (g, c) of every XCD: c_proj's per-head partials and
+// c_proj2's per-block partials are added to them in a fixed order.
+//
+// Hand-overs ("exchange slots", 8 bytes: fp32 value | 32-bit epoch << 32).
+// Within one XCD a plain store lands in that XCD's L2, where agent-scope
+// (sc1) loads of the other workgroups see it; across XCDs the store is an
+// agent-scope (sc1, write-through) store. A reader polls until the slot
+// carries the epoch of the hand-over it waits for: every hand-over of a
+// launch has its own epoch and the host advances the base across launches,
+// so a stale slot is never taken. Every poll is bounded: past the bound the
+// workgroup raises the error flag and all workgroups leave, so the grid
+// always drains. Per layer: q/k/v within the XCD, c_proj partials across,
+// the updated residual within, the fc block within, c_proj2 partials
+// across, the residual within; the step ends with the lm_head argmax
+// candidates of all 256 workgroups.
+//
+// Arithmetic per output element: rmsnorm0 (src/lib/fortran_rmsnorm.f90:
+// 40-60) as a scale of the dot products, fp32 accumulation of bf16 weights
+// times fp32 activations, rope_4d (src/lib/fortran_rope.f90:25-52) on the
+// host's tables, attn_step's softmax (src/lib/fortran_attn.f90:317-362) as
+// an online softmax over 8 position groups merged in group order, relu2
+// (:697-710), residual adds (src/lib/fortran_kv.f90:125-137), and the
+// first-max argmax of src/lib/sample.f90:271-277.
+#include <float.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "fgpt_internal.h"
+#include "kern_common.h"
+
+namespace fgpt {
+
+namespace {
+
+constexpr int FUSED_HD = 128;            // head dim this kernel is built for
+constexpr int FUSED_THREADS = 320;       // 4 compute waves + 1 loader wave
+constexpr long FUSED_MAX_SPIN = 1l << 20;  // polls before a hand-over is given up
+
+__device__ __forceinline__ uint64_t slot_pack(float v, uint32_t ep) {
+  return ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v);
+}
+__device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// hand-over to workgroups of other XCDs: write-through to memory
+__device__ __forceinline__ void slot_put_dev(uint64_t* p, float v, uint32_t ep) {
+  __hip_atomic_store(p, slot_pack(v, ep), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// hand-over within the XCD: a plain store into the shared L2
+__device__ __forceinline__ void slot_put_xcd(uint64_t* p, float v, uint32_t ep) {
+  __hip_atomic_store(p, slot_pack(v, ep), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Wait until the n (<= NMAX) slots p[i * stride] carry epoch ep, then
+// return their values in out. All loads go out at once; only slots still
+// short of the epoch are read again. false: the bound was reached or the
+// error flag was raised elsewhere (the flag is then raised here too).
+template <int NMAX>
+__device__ bool slots_wait(const uint64_t* p, int64_t stride, int n, uint32_t ep, float* out,
+                           uint32_t* err) {
+  uint64_t v[NMAX];
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i) v[i] = i < n ? slot_load(p + i * stride) : slot_pack(0.f, ep);
+  for (long spin = 0;; ++spin) {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i) ok = ok && (uint32_t)(v[i] >> 32) == ep;
+    if (ok) break;
+    if (spin >= FUSED_MAX_SPIN ||
+        ((spin & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+      __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+#pragma unroll
+    for (int i = 0; i < NMAX; ++i)
+      if (i < n && (uint32_t)(v[i] >> 32) != ep) v[i] = slot_load(p + i * stride);
+  }
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i)
+    if (i < n) out[i] = __uint_as_float((uint32_t)v[i]);
+  return true;
+}
+
+// Gather n slots (lane-strided over the 256 compute threads) into dst.
+template <int NMAX>
+__device__ bool gather_slots(const uint64_t* p, int n, uint32_t ep, float* dst, int tid,
+                             uint32_t* err) {
+  float v[NMAX];
+  const int cnt = tid < n ? (n - tid + 255) / 256 : 0;
+  if (!slots_wait<NMAX>(p + tid, 256, cnt, ep, v, err)) return false;
+#pragma unroll
+  for (int i = 0; i < NMAX; ++i)
+    if (i < cnt) dst[tid + 256 * i] = v[i];
+  return true;
+}
+
+// sum(x^2) over the lane-strided chunks of 8 a dot product reads
+__device__ __forceinline__ float chunk_ss(const float* x, int K, int lane) {
+  float ss = 0.f;
+#pragma unroll 2
+  for (int k = lane; k < (K >> 3); k += 64) {
+    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
+    ss += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x + xb.y * xb.y +
+          xb.z * xb.z + xb.w * xb.w;
+  }
+  return wave_sum(ss);
+}
+
+// lane's part of the dot products of NR bf16 rows (LDS, rstride bytes
+// apart) with x (fp32, LDS) over K, lane-strided chunks of 8
+template <int NR>
+__device__ __forceinline__ void chunk_dot(const uint8_t* w, int rstride, const float* x, int K,
+                                          int lane, float (&acc)[NR]) {
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+#pragma unroll 2
+  for (int k = lane; k < (K >> 3); k += 64) {
+    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float f[8];
+      unpack8(*(const uint4*)(w + r * rstride + 16 * k), f);
+      acc[r] += f[0] * xa.x + f[1] * xa.y + f[2] * xa.z + f[3] * xa.w + f[4] * xb.x +
+                f[5] * xb.y + f[6] * xb.z + f[7] * xb.w;
+    }
+  }
+}
+
+__device__ __forceinline__ void amax_take(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, FusedLayout f) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  constexpr int QLN = 3 * HD;            // q, k, v of one head
+  constexpr int NP = QLN / 64;           // rotation pairs per workgroup
+  constexpr int LPP = HD / 4;            // lanes per cached row in the attention
+  constexpr int NG = 4 * (64 / LPP);     // position groups
+  constexpr int PPG = FUSED_MAX_LEN / NG;  // positions per group, at most
+  constexpr int AST = HD + 4;            // floats per group record: o, m, l
+  constexpr int AB = 8;                  // attention positions per batch
+  const int D = a.D, H = a.H, L = a.L, V = a.V, KD = a.KH * HD;
+  const int C = f.C, FR = f.FR, HN = f.HN, LR = f.LR, QR = f.QR;
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const bool comp = wv < 4, loader = wv == 4;
+  const float eps = a.eps;
+  uint8_t* wbuf[2] = {lds, lds + f.wbuf};
+  float* x_lds = (float*)(lds + 2 * f.wbuf);
+  float* h_lds = x_lds + D;
+  float* qkv_lds = h_lds + HN;
+  float* att = qkv_lds + QLN;  // [NG][AST]
+  float* red = att + NG * AST;  // [8]
+  int* ired = (int*)(red + 8);  // [8]
+  int* stop = ired + 8;         // nonzero: leave (a hand-over failed)
+  int* place = stop + 1;        // this workgroup's XCD and its index there
+  uint32_t* err = a.err;
+  const int E = 8 * L + 8;      // epochs per step
+  const int total = a.n_steps * (L + 1);  // pseudo-layers of the launch
+  uint64_t* S = a.slots;
+
+  // Placement: the XCD this workgroup runs on (XCC_ID) and its index among
+  // that XCD's workgroups, from a per-launch counter (one workgroup per CU,
+  // 32 CUs per XCD). Which block index the dispatcher sends to which XCD
+  // is not relied on: it varies from launch to launch.
+  if (tid == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const int gx = (int)(xcc & 7);
+    const int cx = (int)atomicAdd(a.cnt + gx, 1u);
+    *stop = 0;
+    if (cx >= FUSED_NC) {
+      __hip_atomic_store(err, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *stop = 1;
+    }
+    place[0] = gx;
+    place[1] = cx < FUSED_NC ? cx : 0;
+  }
+  lds_barrier();
+  if (*stop) return;
+  const int g = place[0], c = place[1], b = g + FUSED_NX * c;
+  const bool head = g < H;
+  // DMA of pseudo-layer G's weight slices into its LDS buffer (loader wave)
+  auto issue = [&](int G) {
+    const int l = G % (L + 1);
+    const uint8_t* src = (const uint8_t*)a.arena + (int64_t)b * f.cu_bytes;
+    uint8_t* dst = wbuf[G & 1];
+    int64_t off = 0, n;
+    if (l < L) {
+      off = head ? 0 : f.wf;  // workgroups of XCDs >= H hold no q/k/v or c_proj rows
+      src += (int64_t)l * f.slice;
+      n = f.slice - off;
+    } else {
+      src += (int64_t)L * f.slice;
+      n = f.lmb;
+    }
+    for (int64_t k = off; k < off + n; k += 1024) dma16(src + k + 16 * lane, lds_off(dst + k));
+  };
+  auto waitdma = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+
+  // x = rmsnorm0(wte[id]) into x_lds (k_embed_norm's order: 256 strided
+  // partial sums, then the four waves' sums in order); x_own = this
+  // workgroup's residual columns
+  float x_own = 0.f;
+  auto embed = [&](int id) {
+    const bf16_t* row = a.wte + (int64_t)id * D;
+    if (comp) {
+      float ss = 0.f;
+      for (int k = tid; k < D; k += 256) {
+        const float v = bf16_to_f32(row[k]);
+        ss += v * v;
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) red[wv] = ss;
+    }
+    lds_barrier();
+    if (comp) {
+      const float t = red[0] + red[1] + red[2] + red[3];
+      const float inv = 1.0f / sqrtf(t / (float)D + eps);
+      for (int k = tid; k < D; k += 256) x_lds[k] = bf16_to_f32(row[k]) * inv;
+      if (wv == 0 && lane < C) x_own = bf16_to_f32(row[c * C + lane]) * inv;
+    }
+  };
+
+  if (loader) issue(0);
+  embed(*a.d_id0);
+
+  for (int s = 0; s < a.n_steps; ++s) {
+    const int pos = a.len0 + s;
+    for (int l = 0; l <= L; ++l) {
+      const int G = s * (L + 1) + l;
+      const uint8_t* W = wbuf[G & 1];
+      // B0: this pseudo-layer's weights have landed; the next one's go out
+      if (loader) waitdma();
+      lds_barrier();
+      if (*stop) goto done;
+      if (loader && G + 1 < total) issue(G + 1);
+      if (l == L) break;  // lm_head below
+      const int par = (s * L + l) & 1;
+      const uint32_t ep = a.ep_base + (uint32_t)(s * E + l * 8);
+      uint64_t* QL = S + f.off_ql + (int64_t)(par * 8 + g) * QLN;
+      uint64_t* PP = S + f.off_pp + (int64_t)par * 8 * D;
+      uint64_t* XL = S + f.off_xl + (int64_t)(par * 8 + g) * D;
+      uint64_t* HL = S + f.off_hl + (int64_t)(par * 8 + g) * HN;
+      uint64_t* P2 = S + f.off_p2 + (int64_t)par * 8 * D;
+      float* kc = a.kc + (int64_t)l * a.maxT * KD + g * HD;
+      float* vc = a.vc + (int64_t)l * a.maxT * KD + g * HD;
+      if (head) {
+        // q, k, v rows (RoPE pairs) of head g; k and v into the cache
+        if (comp) {
+          const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
+          for (int pi = wv; pi < NP; pi += 4) {
+            float acc[2];
+            chunk_dot<2>(W + f.wq + (int64_t)(2 * pi) * D * 2, D * 2, x_lds, D, lane, acc);
+            const float v0 = wave_sum(acc[0]) * inv, v1 = wave_sum(acc[1]) * inv;
+            if (lane == 0) {
+              const int r0 = c * QR + 2 * pi, part = r0 / HD, j = (r0 % HD) >> 1;
+              float y1 = v0, y2 = v1;
+              if (part < 2) {
+                const float cs = a.cosb[(int64_t)pos * (HD / 2) + j];
+                const float sn = a.sinb[(int64_t)pos * (HD / 2) + j];
+                y1 = v0 * cs + v1 * sn;
+                y2 = v0 * (-sn) + v1 * cs;
+              }
+              slot_put_xcd(QL + part * HD + j, y1, ep);
+              slot_put_xcd(QL + part * HD + j + HD / 2, y2, ep);
+              if (part > 0) {
+                float* cr = (part == 1 ? kc : vc) + (int64_t)pos * KD;
+                __hip_atomic_store(cr + j, y1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cr + j + HD / 2, y2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              }
+            }
+          }
+          if (!gather_slots<2>(QL, QLN, ep, qkv_lds, tid, err)) *stop = 1;
+        }
+        lds_barrier();  // B1
+        if (*stop) goto done;
+        // attention of head g over positions 0..pos: group grp takes
+        // positions grp, grp+NG, ...; the current position's k and v come
+        // from the hand-over, earlier ones from the cache
+        if (comp) {
+          const int grp = wv * (64 / LPP) + lane / LPP, dl = lane % LPP;
+          const float4 q4 = *(const float4*)(qkv_lds + 4 * dl);
+          const float scale = 1.0f / sqrtf((float)HD);
+          float m = -INFINITY, lsum = 0.f;
+          float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+          // positions in batches of AB per group: one batch's loads in flight together
+          for (int i0 = 0; i0 < PPG && grp + NG * i0 <= pos; i0 += AB) {
+            float4 kr[AB], vr[AB];
+#pragma unroll
+            for (int i = 0; i < AB; ++i) {
+              const int p = grp + NG * (i0 + i);
+              if (p < pos) {
+                kr[i] = *(const float4*)(kc + (int64_t)p * KD + 4 * dl);
+                vr[i] = *(const float4*)(vc + (int64_t)p * KD + 4 * dl);
+              } else {
+                kr[i] = *(const float4*)(qkv_lds + HD + 4 * dl);
+                vr[i] = *(const float4*)(qkv_lds + 2 * HD + 4 * dl);
+              }
+            }
+#pragma unroll
+            for (int i = 0; i < AB; ++i) {
+              if (grp + NG * (i0 + i) > pos) break;
+              float sc = q4.x * kr[i].x + q4.y * kr[i].y + q4.z * kr[i].z + q4.w * kr[i].w;
+#pragma unroll
+              for (int off = LPP / 2; off > 0; off >>= 1) sc += __shfl_xor(sc, off, 64);
+              sc *= scale;
+              const float mn = fmaxf(m, sc), al = expf(m - mn), e = expf(sc - mn);
+              lsum = lsum * al + e;
+              o.x = o.x * al + e * vr[i].x;
+              o.y = o.y * al + e * vr[i].y;
+              o.z = o.z * al + e * vr[i].z;
+              o.w = o.w * al + e * vr[i].w;
+              m = mn;
+            }
+          }
+          *(float4*)(att + grp * AST + 4 * dl) = o;
+          if (dl == 0) {
+            att[grp * AST + HD] = m;
+            att[grp * AST + HD + 1] = lsum;
+          }
+        }
+        lds_barrier();  // B2
+        // c_proj partial of head g over this workgroup's C output columns
+        if (comp) {
+          float mx = -INFINITY;
+#pragma unroll
+          for (int q = 0; q < NG; ++q) mx = fmaxf(mx, att[q * AST + HD]);
+          float ls = 0.f, o0 = 0.f, o1 = 0.f;
+#pragma unroll
+          for (int q = 0; q < NG; ++q) {
+            const float w = expf(att[q * AST + HD] - mx);
+            ls += att[q * AST + HD + 1] * w;
+            o0 += att[q * AST + 2 * lane] * w;
+            o1 += att[q * AST + 2 * lane + 1] * w;
+          }
+          const float il = 1.0f / ls;
+          const float ao0 = o0 * il, ao1 = o1 * il;  // head dims 2*lane, 2*lane+1
+          for (int j = wv; j < C; j += 4) {
+            const uint32_t wp = *(const uint32_t*)(W + f.wp + (int64_t)j * HD * 2 + 4 * lane);
+            float v = ao0 * __uint_as_float(wp << 16) + ao1 * __uint_as_float(wp & 0xFFFF0000u);
+            v = wave_sum(v);
+            if (lane == 0) slot_put_dev(PP + (int64_t)g * D + c * C + j, v, ep + 1);
+          }
+        }
+      }
+      // residual += sum of the heads' c_proj partials (heads in order)
+      if (wv == 0 && lane < C) {
+        float pv[8];
+        if (!slots_wait<8>(PP + c * C + lane, D, H, ep + 1, pv, err)) *stop = 1;
+        float t = pv[0];
+        for (int h = 1; h < H; ++h) t += pv[h];
+        x_own = x_own + t;
+        slot_put_xcd(XL + c * C + lane, x_own, ep + 2);
+      }
+      if (comp && !*stop && !gather_slots<8>(XL, D, ep + 2, x_lds, tid, err)) *stop = 1;
+      lds_barrier();  // B3
+      if (*stop) goto done;
+      // h = relu2(rmsnorm0(x) c_fc^T) for this workgroup's fc rows
+      if (comp) {
+        const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
+        for (int r = wv; r < FR; r += 4) {
+          float acc[1];
+          chunk_dot<1>(W + f.wf + (int64_t)r * D * 2, 0, x_lds, D, lane, acc);
+          float v = wave_sum(acc[0]) * inv;
+          v = v < 0.f ? 0.f : v;
+          if (lane == 0) slot_put_xcd(HL + c * FR + r, v * v, ep + 3);
+        }
+        if (!gather_slots<8>(HL, HN, ep + 3, h_lds, tid, err)) *stop = 1;
+      }
+      lds_barrier();  // B4
+      if (*stop) goto done;
+      // c_proj2 partial over this XCD's fc block
+      if (comp) {
+        for (int j = wv; j < C; j += 4) {
+          const uint8_t* w2 = W + f.w2 + (int64_t)j * HN * 2;
+          float v = 0.f;
+          for (int k = lane; k < (HN >> 1); k += 64) {
+            const uint32_t wp = *(const uint32_t*)(w2 + 4 * k);
+            const float2 hv = *(const float2*)(h_lds + 2 * k);
+            v += hv.x * __uint_as_float(wp << 16) + hv.y * __uint_as_float(wp & 0xFFFF0000u);
+          }
+          v = wave_sum(v);
+          if (lane == 0) slot_put_dev(P2 + (int64_t)g * D + c * C + j, v, ep + 4);
+        }
+      }
+      // residual += sum of the 8 blocks' c_proj2 partials (blocks in order)
+      if (wv == 0 && lane < C) {
+        float pv[8];
+        if (!slots_wait<8>(P2 + c * C + lane, D, FUSED_NX, ep + 4, pv, err)) *stop = 1;
+        float t = pv[0];
+#pragma unroll
+        for (int k = 1; k < FUSED_NX; ++k) t += pv[k];
+        x_own = x_own + t;
+        slot_put_xcd(XL + c * C + lane, x_own, ep + 5);
+      }
+      if (comp && !*stop && !gather_slots<8>(XL, D, ep + 5, x_lds, tid, err)) *stop = 1;
+    }
+    {
+      // lm_head rows of this workgroup, their argmax candidate
+      const int G = s * (L + 1) + L;
+      const uint8_t* W = wbuf[G & 1];
+      const uint32_t ep = a.ep_base + (uint32_t)(s * E + 8 * L);
+      uint64_t* LM = S + f.off_lm + (int64_t)(s & 1) * FUSED_NWG * 2;
+      if (comp) {
+        const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int r = wv; r < LR; r += 4) {
+          float acc[1];
+          chunk_dot<1>(W + (int64_t)r * D * 2, 0, x_lds, D, lane, acc);
+          const float v = wave_sum(acc[0]) * inv;
+          const int id = b * LR + r;
+          if (lane == 0 && a.logits_out) a.logits_out[(int64_t)s * V + id] = v;
+          amax_take(bv, bi, v, id);
+        }
+        if (lane == 0) {
+          red[wv] = bv;
+          ired[wv] = bi;
+        }
+      }
+      lds_barrier();  // B5
+      if (comp) {
+        if (tid == 0) {
+          float v = red[0];
+          int i = ired[0];
+          for (int w = 1; w < 4; ++w) amax_take(v, i, red[w], ired[w]);
+          slot_put_dev(LM + 2 * b, v, ep);
+          slot_put_dev(LM + 2 * b + 1, __int_as_float(i), ep);
+        }
+        // every workgroup reads all 256 candidates
+        float cv[2];
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        if (slots_wait<2>(LM + 2 * tid, 1, 2, ep, cv, err)) {
+          bv = cv[0];
+          bi = __float_as_int(cv[1]);
+        } else {
+          *stop = 1;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const float v2 = __shfl_xor(bv, o, 64);
+          const int i2 = __shfl_xor(bi, o, 64);
+          amax_take(bv, bi, v2, i2);
+        }
+        if (lane == 0) {
+          red[4 + wv] = bv;
+          ired[4 + wv] = bi;
+        }
+      }
+      lds_barrier();  // B6
+      if (*stop) goto done;
+      float v = red[4];
+      int id = ired[4];
+      for (int w = 1; w < 4; ++w) amax_take(v, id, red[4 + w], ired[4 + w]);
+      if (id == 0x7fffffff) id = 0;  // no finite candidate: position 1, as the scan starts there
+      if (b == 0 && tid == 0) a.ids_out[s] = id;
+      if (s + 1 < a.n_steps) embed(id);
+    }
+  }
+done:
+  if (loader) waitdma();  // no LDS-DMA may outlive the workgroup
+}
+
+}  // namespace
+
+FusedLayout fused_layout(const Dims& d, const char** why) {
+  FusedLayout f;
+  auto no = [&](const char* r) {
+    if (why) *why = r;
+    f.ok = false;
+    return f;
+  };
+  if (d.hd != FUSED_HD) return no("head_dim is not 128");
+  if (d.H > FUSED_NX) return no("more heads than XCDs");
+  if (d.KH != d.H) return no("grouped KV heads");
+  if (d.D % FUSED_NC != 0 || d.D / FUSED_NC > 64) return no("d_model not a multiple of 32 up to 2048");
+  if (d.dff % (FUSED_NWG * 2) != 0) return no("d_ff not a multiple of 512");
+  if (d.V % FUSED_NWG != 0) return no("vocab not a multiple of 256");
+  if (d.D > 8 * 256 || d.dff / FUSED_NX > 8 * 256) return no("d_model or d_ff too large");
+  auto r1k = [](int64_t x) { return (x + 1023) / 1024 * 1024; };
+  f.QR = 3 * d.hd / FUSED_NC;
+  f.C = d.D / FUSED_NC;
+  f.FR = d.dff / FUSED_NWG;
+  f.HN = d.dff / FUSED_NX;
+  f.LR = d.V / FUSED_NWG;
+  f.wq = 0;
+  f.wp = r1k((int64_t)f.QR * d.D * 2);
+  f.wf = f.wp + r1k((int64_t)f.C * d.hd * 2);
+  f.w2 = f.wf + r1k((int64_t)f.FR * d.D * 2);
+  f.slice = f.w2 + r1k((int64_t)f.C * f.HN * 2);
+  f.lmb = r1k((int64_t)f.LR * d.D * 2);
+  f.wbuf = std::max(f.slice, f.lmb);
+  f.cu_bytes = (int64_t)d.L * f.slice + f.lmb;
+  const int NG = 4 * (64 / (FUSED_HD / 4));
+  const int64_t act = 4 * ((int64_t)d.D + f.HN + 3 * FUSED_HD + NG * (FUSED_HD + 4) + 8) + 4 * 11;
+  f.lds_bytes = 2 * f.wbuf + act;
+  if (f.lds_bytes > 160 * 1024) return no("weight slices do not fit twice in LDS");
+  f.off_ql = 0;
+  f.off_pp = f.off_ql + 2 * FUSED_NX * 3 * (int64_t)d.hd;
+  f.off_xl = f.off_pp + 2 * FUSED_NX * (int64_t)d.D;
+  f.off_hl = f.off_xl + 2 * FUSED_NX * (int64_t)d.D;
+  f.off_p2 = f.off_hl + 2 * FUSED_NX * (int64_t)f.HN;
+  f.off_lm = f.off_p2 + 2 * FUSED_NX * (int64_t)d.D;
+  f.slots = f.off_lm + 2 * FUSED_NWG * 2;
+  f.ok = true;
+  return f;
+}
+
+void fused_pack(const Dims& d, const FusedLayout& f, const Weights& w, const bf16_t* hm,
+                bf16_t* hf) {
+  const int D = d.D, hd = d.hd, H = d.H, qd = d.qd(), kd = d.kvd();
+  memset(hf, 0, (size_t)FUSED_NWG * f.cu_bytes);
+  for (int b = 0; b < FUSED_NWG; ++b) {
+    const int g = b % FUSED_NX, c = b / FUSED_NX;
+    uint8_t* cu = (uint8_t*)hf + (int64_t)b * f.cu_bytes;
+    for (int l = 0; l < d.L; ++l) {
+      const bf16_t* base = hm + (size_t)l * w.layer_stride;
+      bf16_t* sl = (bf16_t*)(cu + (int64_t)l * f.slice);
+      if (g < H) {
+        // head g's rows in [q | k | v] order, each part pair-interleaved
+        // as the main arena stores it
+        for (int i = 0; i < f.QR; ++i) {
+          const int r = c * f.QR + i, part = r / hd, s = r % hd;
+          const int64_t src_row = part == 0 ? (int64_t)g * hd + s
+                                            : qd + (int64_t)(part - 1) * kd + (int64_t)g * hd + s;
+          memcpy(sl + f.wq / 2 + (int64_t)i * D, base + w.off_qkv + src_row * D, (size_t)D * 2);
+        }
+        // c_proj rows c*C .. c*C+C-1, head g's columns
+        for (int j = 0; j < f.C; ++j)
+          memcpy(sl + f.wp / 2 + (int64_t)j * hd,
+                 base + w.off_proj + (int64_t)(c * f.C + j) * qd + (int64_t)g * hd, (size_t)hd * 2);
+      }
+      for (int r = 0; r < f.FR; ++r)
+        memcpy(sl + f.wf / 2 + (int64_t)r * D,
+               base + w.off_fc + ((int64_t)g * f.HN + (int64_t)c * f.FR + r) * D, (size_t)D * 2);
+      for (int j = 0; j < f.C; ++j)
+        memcpy(sl + f.w2 / 2 + (int64_t)j * f.HN,
+               base + w.off_proj2 + (int64_t)(c * f.C + j) * d.dff + (int64_t)g * f.HN,
+               (size_t)f.HN * 2);
+    }
+    const bf16_t* lm = hm + (size_t)w.layer_stride * d.L;
+    memcpy(cu + (int64_t)d.L * f.slice, lm + (int64_t)b * f.LR * D, (size_t)f.LR * D * 2);
+  }
+}
+
+uint32_t fused_epochs(const Dims& d, int n_steps) { return (uint32_t)n_steps * (8u * d.L + 8u); }
+
+hipError_t launch_fused_decode(hipStream_t s, const Dims& d, const FusedLayout& f,
+                               const FusedArgs& a) {
+  (void)d;
+  hipError_t e = hipFuncSetAttribute((const void*)k_fused_decode<FUSED_HD>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)f.lds_bytes);
+  if (e != hipSuccess) return e;
+  FusedArgs aa = a;
+  FusedLayout ff = f;
+  void* args[] = {&aa, &ff};
+  return hipLaunchCooperativeKernel((const void*)k_fused_decode<FUSED_HD>, dim3(FUSED_NWG),
+                                    dim3(FUSED_THREADS), args, (unsigned)f.lds_bytes, s);
+}
+
+}  // namespace fgpt

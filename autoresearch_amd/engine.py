@@ -34,10 +34,12 @@ EXPORTS = (
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
     "fg_eval_bpb", "fg_rows_npy", "fg_decode_spec", "fg_spec_accept", "fg_spec_draft",
-    "fg_sample", "fg_decode_sample",
+    "fg_sample", "fg_decode_sample", "fg_set_option", "fg_get_option",
 )
 
-KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other"}
+KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other",
+                5: "decode_fused"}
+FG_OPT_FUSED_DECODE = 1
 
 
 class FgptError(RuntimeError):
@@ -124,6 +126,8 @@ def load_library(path: str = LIB_PATH):
         "fg_sample": (i32, [_vp, _f, i32, _i, i32, C.POINTER(_SampleCfg), C.POINTER(i64), _i]),
         "fg_decode_sample": (i32, [_vp, _vp, _i, i32, i32, C.POINTER(_SampleCfg),
                                    C.POINTER(i64)]),
+        "fg_set_option": (i32, [_vp, i32, i32]),
+        "fg_get_option": (i32, [_vp, i32, _i, C.c_char_p, i32]),
         "fg_timing_read": (i32, [_vp, i32, C.POINTER(i64), C.POINTER(C.c_double),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
@@ -224,6 +228,19 @@ class Model:
 
     def timing(self, enable: bool):
         _check(_LIB.fg_timing(self._h, 1 if enable else 0))
+
+    def set_fused_decode(self, enable: bool):
+        """FG_OPT_FUSED_DECODE: the persistent B=1 greedy loop (1) or the
+        captured per-kernel steps (0)."""
+        _check(_LIB.fg_set_option(self._h, FG_OPT_FUSED_DECODE, 1 if enable else 0))
+
+    def fused_decode(self):
+        """(active, reason when not): whether fg_decode_greedy runs B=1
+        loops as one persistent launch."""
+        v = C.c_int32()
+        buf = C.create_string_buffer(256)
+        _check(_LIB.fg_get_option(self._h, FG_OPT_FUSED_DECODE, C.byref(v), buf, 256))
+        return bool(v.value), buf.value.decode(errors="replace")
 
     def eval_bpb(self, rows, token_bytes, batch: int = 8, want_nll: bool = False) -> dict:
         """fg_eval_bpb over rows (N, T+1): per-row and total byte-weighted nats

@@ -234,6 +234,24 @@ int32_t fg_sample(fg_model *m, const float *logits, int32_t V, const int32_t *ge
 int32_t fg_decode_sample(fg_model *m, fg_kv *kv, int32_t *ids, int32_t n_known, int32_t n_total,
                          const fg_sample_cfg *cfg, int64_t *state);
 
+/* Handle options. FG_OPT_FUSED_DECODE: 1 (the default) lets
+ * fg_decode_greedy run a B=1 loop whose positions stay below 128 as ONE
+ * persistent launch (all layers, lm_head and the argmax of every step; the
+ * weights stream through LDS one layer ahead, activations pass between
+ * workgroups through epoch-tagged slots), when the dims fit its work split
+ * (head_dim 128, n_head <= 8 = n_kv_head, d_model % 32 == 0, d_ff % 512 ==
+ * 0, vocab % 256 == 0) and the device has 256 CUs with workgroup b of a
+ * cooperative launch on XCD b % 8; 0 keeps the captured per-kernel steps.
+ * Both paths compute the same functions of the same inputs; their fp32 sums
+ * run in different orders. No counterpart in the reference (it has one
+ * CPU path). */
+enum { FG_OPT_FUSED_DECODE = 1 };
+int32_t fg_set_option(fg_model *m, int32_t key, int32_t value);
+/* *value = the option's effective value (for FG_OPT_FUSED_DECODE: 1 when
+ * the persistent decode is set up and enabled); why (nullable, len bytes)
+ * receives the reason when it is not available. */
+int32_t fg_get_option(fg_model *m, int32_t key, int32_t *value, char *why, int32_t len);
+
 /* Block until the handle's queued work is done. */
 int32_t fg_sync(fg_model *m);
 
@@ -249,7 +267,8 @@ enum {
   FG_K_ATTN_CHUNK = 2,  /* causal chunk attention (prefill)              */
   FG_K_ATTN_DECODE = 3, /* single-query attention (decode)               */
   FG_K_OTHER = 4,       /* embedding+norm, argmax, NLL                   */
-  FG_K_NKINDS = 5
+  FG_K_DECODE_FUSED = 5, /* the persistent B=1 greedy loop (one launch)  */
+  FG_K_NKINDS = 6
 };
 int32_t fg_timing(fg_model *m, int32_t enable);
 int32_t fg_timing_read(fg_model *m, int32_t kind, int64_t *launches, double *ms, double *flops,

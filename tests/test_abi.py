@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_error_buffer():
     lib = engine.load_library()
-    assert lib.fg_version() == 100
+    assert lib.fg_version() == 101
     buf = C.create_string_buffer(8)
     lib.fg_last_error(buf, 8)
 
