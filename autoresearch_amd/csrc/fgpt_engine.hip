@@ -3,6 +3,7 @@
 // gpt_forward / gpt_step / gpt_step_multi (14NGiestas/autoresearch
 // src/lib/fortran_gpt.f90:54-199, src/lib/fortran_kv.f90:26-289).
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -1036,9 +1037,34 @@ int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, in
     bytes += wbytes + 2.0 * d.D + (double)d.L * d.kvd() * 4 * 2 * (len + 1);
     flops += wbytes + (double)d.L * 4 * d.hd * d.H * len;
   }
+  // FGPT_FUSED_TRACE=<file>: append the phase timestamps of one step (the
+  // second, when there is one) of every workgroup to <file> (diagnostic)
+  const char* tpath = getenv("FGPT_FUSED_TRACE");
+  const size_t tn = (size_t)FUSED_NWG * (d.L + 1) * 32;
+  a.trace = nullptr;  // (null: the kernel built without timestamps)
+  a.trace_step = n_steps > 1 ? 1 : 0;
+  if (tpath && *tpath) {
+    HIPCHK(hipMalloc((void**)&a.trace, tn * 8));
+    HIPCHK(hipMemsetAsync(a.trace, 0, tn * 8, s));
+  }
   hipError_t e = hipSuccess;
   timed(m, s, FG_K_DECODE_FUSED, flops, bytes, [&] { e = launch_fused_decode(s, d, m->fl, a); });
   m->fused_ep += eps;
+  if (a.trace) {
+    std::vector<uint64_t> ht(tn);
+    if (e == hipSuccess) e = hipMemcpyAsync(ht.data(), a.trace, tn * 8, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(a.trace);
+    if (e == hipSuccess) {
+      FILE* fp = fopen(tpath, "ab");
+      if (fp) {
+        const int32_t hdr[4] = {FUSED_NWG, d.L + 1, 32, n_steps};
+        fwrite(hdr, 4, 4, fp);
+        fwrite(ht.data(), 8, tn, fp);
+        fclose(fp);
+      }
+    }
+  }
   if (e != hipSuccess) return seterr(FG_EHIP, "persistent decode launch: %s", hipGetErrorString(e));
   return FG_OK;
 }

@@ -302,6 +302,8 @@ struct FusedArgs {
   uint32_t* cnt;         // [8] workgroups placed per XCD so far; zeroed before
   int D, H, KH, L, V, dff;
   float eps;
+  uint64_t* trace;       // null, or [256][L+1][32] phase timestamps of step trace_step
+  int trace_step;
 };
 // Epochs one launch of n_steps uses (the next launch starts past them).
 uint32_t fused_epochs(const Dims& d, int n_steps);

@@ -147,6 +147,48 @@ __device__ __forceinline__ void chunk_dot(const uint8_t* w, int rstride, const f
   }
 }
 
+// chunk_dot that also returns the lane's sum of x^2 over the chunks it read
+template <int NR>
+__device__ __forceinline__ float chunk_dot_ss(const uint8_t* w, int rstride, const float* x, int K,
+                                              int lane, float (&acc)[NR]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+#pragma unroll 2
+  for (int k = lane; k < (K >> 3); k += 64) {
+    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
+    ss += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x + xb.y * xb.y +
+          xb.z * xb.z + xb.w * xb.w;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float f[8];
+      unpack8(*(const uint4*)(w + r * rstride + 16 * k), f);
+      acc[r] += f[0] * xa.x + f[1] * xa.y + f[2] * xa.z + f[3] * xa.w + f[4] * xb.x +
+                f[5] * xb.y + f[6] * xb.z + f[7] * xb.w;
+    }
+  }
+  return ss;
+}
+
+// chunk_dot for NR rows at arbitrary byte offsets from w
+template <int NR>
+__device__ __forceinline__ void chunk_dot_at(const uint8_t* w, const int (&roff)[NR], const float* x,
+                                             int K, int lane, float (&acc)[NR]) {
+#pragma unroll
+  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
+#pragma unroll 2
+  for (int k = lane; k < (K >> 3); k += 64) {
+    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float f[8];
+      unpack8(*(const uint4*)(w + roff[r] + 16 * k), f);
+      acc[r] += f[0] * xa.x + f[1] * xa.y + f[2] * xa.z + f[3] * xa.w + f[4] * xb.x +
+                f[5] * xb.y + f[6] * xb.z + f[7] * xb.w;
+    }
+  }
+}
+
 __device__ __forceinline__ void amax_take(float& v, int& i, float v2, int i2) {
   if (v2 > v || (v2 == v && i2 < i)) {
     v = v2;
@@ -154,30 +196,92 @@ __device__ __forceinline__ void amax_take(float& v, int& i, float v2, int i2) {
   }
 }
 
-template <int HD>
-__global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, FusedLayout f) {
+constexpr int64_t round1k(int64_t x) { return (x + 1023) / 1024 * 1024; }
+
+// The work split's sizes for one model shape (head_dim 128, d_ff = 4
+// d_model); fused_layout computes the same values at run time.
+template <int D_, int H_, int V_>
+struct FusedShape {
+  static constexpr int HD = 128, D = D_, H = H_, V = V_, DFF = 4 * D_;
+  static constexpr int QR = 3 * HD / FUSED_NC, C = D / FUSED_NC, FR = DFF / FUSED_NWG;
+  static constexpr int HN = DFF / FUSED_NX, LR = V / FUSED_NWG;
+  static constexpr int64_t WQ = 0, WP = round1k((int64_t)QR * D * 2);
+  static constexpr int64_t WF = WP + round1k((int64_t)C * HD * 2);
+  static constexpr int64_t W2 = WF + round1k((int64_t)FR * D * 2);
+  static constexpr int64_t SLICE = W2 + round1k((int64_t)C * HN * 2);
+  static constexpr int64_t LMB = round1k((int64_t)LR * D * 2);
+  static constexpr int64_t WBUF = SLICE > LMB ? SLICE : LMB;
+  static constexpr int64_t OFF_QL = 0, OFF_PP = 2 * FUSED_NX * 3 * HD;
+  static constexpr int64_t OFF_XL = OFF_PP + 2 * FUSED_NX * D;
+  static constexpr int64_t OFF_HL = OFF_XL + 2 * FUSED_NX * D;
+  static constexpr int64_t OFF_P2 = OFF_HL + 2 * FUSED_NX * HN;
+  static constexpr int64_t OFF_LM = OFF_P2 + 2 * FUSED_NX * D;
+};
+// The shapes the persistent decode is built for: depth-12's (d_model 768,
+// 6 heads, vocab 8192) and a small one the tests run.
+typedef FusedShape<768, 6, 8192> ShapeD12;
+typedef FusedShape<256, 2, 1024> ShapeSmall;
+
+// Sums over the wave of RP (4 or 8) per-lane values at once: v[r] of every
+// lane lands in this wave's LDS scratch (RP x 64 floats), each group of
+// LPO = 64/RP lanes adds RP consecutive partials of one value, then a DPP
+// butterfly over the group (quad permutes, then the half-row and row
+// mirrors, which pair the same lanes as strides 4 and 8 once the smaller
+// groups are uniform). The sum of v[r] is left in lanes [r*LPO, (r+1)*LPO).
+template <int RP>
+__device__ __forceinline__ float multi_sum(const float (&v)[RP], float* scr, int lane) {
+  constexpr int LPO = 64 / RP;
+  static_assert(RP == 4 || RP == 8, "groups of 16 or 8 lanes");
+#pragma unroll
+  for (int r = 0; r < RP; ++r) scr[r * 64 + lane] = v[r];
+  const float* p = scr + (lane / LPO) * 64 + (lane % LPO) * RP;
+  const float4 a = *(const float4*)p;
+  float t = (a.x + a.y) + (a.z + a.w);
+  if (RP == 8) {
+    const float4 b = *(const float4*)(p + 4);
+    t += (b.x + b.y) + (b.z + b.w);
+  }
+  t += dpp_f<0xB1>(t);
+  t += dpp_f<0x4E>(t);
+  t += dpp_f<0x141>(t);
+  if (LPO == 16) t += dpp_f<0x140>(t);
+  return t;
+}
+
+__device__ __forceinline__ float lane_value(float v, int src) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
+}
+
+template <class Sh, bool TRACE>
+__global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
+  constexpr int HD = Sh::HD;
   constexpr int QLN = 3 * HD;            // q, k, v of one head
-  constexpr int NP = QLN / 64;           // rotation pairs per workgroup
+  constexpr int NP = QLN / 64;           // rotation pairs per workgroup (6)
   constexpr int LPP = HD / 4;            // lanes per cached row in the attention
   constexpr int NG = 4 * (64 / LPP);     // position groups
   constexpr int PPG = FUSED_MAX_LEN / NG;  // positions per group, at most
   constexpr int AST = HD + 4;            // floats per group record: o, m, l
   constexpr int AB = 8;                  // attention positions per batch
-  const int D = a.D, H = a.H, L = a.L, V = a.V, KD = a.KH * HD;
-  const int C = f.C, FR = f.FR, HN = f.HN, LR = f.LR, QR = f.QR;
+  static_assert(LPP == 32 && NP == 6, "the work split is laid out for head_dim 128");
+  constexpr int D = Sh::D, H = Sh::H, V = Sh::V, KD = Sh::H * HD;
+  constexpr int C = Sh::C, FR = Sh::FR, HN = Sh::HN, LR = Sh::LR, QR = Sh::QR;
+  const int L = a.L;
+  const int64_t cu_bytes = (int64_t)L * Sh::SLICE + Sh::LMB;
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
   const bool comp = wv < 4, loader = wv == 4;
   const float eps = a.eps;
-  uint8_t* wbuf[2] = {lds, lds + f.wbuf};
-  float* x_lds = (float*)(lds + 2 * f.wbuf);
+  float* x_lds = (float*)(lds + 2 * Sh::WBUF);
   float* h_lds = x_lds + D;
   float* qkv_lds = h_lds + HN;
-  float* att = qkv_lds + QLN;  // [NG][AST]
-  float* red = att + NG * AST;  // [8]
+  float* att = qkv_lds + QLN;   // [NG][AST]
+  float* scr0 = att + NG * AST;  // reduction scratch, [4 waves][8][64] (16-byte aligned)
+  float* scr = scr0 + (comp ? wv : 0) * 8 * 64;  // this wave's
+  float* red = scr0 + 4 * 8 * 64;  // [8]
   int* ired = (int*)(red + 8);  // [8]
   int* stop = ired + 8;         // nonzero: leave (a hand-over failed)
   int* place = stop + 1;        // this workgroup's XCD and its index there
+  float* rope = (float*)(place + 2);  // cos, sin of the step's position [2][HD/2]
   uint32_t* err = a.err;
   const int E = 8 * L + 8;      // epochs per step
   const int total = a.n_steps * (L + 1);  // pseudo-layers of the launch
@@ -204,30 +308,41 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
   if (*stop) return;
   const int g = place[0], c = place[1], b = g + FUSED_NX * c;
   const bool head = g < H;
-  // DMA of pseudo-layer G's weight slices into its LDS buffer (loader wave)
-  auto issue = [&](int G) {
+  // optional phase timestamps (100 MHz device clock) of one step
+  auto mark = [&](int s, int l, int k) {
+    if (TRACE && s == a.trace_step && tid == (k == 14 || k == 15 ? 256 : 0))
+      a.trace[((int64_t)b * (L + 1) + l) * 32 + k] = __builtin_amdgcn_s_memrealtime();
+  };
+  // DMA of pseudo-layer G's weight slices into its LDS buffer (loader
+  // wave), in three parts issued at three barriers of the pseudo-layer
+  // before, so the stream into LDS is spread over the whole layer
+  auto issue = [&](int G, int part) {
     const int l = G % (L + 1);
-    const uint8_t* src = (const uint8_t*)a.arena + (int64_t)b * f.cu_bytes;
-    uint8_t* dst = wbuf[G & 1];
+    const uint8_t* src = (const uint8_t*)a.arena + (int64_t)b * cu_bytes;
+    uint8_t* dst = lds + (G & 1) * Sh::WBUF;
     int64_t off = 0, n;
     if (l < L) {
-      off = head ? 0 : f.wf;  // workgroups of XCDs >= H hold no q/k/v or c_proj rows
-      src += (int64_t)l * f.slice;
-      n = f.slice - off;
+      off = head ? 0 : Sh::WF;  // workgroups of XCDs >= H hold no q/k/v or c_proj rows
+      src += (int64_t)l * Sh::SLICE;
+      n = Sh::SLICE - off;
     } else {
-      src += (int64_t)L * f.slice;
-      n = f.lmb;
+      src += (int64_t)L * Sh::SLICE;
+      n = Sh::LMB;
     }
-    for (int64_t k = off; k < off + n; k += 1024) dma16(src + k + 16 * lane, lds_off(dst + k));
+    const int64_t nch = n / 1024, k0 = part * nch / 3, k1 = (part + 1) * nch / 3;
+    for (int64_t k = off + 1024 * k0; k < off + 1024 * k1; k += 1024)
+      dma16(src + k + 16 * lane, lds_off(dst + k));
   };
   auto waitdma = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
 
   // x = rmsnorm0(wte[id]) into x_lds (k_embed_norm's order: 256 strided
-  // partial sums, then the four waves' sums in order); x_own = this
-  // workgroup's residual columns
+  // partial sums, then the four waves' sums in order), x_own = this
+  // workgroup's residual columns, and the RoPE row of position pos
   float x_own = 0.f;
-  auto embed = [&](int id) {
+  auto embed = [&](int id, int pos) {
     const bf16_t* row = a.wte + (int64_t)id * D;
+    if (comp && tid < HD) rope[tid] = tid < HD / 2 ? a.cosb[(int64_t)pos * (HD / 2) + tid]
+                                                   : a.sinb[(int64_t)pos * (HD / 2) + tid - HD / 2];
     if (comp) {
       float ss = 0.f;
       for (int k = tid; k < D; k += 256) {
@@ -246,69 +361,92 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
     }
   };
 
-  if (loader) issue(0);
-  embed(*a.d_id0);
+  if (loader) {
+    issue(0, 0);
+    issue(0, 1);
+    issue(0, 2);
+  }
+  embed(*a.d_id0, a.len0);
 
   for (int s = 0; s < a.n_steps; ++s) {
     const int pos = a.len0 + s;
     for (int l = 0; l <= L; ++l) {
       const int G = s * (L + 1) + l;
-      const uint8_t* W = wbuf[G & 1];
+      const uint8_t* W = lds + (G & 1) * Sh::WBUF;  // (an LDS address: ds_read, not flat)
       // B0: this pseudo-layer's weights have landed; the next one's go out
+      mark(s, l, 14);
       if (loader) waitdma();
+      mark(s, l, 15);
       lds_barrier();
+      mark(s, l, 0);
+      if (TRACE && s == a.trace_step && tid == 0)
+        a.trace[((int64_t)b * (L + 1) + l) * 32 + 24] = __builtin_readcyclecounter();
       if (*stop) goto done;
-      if (loader && G + 1 < total) issue(G + 1);
+      if (loader && G + 1 < total) issue(G + 1, 0);
       if (l == L) break;  // lm_head below
       const int par = (s * L + l) & 1;
       const uint32_t ep = a.ep_base + (uint32_t)(s * E + l * 8);
-      uint64_t* QL = S + f.off_ql + (int64_t)(par * 8 + g) * QLN;
-      uint64_t* PP = S + f.off_pp + (int64_t)par * 8 * D;
-      uint64_t* XL = S + f.off_xl + (int64_t)(par * 8 + g) * D;
-      uint64_t* HL = S + f.off_hl + (int64_t)(par * 8 + g) * HN;
-      uint64_t* P2 = S + f.off_p2 + (int64_t)par * 8 * D;
+      uint64_t* QL = S + Sh::OFF_QL + (int64_t)(par * 8 + g) * QLN;
+      uint64_t* PP = S + Sh::OFF_PP + (int64_t)par * 8 * D;
+      uint64_t* XL = S + Sh::OFF_XL + (int64_t)(par * 8 + g) * D;
+      uint64_t* HL = S + Sh::OFF_HL + (int64_t)(par * 8 + g) * HN;
+      uint64_t* P2 = S + Sh::OFF_P2 + (int64_t)par * 8 * D;
       float* kc = a.kc + (int64_t)l * a.maxT * KD + g * HD;
       float* vc = a.vc + (int64_t)l * a.maxT * KD + g * HD;
       if (head) {
-        // q, k, v rows (RoPE pairs) of head g; k and v into the cache
+        // q, k, v rows of head g: wave w takes RoPE pairs w and w+4 (of 6)
         if (comp) {
-          const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
-          for (int pi = wv; pi < NP; pi += 4) {
-            float acc[2];
-            chunk_dot<2>(W + f.wq + (int64_t)(2 * pi) * D * 2, D * 2, x_lds, D, lane, acc);
-            const float v0 = wave_sum(acc[0]) * inv, v1 = wave_sum(acc[1]) * inv;
-            if (lane == 0) {
-              const int r0 = c * QR + 2 * pi, part = r0 / HD, j = (r0 % HD) >> 1;
-              float y1 = v0, y2 = v1;
-              if (part < 2) {
-                const float cs = a.cosb[(int64_t)pos * (HD / 2) + j];
-                const float sn = a.sinb[(int64_t)pos * (HD / 2) + j];
-                y1 = v0 * cs + v1 * sn;
-                y2 = v0 * (-sn) + v1 * cs;
-              }
-              slot_put_xcd(QL + part * HD + j, y1, ep);
-              slot_put_xcd(QL + part * HD + j + HD / 2, y2, ep);
-              if (part > 0) {
-                float* cr = (part == 1 ? kc : vc) + (int64_t)pos * KD;
-                __hip_atomic_store(cr + j, y1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(cr + j + HD / 2, y2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              }
+          const bool two = wv + 4 < NP;
+          float acc[4] = {0.f, 0.f, 0.f, 0.f};
+          float ss;
+          {
+            float t[2];
+            ss = chunk_dot_ss<2>(W + Sh::WQ + (int64_t)(2 * wv) * D * 2, D * 2, x_lds, D, lane, t);
+            acc[0] = t[0];
+            acc[1] = t[1];
+            if (two) {
+              chunk_dot<2>(W + Sh::WQ + (int64_t)(2 * (wv + 4)) * D * 2, D * 2, x_lds, D, lane, t);
+              acc[2] = t[0];
+              acc[3] = t[1];
             }
           }
+          const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
+          const float r4 = multi_sum<4>(acc, scr, lane);
+          const float rv[4] = {lane_value(r4, 0) * inv, lane_value(r4, 16) * inv,
+                               lane_value(r4, 32) * inv, lane_value(r4, 48) * inv};
+          if (lane < (two ? 2 : 1)) {
+            const int pi = wv + 4 * lane;
+            const float v0 = lane ? rv[2] : rv[0], v1 = lane ? rv[3] : rv[1];
+            const int r0 = c * QR + 2 * pi, part = r0 / HD, j = (r0 % HD) >> 1;
+            float y1 = v0, y2 = v1;
+            if (part < 2) {
+              const float cs = rope[j], sn = rope[HD / 2 + j];
+              y1 = v0 * cs + v1 * sn;
+              y2 = v0 * (-sn) + v1 * cs;
+            }
+            slot_put_xcd(QL + part * HD + j, y1, ep);
+            slot_put_xcd(QL + part * HD + j + HD / 2, y2, ep);
+            if (part > 0) {  // (head g's cache rows are written and read by XCD g only)
+              float* cr = (part == 1 ? kc : vc) + (int64_t)pos * KD;
+              cr[j] = y1;
+              cr[j + HD / 2] = y2;
+            }
+          }
+          mark(s, l, 1);
           if (!gather_slots<2>(QL, QLN, ep, qkv_lds, tid, err)) *stop = 1;
         }
         lds_barrier();  // B1
+        mark(s, l, 2);
         if (*stop) goto done;
-        // attention of head g over positions 0..pos: group grp takes
-        // positions grp, grp+NG, ...; the current position's k and v come
-        // from the hand-over, earlier ones from the cache
+        // attention of head g over positions 0..pos: group grp (half a
+        // wave) takes positions grp, grp+NG, ...; the current position's k
+        // and v come from the hand-over, earlier ones from the cache
         if (comp) {
-          const int grp = wv * (64 / LPP) + lane / LPP, dl = lane % LPP;
+          const int grp = wv * 2 + (lane >> 5), dl = lane & 31;
           const float4 q4 = *(const float4*)(qkv_lds + 4 * dl);
           const float scale = 1.0f / sqrtf((float)HD);
           float m = -INFINITY, lsum = 0.f;
           float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-          // positions in batches of AB per group: one batch's loads in flight together
           for (int i0 = 0; i0 < PPG && grp + NG * i0 <= pos; i0 += AB) {
             float4 kr[AB], vr[AB];
 #pragma unroll
@@ -322,21 +460,32 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
                 vr[i] = *(const float4*)(qkv_lds + 2 * HD + 4 * dl);
               }
             }
+            // the batch's scores (independent half-wave sums), then one
+            // online-softmax update for the batch
+            float sc[AB];
+            float mb = -INFINITY;
 #pragma unroll
             for (int i = 0; i < AB; ++i) {
-              if (grp + NG * (i0 + i) > pos) break;
-              float sc = q4.x * kr[i].x + q4.y * kr[i].y + q4.z * kr[i].z + q4.w * kr[i].w;
-#pragma unroll
-              for (int off = LPP / 2; off > 0; off >>= 1) sc += __shfl_xor(sc, off, 64);
-              sc *= scale;
-              const float mn = fmaxf(m, sc), al = expf(m - mn), e = expf(sc - mn);
-              lsum = lsum * al + e;
-              o.x = o.x * al + e * vr[i].x;
-              o.y = o.y * al + e * vr[i].y;
-              o.z = o.z * al + e * vr[i].z;
-              o.w = o.w * al + e * vr[i].w;
-              m = mn;
+              const float dp = q4.x * kr[i].x + q4.y * kr[i].y + q4.z * kr[i].z + q4.w * kr[i].w;
+              sc[i] = grp + NG * (i0 + i) <= pos ? half_sum(dp) * scale : -INFINITY;
+              mb = fmaxf(mb, sc[i]);
             }
+            const float mn = fmaxf(m, mb), al = expf(m - mn);
+            lsum *= al;
+            o.x *= al;
+            o.y *= al;
+            o.z *= al;
+            o.w *= al;
+#pragma unroll
+            for (int i = 0; i < AB; ++i) {
+              const float e = expf(sc[i] - mn);
+              lsum += e;
+              o.x += e * vr[i].x;
+              o.y += e * vr[i].y;
+              o.z += e * vr[i].z;
+              o.w += e * vr[i].w;
+            }
+            m = mn;
           }
           *(float4*)(att + grp * AST + 4 * dl) = o;
           if (dl == 0) {
@@ -345,7 +494,9 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
           }
         }
         lds_barrier();  // B2
-        // c_proj partial of head g over this workgroup's C output columns
+        mark(s, l, 3);
+        // c_proj partial of head g over this workgroup's C output columns:
+        // wave w takes outputs w, w+4, ...
         if (comp) {
           float mx = -INFINITY;
 #pragma unroll
@@ -360,12 +511,19 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
           }
           const float il = 1.0f / ls;
           const float ao0 = o0 * il, ao1 = o1 * il;  // head dims 2*lane, 2*lane+1
-          for (int j = wv; j < C; j += 4) {
-            const uint32_t wp = *(const uint32_t*)(W + f.wp + (int64_t)j * HD * 2 + 4 * lane);
-            float v = ao0 * __uint_as_float(wp << 16) + ao1 * __uint_as_float(wp & 0xFFFF0000u);
-            v = wave_sum(v);
-            if (lane == 0) slot_put_dev(PP + (int64_t)g * D + c * C + j, v, ep + 1);
+          for (int j0 = wv; j0 < C; j0 += 32) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int j = min(j0 + 4 * i, C - 1);
+              const uint32_t wp = *(const uint32_t*)(W + Sh::WP + (int64_t)j * HD * 2 + 4 * lane);
+              v[i] = ao0 * __uint_as_float(wp << 16) + ao1 * __uint_as_float(wp & 0xFFFF0000u);
+            }
+            const float t = multi_sum<8>(v, scr, lane);
+            const int j = j0 + 4 * (lane >> 3);
+            if ((lane & 7) == 0 && j < C) slot_put_dev(PP + (int64_t)g * D + c * C + j, t, ep + 1);
           }
+          mark(s, l, 4);
         }
       }
       // residual += sum of the heads' c_proj partials (heads in order)
@@ -377,36 +535,55 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
         x_own = x_own + t;
         slot_put_xcd(XL + c * C + lane, x_own, ep + 2);
       }
+      mark(s, l, 5);
       if (comp && !*stop && !gather_slots<8>(XL, D, ep + 2, x_lds, tid, err)) *stop = 1;
       lds_barrier();  // B3
+      mark(s, l, 6);
       if (*stop) goto done;
-      // h = relu2(rmsnorm0(x) c_fc^T) for this workgroup's fc rows
+      if (loader && G + 1 < total) issue(G + 1, 1);
+      // h = relu2(rmsnorm0(x) c_fc^T) for this workgroup's fc rows: wave w
+      // takes rows w, w+4, ... (four at a time)
       if (comp) {
         const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
-        for (int r = wv; r < FR; r += 4) {
-          float acc[1];
-          chunk_dot<1>(W + f.wf + (int64_t)r * D * 2, 0, x_lds, D, lane, acc);
-          float v = wave_sum(acc[0]) * inv;
-          v = v < 0.f ? 0.f : v;
-          if (lane == 0) slot_put_xcd(HL + c * FR + r, v * v, ep + 3);
+        for (int r0 = wv; r0 < FR; r0 += 16) {
+          float acc[4];
+          int ro[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ro[i] = min(r0 + 4 * i, FR - 1) * D * 2;  // (rows past FR: ignored)
+          chunk_dot_at<4>(W + Sh::WF, ro, x_lds, D, lane, acc);
+          float t = multi_sum<4>(acc, scr, lane) * inv;
+          t = t < 0.f ? 0.f : t;
+          const int r = r0 + 4 * (lane >> 4);
+          if ((lane & 15) == 0 && r < FR) slot_put_xcd(HL + c * FR + r, t * t, ep + 3);
         }
+        mark(s, l, 7);
         if (!gather_slots<8>(HL, HN, ep + 3, h_lds, tid, err)) *stop = 1;
       }
       lds_barrier();  // B4
+      mark(s, l, 8);
       if (*stop) goto done;
-      // c_proj2 partial over this XCD's fc block
+      if (loader && G + 1 < total) issue(G + 1, 2);
+      // c_proj2 partial over this XCD's fc block: wave w takes outputs w,
+      // w+4, ... (eight at a time)
       if (comp) {
-        for (int j = wv; j < C; j += 4) {
-          const uint8_t* w2 = W + f.w2 + (int64_t)j * HN * 2;
-          float v = 0.f;
+        for (int j0 = wv; j0 < C; j0 += 32) {
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = 0.f;
           for (int k = lane; k < (HN >> 1); k += 64) {
-            const uint32_t wp = *(const uint32_t*)(w2 + 4 * k);
             const float2 hv = *(const float2*)(h_lds + 2 * k);
-            v += hv.x * __uint_as_float(wp << 16) + hv.y * __uint_as_float(wp & 0xFFFF0000u);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int j = min(j0 + 4 * i, C - 1);
+              const uint32_t wp = *(const uint32_t*)(W + Sh::W2 + (int64_t)j * HN * 2 + 4 * k);
+              v[i] += hv.x * __uint_as_float(wp << 16) + hv.y * __uint_as_float(wp & 0xFFFF0000u);
+            }
           }
-          v = wave_sum(v);
-          if (lane == 0) slot_put_dev(P2 + (int64_t)g * D + c * C + j, v, ep + 4);
+          const float t = multi_sum<8>(v, scr, lane);
+          const int j = j0 + 4 * (lane >> 3);
+          if ((lane & 7) == 0 && j < C) slot_put_dev(P2 + (int64_t)g * D + c * C + j, t, ep + 4);
         }
+        mark(s, l, 9);
       }
       // residual += sum of the 8 blocks' c_proj2 partials (blocks in order)
       if (wv == 0 && lane < C) {
@@ -418,32 +595,45 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
         x_own = x_own + t;
         slot_put_xcd(XL + c * C + lane, x_own, ep + 5);
       }
+      mark(s, l, 10);
       if (comp && !*stop && !gather_slots<8>(XL, D, ep + 5, x_lds, tid, err)) *stop = 1;
+      mark(s, l, 11);
+      if (TRACE && s == a.trace_step && tid == 0)
+        a.trace[((int64_t)b * (L + 1) + l) * 32 + 25] = __builtin_readcyclecounter();
     }
     {
-      // lm_head rows of this workgroup, their argmax candidate
+      // lm_head rows of this workgroup (wave w: rows w, w+4, ..., eight at
+      // a time) and their first-max argmax candidate
       const int G = s * (L + 1) + L;
-      const uint8_t* W = wbuf[G & 1];
+      const uint8_t* W = lds + (G & 1) * Sh::WBUF;
       const uint32_t ep = a.ep_base + (uint32_t)(s * E + 8 * L);
-      uint64_t* LM = S + f.off_lm + (int64_t)(s & 1) * FUSED_NWG * 2;
+      uint64_t* LM = S + Sh::OFF_LM + (int64_t)(s & 1) * FUSED_NWG * 2;
       if (comp) {
         const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
         float bv = -INFINITY;
         int bi = 0x7fffffff;
-        for (int r = wv; r < LR; r += 4) {
-          float acc[1];
-          chunk_dot<1>(W + (int64_t)r * D * 2, 0, x_lds, D, lane, acc);
-          const float v = wave_sum(acc[0]) * inv;
-          const int id = b * LR + r;
-          if (lane == 0 && a.logits_out) a.logits_out[(int64_t)s * V + id] = v;
-          amax_take(bv, bi, v, id);
+        for (int r0 = wv; r0 < LR; r0 += 32) {
+          float acc[8];
+          int ro[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ro[i] = min(r0 + 4 * i, LR - 1) * D * 2;  // (rows past LR: ignored)
+          chunk_dot_at<8>(W, ro, x_lds, D, lane, acc);
+          const float v = multi_sum<8>(acc, scr, lane) * inv;
+          const int r = r0 + 4 * (lane >> 3), id = b * LR + r;
+          if ((lane & 7) == 0 && r < LR && a.logits_out) a.logits_out[(int64_t)s * V + id] = v;
+          // rows in increasing order across the eight groups
+#pragma unroll
+          for (int q = 0; q < 8; ++q)
+            if (r0 + 4 * q < LR) amax_take(bv, bi, lane_value(v, 8 * q), b * LR + r0 + 4 * q);
         }
         if (lane == 0) {
           red[wv] = bv;
           ired[wv] = bi;
         }
+        mark(s, L, 1);
       }
       lds_barrier();  // B5
+      if (loader && G + 1 < total) issue(G + 1, 1);
       if (comp) {
         if (tid == 0) {
           float v = red[0];
@@ -473,14 +663,17 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a, Fus
           ired[4 + wv] = bi;
         }
       }
+      mark(s, L, 2);
       lds_barrier();  // B6
+      mark(s, L, 3);
       if (*stop) goto done;
+      if (loader && G + 1 < total) issue(G + 1, 2);
       float v = red[4];
       int id = ired[4];
       for (int w = 1; w < 4; ++w) amax_take(v, id, red[4 + w], ired[4 + w]);
       if (id == 0x7fffffff) id = 0;  // no finite candidate: position 1, as the scan starts there
       if (b == 0 && tid == 0) a.ids_out[s] = id;
-      if (s + 1 < a.n_steps) embed(id);
+      if (s + 1 < a.n_steps) embed(id, pos + 1);
     }
   }
 done:
@@ -503,6 +696,10 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
   if (d.dff % (FUSED_NWG * 2) != 0) return no("d_ff not a multiple of 512");
   if (d.V % FUSED_NWG != 0) return no("vocab not a multiple of 256");
   if (d.D > 8 * 256 || d.dff / FUSED_NX > 8 * 256) return no("d_model or d_ff too large");
+  if (d.dff != 4 * d.D || !((d.D == ShapeD12::D && d.H == ShapeD12::H && d.V == ShapeD12::V) ||
+                            (d.D == ShapeSmall::D && d.H == ShapeSmall::H && d.V == ShapeSmall::V)))
+    return no("no persistent-decode build for these dims (d_model 768 / 6 heads / vocab 8192, "
+              "or 256 / 2 / 1024)");
   auto r1k = [](int64_t x) { return (x + 1023) / 1024 * 1024; };
   f.QR = 3 * d.hd / FUSED_NC;
   f.C = d.D / FUSED_NC;
@@ -518,7 +715,10 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
   f.wbuf = std::max(f.slice, f.lmb);
   f.cu_bytes = (int64_t)d.L * f.slice + f.lmb;
   const int NG = 4 * (64 / (FUSED_HD / 4));
-  const int64_t act = 4 * ((int64_t)d.D + f.HN + 3 * FUSED_HD + NG * (FUSED_HD + 4) + 8) + 4 * 11;
+  // x, h, q/k/v, attention groups, reduction scratch, red, ired, stop,
+  // place, rope (floats / ints)
+  const int64_t act = 4 * ((int64_t)d.D + f.HN + 3 * FUSED_HD + NG * (FUSED_HD + 4) + 4 * 8 * 64 +
+                           8 + 8 + 1 + 2 + FUSED_HD);
   f.lds_bytes = 2 * f.wbuf + act;
   if (f.lds_bytes > 160 * 1024) return no("weight slices do not fit twice in LDS");
   f.off_ql = 0;
@@ -571,17 +771,27 @@ void fused_pack(const Dims& d, const FusedLayout& f, const Weights& w, const bf1
 
 uint32_t fused_epochs(const Dims& d, int n_steps) { return (uint32_t)n_steps * (8u * d.L + 8u); }
 
-hipError_t launch_fused_decode(hipStream_t s, const Dims& d, const FusedLayout& f,
-                               const FusedArgs& a) {
-  (void)d;
-  hipError_t e = hipFuncSetAttribute((const void*)k_fused_decode<FUSED_HD>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)f.lds_bytes);
+template <class Sh>
+static hipError_t launch_shape(hipStream_t s, const FusedLayout& f, const FusedArgs& a) {
+  if (f.slice != Sh::SLICE || f.lmb != Sh::LMB || f.wbuf != Sh::WBUF || f.wf != Sh::WF ||
+      f.off_lm != Sh::OFF_LM)
+    return hipErrorInvalidValue;  // (host and device layouts disagree)
+  const void* k = a.trace ? (const void*)k_fused_decode<Sh, true> : (const void*)k_fused_decode<Sh, false>;
+  hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)f.lds_bytes);
   if (e != hipSuccess) return e;
   FusedArgs aa = a;
-  FusedLayout ff = f;
-  void* args[] = {&aa, &ff};
-  return hipLaunchCooperativeKernel((const void*)k_fused_decode<FUSED_HD>, dim3(FUSED_NWG),
-                                    dim3(FUSED_THREADS), args, (unsigned)f.lds_bytes, s);
+  void* args[] = {&aa};
+  return hipLaunchCooperativeKernel(k, dim3(FUSED_NWG), dim3(FUSED_THREADS), args,
+                                    (unsigned)f.lds_bytes, s);
+}
+
+hipError_t launch_fused_decode(hipStream_t s, const Dims& d, const FusedLayout& f,
+                               const FusedArgs& a) {
+  if (d.D == ShapeD12::D && d.H == ShapeD12::H && d.V == ShapeD12::V)
+    return launch_shape<ShapeD12>(s, f, a);
+  if (d.D == ShapeSmall::D && d.H == ShapeSmall::H && d.V == ShapeSmall::V)
+    return launch_shape<ShapeSmall>(s, f, a);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace fgpt
