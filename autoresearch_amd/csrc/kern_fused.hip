@@ -115,78 +115,70 @@ __device__ bool gather_slots(const uint64_t* p, int n, uint32_t ep, float* dst, 
   return true;
 }
 
-// sum(x^2) over the lane-strided chunks of 8 a dot product reads
-__device__ __forceinline__ float chunk_ss(const float* x, int K, int lane) {
-  float ss = 0.f;
-#pragma unroll 2
-  for (int k = lane; k < (K >> 3); k += 64) {
-    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
-    ss += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x + xb.y * xb.y +
-          xb.z * xb.z + xb.w * xb.w;
+// The lane's part of the dot products of NR bf16 rows (LDS, at byte
+// offsets roff from w) with fp32 x (LDS) over K (a multiple of 128): the
+// lane takes elements [CE k, CE k + CE) for k = lane, lane+64, ... (CE = 4
+// when K is a multiple of 256, else 2, so every lane has the same count).
+// Every load of the lane's chunks is issued before any arithmetic.
+template <int NR, int K>
+__device__ __forceinline__ void dot_rows(const uint8_t* w, const int (&roff)[NR], const float* x,
+                                         int lane, float (&acc)[NR]) {
+  static_assert(K % 128 == 0, "K a multiple of 128");
+  constexpr int CE = K % 256 == 0 ? 4 : 2;
+  constexpr int IT = K / (64 * CE);
+  if constexpr (CE == 4) {
+    float4 xv[IT];
+    uint2 wv[IT][NR];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      xv[i] = *(const float4*)(x + 4 * (lane + 64 * i));
+#pragma unroll
+      for (int r = 0; r < NR; ++r) wv[i][r] = *(const uint2*)(w + roff[r] + 8 * (lane + 64 * i));
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < IT; ++i)
+        t += xv[i].x * __uint_as_float(wv[i][r].x << 16) +
+             xv[i].y * __uint_as_float(wv[i][r].x & 0xFFFF0000u) +
+             xv[i].z * __uint_as_float(wv[i][r].y << 16) +
+             xv[i].w * __uint_as_float(wv[i][r].y & 0xFFFF0000u);
+      acc[r] = t;
+    }
+  } else {
+    float2 xv[IT];
+    uint32_t wv[IT][NR];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      xv[i] = *(const float2*)(x + 2 * (lane + 64 * i));
+#pragma unroll
+      for (int r = 0; r < NR; ++r) wv[i][r] = *(const uint32_t*)(w + roff[r] + 4 * (lane + 64 * i));
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < IT; ++i)
+        t += xv[i].x * __uint_as_float(wv[i][r] << 16) +
+             xv[i].y * __uint_as_float(wv[i][r] & 0xFFFF0000u);
+      acc[r] = t;
+    }
   }
+}
+
+// sum(x^2) over the wave, x (LDS) of K elements in dot_rows' lane split
+template <int K>
+__device__ __forceinline__ float sumsq(const float* x, int lane) {
+  constexpr int IT = K / 256;
+  float4 xv[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) xv[i] = *(const float4*)(x + 4 * (lane + 64 * i));
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < IT; ++i)
+    ss += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
   return wave_sum(ss);
-}
-
-// lane's part of the dot products of NR bf16 rows (LDS, rstride bytes
-// apart) with x (fp32, LDS) over K, lane-strided chunks of 8
-template <int NR>
-__device__ __forceinline__ void chunk_dot(const uint8_t* w, int rstride, const float* x, int K,
-                                          int lane, float (&acc)[NR]) {
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
-#pragma unroll 2
-  for (int k = lane; k < (K >> 3); k += 64) {
-    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float f[8];
-      unpack8(*(const uint4*)(w + r * rstride + 16 * k), f);
-      acc[r] += f[0] * xa.x + f[1] * xa.y + f[2] * xa.z + f[3] * xa.w + f[4] * xb.x +
-                f[5] * xb.y + f[6] * xb.z + f[7] * xb.w;
-    }
-  }
-}
-
-// chunk_dot that also returns the lane's sum of x^2 over the chunks it read
-template <int NR>
-__device__ __forceinline__ float chunk_dot_ss(const uint8_t* w, int rstride, const float* x, int K,
-                                              int lane, float (&acc)[NR]) {
-  float ss = 0.f;
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
-#pragma unroll 2
-  for (int k = lane; k < (K >> 3); k += 64) {
-    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
-    ss += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x + xb.y * xb.y +
-          xb.z * xb.z + xb.w * xb.w;
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float f[8];
-      unpack8(*(const uint4*)(w + r * rstride + 16 * k), f);
-      acc[r] += f[0] * xa.x + f[1] * xa.y + f[2] * xa.z + f[3] * xa.w + f[4] * xb.x +
-                f[5] * xb.y + f[6] * xb.z + f[7] * xb.w;
-    }
-  }
-  return ss;
-}
-
-// chunk_dot for NR rows at arbitrary byte offsets from w
-template <int NR>
-__device__ __forceinline__ void chunk_dot_at(const uint8_t* w, const int (&roff)[NR], const float* x,
-                                             int K, int lane, float (&acc)[NR]) {
-#pragma unroll
-  for (int r = 0; r < NR; ++r) acc[r] = 0.f;
-#pragma unroll 2
-  for (int k = lane; k < (K >> 3); k += 64) {
-    const float4 xa = *(const float4*)(x + 8 * k), xb = *(const float4*)(x + 8 * k + 4);
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float f[8];
-      unpack8(*(const uint4*)(w + roff[r] + 16 * k), f);
-      acc[r] += f[0] * xa.x + f[1] * xa.y + f[2] * xa.z + f[3] * xa.w + f[4] * xb.x +
-                f[5] * xb.y + f[6] * xb.z + f[7] * xb.w;
-    }
-  }
 }
 
 __device__ __forceinline__ void amax_take(float& v, int& i, float v2, int i2) {
@@ -216,6 +208,7 @@ struct FusedShape {
   static constexpr int64_t OFF_HL = OFF_XL + 2 * FUSED_NX * D;
   static constexpr int64_t OFF_P2 = OFF_HL + 2 * FUSED_NX * HN;
   static constexpr int64_t OFF_LM = OFF_P2 + 2 * FUSED_NX * D;
+  static constexpr int64_t SLOTS = OFF_LM + 2 * FUSED_NWG * 2 + 2 * FUSED_NX * 2;
 };
 // The shapes the persistent decode is built for: depth-12's (d_model 768,
 // 6 heads, vocab 8192) and a small one the tests run.
@@ -397,20 +390,12 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
         // q, k, v rows of head g: wave w takes RoPE pairs w and w+4 (of 6)
         if (comp) {
           const bool two = wv + 4 < NP;
-          float acc[4] = {0.f, 0.f, 0.f, 0.f};
-          float ss;
-          {
-            float t[2];
-            ss = chunk_dot_ss<2>(W + Sh::WQ + (int64_t)(2 * wv) * D * 2, D * 2, x_lds, D, lane, t);
-            acc[0] = t[0];
-            acc[1] = t[1];
-            if (two) {
-              chunk_dot<2>(W + Sh::WQ + (int64_t)(2 * (wv + 4)) * D * 2, D * 2, x_lds, D, lane, t);
-              acc[2] = t[0];
-              acc[3] = t[1];
-            }
-          }
-          const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
+          // rows 2w, 2w+1 and (when there is a second pair) 2w+8, 2w+9
+          const int ro[4] = {2 * wv * D * 2, (2 * wv + 1) * D * 2, (two ? 2 * wv + 8 : 2 * wv) * D * 2,
+                             (two ? 2 * wv + 9 : 2 * wv + 1) * D * 2};
+          float acc[4];
+          dot_rows<4, D>(W + Sh::WQ, ro, x_lds, lane, acc);
+          const float inv = 1.0f / sqrtf(sumsq<D>(x_lds, lane) / (float)D + eps);
           const float r4 = multi_sum<4>(acc, scr, lane);
           const float rv[4] = {lane_value(r4, 0) * inv, lane_value(r4, 16) * inv,
                                lane_value(r4, 32) * inv, lane_value(r4, 48) * inv};
@@ -433,31 +418,42 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
             }
           }
           mark(s, l, 1);
+        }
+        // attention of head g over positions 0..pos: group grp (half a
+        // wave) takes positions grp, grp+NG, ...; the current position's k
+        // and v come from the hand-over, earlier ones from the cache. The
+        // first batch's cache rows are requested before the wait for q/k/v.
+        const int grp = wv * 2 + (lane >> 5), dl = lane & 31;
+        float4 kr[AB], vr[AB];
+        if (comp) {
+#pragma unroll
+          for (int i = 0; i < AB; ++i) {
+            const int p = grp + NG * i;
+            if (p < pos) {
+              kr[i] = *(const float4*)(kc + (int64_t)p * KD + 4 * dl);
+              vr[i] = *(const float4*)(vc + (int64_t)p * KD + 4 * dl);
+            }
+          }
           if (!gather_slots<2>(QL, QLN, ep, qkv_lds, tid, err)) *stop = 1;
         }
         lds_barrier();  // B1
         mark(s, l, 2);
         if (*stop) goto done;
-        // attention of head g over positions 0..pos: group grp (half a
-        // wave) takes positions grp, grp+NG, ...; the current position's k
-        // and v come from the hand-over, earlier ones from the cache
         if (comp) {
-          const int grp = wv * 2 + (lane >> 5), dl = lane & 31;
           const float4 q4 = *(const float4*)(qkv_lds + 4 * dl);
           const float scale = 1.0f / sqrtf((float)HD);
           float m = -INFINITY, lsum = 0.f;
           float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
           for (int i0 = 0; i0 < PPG && grp + NG * i0 <= pos; i0 += AB) {
-            float4 kr[AB], vr[AB];
 #pragma unroll
             for (int i = 0; i < AB; ++i) {
               const int p = grp + NG * (i0 + i);
-              if (p < pos) {
-                kr[i] = *(const float4*)(kc + (int64_t)p * KD + 4 * dl);
-                vr[i] = *(const float4*)(vc + (int64_t)p * KD + 4 * dl);
-              } else {
+              if (p >= pos) {
                 kr[i] = *(const float4*)(qkv_lds + HD + 4 * dl);
                 vr[i] = *(const float4*)(qkv_lds + 2 * HD + 4 * dl);
+              } else if (i0 > 0) {
+                kr[i] = *(const float4*)(kc + (int64_t)p * KD + 4 * dl);
+                vr[i] = *(const float4*)(vc + (int64_t)p * KD + 4 * dl);
               }
             }
             // the batch's scores (independent half-wave sums), then one
@@ -470,7 +466,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
               sc[i] = grp + NG * (i0 + i) <= pos ? half_sum(dp) * scale : -INFINITY;
               mb = fmaxf(mb, sc[i]);
             }
-            const float mn = fmaxf(m, mb), al = expf(m - mn);
+            const float mn = fmaxf(m, mb), al = __expf(m - mn);
             lsum *= al;
             o.x *= al;
             o.y *= al;
@@ -478,7 +474,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
             o.w *= al;
 #pragma unroll
             for (int i = 0; i < AB; ++i) {
-              const float e = expf(sc[i] - mn);
+              const float e = __expf(sc[i] - mn);
               lsum += e;
               o.x += e * vr[i].x;
               o.y += e * vr[i].y;
@@ -504,7 +500,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
           float ls = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
           for (int q = 0; q < NG; ++q) {
-            const float w = expf(att[q * AST + HD] - mx);
+            const float w = __expf(att[q * AST + HD] - mx);
             ls += att[q * AST + HD + 1] * w;
             o0 += att[q * AST + 2 * lane] * w;
             o1 += att[q * AST + 2 * lane + 1] * w;
@@ -544,13 +540,13 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       // h = relu2(rmsnorm0(x) c_fc^T) for this workgroup's fc rows: wave w
       // takes rows w, w+4, ... (four at a time)
       if (comp) {
-        const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
+        const float inv = 1.0f / sqrtf(sumsq<D>(x_lds, lane) / (float)D + eps);
         for (int r0 = wv; r0 < FR; r0 += 16) {
           float acc[4];
           int ro[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) ro[i] = min(r0 + 4 * i, FR - 1) * D * 2;  // (rows past FR: ignored)
-          chunk_dot_at<4>(W + Sh::WF, ro, x_lds, D, lane, acc);
+          dot_rows<4, D>(W + Sh::WF, ro, x_lds, lane, acc);
           float t = multi_sum<4>(acc, scr, lane) * inv;
           t = t < 0.f ? 0.f : t;
           const int r = r0 + 4 * (lane >> 4);
@@ -568,17 +564,10 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       if (comp) {
         for (int j0 = wv; j0 < C; j0 += 32) {
           float v[8];
+          int ro[8];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] = 0.f;
-          for (int k = lane; k < (HN >> 1); k += 64) {
-            const float2 hv = *(const float2*)(h_lds + 2 * k);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const int j = min(j0 + 4 * i, C - 1);
-              const uint32_t wp = *(const uint32_t*)(W + Sh::W2 + (int64_t)j * HN * 2 + 4 * k);
-              v[i] += hv.x * __uint_as_float(wp << 16) + hv.y * __uint_as_float(wp & 0xFFFF0000u);
-            }
-          }
+          for (int i = 0; i < 8; ++i) ro[i] = min(j0 + 4 * i, C - 1) * HN * 2;  // (outputs past C: ignored)
+          dot_rows<8, HN>(W + Sh::W2, ro, h_lds, lane, v);
           const float t = multi_sum<8>(v, scr, lane);
           const int j = j0 + 4 * (lane >> 3);
           if ((lane & 7) == 0 && j < C) slot_put_dev(P2 + (int64_t)g * D + c * C + j, t, ep + 4);
@@ -607,17 +596,28 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       const int G = s * (L + 1) + L;
       const uint8_t* W = lds + (G & 1) * Sh::WBUF;
       const uint32_t ep = a.ep_base + (uint32_t)(s * E + 8 * L);
-      uint64_t* LM = S + Sh::OFF_LM + (int64_t)(s & 1) * FUSED_NWG * 2;
+      // argmax candidates: per workgroup within its XCD [2][8][32][2], then
+      // per XCD across [2][8][2]
+      uint64_t* LMX = S + Sh::OFF_LM + ((int64_t)(s & 1) * FUSED_NX + g) * FUSED_NC * 2;
+      uint64_t* LMG = S + Sh::OFF_LM + 2 * FUSED_NWG * 2 + (int64_t)(s & 1) * FUSED_NX * 2;
       if (comp) {
-        const float inv = 1.0f / sqrtf(chunk_ss(x_lds, D, lane) / (float)D + eps);
+        const float inv = 1.0f / sqrtf(sumsq<D>(x_lds, lane) / (float)D + eps);
         float bv = -INFINITY;
         int bi = 0x7fffffff;
         for (int r0 = wv; r0 < LR; r0 += 32) {
           float acc[8];
-          int ro[8];
+          int ro[2][4];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) ro[i] = min(r0 + 4 * i, LR - 1) * D * 2;  // (rows past LR: ignored)
-          chunk_dot_at<8>(W, ro, x_lds, D, lane, acc);
+          for (int i = 0; i < 8; ++i) ro[i >> 2][i & 3] = min(r0 + 4 * i, LR - 1) * D * 2;  // (rows past LR: ignored)
+          {
+            float t[4];
+            dot_rows<4, D>(W, ro[0], x_lds, lane, t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = t[i];
+            dot_rows<4, D>(W, ro[1], x_lds, lane, t);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[4 + i] = t[i];
+          }
           const float v = multi_sum<8>(acc, scr, lane) * inv;
           const int r = r0 + 4 * (lane >> 3), id = b * LR + r;
           if ((lane & 7) == 0 && r < LR && a.logits_out) a.logits_out[(int64_t)s * V + id] = v;
@@ -634,33 +634,57 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       }
       lds_barrier();  // B5
       if (loader && G + 1 < total) issue(G + 1, 1);
-      if (comp) {
-        if (tid == 0) {
+      // the first-max argmax over all 256 candidates in two hand-overs: the
+      // 32 candidates of this XCD (every workgroup of it reduces them
+      // alike), then the 8 XCD winners (wave 0 only)
+      if (wv == 0) {
+        if (lane == 0) {
           float v = red[0];
           int i = ired[0];
           for (int w = 1; w < 4; ++w) amax_take(v, i, red[w], ired[w]);
-          slot_put_dev(LM + 2 * b, v, ep);
-          slot_put_dev(LM + 2 * b + 1, __int_as_float(i), ep);
+          slot_put_xcd(LMX + 2 * c, v, ep);
+          slot_put_xcd(LMX + 2 * c + 1, __int_as_float(i), ep);
         }
-        // every workgroup reads all 256 candidates
         float cv[2];
         float bv = -INFINITY;
         int bi = 0x7fffffff;
-        if (slots_wait<2>(LM + 2 * tid, 1, 2, ep, cv, err)) {
-          bv = cv[0];
-          bi = __float_as_int(cv[1]);
-        } else {
-          *stop = 1;
+        if (lane < FUSED_NC) {
+          if (slots_wait<2>(LMX + 2 * lane, 1, 2, ep, cv, err)) {
+            bv = cv[0];
+            bi = __float_as_int(cv[1]);
+          } else {
+            *stop = 1;
+          }
         }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
+        for (int o = 16; o > 0; o >>= 1) {
+          const float v2 = __shfl_xor(bv, o, 64);
+          const int i2 = __shfl_xor(bi, o, 64);
+          amax_take(bv, bi, v2, i2);
+        }
+        if (lane == 0 && c == 0) {
+          slot_put_dev(LMG + 2 * g, bv, ep + 1);
+          slot_put_dev(LMG + 2 * g + 1, __int_as_float(bi), ep + 1);
+        }
+        bv = -INFINITY;
+        bi = 0x7fffffff;
+        if (lane < FUSED_NX && !*stop) {
+          if (slots_wait<2>(LMG + 2 * lane, 1, 2, ep + 1, cv, err)) {
+            bv = cv[0];
+            bi = __float_as_int(cv[1]);
+          } else {
+            *stop = 1;
+          }
+        }
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1) {
           const float v2 = __shfl_xor(bv, o, 64);
           const int i2 = __shfl_xor(bi, o, 64);
           amax_take(bv, bi, v2, i2);
         }
         if (lane == 0) {
-          red[4 + wv] = bv;
-          ired[4 + wv] = bi;
+          red[4] = bv;
+          ired[4] = bi;
         }
       }
       mark(s, L, 2);
@@ -668,9 +692,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       mark(s, L, 3);
       if (*stop) goto done;
       if (loader && G + 1 < total) issue(G + 1, 2);
-      float v = red[4];
       int id = ired[4];
-      for (int w = 1; w < 4; ++w) amax_take(v, id, red[4 + w], ired[4 + w]);
       if (id == 0x7fffffff) id = 0;  // no finite candidate: position 1, as the scan starts there
       if (b == 0 && tid == 0) a.ids_out[s] = id;
       if (s + 1 < a.n_steps) embed(id, pos + 1);
@@ -727,7 +749,7 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
   f.off_hl = f.off_xl + 2 * FUSED_NX * (int64_t)d.D;
   f.off_p2 = f.off_hl + 2 * FUSED_NX * (int64_t)f.HN;
   f.off_lm = f.off_p2 + 2 * FUSED_NX * (int64_t)d.D;
-  f.slots = f.off_lm + 2 * FUSED_NWG * 2;
+  f.slots = f.off_lm + 2 * FUSED_NWG * 2 + 2 * FUSED_NX * 2;
   f.ok = true;
   return f;
 }
@@ -774,7 +796,7 @@ uint32_t fused_epochs(const Dims& d, int n_steps) { return (uint32_t)n_steps * (
 template <class Sh>
 static hipError_t launch_shape(hipStream_t s, const FusedLayout& f, const FusedArgs& a) {
   if (f.slice != Sh::SLICE || f.lmb != Sh::LMB || f.wbuf != Sh::WBUF || f.wf != Sh::WF ||
-      f.off_lm != Sh::OFF_LM)
+      f.off_lm != Sh::OFF_LM || f.slots != Sh::SLOTS)
     return hipErrorInvalidValue;  // (host and device layouts disagree)
   const void* k = a.trace ? (const void*)k_fused_decode<Sh, true> : (const void*)k_fused_decode<Sh, false>;
   hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)f.lds_bytes);
