@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <atomic>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -414,10 +415,10 @@ void linear(fg_model* m, hipStream_t s, GemvEpi epi, const GemvArgs& a, const in
     timed(m, s, FG_K_GEMV, flops, bytes, [&] { launch_gemv_pos(s, epi, a, d_pos); });
 }
 
-GemvArgs base_args(fg_model* m) {
+GemvArgs base_args(fg_model* m, const Work& ws) {
   GemvArgs a;
   memset(&a, 0, sizeof a);
-  a.part = m->ws.part;
+  a.part = ws.part;
   a.eps = m->d.eps;
   a.cosb = m->d_cos;
   a.sinb = m->d_sin;
@@ -445,9 +446,10 @@ struct PassOpts {
 // it stands for (a speculative verification pass).
 void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, int pos0,
                  const int32_t* d_pos, float* kc, float* vc, int maxT, int64_t lstride,
-                 float* dec_part, float* logits, const PassOpts& o = PassOpts()) {
+                 float* dec_part, float* logits, const PassOpts& o = PassOpts(),
+                 Work* ws_in = nullptr) {
   const Dims& d = m->d;
-  Work& ws = m->ws;
+  Work& ws = ws_in ? *ws_in : m->ws;
   const int rows = B * T;
   const bool gm = !o.rows_single && use_gemm(d, rows);
   const int pos_host = o.pos_host < 0 ? pos0 : o.pos_host;
@@ -470,7 +472,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   for (int l = 0; l < d.L; ++l) {
     float* lk = kc ? kc + l * lstride : nullptr;  // null: no persistent cache (gpt_forward)
     float* lv = vc ? vc + l * lstride : nullptr;
-    GemvArgs a = base_args(m);
+    GemvArgs a = base_args(m, ws);
     a.M = rows;
     a.d_M = o.d_rows;
     a.T = T;
@@ -530,7 +532,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     linear(m, s, GV_RESID, a, d_pos, gm);
     nt = gemm_ssq_parts(rows, d.D, d.dff);
   }
-  GemvArgs a = base_args(m);
+  GemvArgs a = base_args(m, ws);
   a.M = rows; a.T = T; a.d_M = o.d_rows;
   a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
   a.w = m->w.lm; a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
@@ -1077,6 +1079,83 @@ extern "C" int32_t fg_step(fg_model* m, fg_kv* kv, const int32_t* ids, float* lo
   RCCHK(check_ids(m, ids, kv->B));
   GUARD(m);
   return kv_pass(m, kv, ids, 1, logits, next_ids);
+}
+
+// ------------------------------------------------------------ no-allocation step
+// fg_step_dev_noalloc keeps the step's activations (x, q, attention output,
+// relu2(fc)) and the single-query attention's per-chunk partials in this
+// file-scope device array, one copy per GPU, instead of memory the library
+// allocates. Its device address is taken once per device with
+// hipGetSymbolAddress; host code uses only that address, never the name.
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+constexpr int NOALLOC_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+namespace {
+
+// The scratch array's address on device dev (current), looked up on first use.
+int32_t scratch_on(int dev, uint8_t** out) {
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return seterr(FG_EARG, "device %d beyond the %d this build tracks", dev, NOALLOC_MAX_DEVICES);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return seterr(FG_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = (uint8_t*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FG_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+}  // namespace
+
+// gpt_step for the kv's B sequences on device buffers with no allocation:
+// the kernels of fg_step's single-row path (GEMV linears, single-query
+// attention, argmax), their scratch in the array above.
+extern "C" int32_t fg_step_dev_noalloc(fg_model* m, fg_kv* kv, const int32_t* d_ids,
+                                       float* d_logits, int32_t* d_next, void* stream) {
+  if (!m || !kv || !d_ids || !d_logits || kv->m != m) return seterr(FG_EARG, "bad argument");
+  GUARD(m);
+  const Dims& d = m->d;
+  const int B = kv->B;
+  if (use_gemm(d, B))
+    return seterr(FG_EARG, "fg_step_dev_noalloc serves the single-row path: %d sequences at "
+                           "d_model %d need the GEMM path (at most %d here)",
+                  B, d.D, d.dff * 4 * 4 > 65536 ? 65536 / (d.dff * 4) : 4);
+  if (kv->len + 1 > kv->maxT)
+    return seterr(FG_EFULL, "cache full (raise maxT): len %d + 1 > %d", kv->len, kv->maxT);
+  RCCHK(check_rope(m, kv->len + 1));
+  const size_t act = align256((size_t)B * (d.D + 2 * d.qd() + d.dff) * 4);
+  const size_t part = (size_t)attn_decode_scratch_floats(d, B, kv->maxT) * 4;
+  if (act + part > NOALLOC_SCRATCH_BYTES)
+    return seterr(FG_EARG, "this step needs %zu bytes of scratch (B=%d, maxT=%d), above the %zu "
+                           "the library holds",
+                  act + part, B, kv->maxT, NOALLOC_SCRATCH_BYTES);
+  uint8_t* sp = nullptr;
+  RCCHK(scratch_on(m->device, &sp));
+  Work w;
+  w.rows = B;
+  w.x = (float*)sp;
+  w.q = w.x + (size_t)B * d.D;
+  w.ao = w.q + (size_t)B * d.qd();
+  w.h = w.ao + (size_t)B * d.qd();
+  float* dec_part = (float*)(sp + act);
+  hipStream_t s = stream ? (hipStream_t)stream : m->stream;
+  const bool tm = m->timing;  // (timing records events: not on this path)
+  m->timing = false;
+  layer_stack(m, s, d_ids, B, 1, kv->len, nullptr, kv->k, kv->v, kv->maxT,
+              (int64_t)B * kv->maxT * d.kvd(), dec_part, d_logits, PassOpts(), &w);
+  if (d_next) launch_argmax(s, d_logits, B, d.V, d_next);
+  m->timing = tm;
+  HIPCHK(hipGetLastError());
+  kv->len += 1;
+  return FG_OK;
 }
 
 extern "C" int32_t fg_step_multi(fg_model* m, fg_kv* kv, const int32_t* ids, int32_t TB,

@@ -34,7 +34,7 @@ EXPORTS = (
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
     "fg_eval_bpb", "fg_rows_npy", "fg_decode_spec", "fg_spec_accept", "fg_spec_draft",
-    "fg_sample", "fg_decode_sample", "fg_set_option", "fg_get_option",
+    "fg_sample", "fg_decode_sample", "fg_set_option", "fg_get_option", "fg_step_dev_noalloc",
 )
 
 KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other",
@@ -127,6 +127,7 @@ def load_library(path: str = LIB_PATH):
         "fg_decode_sample": (i32, [_vp, _vp, _i, i32, i32, C.POINTER(_SampleCfg),
                                    C.POINTER(i64)]),
         "fg_set_option": (i32, [_vp, i32, i32]),
+        "fg_step_dev_noalloc": (i32, [_vp, _vp, _vp, _vp, _vp, _vp]),
         "fg_get_option": (i32, [_vp, i32, _i, C.c_char_p, i32]),
         "fg_timing_read": (i32, [_vp, i32, C.POINTER(i64), C.POINTER(C.c_double),
                                  C.POINTER(C.c_double), C.POINTER(C.c_double)]),
@@ -329,6 +330,12 @@ class KV:
         nxt = np.empty(self.B, np.int32)
         _check(_LIB.fg_step(self.m.handle, self._h, _ip(ids), _fp(lg), _ip(nxt)))
         return (lg.reshape(self.B, -1) if lg is not None else None), nxt
+
+    def step_dev_noalloc(self, d_ids: int, d_logits: int, d_next: int = 0, stream: int = 0):
+        """fg_step_dev_noalloc on device pointers (ints): one cached step whose
+        scratch is the library's own device array (no allocation)."""
+        _check(_LIB.fg_step_dev_noalloc(self.m.handle, self._h, d_ids, d_logits, d_next or None,
+                                        stream or None))
 
     def step_multi(self, ids, want_logits: bool = True):
         ids = _i32(ids).reshape(self.B, -1)

@@ -143,6 +143,21 @@ int32_t fg_kv_read(fg_kv *kv, float *k_out, float *v_out);
  * greedy argmax (src/lib/sample.f90:271-277). Advances cache_len by 1. */
 int32_t fg_step(fg_model *m, fg_kv *kv, const int32_t *ids, float *logits, int32_t *next_ids);
 
+/* fg_step on device buffers that allocates nothing: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * d_ids (B, device) in; d_logits (B*V, device) out; d_next (B, device,
+ * nullable) = the argmax of each row. Enqueued on `stream` (NULL = the
+ * handle's stream) without host synchronisation; advances cache_len by 1.
+ * The kv's B must take the single-row path (B <= 4 at depth-12's dims;
+ * FG_EARG otherwise). The step's activations and attention partials live
+ * in one 4 MiB device array the library holds per GPU (FG_EARG when B and
+ * maxT need more); every call on a GPU shares it, so calls that overlap on
+ * one GPU race. Nothing in it needs clearing: each kernel writes what it
+ * reads later. Invalid ids are not checked on the host (they embed to NaN). */
+int32_t fg_step_dev_noalloc(fg_model *m, fg_kv *kv, const int32_t *d_ids, float *d_logits,
+                            int32_t *d_next, void *stream);
+
 /* gpt_step_multi (src/lib/fortran_kv.f90:160-289): TB tokens of each of the
  * B sequences at positions cache_len..cache_len+TB-1; logits (B*TB*V,
  * nullable), next_ids (B, nullable) = argmax of each sequence's last row.

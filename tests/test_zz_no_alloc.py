@@ -1,0 +1,117 @@
+"""fg_step_dev_noalloc (a cached step that allocates nothing: its scratch is
+the library's own per-GPU device array) against fg_step, through the C ABI,
+on twin caches filled by the same prefill: the same kernels on the same
+inputs, so logits, next ids and the cache rows written must be identical.
+Two calls in a row, the second with fewer sequences, then the refusals.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from autoresearch_amd import engine
+from autoresearch_amd.weights import D12, Dims, rope_tables, seeded_weights, uniform_ids
+
+pytestmark = pytest.mark.gpu
+
+
+class DevBuf:
+    """A device buffer from the HIP runtime libfgpt.so is linked against
+    (test plumbing only: the step under test takes device pointers)."""
+
+    hip = None
+
+    def __init__(self, arr):
+        if DevBuf.hip is None:
+            engine.load_library()
+            DevBuf.hip = C.CDLL("libamdhip64.so.7")
+        self.nbytes = arr.nbytes
+        self.dtype = arr.dtype
+        self.p = C.c_void_p()
+        assert DevBuf.hip.hipMalloc(C.byref(self.p), C.c_size_t(self.nbytes)) == 0
+        self.put(arr)
+
+    def put(self, arr):
+        a = np.ascontiguousarray(arr, dtype=self.dtype)
+        assert DevBuf.hip.hipMemcpy(self.p, a.ctypes.data_as(C.c_void_p), C.c_size_t(self.nbytes), 1) == 0
+
+    def get(self):
+        out = np.empty(self.nbytes // self.dtype.itemsize, self.dtype)
+        assert DevBuf.hip.hipDeviceSynchronize() == 0
+        assert DevBuf.hip.hipMemcpy(out.ctypes.data_as(C.c_void_p), self.p, C.c_size_t(self.nbytes), 2) == 0
+        return out
+
+    @property
+    def ptr(self):
+        return self.p.value
+
+    def free(self):
+        DevBuf.hip.hipFree(self.p)
+
+
+@pytest.fixture(scope="module")
+def d12():
+    m = engine.Model(D12, stacks=seeded_weights(D12, 1234))
+    c, s = rope_tables(64, D12.head_dim)
+    m.set_rope(c.reshape(-1), s.reshape(-1))
+    yield D12, m
+    m.close()
+
+
+def noalloc_vs_step(d, m, B, P, seed, n_steps=3):
+    prompts = uniform_ids(seed, B * P, d.vocab).reshape(B, P)
+    ka, kb = m.kv(B, P + n_steps), m.kv(B, P + n_steps)
+    for kv in (ka, kb):
+        kv.step_multi(prompts[:, :-1], want_logits=False)
+    ids = prompts[:, -1].astype(np.int32)
+    d_ids = DevBuf(ids)
+    d_lg = DevBuf(np.zeros(B * d.vocab, np.float32))
+    d_nx = DevBuf(np.zeros(B, np.int32))
+    for _ in range(n_steps):
+        lg_a, nx_a = ka.step(ids)
+        kb.step_dev_noalloc(d_ids.ptr, d_lg.ptr, d_nx.ptr)
+        m.sync()
+        lg_b = d_lg.get().reshape(B, d.vocab)
+        nx_b = d_nx.get()
+        assert np.array_equal(nx_a, nx_b)
+        assert np.array_equal(lg_a, lg_b)
+        ids = nx_a.astype(np.int32)
+        d_ids.put(ids)
+    for b_ in (d_ids, d_lg, d_nx):
+        b_.free()
+    assert ka.len == kb.len == P - 1 + n_steps
+    (k_a, v_a), (k_b, v_b) = ka.read(), kb.read()
+    assert np.array_equal(k_a, k_b) and np.array_equal(v_a, v_b)
+    ka.close()
+    kb.close()
+
+
+def test_noalloc_step_equals_step_then_smaller(d12):
+    d, m = d12
+    noalloc_vs_step(d, m, B=4, P=9, seed=3)
+    noalloc_vs_step(d, m, B=2, P=5, seed=4)
+
+
+def test_noalloc_refusals(d12):
+    d, m = d12
+    d_ids = DevBuf(np.zeros(8, np.int32))
+    d_lg = DevBuf(np.zeros(8 * d.vocab, np.float32))
+    kv = m.kv(8, 16)  # 8 sequences take the GEMM path
+    with pytest.raises(engine.FgptError, match="single-row path"):
+        kv.step_dev_noalloc(d_ids.ptr, d_lg.ptr)
+    kv.close()
+    # 4 sequences x 8 heads x 16000 positions of attention partials exceed
+    # the 4 MiB array
+    dw = Dims(n_layer=1, d_model=1024, n_head=8, n_kv_head=8, head_dim=128, vocab=256)
+    mw = engine.Model(dw, stacks=seeded_weights(dw, 1))
+    c, s = rope_tables(4, dw.head_dim)
+    mw.set_rope(c.reshape(-1), s.reshape(-1))
+    kv = mw.kv(4, 16000)
+    d_lw = DevBuf(np.zeros(4 * dw.vocab, np.float32))
+    with pytest.raises(engine.FgptError, match="scratch"):
+        kv.step_dev_noalloc(d_ids.ptr, d_lw.ptr)
+    assert kv.len == 0
+    kv.close()
+    mw.close()
+    for b_ in (d_ids, d_lg, d_lw):
+        b_.free()
