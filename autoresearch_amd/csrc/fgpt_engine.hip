@@ -104,6 +104,7 @@ struct fg_model {
 struct fg_kv {
   fg_model* m = nullptr;
   int B = 0, maxT = 0, len = 0;
+  int filled = 0;  // positions this cache has computed (high-water mark of len)
   float* k = nullptr;  // [L][B][maxT][KH*hd]
   float* v = nullptr;
   int32_t* d_len = nullptr;  // device copy of len for replayed steps; d_len[1] = len at
@@ -846,6 +847,8 @@ extern "C" int32_t fg_kv_len(const fg_kv* kv, int32_t* len) {
 extern "C" int32_t fg_kv_set_len(fg_kv* kv, int32_t len) {
   if (!kv) return seterr(FG_EARG, "NULL argument");
   if (len < 0 || len > kv->maxT) return seterr(FG_EARG, "len %d outside [0, %d]", len, kv->maxT);
+  if (len > kv->filled)
+    return seterr(FG_EARG, "len %d: this cache has computed only %d positions", len, kv->filled);
   kv->len = len;
   return FG_OK;
 }
@@ -905,6 +908,7 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
     HIPCHK(hipMemcpyAsync(logits, m->ws.logits, rows * m->d.V * 4, hipMemcpyDeviceToHost, s));
   HIPCHK(hipStreamSynchronize(s));
   kv->len += TB;
+  kv->filled = std::max(kv->filled, kv->len);
   return FG_OK;
 }
 
@@ -1155,6 +1159,7 @@ extern "C" int32_t fg_step_dev_noalloc(fg_model* m, fg_kv* kv, const int32_t* d_
   m->timing = tm;
   HIPCHK(hipGetLastError());
   kv->len += 1;
+  kv->filled = std::max(kv->filled, kv->len);
   return FG_OK;
 }
 
@@ -1222,6 +1227,7 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
                              : "a hand-over between workgroups timed out");
   }
   kv->len += n_steps;
+  kv->filled = std::max(kv->filled, kv->len);
   return FG_OK;
 }
 
@@ -1348,6 +1354,7 @@ extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t 
                         hipMemcpyDeviceToHost, s));
   HIPCHK(hipStreamSynchronize(s));
   kv->len = n_total - 1;
+  kv->filled = std::max(kv->filled, kv->len);
   if (stats) *stats = fg_spec_stats{h->passes, h->accepted, h->proposed, h->plain, h->pauses};
   return FG_OK;
 }
@@ -1513,6 +1520,7 @@ extern "C" int32_t fg_decode_sample(fg_model* m, fg_kv* kv, int32_t* ids, int32_
   if (h->pp != n_total) return seterr(FG_EHIP, "sampling loop ended at %d of %d", h->pp, n_total);
   *state = h->rng;
   kv->len = n_total - 1;
+  kv->filled = std::max(kv->filled, kv->len);
   return FG_OK;
 }
 

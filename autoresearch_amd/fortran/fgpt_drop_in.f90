@@ -8,12 +8,17 @@
 !
 ! What changes under the same arguments:
 !  - The weights are uploaded to HBM (bf16, exact) on the first call and kept
-!    there. Later calls with the same arrays (same addresses and dims) reuse
-!    them; different arrays re-upload. Weights changed in place are not seen:
-!    call fgpt_release() after changing them.
-!  - The KV cache lives in HBM. cache_k / cache_v are accepted and left
-!    untouched; cache_len is honoured in and out exactly as in the reference
-!    (resetting it to 0 starts a new sequence).
+!    there: one engine model per distinct (weight arrays, dims, eps), so a
+!    caller that alternates the full depth and a truncated n_layer over the
+!    same stacked arrays (spec_bench's drafter) keeps one upload of each.
+!    Weights changed in place are not seen: call fgpt_release() after
+!    changing them.
+!  - The KV cache lives in HBM: one device cache per caller cache (the
+!    address of cache_k) and model, B and maxT, so distinct host caches stay
+!    distinct. cache_k / cache_v are accepted and left untouched; cache_len
+!    is honoured in and out exactly as in the reference (resetting it to 0
+!    starts a new sequence, rolling it back re-uses the rows below it); a
+!    cache_len past the positions that cache has computed stops the program.
 !  - RoPE rows are taken from the caller's tables on every call (the rows of
 !    the positions being computed), as the reference uses them.
 !  - Errors stop the program with the engine's message, the reference's
@@ -27,11 +32,26 @@ module fgpt_drop_in_mod
   public :: gpt_forward, gpt_step, gpt_step_multi, load_gpt_weights, fgpt_release, &
       fgpt_handles, accept_prefix, lookup_draft, sample_next
 
+  ! engine models by (weight array addresses, dims, eps) and device caches
+  ! by (address of the caller's cache_k, model, B, maxT)
+  integer, parameter :: NMODELS = 4, NCACHES = 8
+  type model_slot
+    type(c_ptr) :: h = c_null_ptr
+    integer(c_intptr_t) :: key(8) = 0
+    integer :: dims(6) = -1
+    real(c_float) :: eps = 0.0
+  end type model_slot
+  type kv_slot
+    type(c_ptr) :: h = c_null_ptr
+    integer(c_intptr_t) :: cache = 0
+    integer :: model = 0, bb = -1, maxt = -1
+  end type kv_slot
+  type(model_slot), save :: g_models(NMODELS)
+  type(kv_slot), save :: g_caches(NCACHES)
+  ! the model and cache of the latest call (fgpt_handles, sample_next)
   type(c_ptr), save :: g_model = c_null_ptr
   type(c_ptr), save :: g_kv = c_null_ptr
-  integer(c_intptr_t), save :: g_key(8) = 0
-  integer, save :: g_dims(6) = -1
-  integer, save :: g_kv_b = -1, g_kv_maxt = -1
+  integer, save :: g_imodel = 0
 
 contains
 
@@ -42,8 +62,8 @@ contains
     error stop 1
   end subroutine die
 
-  ! Bind the engine model to these weight arrays (upload on first use or
-  ! when the arrays or dims change).
+  ! Bind the engine model of these weight arrays and dims (uploaded on
+  ! first use); it becomes g_model.
   subroutine bind_model(wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, &
       vocab_size, d_model, n_head, n_kv_head, head_dim, n_layer, eps)
     real(c_float), intent(in), target :: wte(:), c_q(:), c_k(:), c_v(:), c_proj(:), &
@@ -51,7 +71,7 @@ contains
     integer(c_int), intent(in) :: vocab_size, d_model, n_head, n_kv_head, head_dim, n_layer
     real(c_float), intent(in) :: eps
     integer(c_intptr_t) :: key(8)
-    integer :: dims(6)
+    integer :: dims(6), i, free
     type(fg_dims) :: fd
     integer(c_int32_t) :: rc
 
@@ -60,8 +80,24 @@ contains
         transfer(c_loc(c_proj), 0_c_intptr_t), transfer(c_loc(c_fc), 0_c_intptr_t), &
         transfer(c_loc(c_proj2), 0_c_intptr_t), transfer(c_loc(lm_head), 0_c_intptr_t)]
     dims = [n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size]
-    if (c_associated(g_model) .and. all(key == g_key) .and. all(dims == g_dims)) return
-    call fgpt_release()
+    free = 0
+    do i = 1, NMODELS
+      if (c_associated(g_models(i)%h)) then
+        if (all(g_models(i)%key == key) .and. all(g_models(i)%dims == dims) .and. &
+            g_models(i)%eps == eps) then
+          g_imodel = i
+          g_model = g_models(i)%h
+          return
+        end if
+      else if (free == 0) then
+        free = i
+      end if
+    end do
+    if (free == 0) then
+      write (error_unit, '(A,I0,A)') 'fgpt: more than ', NMODELS, &
+          ' distinct weight sets or depths in use (call fgpt_release())'
+      error stop 1
+    end if
     if (size(wte) < vocab_size*d_model .or. size(lm_head) < vocab_size*d_model .or. &
         size(c_q) < n_layer*n_head*head_dim*d_model .or. &
         size(c_k) < n_layer*n_kv_head*head_dim*d_model .or. &
@@ -72,35 +108,66 @@ contains
       error stop 1
     end if
     fd = fg_dims(n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size, eps)
-    rc = fg_model_create(fd, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, g_model)
+    rc = fg_model_create(fd, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, g_models(free)%h)
     if (rc /= FG_OK) call die('fgpt: weight upload', rc)
-    g_key = key
-    g_dims = dims
+    g_models(free)%key = key
+    g_models(free)%dims = dims
+    g_models(free)%eps = eps
+    g_imodel = free
+    g_model = g_models(free)%h
   end subroutine bind_model
 
-  subroutine bind_kv(bb, maxt)
+  ! Bind the device cache of the caller's cache (its address) for the
+  ! current model, B sequences of maxt positions; it becomes g_kv.
+  subroutine bind_kv(cache_k, bb, maxt)
+    real(c_float), intent(in), target :: cache_k(:)
     integer(c_int), intent(in) :: bb, maxt
+    integer(c_intptr_t) :: addr
+    integer :: i, free
     integer(c_int32_t) :: rc
-    if (c_associated(g_kv) .and. g_kv_b == bb .and. g_kv_maxt == maxt) return
-    if (c_associated(g_kv)) rc = fg_kv_destroy(g_kv)
-    g_kv = c_null_ptr
-    rc = fg_kv_create(g_model, bb, maxt, g_kv)
+
+    addr = transfer(c_loc(cache_k), 0_c_intptr_t)
+    free = 0
+    do i = 1, NCACHES
+      if (c_associated(g_caches(i)%h)) then
+        if (g_caches(i)%cache == addr .and. g_caches(i)%model == g_imodel .and. &
+            g_caches(i)%bb == bb .and. g_caches(i)%maxt == maxt) then
+          g_kv = g_caches(i)%h
+          return
+        end if
+      else if (free == 0) then
+        free = i
+      end if
+    end do
+    if (free == 0) then
+      write (error_unit, '(A,I0,A)') 'fgpt: more than ', NCACHES, &
+          ' distinct caches in use (call fgpt_release())'
+      error stop 1
+    end if
+    rc = fg_kv_create(g_model, bb, maxt, g_caches(free)%h)
     if (rc /= FG_OK) call die('fgpt: KV cache', rc)
-    g_kv_b = bb
-    g_kv_maxt = maxt
+    g_caches(free)%cache = addr
+    g_caches(free)%model = g_imodel
+    g_caches(free)%bb = bb
+    g_caches(free)%maxt = maxt
+    g_kv = g_caches(free)%h
   end subroutine bind_kv
 
-  ! Drop the device model and cache (the next call re-uploads).
+  ! Drop every device model and cache (the next call uploads again).
   subroutine fgpt_release()
     integer(c_int32_t) :: rc
-    if (c_associated(g_kv)) rc = fg_kv_destroy(g_kv)
-    if (c_associated(g_model)) rc = fg_model_destroy(g_model)
+    integer :: i
+    do i = 1, NCACHES
+      if (c_associated(g_caches(i)%h)) rc = fg_kv_destroy(g_caches(i)%h)
+      g_caches(i) = kv_slot()
+    end do
+    do i = 1, NMODELS
+      if (c_associated(g_models(i)%h)) rc = fg_model_destroy(g_models(i)%h)
+      g_models(i) = model_slot()
+    end do
     g_kv = c_null_ptr
     g_model = c_null_ptr
-    g_key = 0
-    g_dims = -1
-    g_kv_b = -1
-    g_kv_maxt = -1
+    g_imodel = 0
   end subroutine fgpt_release
 
   ! The engine handles behind the drop-in calls (for callers that also use
@@ -112,10 +179,12 @@ contains
   end subroutine fgpt_handles
 
   ! src/lib/fortran_gpt.f90:54-199. attn_blas selects another summation
-  ! order in the reference; here there is one attention kernel, so it is
-  ! accepted and has no effect. attn_qk (QK-hop) is not part of this path.
-  ! pos_frac / pos_n are attention statistics of the attn_blas path and are
-  ! left untouched.
+  ! order of the same attention in the reference (attn_sgemm); here there is
+  ! one attention kernel, so attn_blas alone is accepted. With attn_blas the
+  ! reference also accumulates its positive-score statistics into pos_frac
+  ! / pos_n (src/lib/fortran_attn.f90:247-300): this engine does not produce
+  ! them, so asking for them stops the program. attn_qk (QK-hop) is not part
+  ! of this path and stops it too.
   subroutine gpt_forward(idx, cos_buf, sin_buf, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, &
       lm_head, outp, BB, TT, vocab_size, d_model, n_head, n_kv_head, head_dim, n_layer, eps, &
       attn_blas, attn_qk, pos_frac, pos_n)
@@ -135,6 +204,13 @@ contains
     if (present(attn_qk)) then
       if (attn_qk) then
         write (error_unit, '(A)') 'gpt_forward: attn_qk (QK-hop) is not supported by this engine'
+        error stop 1
+      end if
+    end if
+    if (present(attn_blas)) then
+      if (attn_blas .and. (present(pos_frac) .or. present(pos_n))) then
+        write (error_unit, '(A)') 'gpt_forward: the attn_blas positive-score statistics ' // &
+            '(pos_frac / pos_n) are not produced by this engine'
         error stop 1
       end if
     end if
@@ -164,7 +240,7 @@ contains
     real(c_float), intent(in) :: cos1(:), sin1(:)
     real(c_float), intent(in), target :: wte(:), c_q(:), c_k(:), c_v(:), c_proj(:), c_fc(:), &
         c_proj2(:), lm_head(:)
-    real(c_float), intent(inout) :: cache_k(:), cache_v(:)
+    real(c_float), intent(inout), target :: cache_k(:), cache_v(:)
     real(c_float), intent(out) :: out1(:)
     integer(c_int32_t) :: rc
 
@@ -174,7 +250,7 @@ contains
     end if
     call bind_model(wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, vocab_size, d_model, &
         n_head, n_kv_head, head_dim, n_layer, eps)
-    call bind_kv(BB, maxT)
+    call bind_kv(cache_k, BB, maxT)
     rc = fg_kv_set_len(g_kv, cache_len)
     if (rc /= FG_OK) call die('gpt_step', rc)
     rc = fg_set_rope(g_model, cache_len, 1_c_int32_t, cos1, sin1)
@@ -197,7 +273,7 @@ contains
     real(c_float), intent(in) :: cos_buf(:), sin_buf(:)
     real(c_float), intent(in), target :: wte(:), c_q(:), c_k(:), c_v(:), c_proj(:), c_fc(:), &
         c_proj2(:), lm_head(:)
-    real(c_float), intent(inout) :: cache_k(:), cache_v(:)
+    real(c_float), intent(inout), target :: cache_k(:), cache_v(:)
     real(c_float), intent(out) :: out(:)
     integer(c_int32_t) :: rc
 
@@ -211,7 +287,7 @@ contains
     end if
     call bind_model(wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, vocab_size, d_model, &
         n_head, n_kv_head, head_dim, n_layer, eps)
-    call bind_kv(BB, maxT)
+    call bind_kv(cache_k, BB, maxT)
     rc = fg_kv_set_len(g_kv, cache_len)
     if (rc /= FG_OK) call die('gpt_step_multi', rc)
     rc = fg_set_rope(g_model, cache_len, TB, cos_buf, sin_buf)

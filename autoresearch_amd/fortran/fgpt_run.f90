@@ -27,9 +27,15 @@
 !            423-462, src/lib/sample.f90:153-233): loop=host steps through the
 !            drop-in gpt_step and sample_next, loop=device is one
 !            fg_decode_sample call; the history is the ids generated so far.
-!   spectest the accept rule and the drafter through the drop-in names, on
-!            the known answers of src/test/test_kernels.f90:1556-1650 (host
-!            only).
+!   specbench src/app/spec_bench.f90's truncated-drafter pilot through the
+!            drop-in calls: the drafter is the first DL layers of the same
+!            stacked weights, each model with its own caller cache; both
+!            caches prefilled by gpt_step_multi chunks of 64, a plain greedy
+!            run (gpt_step per id, host argmax), then draft-and-verify
+!            rounds (K+1 drafter gpt_step calls, one target gpt_step_multi
+!            over K+1 rows, accept_prefix, both cache_len rolled back to
+!            p-1). Prints spec_bench's summary lines and stops unless the
+!            two streams are equal; OUT_FILE gets the plain stream.
 !
 ! Usage:
 !   fgpt_run greedy WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [PCHUNK] [host|device]
@@ -37,7 +43,7 @@
 !   fgpt_run bpb    WDIR L D H KH HD V ROWS_NPY TOKEN_BYTES [BATCH] [NLL_OUT]
 !   fgpt_run selftest
 !   fgpt_run spec   WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [K] [MATCH] [PROBE] [MIN_ACC]
-!   fgpt_run spectest
+!   fgpt_run specbench WDIR L D H KH HD V IDS_FILE NPRE NGEN OUT_FILE [K] [DL]
 !   fgpt_run sample WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE TEMP TOPP SEED
 !                   [PRES FREQ REP PWIN PLEN NBLOCK BYTE(0|1) [host|device]]
 ! Ids files are whitespace-separated 0-based integers. Timing goes to stderr.
@@ -65,8 +71,8 @@ program fgpt_run
     call run_selftest()
   case ('spec')
     call run_spec()
-  case ('spectest')
-    call run_spectest()
+  case ('specbench')
+    call run_specbench()
   case ('sample')
     call run_sample()
   case default
@@ -81,7 +87,7 @@ contains
     write (error_unit, '(A)') '       fgpt_run bpb WDIR L D H KH HD V ROWS_NPY TOKEN_BYTES [BATCH] [NLL_OUT]'
     write (error_unit, '(A)') '       fgpt_run selftest'
     write (error_unit, '(A)') '       fgpt_run spec WDIR L D H KH HD V IDS NGEN OUT [K] [MATCH] [PROBE] [MIN_ACC]'
-    write (error_unit, '(A)') '       fgpt_run spectest'
+    write (error_unit, '(A)') '       fgpt_run specbench WDIR L D H KH HD V IDS NPRE NGEN OUT [K] [DL]'
     write (error_unit, '(A)') '       fgpt_run sample WDIR L D H KH HD V IDS NGEN OUT TEMP TOPP SEED ' // &
         '[PRES FREQ REP PWIN PLEN NBLOCK BYTE [host|device]]'
     stop 2
@@ -635,81 +641,174 @@ contains
     call fgpt_release()
   end subroutine run_sample
 
-  ! The reference's accept_prefix and lookup_draft known answers, through
-  ! the drop-in subroutines of the same names (host only).
-  subroutine run_spectest()
-    integer, parameter :: K = 5, NT = 40
-    integer :: draft(K), targ(K+1), tg(NT+K+1), buf(NT+K+1), ids(9), d(6)
-    integer :: na, corr, p, j, ncomm, npass, ncorr, kk, nfail, nchk
+  ! src/app/spec_bench.f90:132-339 with the drop-in calls underneath
+  subroutine run_specbench()
+    character(len=512) :: wdir, ids_file, out_file
+    integer :: L, D, H, KH, HD, V, npre, ngen, kspec, dl, nmax, d2, nids, i, u
+    integer :: clen_t, clen_d, p, npass, naccept_total, ksum, gen_done
+    integer, allocatable :: ids(:), prompt(:), seq_plain(:), seq_spec(:), draft(:), targ(:)
+    real(c_float), allocatable :: wte(:), lm(:), c_q(:), c_k(:), c_v(:), c_pr(:), c_fc(:), c_pr2(:)
+    real(c_float), allocatable :: cos_b(:), sin_b(:), ck_t(:), cv_t(:), ck_d(:), cv_d(:)
+    real(c_float), allocatable :: chunk_out(:), row1(:)
+    real(8) :: ms_plain, ms_spec, t0
 
-    nfail = 0
-    nchk = 0
-    draft(1:4) = [1, 2, 3, 4]
-    targ(1:5) = [1, 2, 9, 9, 7]
-    call accept_prefix(draft, targ, 4, na, corr)
-    call chk(na == 2 .and. corr == 9, 'partial match')
-    draft(1:3) = [1, 2, 3]
-    targ(1:4) = [1, 2, 3, 5]
-    call accept_prefix(draft, targ, 3, na, corr)
-    call chk(na == 3 .and. corr == 5, 'all match: bonus row')
-    draft(1:2) = [1, 2]
-    targ(1:3) = [7, 8, 9]
-    call accept_prefix(draft, targ, 2, na, corr)
-    call chk(na == 0 .and. corr == 7, 'first rejected')
-    targ(1) = 4
-    call accept_prefix(draft, targ, 0, na, corr)
-    call chk(na == 0 .and. corr == 4, 'k=0 is a plain step')
-    do j = 1, NT + K + 1
-      tg(j) = mod(j*7 + 3, 11)
+    if (command_argument_count() < 12) call usage()
+    wdir = sarg(2); L = iarg(3); D = iarg(4); H = iarg(5); KH = iarg(6); HD = iarg(7); V = iarg(8)
+    ids_file = sarg(9); npre = iarg(10); ngen = iarg(11); out_file = sarg(12)
+    kspec = 8
+    if (command_argument_count() >= 13) kspec = iarg(13)
+    dl = 3
+    if (command_argument_count() >= 14) dl = iarg(14)
+    if (dl < 1 .or. dl > L) then
+      write (error_unit, '(A,I0)') 'draft-layers must be in 1..', L
+      stop 1
+    end if
+    if (kspec < 1) then
+      write (error_unit, '(A)') 'spec must be >= 1'
+      stop 1
+    end if
+    call read_ids(trim(ids_file), prompt, nids)
+    if (nids < npre + 2) then
+      write (error_unit, '(A,I0,A,I0)') 'row has ', nids, ' ids, need >= ', npre + 2
+      stop 1
+    end if
+    nmax = npre + ngen + kspec + 4
+    d2 = HD / 2
+    allocate (ids(nmax + 1))
+    ids = 0
+    ids(1:npre) = prompt(1:npre)
+    call load_gpt_weights(trim(wdir), L, D, H, KH, HD, V, wte, lm, c_q, c_k, c_v, c_pr, c_fc, c_pr2)
+    ! the reference's cache shapes: the drop-in keys its device caches by them
+    allocate (ck_t(L*nmax*KH*HD), cv_t(L*nmax*KH*HD), ck_d(dl*nmax*KH*HD), cv_d(dl*nmax*KH*HD))
+    allocate (chunk_out(max(64, kspec + 2)*V), row1(V))
+    allocate (seq_plain(ngen), seq_spec(ngen), draft(kspec), targ(kspec + 1))
+    call rope_tables(nmax, HD, cos_b, sin_b)
+
+    write (*, '(A,I0,A,I0,A,I0,A,I0)') 'prompt=', npre, ' gen=', ngen, ' spec K=', kspec, &
+        ' drafter layers=', dl
+    write (*, '(A,A,A,I0)') 'drafter: ', 'trunc', '  match=', 3
+
+    ! plain greedy: one cached step per token
+    clen_t = 0
+    clen_d = 0
+    call prefill_both()
+    t0 = now()
+    p = npre
+    do i = 1, ngen
+      call gpt_step(ids(p:p), cos_b((p-1)*d2+1:), sin_b((p-1)*d2+1:), wte, c_q, c_k, c_v, c_pr, &
+          c_fc, c_pr2, lm, ck_t, cv_t, clen_t, nmax, row1, 1, V, D, H, KH, HD, L, 1.0e-5_c_float)
+      ids(p + 1) = argmax_i(row1, V) - 1
+      seq_plain(i) = ids(p + 1)
+      p = p + 1
     end do
-    p = 1
-    ncomm = 0
+    ms_plain = 1000*(now() - t0)
+
+    ! greedy draft-and-verify on the same state
+    ids(npre+1:) = 0
+    clen_t = 0
+    clen_d = 0
+    call prefill_both()
     npass = 0
-    ncorr = 0
-    do while (ncomm < NT .and. p <= NT)
-      draft(1:K) = tg(p:p+K-1)
-      if (mod(p, 7) == 0) draft(3) = mod(draft(3) + 1, 11)
-      targ(1:K+1) = tg(p:p+K)
-      call accept_prefix(draft, targ, K, na, corr)
-      buf(ncomm+1:ncomm+na) = draft(1:na)
-      buf(ncomm+na+1) = corr
-      if (na < K) ncorr = ncorr + 1
-      ncomm = ncomm + na + 1
-      p = p + na + 1
-      npass = npass + 1
+    naccept_total = 0
+    ksum = 0
+    p = npre
+    gen_done = 0
+    t0 = now()
+    do while (gen_done < ngen)
+      call spec_round()
     end do
-    call chk(ncomm >= NT, 'simulation commits the span')
-    call chk(all(buf(1:ncomm) == tg(1:ncomm)), 'committed stream == target stream')
-    call chk(ncorr > 0, 'reject path exercised')
-    ids = [5, 1, 2, 3, 9, 1, 2, 3, 7]
-    call lookup_draft(ids, 8, 3, 6, d, kk)
-    call chk(kk == 4 .and. all(d(1:4) == [9, 1, 2, 3]), 'continuation capped at known ids')
-    call lookup_draft(ids, 8, 3, 2, d, kk)
-    call chk(kk == 2 .and. all(d(1:2) == [9, 1]), 'k truncates')
-    ids(1:3) = [5, 1, 2]
-    call lookup_draft(ids, 3, 5, 4, d, kk)
-    call chk(kk == 0, 'm > p-1 is a miss')
-    ids(1:6) = [1, 2, 3, 4, 5, 6]
-    call lookup_draft(ids, 6, 2, 3, d, kk)
-    call chk(kk == 0, 'no earlier occurrence')
-    ids(1:6) = [7, 8, 9, 7, 8, 9]
-    call lookup_draft(ids, 6, 3, 5, d, kk)
-    call chk(kk == 3 .and. all(d(1:3) == [7, 8, 9]), 'match at position 1')
-    write (*, '(A,I0,A,I0,A)') 'spectest: ', nchk - nfail, ' of ', nchk, ' checks passed'
-    if (nfail > 0) stop 1
+    ms_spec = 1000*(now() - t0)
+    seq_spec(1:ngen) = ids(npre+1:npre+ngen)
+
+    write (*, '(A,F10.1,A,F10.2,A)') 'plain : ', ms_plain, ' ms   ', &
+        ngen / max(1.0d-6, ms_plain/1000), ' tok/s'
+    write (*, '(A,F10.1,A,F10.2,A)') 'spec  : ', ms_spec, ' ms   ', &
+        ngen / max(1.0d-6, ms_spec/1000), ' tok/s'
+    write (*, '(A,F8.2,A)') 'speedup: ', ms_plain / max(1.0d-6, ms_spec), 'x'
+    write (*, '(A,F8.2,A,F8.2,A,F8.2)') 'passes=', real(npass), ' tokens/pass=', &
+        real(ngen)/real(max(1, npass)), ' mean n_accept=', real(naccept_total)/real(max(1, npass))
+    write (*, '(A,F8.2)') 'mean acceptance rate (nacc/k_eff) = ', &
+        real(naccept_total) / real(max(1, ksum))
+    write (*, '(A,F8.2)') 'mean drafts proposed per pass = ', real(ksum) / real(max(1, npass))
+    open (newunit=u, file=trim(out_file), status='replace', action='write')
+    do i = 1, ngen
+      write (u, '(I0)') seq_plain(i)
+    end do
+    close (u)
+    call fgpt_release()
+    if (all(seq_plain == seq_spec)) then
+      write (*, '(A)') 'EQUIVALENCE ok: spec stream == plain greedy stream'
+    else
+      write (*, '(A)') 'EQUIVALENCE FAILED: spec stream differs from plain greedy'
+      stop 1
+    end if
 
   contains
 
-    subroutine chk(ok, what)
-      logical, intent(in) :: ok
-      character(*), intent(in) :: what
-      nchk = nchk + 1
-      if (.not. ok) then
-        nfail = nfail + 1
-        write (*, '(2A)') 'FAIL: ', what
-      end if
-    end subroutine chk
-  end subroutine run_spectest
+    integer function argmax_i(x, n)
+      integer, intent(in) :: n
+      real(c_float), intent(in) :: x(n)
+      integer :: t
+      argmax_i = 1
+      do t = 2, n
+        if (x(t) > x(argmax_i)) argmax_i = t
+      end do
+    end function argmax_i
+
+    ! positions 1..npre-1 into both caches, chunks of 64
+    subroutine prefill_both()
+      integer :: srow, tb
+      srow = 1
+      do while (srow <= npre - 1)
+        tb = min(64, npre - srow)
+        call gpt_step_multi(ids(srow:srow+tb-1), cos_b((srow-1)*d2+1:), sin_b((srow-1)*d2+1:), &
+            wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, ck_t, cv_t, clen_t, nmax, chunk_out, &
+            1, V, D, H, KH, HD, L, tb, 1.0e-5_c_float)
+        call gpt_step_multi(ids(srow:srow+tb-1), cos_b((srow-1)*d2+1:), sin_b((srow-1)*d2+1:), &
+            wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, ck_d, cv_d, clen_d, nmax, chunk_out, &
+            1, V, D, H, KH, HD, dl, tb, 1.0e-5_c_float)
+        srow = srow + tb
+      end do
+    end subroutine prefill_both
+
+    ! one draft-and-verify round; invariant clen_t = clen_d = p-1, ids(p)
+    ! the pending token
+    subroutine spec_round()
+      integer :: inp(kspec + 1), j, na, corr
+      call gpt_step(ids(p:p), cos_b((p-1)*d2+1:), sin_b((p-1)*d2+1:), wte, c_q, c_k, c_v, c_pr, &
+          c_fc, c_pr2, lm, ck_d, cv_d, clen_d, nmax, row1, 1, V, D, H, KH, HD, dl, 1.0e-5_c_float)
+      draft(1) = argmax_i(row1, V) - 1
+      do j = 1, kspec - 1
+        call gpt_step(draft(j:j), cos_b((p+j-1)*d2+1:), sin_b((p+j-1)*d2+1:), wte, c_q, c_k, &
+            c_v, c_pr, c_fc, c_pr2, lm, ck_d, cv_d, clen_d, nmax, row1, 1, V, D, H, KH, HD, dl, &
+            1.0e-5_c_float)
+        draft(j + 1) = argmax_i(row1, V) - 1
+      end do
+      ! keeps the drafter cache valid through p+K for the all-accepted case
+      call gpt_step(draft(kspec:kspec), cos_b((p+kspec-1)*d2+1:), sin_b((p+kspec-1)*d2+1:), &
+          wte, c_q, c_k, c_v, c_pr, c_fc, c_pr2, lm, ck_d, cv_d, clen_d, nmax, row1, 1, V, D, H, &
+          KH, HD, dl, 1.0e-5_c_float)
+      ksum = ksum + kspec
+      inp(1) = ids(p)
+      inp(2:kspec+1) = draft(1:kspec)
+      call gpt_step_multi(inp, cos_b((p-1)*d2+1:), sin_b((p-1)*d2+1:), wte, c_q, c_k, c_v, &
+          c_pr, c_fc, c_pr2, lm, ck_t, cv_t, clen_t, nmax, chunk_out, 1, V, D, H, KH, HD, L, &
+          kspec + 1, 1.0e-5_c_float)
+      do j = 1, kspec + 1
+        targ(j) = argmax_i(chunk_out((j-1)*V+1:j*V), V) - 1
+      end do
+      call accept_prefix(draft, targ, kspec, na, corr)
+      naccept_total = naccept_total + na
+      npass = npass + 1
+      if (na > 0) ids(p+1:p+na) = draft(1:na)
+      ids(p + na + 1) = corr
+      p = p + na + 1
+      gen_done = p - npre
+      ! both caches back to one behind the new pending token
+      clen_t = p - 1
+      clen_d = p - 1
+    end subroutine spec_round
+  end subroutine run_specbench
 
   ! frand of src/test/test_kernels.f90:115-119, explicit 32-bit wrap
   real(c_float) function frand(seed)

@@ -132,7 +132,10 @@ int32_t fg_forward_dev(fg_model *m, const int32_t *d_ids, int32_t B, int32_t T,
  * (replaces the caller-owned host cache_k/cache_v of fortran_kv.f90:9-12). */
 int32_t fg_kv_create(fg_model *m, int32_t B, int32_t maxT, fg_kv **out);
 int32_t fg_kv_destroy(fg_kv *kv);
-/* cache_len in/out of gpt_step: the number of filled positions. */
+/* cache_len in/out of gpt_step: the number of filled positions. set_len
+ * rolls the length back (or forward again) within the positions this cache
+ * has computed; a length past them fails with FG_EARG (those rows were
+ * never written). */
 int32_t fg_kv_len(const fg_kv *kv, int32_t *len);
 int32_t fg_kv_set_len(fg_kv *kv, int32_t len);
 /* Copy the cache back in the reference layout (L, B, maxT, KVH*hd) fp32. */

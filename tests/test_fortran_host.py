@@ -181,12 +181,64 @@ def test_fortran_bpb_rows_npy(tmp_path):
     assert abs(float(kv["bpb"]) - bpb) < 1e-4 * bpb + 1e-5
 
 
-def test_fortran_spectest_reference_kats():
+def test_fortran_spectest_reference_kats(tmp_path):
     """accept_prefix / lookup_draft through the drop-in names on the
-    reference's known answers (host functions: no device needed)."""
-    r = run(["spectest"], timeout=60)
+    reference's known answers (host functions: no device needed). The KAT
+    program (tests/fortran/spectest_kats.f90) is compiled here against the
+    built drop-in modules."""
+    from autoresearch_amd import build as B
+    fmod = os.path.join(B.BUILD, "fmod")
+    objs = [os.path.join(B.BUILD, s.replace(".f90", ".o")) for s in B.F_SOURCES]
+    assert all(os.path.exists(o) for o in objs), "build() must compile the Fortran modules"
+    exe = str(tmp_path / "spectest_kats")
+    c = subprocess.run([B.FLANG, "-O1", "-I", fmod, os.path.join(ROOT, "tests", "fortran",
+                        "spectest_kats.f90"), *objs, "-L", B.PKG, "-lfgpt",
+                        f"-Wl,-rpath,{B.PKG}", "-o", exe], capture_output=True, text=True,
+                       timeout=120)
+    assert c.returncode == 0, c.stdout + c.stderr
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
     print(r.stdout, r.stderr)
     assert r.returncode == 0 and "spectest: 12 of 12 checks passed" in r.stdout
+
+
+@pytest.mark.gpu
+def test_fortran_specbench_trunc_drafter(tmp_path):
+    """src/app/spec_bench.f90's truncated-drafter run through the drop-in:
+    target and drafter (first 1 of 2 layers of the same arrays) on two
+    caller caches, prefill of both, a plain greedy run, then draft-and-verify
+    rounds with cache_len rolled back on both caches. The plain stream must
+    be the oracle's greedy ids and the speculative stream must equal it."""
+    d = SMALL
+    w = seeded_weights(d, 31)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=160)
+    ids = uniform_ids(47, 40, d.vocab)
+    np.savetxt(tmp_path / "rows.txt", ids[None, :], fmt="%d")
+    npre, ngen = 33, 48
+    r = run(["specbench", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"),
+             str(npre), str(ngen), str(tmp_path / "o.txt"), "4", "1"])
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "EQUIVALENCE ok" in r.stdout and "passes=" in r.stdout
+    got = np.loadtxt(tmp_path / "o.txt", dtype=np.int32).reshape(-1)
+    assert np.array_equal(got, oracle_greedy(d, w, ids[:npre], ngen))
+
+
+@pytest.mark.gpu
+def test_fortran_specbench_depth12(tmp_path):
+    """The same run at the depth-12 shape with spec_bench's defaults (K=8,
+    3 drafter layers), 64 prompt ids and 32 generated."""
+    d = D12
+    w = seeded_weights(d, 1234)
+    write_npy_dir(str(tmp_path / "w"), d, w)
+    ids = uniform_ids(48, 70, d.vocab)
+    np.savetxt(tmp_path / "rows.txt", ids[None, :], fmt="%d")
+    r = run(["specbench", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"), "64",
+             "32", str(tmp_path / "o.txt")])
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "EQUIVALENCE ok" in r.stdout
+    got = np.loadtxt(tmp_path / "o.txt", dtype=np.int32).reshape(-1)
+    assert np.array_equal(got, oracle_greedy(d, w, ids[:64], 32))
 
 
 @pytest.mark.gpu

@@ -212,6 +212,30 @@ def test_greedy_depth12_prompt16_steps32(d12):
     kv.close()
 
 
+def test_set_len_within_computed_positions():
+    """set_len rolls back and forward again within the positions the cache
+    has computed (a rejected draft's rows are recomputed before use); past
+    them it fails instead of reading rows nothing wrote."""
+    d = SMALL
+    w = seeded_weights(d, 9)
+    m = engine.Model(d, stacks=w)
+    c, s = tables(d, 32)
+    m.set_rope(c, s)
+    kv = engine.KV(m, 1, 32)
+    ids = uniform_ids(77, 12, d.vocab)
+    ref, _ = kv.step_multi(ids[:8])
+    kv.len = 3
+    kv.len = 8
+    with pytest.raises(engine.FgptError, match="computed only 8"):
+        kv.len = 9
+    assert kv.len == 8
+    kv.len = 5
+    again, _ = kv.step_multi(ids[5:8])
+    assert relerr(again.reshape(3, -1), ref.reshape(8, -1)[5:8]) < 1e-5
+    kv.close()
+    m.close()
+
+
 @pytest.mark.parametrize("B", [3, 6])
 def test_batched_decode_rows_independent(B):
     """B sequences decoded together equal B independent B=1 oracle runs
