@@ -165,6 +165,29 @@ hipEvent_t get_event(fg_model* m) {
 // algorithmic flops / bytes of the launch for fg_timing_read.
 template <class F>
 void timed(fg_model* m, hipStream_t s, int kind, double flops, double bytes, F&& f) {
+  (void)s;
+  if (!m->timing) {
+    f();
+    return;
+  }
+  hipEvent_t a = get_event(m), b = get_event(m);
+  LaunchEvents& e = launch_events();
+  e = LaunchEvents{a, b, 0};
+  f();  // its kernels record a (the first) and b (each) in their dispatch
+  const int n = e.n;
+  e = LaunchEvents{};
+  if (n > 0) {
+    m->trecs.push_back({kind, a, b, flops, bytes});
+  } else {
+    m->evpool.push_back(a);
+    m->evpool.push_back(b);
+  }
+}
+
+// The same for a launch that cannot carry events (the cooperative launch):
+// events recorded on the stream around it.
+template <class F>
+void timed_stream(fg_model* m, hipStream_t s, int kind, double flops, double bytes, F&& f) {
   if (!m->timing) {
     f();
     return;
@@ -1054,7 +1077,8 @@ int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, in
     HIPCHK(hipMemsetAsync(a.trace, 0, tn * 8, s));
   }
   hipError_t e = hipSuccess;
-  timed(m, s, FG_K_DECODE_FUSED, flops, bytes, [&] { e = launch_fused_decode(s, d, m->fl, a); });
+  timed_stream(m, s, FG_K_DECODE_FUSED, flops, bytes,
+               [&] { e = launch_fused_decode(s, d, m->fl, a); });
   m->fused_ep += eps;
   if (a.trace) {
     std::vector<uint64_t> ht(tn);
@@ -1576,6 +1600,8 @@ extern "C" int32_t fg_timing_read(fg_model* m, int32_t kind, int64_t* launches, 
   for (auto& r : m->trecs) {
     if (r.kind != kind) continue;
     float e = 0.f;
+    // (launches on a caller's stream: wait for the record's own end event)
+    HIPCHK(hipEventSynchronize(r.b));
     HIPCHK(hipEventElapsedTime(&e, r.a, r.b));
     ++n;
     t += e;

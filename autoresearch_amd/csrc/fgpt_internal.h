@@ -10,6 +10,21 @@
 
 namespace fgpt {
 
+// Kernel timing: while a timed region is open on this thread (the engine's
+// fg_timing), the launches in it carry the region's events in their dispatch
+// packet (hipExtLaunchKernelGGL): the first launch the start event, every
+// launch the stop event. The events then hold the kernels' own begin and end
+// timestamps, not the stream's, so a region's time does not include the
+// dispatch gap in front of its first kernel.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+  int n = 0;
+};
+inline LaunchEvents& launch_events() {
+  static thread_local LaunchEvents e;
+  return e;
+}
+
 // Set the calling thread's error (code + message, see fg_last_error); returns code.
 int32_t set_error(int32_t code, const char* msg);
 

@@ -456,18 +456,18 @@ void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const ui
   const bool split = p.iph > p.nqb;  // some query block spans several chunks
   const dim3 mgrid((unsigned)(p.nbh * p.nqb * 4));
   if (d.hd == 128) {
-    hipLaunchKernelGGL(k_attn_mfma<128>, grid, dim3(512), 2 * 4 * SK * 256, s, p);
-    if (split) hipLaunchKernelGGL(k_attn_merge<128>, mgrid, dim3(256), 0, s, p);
+    FG_LAUNCH(k_attn_mfma<128>, grid, dim3(512), 2 * 4 * SK * 256, s, p);
+    if (split) FG_LAUNCH(k_attn_merge<128>, mgrid, dim3(256), 0, s, p);
   } else {
-    hipLaunchKernelGGL(k_attn_mfma<64>, grid, dim3(512), 2 * 4 * SK * 128, s, p);
-    if (split) hipLaunchKernelGGL(k_attn_merge<64>, mgrid, dim3(256), 0, s, p);
+    FG_LAUNCH(k_attn_mfma<64>, grid, dim3(512), 2 * 4 * SK * 128, s, p);
+    if (split) FG_LAUNCH(k_attn_merge<64>, mgrid, dim3(256), 0, s, p);
   }
 }
 
 void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const float* vc, int B,
                         int maxT, int n, int npos, int64_t kv_plane, uint16_t* ks, uint16_t* vt) {
   if (n <= 0) return;
-  hipLaunchKernelGGL(k_split_cache, dim3(n, B), dim3(256), 0, s, kc, vc, d.KH, d.hd, maxT, n, npos,
+  FG_LAUNCH(k_split_cache, dim3(n, B), dim3(256), 0, s, kc, vc, d.KH, d.hd, maxT, n, npos,
                      kv_plane, ks, vt);
 }
 

@@ -1,9 +1,25 @@
 // kern_common.h -- device helpers shared by the gfx950 kernels.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace fgpt {
+
+// FG_LAUNCH: a kernel launch that carries the open timed region's events
+// (LaunchEvents, fgpt_internal.h) in its dispatch packet when there is one.
+#define FG_LAUNCH(kernel, grid, block, shmem, stream, ...)                                    \
+  do {                                                                                        \
+    ::fgpt::LaunchEvents& fg_ev_ = ::fgpt::launch_events();                                   \
+    if (fg_ev_.stop) {                                                                        \
+      hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)(shmem), stream,                   \
+                            fg_ev_.n == 0 ? fg_ev_.start : nullptr, fg_ev_.stop, 0u,          \
+                            __VA_ARGS__);                                                     \
+      ++fg_ev_.n;                                                                             \
+    } else {                                                                                  \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                    \
+    }                                                                                         \
+  } while (0)
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(((uint32_t)b) << 16);

@@ -91,7 +91,7 @@ void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const in
                        int64_t rows, float* x, uint16_t* xs, int64_t plane, float* ssq,
                        const int32_t* d_rows) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_embed_norm, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V, d.eps,
+  FG_LAUNCH(k_embed_norm, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V, d.eps,
                      x, xs, plane, ssq, d_rows);
 }
 
@@ -217,7 +217,7 @@ static void gemv_grid(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   const int nunits = (a.N + R - 1) / R;
   int grid = (nunits + 3) / 4;
   if (grid > 2048) grid = 2048;
-  hipLaunchKernelGGL((k_gemv<M, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos);
+  FG_LAUNCH((k_gemv<M, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos);
 }
 
 template <int EPI>
@@ -226,7 +226,7 @@ static void gemv_m(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   if (a.d_M) {  // a.M = the most rows the launch can be given
     int grid = (a.N / R + 3) / 4;
     if (grid > 2048) grid = 2048;
-    hipLaunchKernelGGL((k_gemv_live<EPI>), dim3(grid, (a.M + 3) / 4), dim3(256), 0, s, a, d_pos);
+    FG_LAUNCH((k_gemv_live<EPI>), dim3(grid, (a.M + 3) / 4), dim3(256), 0, s, a, d_pos);
   } else if (a.M <= 1) {
     gemv_grid<1, EPI, R>(s, a, d_pos);
   } else if (a.M == 2) {
@@ -452,17 +452,17 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   const dim3 grid((unsigned)(rows * d.H), (unsigned)a.nchunk);
   const dim3 mgrid((unsigned)(rows * d.H));
   if (d.hd == 128 && dpc == 128) {
-    hipLaunchKernelGGL((k_attn_dec<128, 128>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<128, 128>), mgrid, dim3(64), 0, s, a);
+    FG_LAUNCH((k_attn_dec<128, 128>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<128, 128>), mgrid, dim3(64), 0, s, a);
   } else if (d.hd == 128) {
-    hipLaunchKernelGGL((k_attn_dec<128, DPC_MIN>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<128, DPC_MIN>), mgrid, dim3(64), 0, s, a);
+    FG_LAUNCH((k_attn_dec<128, DPC_MIN>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<128, DPC_MIN>), mgrid, dim3(64), 0, s, a);
   } else if (dpc == 128) {
-    hipLaunchKernelGGL((k_attn_dec<64, 128>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<64, 128>), mgrid, dim3(64), 0, s, a);
+    FG_LAUNCH((k_attn_dec<64, 128>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<64, 128>), mgrid, dim3(64), 0, s, a);
   } else {
-    hipLaunchKernelGGL((k_attn_dec<64, DPC_MIN>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) hipLaunchKernelGGL((k_attn_dec_merge<64, DPC_MIN>), mgrid, dim3(64), 0, s, a);
+    FG_LAUNCH((k_attn_dec<64, DPC_MIN>), grid, dim3(256), 0, s, a);
+    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<64, DPC_MIN>), mgrid, dim3(64), 0, s, a);
   }
 }
 
@@ -528,9 +528,9 @@ __global__ void k_advance(int32_t* d_len) {
 
 void launch_argmax_step(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out,
                         int32_t* out2, int32_t* d_len, const int32_t* d_len0, float* lgs_out) {
-  hipLaunchKernelGGL(k_argmax, dim3((unsigned)rows), dim3(256), 0, s, logits, V, out, out2, d_len,
+  FG_LAUNCH(k_argmax, dim3((unsigned)rows), dim3(256), 0, s, logits, V, out, out2, d_len,
                      d_len0, lgs_out);
-  if (d_len) hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, d_len);
+  if (d_len) FG_LAUNCH(k_advance, dim3(1), dim3(64), 0, s, d_len);
 }
 
 // The end of a GEMV-path greedy step in one single-block launch: for each of
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(1024) void k_greedy_tail(const float* __restrict__ 
 void launch_greedy_tail(hipStream_t s, const Dims& d, const float* logits, int rows,
                         const bf16_t* wte, int32_t* ids, int32_t* out2, int32_t* d_len,
                         const int32_t* d_len0, float* lgs_out, float* x) {
-  hipLaunchKernelGGL(k_greedy_tail, dim3(1), dim3(1024), 0, s, logits, rows, d.V, d.D, d.eps, wte,
+  FG_LAUNCH(k_greedy_tail, dim3(1), dim3(1024), 0, s, logits, rows, d.V, d.D, d.eps, wte,
                      ids, out2, d_len, d_len0, lgs_out, x);
 }
 
@@ -747,11 +747,11 @@ __global__ __launch_bounds__(1024) void k_spec_commit(SpecDev* __restrict__ st,
 }
 
 void launch_spec_draft(hipStream_t s, SpecDev* st, const int32_t* ids) {
-  hipLaunchKernelGGL(k_spec_draft, dim3(1), dim3(256), 0, s, st, ids);
+  FG_LAUNCH(k_spec_draft, dim3(1), dim3(256), 0, s, st, ids);
 }
 
 void launch_spec_commit(hipStream_t s, SpecDev* st, const float* logits, int V, int32_t* ids) {
-  hipLaunchKernelGGL(k_spec_commit, dim3(1), dim3(1024), 0, s, st, logits, V, ids);
+  FG_LAUNCH(k_spec_commit, dim3(1), dim3(1024), 0, s, st, logits, V, ids);
 }
 
 void launch_argmax(hipStream_t s, const float* logits, int64_t rows, int V, int32_t* out) {
@@ -834,7 +834,7 @@ __global__ __launch_bounds__(256) void k_bpb_rows(const float* __restrict__ nll,
 void launch_bpb_rows(hipStream_t s, const float* nll, const int32_t* tgt, int rows, int T,
                      const int32_t* tbytes, double* row_nats, long long* row_bytes) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(k_bpb_rows, dim3((unsigned)rows), dim3(256), 0, s, nll, tgt, T, tbytes,
+  FG_LAUNCH(k_bpb_rows, dim3((unsigned)rows), dim3(256), 0, s, nll, tgt, T, tbytes,
                      row_nats, row_bytes);
 }
 
@@ -843,11 +843,11 @@ void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t 
   if (rows <= 0) return;
   // V % 64 == 0, so a row is whole float4s
   if (V <= 256 * 4 * 8)
-    hipLaunchKernelGGL(k_nll<8>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
+    FG_LAUNCH(k_nll<8>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
   else if (V <= 256 * 4 * 16)
-    hipLaunchKernelGGL(k_nll<16>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
+    FG_LAUNCH(k_nll<16>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
   else
-    hipLaunchKernelGGL(k_nll<0>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
+    FG_LAUNCH(k_nll<0>, dim3((unsigned)rows), dim3(256), 0, s, logits, tgt, V, out);
 }
 
 }  // namespace fgpt

@@ -642,7 +642,7 @@ void launch_cfg2(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
     attr = true;
   }
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((k_gemm2<EPI, NWM, NWN, WM, WN, NST>), g, dim3(64 * NWM * NWN), lds, s, a,
+  FG_LAUNCH((k_gemm2<EPI, NWM, NWN, WM, WN, NST>), g, dim3(64 * NWM * NWN), lds, s, a,
                      d_pos);
 }
 
@@ -662,7 +662,7 @@ void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
     attr = true;
   }
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
-  hipLaunchKernelGGL((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG>), g, dim3(64 * NWM * NWN * KG),
+  FG_LAUNCH((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG>), g, dim3(64 * NWM * NWN * KG),
                      lds, s, a, d_pos);
 }
 
@@ -788,9 +788,9 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   if (sp > 1) {
     constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
     const dim3 g(a.N / 64, (unsigned)((a.M + 63) / 64), (unsigned)sp);
-    hipLaunchKernelGGL((k_gemm<EPI, 64, 64, 2, 2, 32, 4>), g, dim3(256), lds, s, a, d_pos);
+    FG_LAUNCH((k_gemm<EPI, 64, 64, 2, 2, 32, 4>), g, dim3(256), lds, s, a, d_pos);
     const dim3 rg((unsigned)a.M, (unsigned)((a.N + RED_COLS - 1) / RED_COLS));
-    hipLaunchKernelGGL((k_splitk_reduce<EPI>), rg, dim3(256), 0, s, a, sp, d_pos);
+    FG_LAUNCH((k_splitk_reduce<EPI>), rg, dim3(256), 0, s, a, sp, d_pos);
     return;
   }
   GemvArgs b = a;

@@ -436,7 +436,7 @@ void launch_sample_one(hipStream_t s, const float* logits, int V, const int32_t*
   const int np2 = sample_np2(V);
   const int64_t lds = sample_lds_bytes(V);
   raise_lds((const void*)k_sample_one, lds);
-  hipLaunchKernelGGL(k_sample_one, dim3(1), dim3(ST), (unsigned)lds, s, logits, V, np2, gen, ngen,
+  FG_LAUNCH(k_sample_one, dim3(1), dim3(ST), (unsigned)lds, s, logits, V, np2, gen, ngen,
                      c, state, out);
 }
 
@@ -444,7 +444,7 @@ void launch_sample_step(hipStream_t s, SampleDev* sd, const float* logits, int V
   const int np2 = sample_np2(V);
   const int64_t lds = sample_lds_bytes(V);
   raise_lds((const void*)k_sample_step, lds);
-  hipLaunchKernelGGL(k_sample_step, dim3(1), dim3(ST), (unsigned)lds, s, sd, logits, V, np2, ids);
+  FG_LAUNCH(k_sample_step, dim3(1), dim3(ST), (unsigned)lds, s, sd, logits, V, np2, ids);
 }
 
 }  // namespace fgpt

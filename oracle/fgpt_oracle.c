@@ -17,11 +17,22 @@
 #include "fgpt_oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
+
+/* malloc that stops the program when memory runs out */
+static void *xmalloc(size_t n) {
+  void *p = malloc(n ? n : 1);
+  if (!p) {
+    fprintf(stderr, "oracle: cannot allocate %zu bytes\n", n);
+    abort();
+  }
+  return p;
+}
 
 int32_t or_num_threads(void) {
 #ifdef _OPENMP
@@ -92,12 +103,48 @@ void or_rmsnorm0(const float *x, float *y, int64_t N, int32_t C, float eps) {
  * as the naive loop. */
 #define LIN_RB 8   /* rows of x per block */
 #define LIN_OB 256 /* outputs per block   */
-void or_linear(const float *x, const float *w, float *y, int64_t BT,
-               int32_t IF, int32_t OF) {
-  float *wt = (float *)malloc(sizeof(float) * (size_t)IF * (size_t)OF);
+
+/* Transposed weight copies kept between calls while or_wt_cache(1) is in
+ * force, keyed by (w, IF, OF). The caller that turns it on promises the
+ * weight arrays neither move nor change until it turns it off again (which
+ * frees the copies); with it off (the default) every call transposes. */
+#define WT_MAX 512
+static struct { const float *w; int32_t IF, OF; float *wt; } g_wt[WT_MAX];
+static int g_wt_n = 0, g_wt_on = 0;
+
+void or_wt_cache(int32_t on) {
+  for (int i = 0; i < g_wt_n; ++i) free(g_wt[i].wt);
+  g_wt_n = 0;
+  g_wt_on = on != 0;
+}
+
+static float *transposed(const float *w, int32_t IF, int32_t OF, int *owned) {
+  if (g_wt_on)
+    for (int i = 0; i < g_wt_n; ++i)
+      if (g_wt[i].w == w && g_wt[i].IF == IF && g_wt[i].OF == OF) {
+        *owned = 0;
+        return g_wt[i].wt;
+      }
+  float *wt = (float *)xmalloc(sizeof(float) * (size_t)IF * (size_t)OF);
 #pragma omp parallel for schedule(static)
   for (int32_t i = 0; i < IF; ++i)
     for (int32_t o = 0; o < OF; ++o) wt[(int64_t)i * OF + o] = w[(int64_t)o * IF + i];
+  *owned = 1;
+  if (g_wt_on && g_wt_n < WT_MAX) {
+    g_wt[g_wt_n].w = w;
+    g_wt[g_wt_n].IF = IF;
+    g_wt[g_wt_n].OF = OF;
+    g_wt[g_wt_n].wt = wt;
+    ++g_wt_n;
+    *owned = 0;
+  }
+  return wt;
+}
+
+void or_linear(const float *x, const float *w, float *y, int64_t BT,
+               int32_t IF, int32_t OF) {
+  int owned;
+  float *wt = transposed(w, IF, OF, &owned);
   int64_t nrb = (BT + LIN_RB - 1) / LIN_RB;
   int64_t nob = (OF + LIN_OB - 1) / LIN_OB;
 #pragma omp parallel for collapse(2) schedule(dynamic, 1)
@@ -121,7 +168,7 @@ void or_linear(const float *x, const float *w, float *y, int64_t BT,
         memcpy(y + (r0 + r) * OF + o0, acc[r], sizeof(float) * (size_t)no);
     }
   }
-  free(wt);
+  if (owned) free(wt);
 }
 
 /* src/lib/fortran_rope.f90:25-52, half-split rotation:
@@ -182,7 +229,7 @@ void or_causal_attn(const float *q, const float *k, const float *v, float *y,
   int32_t rep = H / KH;
 #pragma omp parallel
   {
-    float *sc = (float *)malloc(sizeof(float) * (size_t)T);
+    float *sc = (float *)xmalloc(sizeof(float) * (size_t)T);
 #pragma omp for collapse(3) schedule(dynamic, 16)
     for (int32_t a = 0; a < B; ++a)
       for (int32_t h = 0; h < H; ++h)
@@ -205,7 +252,7 @@ void or_attn_step(const float *q, const float *K, const float *V, float *y,
   int32_t rep = H / KH;
 #pragma omp parallel
   {
-    float *sc = (float *)malloc(sizeof(float) * (size_t)(TC > 0 ? TC : 1));
+    float *sc = (float *)xmalloc(sizeof(float) * (size_t)(TC > 0 ? TC : 1));
 #pragma omp for collapse(2) schedule(static)
     for (int32_t a = 0; a < B; ++a)
       for (int32_t h = 0; h < H; ++h) {
@@ -228,7 +275,7 @@ void or_attn_chunk(const float *q, const float *K, const float *V, float *y,
   int32_t rep = H / KH;
 #pragma omp parallel
   {
-    float *sc = (float *)malloc(sizeof(float) * (size_t)(TC_PREV + TB));
+    float *sc = (float *)xmalloc(sizeof(float) * (size_t)(TC_PREV + TB));
 #pragma omp for collapse(3) schedule(dynamic, 4)
     for (int32_t a = 0; a < B; ++a)
       for (int32_t iq = 0; iq < TB; ++iq)
@@ -268,11 +315,11 @@ void or_gpt_forward(const int32_t *idx, const float *cosb, const float *sinb,
   int32_t dff = 4 * D, hdd = H * HD, kvd = KH * HD;
   int64_t qsz = (int64_t)hdd * D, ksz = (int64_t)kvd * D, psz = (int64_t)D * hdd;
   int64_t fcsz = (int64_t)dff * D, p2sz = (int64_t)D * dff;
-  float *emd = malloc(sizeof(float) * bt * D), *xn = malloc(sizeof(float) * bt * D);
-  float *sub = malloc(sizeof(float) * bt * D), *ao = malloc(sizeof(float) * bt * D);
-  float *q = malloc(sizeof(float) * bt * hdd), *qr = malloc(sizeof(float) * bt * hdd);
-  float *k = malloc(sizeof(float) * bt * kvd), *kr = malloc(sizeof(float) * bt * kvd);
-  float *v = malloc(sizeof(float) * bt * kvd), *mlp = malloc(sizeof(float) * bt * dff);
+  float *emd = xmalloc(sizeof(float) * bt * D), *xn = xmalloc(sizeof(float) * bt * D);
+  float *sub = xmalloc(sizeof(float) * bt * D), *ao = xmalloc(sizeof(float) * bt * D);
+  float *q = xmalloc(sizeof(float) * bt * hdd), *qr = xmalloc(sizeof(float) * bt * hdd);
+  float *k = xmalloc(sizeof(float) * bt * kvd), *kr = xmalloc(sizeof(float) * bt * kvd);
+  float *v = xmalloc(sizeof(float) * bt * kvd), *mlp = xmalloc(sizeof(float) * bt * dff);
 
   or_wte_lookup(idx, wte, emd, B, T, D);                     /* :136 */
   or_rmsnorm0(emd, xn, bt, D, eps);                          /* :139-142 */
@@ -312,11 +359,11 @@ static void kv_pass(const int32_t *idx, const float *cosb, const float *sinb,
   int32_t dff = 4 * D, hdd = H * HD, kvd = KH * HD;
   int64_t qsz = (int64_t)hdd * D, ksz = (int64_t)kvd * D, psz = (int64_t)D * hdd;
   int64_t fcsz = (int64_t)dff * D, p2sz = (int64_t)D * dff;
-  float *emd = malloc(sizeof(float) * bt * D), *xn = malloc(sizeof(float) * bt * D);
-  float *sub = malloc(sizeof(float) * bt * D), *ao = malloc(sizeof(float) * bt * D);
-  float *q = malloc(sizeof(float) * bt * hdd), *qr = malloc(sizeof(float) * bt * hdd);
-  float *k = malloc(sizeof(float) * bt * kvd), *kr = malloc(sizeof(float) * bt * kvd);
-  float *v = malloc(sizeof(float) * bt * kvd), *mlp = malloc(sizeof(float) * bt * dff);
+  float *emd = xmalloc(sizeof(float) * bt * D), *xn = xmalloc(sizeof(float) * bt * D);
+  float *sub = xmalloc(sizeof(float) * bt * D), *ao = xmalloc(sizeof(float) * bt * D);
+  float *q = xmalloc(sizeof(float) * bt * hdd), *qr = xmalloc(sizeof(float) * bt * hdd);
+  float *k = xmalloc(sizeof(float) * bt * kvd), *kr = xmalloc(sizeof(float) * bt * kvd);
+  float *v = xmalloc(sizeof(float) * bt * kvd), *mlp = xmalloc(sizeof(float) * bt * dff);
 
   or_wte_lookup(idx, wte, emd, B, TB, D);
   or_rmsnorm0(emd, xn, bt, D, eps);

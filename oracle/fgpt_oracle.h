@@ -86,6 +86,10 @@ int32_t or_argmax(const float *logits, int32_t V);
 
 /* Number of OpenMP threads the oracle will use (for reporting). */
 int32_t or_num_threads(void);
+/* on != 0: or_linear keeps the transposed copy of each weight array it sees
+ * (the arrays must not move or change meanwhile); 0: frees them, and every
+ * call transposes again (the default). */
+void or_wt_cache(int32_t on);
 
 #ifdef __cplusplus
 }

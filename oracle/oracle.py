@@ -49,6 +49,7 @@ def lib():
             "or_nll": (None, [_f, _i, _f, i64, i32]),
             "or_argmax": (i32, [_f, i32]),
             "or_num_threads": (i32, []),
+            "or_wt_cache": (None, [i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)

@@ -24,14 +24,39 @@ def test_roofline_arithmetic():
     tm = {"gemm": (49, 1.40, 49 * 7.6e9, 49 * 15.0e6), "attn_chunk": (24, 0.50, 0.0, 0.0)}
     assert bench.dominant(tm) == "gemm"
     launch_s = 1.40e-3 / 49
-    r = bench.roofline_from(tm, "gemm", "mfma")
+    r = bench.roofline(tm["gemm"], tm["gemm"][2], "mfma", "gemm", "profiles/x.md")
     assert r["unit"] == "TFLOP/s" and r["peak"] == 2516.6
     assert r["achieved"] == pytest.approx(7.6e9 / launch_s / 1e12)
     assert r["frac"] == pytest.approx(r["achieved"] / 2516.6)
     assert r["avg_launch_us"] == pytest.approx(launch_s * 1e6)
-    h = bench.roofline_from(tm, "gemm", "hbm")
+    assert r["alg_flop_per_launch"] == pytest.approx(7.6e9)
+    # the linears multiply hi and lo activation planes: twice the MFMA work
+    assert r["mfma_executed_frac"] == pytest.approx(2 * r["frac"])
+    assert r["profile"] == "profiles/x.md"
+    h = bench.roofline(tm["gemm"], tm["gemm"][3], "hbm", "gemm", "profiles/x.md")
     assert h["unit"] == "GB/s" and h["peak"] == 8000.0
     assert h["achieved"] == pytest.approx(15.0e6 / launch_s / 1e9)
+
+
+def test_decode_units_closed_form():
+    """Per-unit decode bytes: bf16 weights but the embedding table once per
+    step, one embedding row and (n+1 read + 1 written) bf16 KV positions per
+    sequence: 182.45 MB + 36 864 B x (n + 2) at depth 12, mean 183.65 MB over
+    the 16-id prompt + 32 steps workload and 3.20 GB over B=64 x 512 steps
+    after 1024-id prompts; the depth-20 GQA model's mean is 747.1 MB."""
+    from autoresearch_amd.weights import D12, GQA20
+    assert bench.kv_pos_bytes(D12) == 36864 and bench.kv_pos_bytes(GQA20) == 20480
+    w12 = 2 * (D12.params - D12.vocab * D12.d_model)
+    assert w12 == pytest.approx(182.45e6, rel=1e-4)
+    assert bench.decode_step_bytes(D12, 1, 15) == w12 + 2 * 768 + 36864 * 17
+    m1 = sum(bench.decode_step_bytes(D12, 1, 15 + i) for i in range(32)) / 32
+    assert m1 == pytest.approx(183.65e6, rel=1e-4)
+    m64 = sum(bench.decode_step_bytes(D12, 64, 1023 + i) for i in range(512)) / 512
+    assert m64 == pytest.approx(3.20e9, rel=2e-3)
+    mg = sum(bench.decode_step_bytes(GQA20, 1, 2047 + i) for i in range(256)) / 256
+    assert mg == pytest.approx(747.1e6, rel=1e-4)
+    assert bench.prefill_flops(D12, 1, 2048) == pytest.approx(451.009314816e9, rel=1e-12)
+    assert bench.prefill_flops(D12, 8, 2048) == pytest.approx(8 * 451.009314816e9, rel=1e-12)
 
 
 def test_prefill_flop_count_closed_form():

@@ -186,6 +186,23 @@ def test_forward_vs_float64_depth12_short():
     assert np.max(np.abs(out - ref)) < 2e-4 * np.abs(ref).max()
 
 
+def test_transposed_weight_cache_changes_nothing():
+    """or_wt_cache(1) (transposed weights kept between calls, for timing the
+    CPU baseline) gives the same bits as transposing on every call."""
+    d, B, T = TINY_GQA, 2, 5
+    w = frand_weights(d, seed=13)
+    ids = ((np.arange(B * T) * 3 + 1) % d.vocab).astype(np.int32)
+    c, s = O.rope_tables(T, d.head_dim)
+    ref = O.gpt_forward(ids, c, s, w, d, B, T)
+    O.lib().or_wt_cache(1)
+    try:
+        a = O.gpt_forward(ids, c, s, w, d, B, T)
+        b = O.gpt_forward(ids, c, s, w, d, B, T)
+    finally:
+        O.lib().or_wt_cache(0)
+    assert np.array_equal(a, ref) and np.array_equal(b, ref)
+
+
 def test_forward_causal_prefix_and_rows():
     d, B, T = TINY_GQA, 3, 6
     w = frand_weights(d, seed=9)
