@@ -105,8 +105,9 @@ struct fg_kv {
   fg_model* m = nullptr;
   int B = 0, maxT = 0, len = 0;
   int filled = 0;  // positions this cache has computed (high-water mark of len)
-  float* k = nullptr;  // [L][B][maxT][KH*hd]
+  float* k = nullptr;  // [L][B][maxT][KH*hd], fp32 or (kv16) bf16 elements
   float* v = nullptr;
+  bool kv16 = false;
   int32_t* d_len = nullptr;  // device copy of len for replayed steps; d_len[1] = len at
                              // the start of the current fg_decode_greedy call
   int32_t* d_ids = nullptr;  // [B] ids fed to the next step
@@ -457,6 +458,7 @@ struct PassOpts {
   bool embed = true;      // false: x already holds the embedded rows
   bool rows_single = false;  // every row as a single cached step (see layer_stack)
   const int32_t* d_rows = nullptr;  // rows_single: rows live, read on the device
+  bool kv16 = false;      // the cache holds bf16 elements
 };
 
 // One pass over rows = B*T token rows: embedding of ids, the layer stack,
@@ -494,14 +496,17 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     });
   int nt = 1;  // partial sums of squares per row of the current residual
   for (int l = 0; l < d.L; ++l) {
-    float* lk = kc ? kc + l * lstride : nullptr;  // null: no persistent cache (gpt_forward)
-    float* lv = vc ? vc + l * lstride : nullptr;
+    // null: no persistent cache (gpt_forward); lstride counts elements
+    const int64_t loff = o.kv16 ? l * lstride / 2 : l * lstride;  // in floats
+    float* lk = kc ? kc + loff : nullptr;
+    float* lv = vc ? vc + loff : nullptr;
     GemvArgs a = base_args(m, ws);
     a.M = rows;
     a.d_M = o.d_rows;
     a.T = T;
     a.pos0 = pos0;
     a.kc = lk;
+    a.kv16 = o.kv16 ? 1 : 0;
     a.vc = lv;
     a.maxT = maxT;
     // q, k, v = rmsnorm(x) Wqkv^T, RoPE on q and k, k/v appended to the cache
@@ -524,13 +529,15 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     uint16_t* aos = gm ? ws.aos : nullptr;
     if (one) {
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
-        launch_attn_decode_pos(s, d, ws.q, lk, lv, B, maxT, d_pos, pos0 + 1, dec_part, ws.ao, aos,
+        launch_attn_decode_pos(s, d, ws.q, lk, lv, o.kv16, B, maxT, d_pos, pos0 + 1, dec_part,
+                               ws.ao, aos,
                                aplane, T, o.d_rows);
       });
     } else {
       if (pos0 > 0)  // earlier cache positions enter the chunk's key planes
         timed(m, s, FG_K_OTHER, 0, (double)B * pos0 * d.kvd() * 16, [&] {
-          launch_split_cache(s, d, lk, lv, B, maxT, pos0, npos, (int64_t)B * npos * d.kvd(),
+          launch_split_cache(s, d, lk, lv, o.kv16, B, maxT, pos0, npos,
+                             (int64_t)B * npos * d.kvd(),
                              m->ks, m->vt);
         });
       timed(m, s, FG_K_ATTN_CHUNK, at_flops, at_bytes, [&] {
@@ -814,9 +821,15 @@ extern "C" int32_t fg_forward_dev(fg_model* m, const int32_t* d_ids, int32_t B, 
 
 // ------------------------------------------------------------------ KV
 extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** out) {
+  return fg_kv_create_ex(m, B, maxT, 0, out);
+}
+
+extern "C" int32_t fg_kv_create_ex(fg_model* m, int32_t B, int32_t maxT, int32_t flags,
+                                   fg_kv** out) {
   if (!m || !out) return seterr(FG_EARG, "NULL argument");
   *out = nullptr;
   if (B < 1 || maxT < 1) return seterr(FG_EARG, "B and maxT must be >= 1");
+  if (flags & ~FG_KV_BF16) return seterr(FG_EARG, "unknown cache flags 0x%x", flags);
   // the largest cache this build is tested with
   if (maxT > 16000) return seterr(FG_EARG, "maxT %d above the 16000 this build supports", maxT);
   GUARD(m);
@@ -824,15 +837,16 @@ extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** ou
   kv->m = m;
   kv->B = B;
   kv->maxT = maxT;
-  const size_t n = (size_t)m->d.L * B * maxT * m->d.kvd();
-  hipError_t e = hipMalloc((void**)&kv->k, n * 4);
-  if (e == hipSuccess) e = hipMalloc((void**)&kv->v, n * 4);
+  kv->kv16 = (flags & FG_KV_BF16) != 0;
+  const size_t n = (size_t)m->d.L * B * maxT * m->d.kvd(), esz = kv->kv16 ? 2 : 4;
+  hipError_t e = hipMalloc((void**)&kv->k, n * esz);
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->v, n * esz);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_len, 8);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_ids, (size_t)B * 4);
   if (e == hipSuccess)
     e = hipMalloc((void**)&kv->d_part, (size_t)attn_decode_scratch_floats(m->d, B, maxT) * 4);
-  if (e == hipSuccess) e = hipMemset(kv->k, 0, n * 4);  // the caller zeroes it in the reference
-  if (e == hipSuccess) e = hipMemset(kv->v, 0, n * 4);
+  if (e == hipSuccess) e = hipMemset(kv->k, 0, n * esz);  // the caller zeroes it in the reference
+  if (e == hipSuccess) e = hipMemset(kv->v, 0, n * esz);
   if (e != hipSuccess) {
     if (kv->k) (void)hipFree(kv->k);
     if (kv->v) (void)hipFree(kv->v);
@@ -840,7 +854,8 @@ extern "C" int32_t fg_kv_create(fg_model* m, int32_t B, int32_t maxT, fg_kv** ou
     if (kv->d_ids) (void)hipFree(kv->d_ids);
     if (kv->d_part) (void)hipFree(kv->d_part);
     delete kv;
-    return seterr(FG_EHIP, "KV cache allocation (%zu bytes): %s", 2 * n * 4, hipGetErrorString(e));
+    return seterr(FG_EHIP, "KV cache allocation (%zu bytes): %s", 2 * n * esz,
+                  hipGetErrorString(e));
   }
   *out = kv;
   return FG_OK;
@@ -882,8 +897,23 @@ extern "C" int32_t fg_kv_read(fg_kv* kv, float* k_out, float* v_out) {
   GUARD(m);
   const size_t n = (size_t)m->d.L * kv->B * kv->maxT * m->d.kvd();
   HIPCHK(hipStreamSynchronize(m->stream));
-  if (k_out) HIPCHK(hipMemcpy(k_out, kv->k, n * 4, hipMemcpyDeviceToHost));
-  if (v_out) HIPCHK(hipMemcpy(v_out, kv->v, n * 4, hipMemcpyDeviceToHost));
+  if (!kv->kv16) {
+    if (k_out) HIPCHK(hipMemcpy(k_out, kv->k, n * 4, hipMemcpyDeviceToHost));
+    if (v_out) HIPCHK(hipMemcpy(v_out, kv->v, n * 4, hipMemcpyDeviceToHost));
+    return FG_OK;
+  }
+  // bf16 elements widened on the host
+  std::vector<uint16_t> h(n);
+  float* outs[2] = {k_out, v_out};
+  const float* src[2] = {kv->k, kv->v};
+  for (int t = 0; t < 2; ++t) {
+    if (!outs[t]) continue;
+    HIPCHK(hipMemcpy(h.data(), src[t], n * 2, hipMemcpyDeviceToHost));
+    for (size_t i = 0; i < n; ++i) {
+      const uint32_t u = (uint32_t)h[i] << 16;
+      memcpy(outs[t] + i, &u, 4);
+    }
+  }
   return FG_OK;
 }
 
@@ -910,12 +940,14 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
     RCCHK(ensure_split(m, (int64_t)B * npos_pad(kv->len + TB) * m->d.kvd()));
     RCCHK(ensure_attn(m, B, TB, kv->len));
   }
-  // (TB == 1 runs the single-query kernel on the fp32 cache)
+  // (TB == 1 runs the single-query kernel on the cache)
   hipStream_t s = m->stream;
   HIPCHK(hipMemcpyAsync(m->ws.ids, h_ids, rows * 4, hipMemcpyHostToDevice, s));
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
+  PassOpts o;
+  o.kv16 = kv->kv16;
   layer_stack(m, s, m->ws.ids, B, TB, kv->len, nullptr, kv->k, kv->v, kv->maxT, lstride,
-              kv->d_part, m->ws.logits);
+              kv->d_part, m->ws.logits, o);
   HIPCHK(hipGetLastError());
   if (next_ids && TB == 1) {
     launch_argmax(s, m->ws.logits, B, m->d.V, m->ws.amax);
@@ -947,6 +979,7 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
   if (use_gemm(m->d, B)) {
     PassOpts o;
     o.pos_host = pos_host;
+    o.kv16 = kv->kv16;
     layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
                 kv->d_part, m->ws.logits, o);
     timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
@@ -960,6 +993,7 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
     PassOpts o;
     o.pos_host = pos_host;
     o.embed = false;
+    o.kv16 = kv->kv16;
     layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
                 kv->d_part, m->ws.logits, o);
     timed(m, s, FG_K_OTHER, 0, (double)B * (m->d.V * 4 * (with_logits ? 2 : 1) + 6 * m->d.D),
@@ -1017,7 +1051,8 @@ int32_t graph_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, in
 }
 
 bool fused_applies(const fg_model* m, const fg_kv* kv, int n_steps) {
-  return m->fused_on && m->fused_w && kv->B == 1 && kv->len + n_steps <= FUSED_MAX_LEN;
+  return m->fused_on && m->fused_w && kv->B == 1 && !kv->kv16 &&
+         kv->len + n_steps <= FUSED_MAX_LEN;
 }
 
 // The whole greedy loop as one persistent launch: ids go to kv->d_out,
@@ -1177,8 +1212,10 @@ extern "C" int32_t fg_step_dev_noalloc(fg_model* m, fg_kv* kv, const int32_t* d_
   hipStream_t s = stream ? (hipStream_t)stream : m->stream;
   const bool tm = m->timing;  // (timing records events: not on this path)
   m->timing = false;
+  PassOpts o;
+  o.kv16 = kv->kv16;
   layer_stack(m, s, d_ids, B, 1, kv->len, nullptr, kv->k, kv->v, kv->maxT,
-              (int64_t)B * kv->maxT * d.kvd(), dec_part, d_logits, PassOpts(), &w);
+              (int64_t)B * kv->maxT * d.kvd(), dec_part, d_logits, o, &w);
   if (d_next) launch_argmax(s, d_logits, B, d.V, d_next);
   m->timing = tm;
   HIPCHK(hipGetLastError());
@@ -1269,6 +1306,7 @@ void spec_round_launches(fg_model* m, fg_kv* kv, hipStream_t s, int maxr, int po
   o.pos_host = pos_host;
   o.rows_single = true;
   o.d_rows = &st->rows;
+  o.kv16 = kv->kv16;
   layer_stack(m, s, st->inp, 1, maxr, 0, &st->len, kv->k, kv->v, kv->maxT,
               (int64_t)kv->maxT * m->d.kvd(), kv->d_spart, m->ws.logits, o);
   timed(m, s, FG_K_OTHER, 0, (double)maxr * m->d.V * 4, [&] {
@@ -1447,6 +1485,7 @@ void sample_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, int pos_host) {
   SampleDev* sd = kv->d_smp;
   PassOpts o;
   o.pos_host = pos_host;
+  o.kv16 = kv->kv16;
   layer_stack(m, s, sd->inp, 1, 1, 0, &sd->len, kv->k, kv->v, kv->maxT,
               (int64_t)kv->maxT * m->d.kvd(), kv->d_part, m->ws.logits, o);
   timed(m, s, FG_K_OTHER, 0, (double)m->d.V * 4, [&] {

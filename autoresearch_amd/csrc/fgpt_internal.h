@@ -123,8 +123,9 @@ struct GemvArgs {
   const float* sinb;
   int pos0;         // position of row 0 (row m is at pos0 + m % T)
   int T;            // rows per sequence
-  float* kc;        // KV cache of this layer, [B][maxT][KH*hd] (nullable)
-  float* vc;
+  float* kc;        // KV cache of this layer, [B][maxT][KH*hd] (nullable); with
+  float* vc;        // kv16 its elements are bf16 (the pointers then address uint16_t)
+  int kv16;
   int maxT;
   int H, KH, hd;
   // bf16 hi/lo copies for the MFMA chunk attention (nullable):
@@ -176,10 +177,11 @@ void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const ui
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
                       int64_t kv_plane, float* scratch, float* y, uint16_t* ys = nullptr,
                       int64_t ys_plane = 0);
-// Fill the hi/lo key/value planes for cache positions [0, n) from the fp32
-// cache of one layer ([B][maxT][KH*hd]).
-void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const float* vc, int B,
-                        int maxT, int n, int npos, int64_t kv_plane, uint16_t* ks, uint16_t* vt);
+// Fill the hi/lo key/value planes for cache positions [0, n) from the cache
+// of one layer ([B][maxT][KH*hd], fp32, or bf16 with kv16: lo planes zero).
+void launch_split_cache(hipStream_t s, const Dims& d, const void* kc, const void* vc, bool kv16,
+                        int B, int maxT, int n, int npos, int64_t kv_plane, uint16_t* ks,
+                        uint16_t* vt);
 
 // Variants whose position / cache length comes from device memory (so a
 // captured decode step replays at successive positions).
@@ -194,9 +196,9 @@ void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_
 // B*qpr, maxT) floats (a multi-chunk step also launches a merge kernel).
 // d_rows (nullable): query rows live this launch (of B*qpr), on the device.
 int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT);
-void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
-                            const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* scratch, float* y, uint16_t* ys = nullptr,
+void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const void* kc,
+                            const void* vc, bool kv16, int B, int maxT, const int32_t* d_len,
+                            int len, float* scratch, float* y, uint16_t* ys = nullptr,
                             int64_t ys_plane = 0, int qpr = 1,
                             const int32_t* d_rows = nullptr);
 // argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +

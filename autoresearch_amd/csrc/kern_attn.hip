@@ -384,9 +384,14 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
   }
 }
 
-// Cache positions [0, n) of one layer, fp32 [B][maxT][KH*hd] -> hi/lo planes.
-__global__ __launch_bounds__(256) void k_split_cache(const float* __restrict__ kc,
-                                                     const float* __restrict__ vc, int KH, int hd,
+// Cache positions [0, n) of one layer, [B][maxT][KH*hd] -> hi/lo planes
+// (a bf16 cache: hi = the element, lo = 0).
+__device__ __forceinline__ float cache_elem(const float* c, int64_t i) { return c[i]; }
+__device__ __forceinline__ float cache_elem(const uint16_t* c, int64_t i) { return bf16_to_f32(c[i]); }
+
+template <class KT>
+__global__ __launch_bounds__(256) void k_split_cache(const KT* __restrict__ kc,
+                                                     const KT* __restrict__ vc, int KH, int hd,
                                                      int maxT, int n, int npos, int64_t kv_plane,
                                                      uint16_t* __restrict__ ks,
                                                      uint16_t* __restrict__ vt) {
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(256) void k_split_cache(const float* __restrict__ k
     const int kvh = i / hd, d = i % hd;
     const int64_t src = ((int64_t)b * maxT + p) * kd + i;
     const int64_t bk = (int64_t)b * KH + kvh;
-    const float kv = kc[src], vv = vc[src];
+    const float kv = cache_elem(kc, src), vv = cache_elem(vc, src);
     uint16_t h = f32_to_bf16_rne(kv);
     const int64_t ko = (bk * npos + p) * hd + d;
     ks[ko] = h;
@@ -464,11 +469,16 @@ void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const ui
   }
 }
 
-void launch_split_cache(hipStream_t s, const Dims& d, const float* kc, const float* vc, int B,
-                        int maxT, int n, int npos, int64_t kv_plane, uint16_t* ks, uint16_t* vt) {
+void launch_split_cache(hipStream_t s, const Dims& d, const void* kc, const void* vc, bool kv16,
+                        int B, int maxT, int n, int npos, int64_t kv_plane, uint16_t* ks,
+                        uint16_t* vt) {
   if (n <= 0) return;
-  FG_LAUNCH(k_split_cache, dim3(n, B), dim3(256), 0, s, kc, vc, d.KH, d.hd, maxT, n, npos,
-                     kv_plane, ks, vt);
+  if (kv16)
+    FG_LAUNCH(k_split_cache<uint16_t>, dim3(n, B), dim3(256), 0, s, (const uint16_t*)kc,
+              (const uint16_t*)vc, d.KH, d.hd, maxT, n, npos, kv_plane, ks, vt);
+  else
+    FG_LAUNCH(k_split_cache<float>, dim3(n, B), dim3(256), 0, s, (const float*)kc,
+              (const float*)vc, d.KH, d.hd, maxT, n, npos, kv_plane, ks, vt);
 }
 
 }  // namespace fgpt

@@ -255,23 +255,25 @@ void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a) {
 // Single-query attention over the cache (attn_step,
 // src/lib/fortran_attn.f90:317-362): the query at position len-1 against
 // cache positions 0..len-1, softmax in the natural domain as the reference
-// has it. Work item = (sequence b, query head h, chunk of DPC positions), so
-// B=64 at len 1536 gives ~9k workgroups instead of 384 serial scans. Each
-// lane holds a float4 of the head dim: hd/4 lanes cover one cached row, a
-// wavefront covers 64/(hd/4) positions per load, and every K and V row of
-// the chunk is loaded up front (V does not depend on the scores), so a
-// chunk costs one memory round trip. A single-chunk call writes the result;
-// otherwise each chunk leaves (max, sum, O) in scratch for k_attn_dec_merge.
-// DPC = 64 positions per chunk; 128 for batches of many sequences, where
-// the longer chunks halve the partial results to merge (the chunk length
-// sets the merge order, so it depends on the sequence count only: every
-// query row of one sequence, and a sequence decoded alone, sums alike)
+// has it. Work item = (sequence row, KV head, group of GH query heads that
+// share it, chunk of DPC positions): each K and V row of the chunk is read
+// once for the GH heads of its group (GQA). A lane holds 8 values of the head
+// dim, so hd/8 lanes cover one cached row and a wavefront PPW rows per load;
+// every K and V row of the chunk is loaded up front (V does not depend on
+// the scores), so a chunk costs one memory round trip. A single-chunk call
+// writes the result; otherwise each chunk leaves (O, max, sum) per head in
+// scratch for k_attn_dec_merge. DPC = 64 positions per chunk; 128 for
+// batches of many sequence-heads, where the longer chunks halve the partial
+// results (the chunk length sets the merge order, so it depends on the
+// sequence count only: every query row of one sequence, and a sequence
+// decoded alone, sums alike). The cache holds fp32 (the reference's) or
+// bf16 elements (KT).
 constexpr int DPC_MIN = 64;
 
 struct DecArgs {
-  const float* q;  // [B][H][hd]
-  const float* kc;  // [B][maxT][KH*hd]
-  const float* vc;
+  const float* q;  // [rows][H][hd]
+  const void* kc;  // [B][maxT][KH*hd], fp32 or bf16
+  const void* vc;
   int H, KH, maxT, nchunk;
   const int32_t* d_len;  // cache length before the step (first query at *d_len), or null
   int len_imm;           // cache length including the first query, if d_len is null
@@ -280,7 +282,7 @@ struct DecArgs {
   float* y;
   uint16_t* ys;
   int64_t ys_plane;
-  float* part;  // [B*H][nchunk][hd + 2]: O, then max and sum
+  float* part;  // [rows*H][nchunk][hd + 2]: O, then max and sum
 };
 
 template <int HD>
@@ -293,128 +295,228 @@ __device__ __forceinline__ void dec_store(const DecArgs& a, int64_t o, int d, fl
   }
 }
 
-template <int HD, int DPC>
+// 8 consecutive cache elements: raw loads (issued together) and their values.
+template <class KT> struct Row8;
+template <> struct Row8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *(const float4*)p;
+    b = *(const float4*)(p + 4);
+  }
+  __device__ __forceinline__ void get(float (&x)[8]) const {
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  }
+};
+template <> struct Row8<uint16_t> {
+  uint4 u;
+  __device__ __forceinline__ void load(const uint16_t* p) { u = *(const uint4*)p; }
+  __device__ __forceinline__ void get(float (&x)[8]) const { unpack8(u, x); }
+};
+
+// Sum over the LPP lanes of each cached row (rows of 8 or 16 lanes): quad
+// permutes, then the half-row (and row) mirror, which pair the same values
+// as strides 4 (and 8) once the smaller groups are uniform.
+template <int LPP>
+__device__ __forceinline__ float row_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  if constexpr (LPP == 16) v += dpp_f<0x140>(v);
+  return v;
+}
+
+template <int HD, int DPC, int GH, class KT>
 __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
-  constexpr int LPP = HD / 4;         // lanes per cached row
-  constexpr int PPW = 64 / LPP;       // positions per wavefront load
-  constexpr int IT = DPC / 4 / PPW;   // loads per wavefront
-  __shared__ float red[8];
-  __shared__ float4 so[4][LPP];
-  const int bh = blockIdx.x, c = blockIdx.y;
-  const int row = bh / a.H, b = row / a.qpr, h = bh % a.H, kvh = h / (a.H / a.KH);
+  constexpr int LPP = HD / 8;        // lanes per cached row
+  constexpr int PPW = 64 / LPP;      // rows per wavefront load
+  constexpr int IT = DPC / 4 / PPW;  // loads per lane and tensor
+  static_assert(LPP == 8 || LPP == 16, "head dim 64 or 128");
+  __shared__ float red[2][4][GH];
+  __shared__ float so[4 * PPW][GH][HD];
+  const int G = a.H / a.KH, ng = G / GH;
+  const int gi = blockIdx.x, c = blockIdx.y;
+  const int row = gi / (a.KH * ng), kvh = (gi / ng) % a.KH, h0 = kvh * G + (gi % ng) * GH;
   if (a.d_rows && row >= *a.d_rows) return;
   const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + row % a.qpr;
   const int p0 = c * DPC;
   if (p0 >= len) return;
   const int nch = (len + DPC - 1) / DPC;
+  const int b = row / a.qpr;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int sub = lane / LPP, dl = lane % LPP;
   const int64_t kd = (int64_t)a.KH * HD;
-  const float* K = a.kc + (int64_t)b * a.maxT * kd + kvh * HD + 4 * dl;
-  const float* V = a.vc + (int64_t)b * a.maxT * kd + kvh * HD + 4 * dl;
-  const float4 qv = *(const float4*)(a.q + (int64_t)bh * HD + 4 * dl);
-  float4 kr[IT], vr[IT];
+  const KT* K = (const KT*)a.kc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
+  const KT* V = (const KT*)a.vc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
+  Row8<KT> kr[IT], vr[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
     const int p = min(p0 + wv * (DPC / 4) + i * PPW + sub, len - 1);
-    kr[i] = *(const float4*)(K + p * kd);
-    vr[i] = *(const float4*)(V + p * kd);
+    kr[i].load(K + p * kd);
+    vr[i].load(V + p * kd);
+  }
+  float qv[GH][8];
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    const float* qp = a.q + ((int64_t)row * a.H + h0 + j) * HD + 8 * dl;
+    const float4 u = *(const float4*)qp, w = *(const float4*)(qp + 4);
+    qv[j][0] = u.x; qv[j][1] = u.y; qv[j][2] = u.z; qv[j][3] = u.w;
+    qv[j][4] = w.x; qv[j][5] = w.y; qv[j][6] = w.z; qv[j][7] = w.w;
   }
   const float scale = 1.0f / sqrtf((float)HD);
-  float sc[IT], mx = -FLT_MAX;
+  float sc[GH][IT], mx[GH];
+#pragma unroll
+  for (int j = 0; j < GH; ++j) mx[j] = -FLT_MAX;
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
-    float v = qv.x * kr[i].x + qv.y * kr[i].y + qv.z * kr[i].z + qv.w * kr[i].w;
-#pragma unroll
-    for (int o = LPP / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    float x[8];
+    kr[i].get(x);
     const int p = p0 + wv * (DPC / 4) + i * PPW + sub;
-    sc[i] = p < len ? v * scale : -INFINITY;
-    mx = fmaxf(mx, sc[i]);
+#pragma unroll
+    for (int j = 0; j < GH; ++j) {
+      float v = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v += qv[j][e] * x[e];
+      v = row_sum<LPP>(v);
+      sc[j][i] = p < len ? v * scale : -INFINITY;
+      mx[j] = fmaxf(mx[j], sc[j][i]);
+    }
   }
-  const float m = block_max<4>(mx, red);
-  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-  float l = 0.f;
+  // maxima over the wavefront's rows, then over the four wavefronts
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    const int iv = __builtin_bit_cast(int, mx[j]);
+    float t = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+#pragma unroll
+    for (int r = 1; r < PPW; ++r)
+      t = fmaxf(t, __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, r * LPP)));
+    if (lane == 0) red[0][wv][j] = t;
+  }
+  __syncthreads();
+  float m[GH], l[GH], o[GH][8];
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    m[j] = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
+    l[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[j][e] = 0.f;
+  }
 #pragma unroll
   for (int i = 0; i < IT; ++i) {
-    const float e = expf(sc[i] - m);
-    l += e;
-    o.x += e * vr[i].x;
-    o.y += e * vr[i].y;
-    o.z += e * vr[i].z;
-    o.w += e * vr[i].w;
-  }
-  // every lane of a row group holds the same e: count each position once
-  l = block_sum<4>(dl == 0 ? l : 0.f, red + 4);
+    float x[8];
+    vr[i].get(x);
 #pragma unroll
-  for (int off = LPP; off < 64; off <<= 1) {
-    o.x += __shfl_xor(o.x, off, 64);
-    o.y += __shfl_xor(o.y, off, 64);
-    o.z += __shfl_xor(o.z, off, 64);
-    o.w += __shfl_xor(o.w, off, 64);
+    for (int j = 0; j < GH; ++j) {
+      const float w = expf(sc[j][i] - m[j]);
+      l[j] += w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[j][e] += w * x[e];
+    }
   }
-  if (sub == 0) so[wv][dl] = o;
+  // per-row partial O to LDS; row sums of the weights (equal in a row's lanes)
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    float4* dst = (float4*)&so[wv * PPW + sub][j][8 * dl];
+    dst[0] = make_float4(o[j][0], o[j][1], o[j][2], o[j][3]);
+    dst[1] = make_float4(o[j][4], o[j][5], o[j][6], o[j][7]);
+    const int iv = __builtin_bit_cast(int, l[j]);
+    float t = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+#pragma unroll
+    for (int r = 1; r < PPW; ++r)
+      t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, r * LPP));
+    if (lane == 0) red[1][wv][j] = t;
+  }
   __syncthreads();
-  if (tid >= LPP) return;
-  float4 t = so[0][tid];
+  // O of each head: the 4*PPW row partials summed in a fixed order
+  for (int q4 = tid; q4 < GH * HD / 4; q4 += 256) {
+    const int j = q4 / (HD / 4), d = 4 * (q4 % (HD / 4));
+    float4 t = *(const float4*)&so[0][j][d];
 #pragma unroll
-  for (int w = 1; w < 4; ++w) {
-    t.x += so[w][tid].x;
-    t.y += so[w][tid].y;
-    t.z += so[w][tid].z;
-    t.w += so[w][tid].w;
-  }
-  if (nch == 1) {
-    const float inv = 1.0f / l;
-    dec_store<HD>(a, (int64_t)bh * HD, 4 * tid, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
-  } else {
-    float* P = a.part + ((int64_t)bh * a.nchunk + c) * (HD + 2);
-    *(float4*)(P + 4 * tid) = t;
-    if (tid == 0) *(float2*)(P + HD) = make_float2(m, l);
+    for (int r = 1; r < 4 * PPW; ++r) {
+      const float4 u = *(const float4*)&so[r][j][d];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    const float lj = (red[1][0][j] + red[1][1][j]) + (red[1][2][j] + red[1][3][j]);
+    const int64_t bh = (int64_t)row * a.H + h0 + j;
+    if (nch == 1) {
+      const float inv = 1.0f / lj;
+      dec_store<HD>(a, bh * HD, d, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
+    } else {
+      float* P = a.part + (bh * a.nchunk + c) * (HD + 2);
+      *(float4*)(P + d) = t;
+      if (d == 0) {
+        float mj = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
+        *(float2*)(P + HD) = make_float2(mj, lj);
+      }
+    }
   }
 }
 
-// Combine the chunks of a multi-chunk step in chunk order.
-template <int HD, int DPC>
-__global__ __launch_bounds__(64) void k_attn_dec_merge(DecArgs a) {
+// Combine the chunks of a multi-chunk step: the maximum over chunks, then
+// 256/(hd/8) chunk groups (group g takes chunks g, g + NG, ..., ascending)
+// whose weighted partial sums are added in group order. Every chunk's loads
+// are issued before the maximum is known.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_dec_merge(DecArgs a, int dpc) {
+  constexpr int LPC = HD / 8, NG = 256 / LPC, CPG = 4;
+  __shared__ float wmax[4];
+  __shared__ float sO[NG][HD];
+  __shared__ float sl[NG];
   const int bh = blockIdx.x, tid = threadIdx.x;
   if (a.d_rows && bh / a.H >= *a.d_rows) return;
   const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + (bh / a.H) % a.qpr;
-  const int nch = (len + DPC - 1) / DPC;
-  if (nch == 1 || tid >= HD / 4) return;
+  const int nch = (len + dpc - 1) / dpc;
+  if (nch == 1) return;
   const float* P = a.part + (int64_t)bh * a.nchunk * (HD + 2);
-  // eight chunks' loads in flight at a time; chunk order is kept
-  float m = -FLT_MAX;
-  for (int c0 = 0; c0 < nch; c0 += 8) {
-    float mk[8];
+  const int g = tid / LPC, dl = tid % LPC;
+  float mx = -FLT_MAX;
+  for (int c = tid; c < nch; c += 256) mx = fmaxf(mx, P[(int64_t)c * (HD + 2) + HD]);
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, l = 0.f, m = 0.f;
+  float2 ml[CPG];
+  float4 ov[CPG][2];
+  auto load = [&](int c0) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) mk[k] = c0 + k < nch ? P[(c0 + k) * (HD + 2) + HD] : -FLT_MAX;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) m = fmaxf(m, mk[k]);
-  }
-  float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-  float l = 0.f;
-  for (int c0 = 0; c0 < nch; c0 += 8) {
-    float2 ml[8];
-    float4 ov[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const bool ok = c0 + k < nch;
-      ml[k] = ok ? *(const float2*)(P + (c0 + k) * (HD + 2) + HD) : make_float2(-FLT_MAX, 0.f);
-      ov[k] = ok ? *(const float4*)(P + (c0 + k) * (HD + 2) + 4 * tid)
-                 : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < CPG; ++k) {
+      const int c = c0 + k * NG;
+      const float* pc = P + (int64_t)(c < nch ? c : 0) * (HD + 2);
+      ml[k] = *(const float2*)(pc + HD);
+      ov[k][0] = *(const float4*)(pc + 8 * dl);
+      ov[k][1] = *(const float4*)(pc + 8 * dl + 4);
     }
+  };
+  auto accumulate = [&](int c0) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      if (c0 + k >= nch) break;
+    for (int k = 0; k < CPG; ++k) {
+      if (c0 + k * NG >= nch) break;
       const float w = expf(ml[k].x - m);
       l += w * ml[k].y;
-      t.x += w * ov[k].x;
-      t.y += w * ov[k].y;
-      t.z += w * ov[k].z;
-      t.w += w * ov[k].w;
+      o[0] += w * ov[k][0].x; o[1] += w * ov[k][0].y; o[2] += w * ov[k][0].z; o[3] += w * ov[k][0].w;
+      o[4] += w * ov[k][1].x; o[5] += w * ov[k][1].y; o[6] += w * ov[k][1].z; o[7] += w * ov[k][1].w;
     }
+  };
+  load(g);  // this group's first chunks, in flight during the maximum's reduction
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+  __syncthreads();
+  m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  accumulate(g);
+  for (int c0 = g + NG * CPG; c0 < nch; c0 += NG * CPG) {
+    load(c0);
+    accumulate(c0);
   }
-  const float inv = 1.0f / l;
+  *(float4*)&sO[g][8 * dl] = make_float4(o[0], o[1], o[2], o[3]);
+  *(float4*)&sO[g][8 * dl + 4] = make_float4(o[4], o[5], o[6], o[7]);
+  if (dl == 0) sl[g] = l;
+  __syncthreads();
+  if (tid >= HD / 4) return;
+  float4 t = *(const float4*)&sO[0][4 * tid];
+  float L = sl[0];
+  for (int k = 1; k < NG; ++k) {
+    const float4 u = *(const float4*)&sO[k][4 * tid];
+    t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    L += sl[k];
+  }
+  const float inv = 1.0f / L;
   dec_store<HD>(a, (int64_t)bh * HD, 4 * tid, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
 }
 
@@ -424,10 +526,52 @@ int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT) {
   return (int64_t)B * d.H * attn_decode_chunks(maxT) * (d.hd + 2);
 }
 
-void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const float* kc,
-                            const float* vc, int B, int maxT, const int32_t* d_len, int len,
-                            float* scratch, float* y, uint16_t* ys, int64_t ys_plane, int qpr,
-                            const int32_t* d_rows) {
+namespace {
+
+// Largest head group that divides the query heads per KV head and keeps the
+// kernel's registers in bounds (8 values x GH heads of q and O per lane).
+int dec_group(int G, int dpc) {
+  static const int opts64[] = {5, 4, 2, 1}, opts128[] = {2, 1};
+  const int* opts = dpc == 128 ? opts128 : opts64;
+  const int n = dpc == 128 ? 2 : 4;
+  for (int i = 0; i < n; ++i)
+    if (G % opts[i] == 0) return opts[i];
+  return 1;
+}
+
+template <int HD, int DPC, class KT>
+void launch_dec_gh(hipStream_t s, const DecArgs& a, int rows, int gh) {
+  const int ng = a.H / a.KH / gh;
+  const dim3 grid((unsigned)(rows * a.KH * ng), (unsigned)a.nchunk);
+  switch (gh) {
+    case 5:
+      if constexpr (DPC == 64) { FG_LAUNCH((k_attn_dec<HD, DPC, 5, KT>), grid, dim3(256), 0, s, a); return; }
+      break;
+    case 4:
+      if constexpr (DPC == 64) { FG_LAUNCH((k_attn_dec<HD, DPC, 4, KT>), grid, dim3(256), 0, s, a); return; }
+      break;
+    case 2: FG_LAUNCH((k_attn_dec<HD, DPC, 2, KT>), grid, dim3(256), 0, s, a); return;
+    default: break;
+  }
+  FG_LAUNCH((k_attn_dec<HD, DPC, 1, KT>), grid, dim3(256), 0, s, a);
+}
+
+template <int HD, class KT>
+void launch_dec_hd(hipStream_t s, const DecArgs& a, int rows, int dpc, int gh) {
+  if (dpc == 128)
+    launch_dec_gh<HD, 128, KT>(s, a, rows, gh);
+  else
+    launch_dec_gh<HD, DPC_MIN, KT>(s, a, rows, gh);
+  if (a.nchunk > 1)
+    FG_LAUNCH((k_attn_dec_merge<HD>), dim3((unsigned)(rows * a.H)), dim3(256), 0, s, a, dpc);
+}
+
+}  // namespace
+
+void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const void* kc,
+                            const void* vc, bool kv16, int B, int maxT, const int32_t* d_len,
+                            int len, float* scratch, float* y, uint16_t* ys, int64_t ys_plane,
+                            int qpr, const int32_t* d_rows) {
   DecArgs a;
   a.q = q;
   a.kc = kc;
@@ -449,20 +593,13 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.ys_plane = ys_plane;
   a.part = scratch;
   const int rows = B * qpr;
-  const dim3 grid((unsigned)(rows * d.H), (unsigned)a.nchunk);
-  const dim3 mgrid((unsigned)(rows * d.H));
-  if (d.hd == 128 && dpc == 128) {
-    FG_LAUNCH((k_attn_dec<128, 128>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<128, 128>), mgrid, dim3(64), 0, s, a);
-  } else if (d.hd == 128) {
-    FG_LAUNCH((k_attn_dec<128, DPC_MIN>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<128, DPC_MIN>), mgrid, dim3(64), 0, s, a);
-  } else if (dpc == 128) {
-    FG_LAUNCH((k_attn_dec<64, 128>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<64, 128>), mgrid, dim3(64), 0, s, a);
+  const int gh = dec_group(d.H / d.KH, dpc);
+  if (d.hd == 128) {
+    if (kv16) launch_dec_hd<128, uint16_t>(s, a, rows, dpc, gh);
+    else launch_dec_hd<128, float>(s, a, rows, dpc, gh);
   } else {
-    FG_LAUNCH((k_attn_dec<64, DPC_MIN>), grid, dim3(256), 0, s, a);
-    if (a.nchunk > 1) FG_LAUNCH((k_attn_dec_merge<64, DPC_MIN>), mgrid, dim3(64), 0, s, a);
+    if (kv16) launch_dec_hd<64, uint16_t>(s, a, rows, dpc, gh);
+    else launch_dec_hd<64, float>(s, a, rows, dpc, gh);
   }
 }
 

@@ -3,8 +3,10 @@
 // A rotation pair (stored rows r, r+1 of the pair-interleaved QKV matrix:
 // head dims j and j+hd/2) arrives for token row m. q and k are rotated
 // (src/lib/fortran_rope.f90:45-46: y1 = x1 c + x2 s, y2 = -x1 s + x2 c);
-// k and the un-rotated v are appended to the fp32 cache at the row's
-// position (src/lib/fortran_kv.f90:112-116). When the split pointers are set
+// k and the un-rotated v are appended to the cache at the row's position
+// (src/lib/fortran_kv.f90:112-116): fp32, or bf16 (RNE) when a.kv16, in
+// which case the split planes carry the rounded value (lo plane zero), so a
+// chunk's attention sees what later steps read from the cache. When the split pointers are set
 // (chunk attention follows), q, k and v are also written as bf16 hi/lo
 // planes in the layouts the MFMA attention kernel reads:
 //   qs [B][H][T][hd], ks [B][KH][npos][hd], vt [B][KH][hd][npos]
@@ -61,6 +63,28 @@ __device__ __forceinline__ void split_bf16x4(const float (&v)[4], uint16_t* p, i
   store_v<NT>(reinterpret_cast<u32x2_t*>(p + plane), u32x2_t{l[0] | (l[1] << 16), l[2] | (l[3] << 16)});
 }
 
+// Cache element stores: fp32, or bf16 (RNE) for a bf16 cache.
+__device__ __forceinline__ void kv_put(const GemvArgs& a, float* c, int64_t i, float v) {
+  if (a.kv16)
+    reinterpret_cast<uint16_t*>(c)[i] = f32_to_bf16_rne(v);
+  else
+    c[i] = v;
+}
+__device__ __forceinline__ void kv_put4(const GemvArgs& a, float* c, int64_t i, float v0, float v1,
+                                        float v2, float v3) {
+  if (a.kv16) {
+    const uint32_t lo = (uint32_t)f32_to_bf16_rne(v0) | ((uint32_t)f32_to_bf16_rne(v1) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16_rne(v2) | ((uint32_t)f32_to_bf16_rne(v3) << 16);
+    *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint16_t*>(c) + i) = u32x2_t{lo, hi};
+  } else {
+    *reinterpret_cast<float4*>(c + i) = make_float4(v0, v1, v2, v3);
+  }
+}
+// The value a bf16 cache holds for v (v itself for an fp32 cache).
+__device__ __forceinline__ float kv_val(const GemvArgs& a, float v) {
+  return a.kv16 ? bf16_to_f32(f32_to_bf16_rne(v)) : v;
+}
+
 // RoPE coefficients of stored column pair r for token row m (q and k
 // columns; v columns take none).
 __device__ __forceinline__ void qkv_pair_coeffs(const GemvArgs& a, int m, int pos0, int r,
@@ -97,28 +121,28 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
       }
     } else {
       if (a.kc) {
-        float* k = a.kc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
-        k[j] = y1;
-        k[j + hd / 2] = y2;
+        const int64_t k = ((int64_t)b * a.maxT + pos) * kd + head * hd;
+        kv_put(a, a.kc, k + j, y1);
+        kv_put(a, a.kc, k + j + hd / 2, y2);
       }
       if (a.ks) {
         uint16_t* p = a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd;
-        split_bf16(y1, p + j, a.kv_plane);
-        split_bf16(y2, p + j + hd / 2, a.kv_plane);
+        split_bf16(kv_val(a, y1), p + j, a.kv_plane);
+        split_bf16(kv_val(a, y2), p + j + hd / 2, a.kv_plane);
       }
     }
   } else {
     const int base = r - qd - kd;
     const int head = base / hd, j = (base % hd) >> 1;
     if (a.vc) {
-      float* v = a.vc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
-      v[j] = x1;
-      v[j + hd / 2] = x2;
+      const int64_t v = ((int64_t)b * a.maxT + pos) * kd + head * hd;
+      kv_put(a, a.vc, v + j, x1);
+      kv_put(a, a.vc, v + j + hd / 2, x2);
     }
     if (a.vt) {
       uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
-      split_bf16(x1, p + (int64_t)j * a.npos, a.kv_plane);
-      split_bf16(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
+      split_bf16(kv_val(a, x1), p + (int64_t)j * a.npos, a.kv_plane);
+      split_bf16(kv_val(a, x2), p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
     }
   }
 }
@@ -157,12 +181,19 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
       }
     } else {
       if (a.kc) {
-        float* k = a.kc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
-        *reinterpret_cast<float4*>(k + j) = make_float4(y1[0], y1[1], y1[2], y1[3]);
-        *reinterpret_cast<float4*>(k + j + hd / 2) = make_float4(y2[0], y2[1], y2[2], y2[3]);
+        const int64_t k = ((int64_t)b * a.maxT + pos) * kd + head * hd;
+        kv_put4(a, a.kc, k + j, y1[0], y1[1], y1[2], y1[3]);
+        kv_put4(a, a.kc, k + j + hd / 2, y2[0], y2[1], y2[2], y2[3]);
       }
       if (a.ks) {
         uint16_t* p = a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd;
+        if (a.kv16) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            y1[i] = kv_val(a, y1[i]);
+            y2[i] = kv_val(a, y2[i]);
+          }
+        }
         split_bf16x4<NT>(y1, p + j, a.kv_plane);
         split_bf16x4<NT>(y2, p + j + hd / 2, a.kv_plane);
       }
@@ -171,16 +202,16 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
     const int base = r8 - qd - kd;
     const int head = base / hd, j = (base % hd) >> 1;
     if (a.vc) {
-      float* v = a.vc + ((int64_t)b * a.maxT + pos) * kd + head * hd;
-      *reinterpret_cast<float4*>(v + j) = make_float4(x[0], x[2], x[4], x[6]);
-      *reinterpret_cast<float4*>(v + j + hd / 2) = make_float4(x[1], x[3], x[5], x[7]);
+      const int64_t v = ((int64_t)b * a.maxT + pos) * kd + head * hd;
+      kv_put4(a, a.vc, v + j, x[0], x[2], x[4], x[6]);
+      kv_put4(a, a.vc, v + j + hd / 2, x[1], x[3], x[5], x[7]);
     }
     if (a.vt) {  // (tiles holding v columns normally take the row-fast path)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
-        split_bf16(x[2 * i], p + (int64_t)(j + i) * a.npos, a.kv_plane);
-        split_bf16(x[2 * i + 1], p + (int64_t)(j + i + hd / 2) * a.npos, a.kv_plane);
+        split_bf16(kv_val(a, x[2 * i]), p + (int64_t)(j + i) * a.npos, a.kv_plane);
+        split_bf16(kv_val(a, x[2 * i + 1]), p + (int64_t)(j + i + hd / 2) * a.npos, a.kv_plane);
       }
     }
   }
@@ -217,16 +248,18 @@ __device__ __forceinline__ void qkv_elem_epilogue(const GemvArgs& a, int m, int 
       else
         a.y[(int64_t)m * qd + head * hd + dim] = yv;
     } else {
-      if (a.kc) a.kc[((int64_t)b * a.maxT + pos) * kd + head * hd + dim] = yv;
+      if (a.kc) kv_put(a, a.kc, ((int64_t)b * a.maxT + pos) * kd + head * hd + dim, yv);
       if (a.ks)
-        split_bf16(yv, a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd + dim, a.kv_plane);
+        split_bf16(kv_val(a, yv), a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd + dim,
+                   a.kv_plane);
     }
   } else {
     const int base = r - qd - kd;
     const int head = base / hd, j = (base % hd) >> 1, dim = odd ? j + hd / 2 : j;
-    if (a.vc) a.vc[((int64_t)b * a.maxT + pos) * kd + head * hd + dim] = own;
+    if (a.vc) kv_put(a, a.vc, ((int64_t)b * a.maxT + pos) * kd + head * hd + dim, own);
     if (a.vt)
-      split_bf16(own, a.vt + (((int64_t)b * a.KH + head) * hd + dim) * a.npos + pos, a.kv_plane);
+      split_bf16(kv_val(a, own), a.vt + (((int64_t)b * a.KH + head) * hd + dim) * a.npos + pos,
+                 a.kv_plane);
   }
 }
 

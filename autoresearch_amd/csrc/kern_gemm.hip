@@ -120,15 +120,22 @@ __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* st
     if (run4) {
       const int base = n - qdk, head = base / hd, j = (base % hd) >> 1, b = mb / a.T;
       uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
+      if (a.kv16) {  // the planes carry what the bf16 cache holds
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x1[i] = kv_val(a, x1[i]);
+          x2[i] = kv_val(a, x2[i]);
+        }
+      }
       split_bf16x4<NT_QKV>(x1, p + (int64_t)j * a.npos, a.kv_plane);
       split_bf16x4<NT_QKV>(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
       if (a.vc) {
         const int kd = a.KH * hd;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float* v = a.vc + ((int64_t)b * a.maxT + pos + i) * kd + head * hd;
-          v[j] = x1[i];
-          v[j + hd / 2] = x2[i];
+          const int64_t v = ((int64_t)b * a.maxT + pos + i) * kd + head * hd;
+          kv_put(a, a.vc, v + j, x1[i]);
+          kv_put(a, a.vc, v + j + hd / 2, x2[i]);
         }
       }
     } else {

@@ -30,7 +30,7 @@ FG_ERRORS = {
 EXPORTS = (
     "fg_version", "fg_last_error", "fg_model_create", "fg_weights_read", "fg_model_load",
     "fg_model_destroy",
-    "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_destroy",
+    "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_create_ex", "fg_kv_destroy",
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
     "fg_eval_bpb", "fg_rows_npy", "fg_decode_spec", "fg_spec_accept", "fg_spec_draft",
@@ -40,6 +40,9 @@ EXPORTS = (
 KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other",
                 5: "decode_fused"}
 FG_OPT_FUSED_DECODE = 1
+
+
+FG_KV_BF16 = 1  # fg_kv_create_ex flag: bf16 K/V cache
 
 
 class FgptError(RuntimeError):
@@ -106,6 +109,7 @@ def load_library(path: str = LIB_PATH):
         "fg_forward": (i32, [_vp, _i, i32, i32, _f, _i, _f]),
         "fg_forward_dev": (i32, [_vp, _vp, i32, i32, _vp, _vp, _vp, _vp]),
         "fg_kv_create": (i32, [_vp, i32, i32, C.POINTER(_vp)]),
+        "fg_kv_create_ex": (i32, [_vp, i32, i32, i32, C.POINTER(_vp)]),
         "fg_kv_destroy": (i32, [_vp]),
         "fg_kv_len": (i32, [_vp, _i]),
         "fg_kv_set_len": (i32, [_vp, i32]),
@@ -284,17 +288,19 @@ class Model:
                               C.byref(c), C.byref(st), C.byref(out)))
         return out.value, st.value
 
-    def kv(self, B: int, maxT: int) -> "KV":
-        return KV(self, B, maxT)
+    def kv(self, B: int, maxT: int, bf16: bool = False) -> "KV":
+        return KV(self, B, maxT, bf16)
 
 
 class KV:
     """A KV cache of B sequences x maxT positions resident in HBM."""
 
-    def __init__(self, m: Model, B: int, maxT: int):
-        self.m, self.B, self.maxT = m, B, maxT
+    def __init__(self, m: Model, B: int, maxT: int, bf16: bool = False):
+        """bf16: K and V held as bf16 (FG_KV_BF16), half the cache bytes."""
+        self.m, self.B, self.maxT, self.bf16 = m, B, maxT, bf16
         self._h = _vp()
-        _check(_LIB.fg_kv_create(m.handle, B, maxT, C.byref(self._h)))
+        _check(_LIB.fg_kv_create_ex(m.handle, B, maxT, FG_KV_BF16 if bf16 else 0,
+                                    C.byref(self._h)))
 
     def close(self):
         if self._h:

@@ -7,7 +7,8 @@ and targets already resident in HBM), one "step" being one full forward.
 Beside it, each with its own roofline and the profiles/ summary it
 reproduces from: the B=1 greedy decode (16-id prompt, 32 cached steps), the
 B=8 x 2048 Zipf eval rows, the B=64 batched decode (1024-id prompts, 512
-steps), the depth-20 GQA model (2048-id prefill, 256 steps), speculative and
+steps, on the bf16 KV cache the workload states, and on the fp32 cache
+beside it), the depth-20 GQA model (2048-id prefill, 256 steps), speculative and
 sampled decoding; and the CPU oracle timed on this host's cores on a bounded
 sample.
 
@@ -173,16 +174,18 @@ def bench_eval_b8(m, d, steps, warmup, torch):
                          "profiles/eval_d12_B8_T2048_kernels.md")
 
 
-def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, profile, prompts=None):
+def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, profile, prompts=None,
+                 kv_bf16=False):
     """Greedy decode of B sequences: chunked prefill of prompt[:-1], then
     n_steps cached steps from the last prompt id, on the device loop
-    (fg_decode_greedy). tok/s from the wall clock over reps loops; the
-    kernel roofline from an fg_timing pass over one loop."""
+    (fg_decode_greedy), on an fp32 or a bf16 KV cache. tok/s from the wall
+    clock over reps loops; the kernel roofline from an fg_timing pass over
+    one loop."""
     from autoresearch_amd.weights import uniform_ids
     maxT = prompt_len + n_steps
     if prompts is None:
         prompts = uniform_ids(42 + B, B * prompt_len, d.vocab).reshape(B, prompt_len)
-    kv = m.kv(B, maxT)
+    kv = m.kv(B, maxT, bf16=kv_bf16)
     t0 = time.perf_counter()
     kv.step_multi(prompts[:, :-1], want_logits=False)
     m.sync()
@@ -203,6 +206,7 @@ def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, profile, prompts=No
     mean_bytes = float(np.mean(step_bytes))
     out = {"B": B, "prompt": prompt_len, "steps": n_steps, "ms_per_step": dt / n_steps * 1e3,
            "tok_s": B * n_steps / dt, "prompt_prefill_s": prefill_s,
+           "kv_cache": "bf16" if kv_bf16 else "fp32",
            "first_ids": ids[:8, 0].tolist(), "alg_bytes_per_step_mean": mean_bytes,
            "whole_step_achieved_gbs": mean_bytes / (dt / n_steps) / 1e9,
            "whole_step_frac": mean_bytes / (dt / n_steps) / 1e9 / HBM_PEAK_GBS,
@@ -488,8 +492,8 @@ def cpu_decode_baseline(d, w, c, s, budget_s: float = 6.0) -> dict:
             "first_ids": ids[:8]}
 
 
-WORKLOADS = ("prefill", "decode_b1", "eval_b8", "decode_b64", "gqa20", "decode_spec",
-             "decode_sample")
+WORKLOADS = ("prefill", "decode_b1", "eval_b8", "decode_b64", "decode_b64_fp32kv", "gqa20",
+             "decode_spec", "decode_sample")
 
 
 def main():
@@ -539,7 +543,10 @@ def main():
                                           profile="profiles/decode_d12_B1_fused.md"),
         "eval_b8": lambda: bench_eval_b8(m, d, max(3, args.steps // 4), 1, torch),
         "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0,
-                                           profile="profiles/decode_d12_B64_kernels.md"),
+                                           profile="profiles/decode_d12_B64_kernels.md",
+                                           kv_bf16=True),
+        "decode_b64_fp32kv": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0,
+                                                  profile="profiles/decode_d12_B64_fp32kv_kernels.md"),
         "gqa20": lambda: bench_gqa20(args.steps, 1, torch),
         "decode_spec": lambda: bench_spec(m, d, reps=3, warmup=1),
         "decode_sample": lambda: bench_sample(m, d, reps=3, warmup=1),

@@ -131,6 +131,13 @@ int32_t fg_forward_dev(fg_model *m, const int32_t *d_ids, int32_t B, int32_t T,
 /* KV cache for B sequences of up to maxT positions, fp32, resident in HBM
  * (replaces the caller-owned host cache_k/cache_v of fortran_kv.f90:9-12). */
 int32_t fg_kv_create(fg_model *m, int32_t B, int32_t maxT, fg_kv **out);
+/* The same with flags: FG_KV_BF16 keeps K and V as bf16 (RNE of the fp32
+ * values the reference stores), half the bytes of every cached step; the
+ * attention of a chunk then also sees the rounded K and V. No counterpart in
+ * the reference (whose cache is fp32); fg_kv_create is flags = 0. The B=1
+ * persistent decode loop runs on fp32 caches only. */
+enum { FG_KV_BF16 = 1 };
+int32_t fg_kv_create_ex(fg_model *m, int32_t B, int32_t maxT, int32_t flags, fg_kv **out);
 int32_t fg_kv_destroy(fg_kv *kv);
 /* cache_len in/out of gpt_step: the number of filled positions. set_len
  * rolls the length back (or forward again) within the positions this cache
@@ -138,7 +145,8 @@ int32_t fg_kv_destroy(fg_kv *kv);
  * never written). */
 int32_t fg_kv_len(const fg_kv *kv, int32_t *len);
 int32_t fg_kv_set_len(fg_kv *kv, int32_t len);
-/* Copy the cache back in the reference layout (L, B, maxT, KVH*hd) fp32. */
+/* Copy the cache back in the reference layout (L, B, maxT, KVH*hd) fp32
+ * (a bf16 cache widened). */
 int32_t fg_kv_read(fg_kv *kv, float *k_out, float *v_out);
 
 /* gpt_step (src/lib/fortran_kv.f90:26-149) for B sequences at position

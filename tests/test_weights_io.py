@@ -101,6 +101,31 @@ def test_arch_id_properties():
     assert arch_id_of("") == "0123456789abcdef"
 
 
+def test_arch_id_golden_vectors(tmp_path):
+    """arch.canonical and arch.id against the reference's own Python twin of
+    fortran_arch (scripts/arch.py:33-63; vectors written by
+    tests/golden/make_arch_vectors.py): the host digest in weights.py, and
+    the engine's C++ one, which accepts a checkpoint carrying the golden id
+    and refuses the same checkpoint with one digit of the id changed."""
+    import json
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "arch_id_vectors.json")))
+    for v in g["vectors"]:
+        assert arch_canonical_of(*v["fields"]) == v["canonical"]
+        assert arch_id_of(v["canonical"]) == v["id"]
+    v = next(x for x in g["vectors"] if x["fields"][:6] == [128, 2, 1, 64, 2, 512])
+    w = seeded_weights(SMALL, 3)
+    ctx, bos = v["fields"][6], v["fields"][7]
+    write_safetensors(str(tmp_path / "ok"), SMALL, w, ctx=ctx, bos=bos,
+                      metadata={"arch.canonical": v["canonical"], "arch.id": v["id"]})
+    got = engine.weights_read(str(tmp_path / "ok"), SMALL)
+    assert np.array_equal(got["wte"], w["wte"])
+    bad = v["id"][:-1] + ("0" if v["id"][-1] != "0" else "1")
+    write_safetensors(str(tmp_path / "bad"), SMALL, w, ctx=ctx, bos=bos,
+                      metadata={"arch.canonical": v["canonical"], "arch.id": bad})
+    with pytest.raises(engine.FgptError, match="arch"):
+        engine.weights_read(str(tmp_path / "bad"), SMALL)
+
+
 def _raw_st(path, header: dict, payload: bytes):
     import json
     h = json.dumps(header).encode()
