@@ -356,10 +356,11 @@ PMC_MATCH = ("k_gemm",)           # kernel-name fragments of that kind
 CALIB_BYTES = 256 << 20           # plain copy of known size: reads and writes this much
 
 
-def pmc_probe():
+def pmc_probe(workload: str = "prefill"):
     """Child of a `rocprofv3 --pmc` run: one warm-up and one measured T=2048
-    prefill, then a 256 MiB device copy whose counter reading calibrates the
-    counter against known bytes."""
+    prefill (or, for decode_b1, two loops of the B=1 decode workload: 16-id
+    prompt, 32 steps), then a 256 MiB device copy whose counter reading
+    calibrates the counter against known bytes."""
     import torch
     from autoresearch_amd import engine
     from autoresearch_amd.weights import D12, seeded_weights, rope_tables, uniform_ids
@@ -367,14 +368,23 @@ def pmc_probe():
     m = engine.Model(d, stacks=seeded_weights(d, SEED))
     c, s = rope_tables(2048, d.head_dim)
     m.set_rope(c.reshape(-1), s.reshape(-1))
-    T = 2048
-    ids = uniform_ids(2, T + 1, d.vocab)
     dev = torch.device("cuda:0")
-    d_ids = torch.from_numpy(ids[:T].copy()).to(dev)
-    d_lg = torch.empty(T * d.vocab, dtype=torch.float32, device=dev)
-    for _ in range(2):
-        m.forward_dev(d_ids.data_ptr(), 1, T, d_lg.data_ptr(), 0, 0, 0)
+    if workload == "decode_b1":
+        prompts = uniform_ids(43, 16, d.vocab).reshape(1, 16)
+        kv = m.kv(1, 48)
+        kv.step_multi(prompts[:, :-1], want_logits=False)
+        for _ in range(2):
+            kv.len = 15
+            kv.decode_greedy(prompts[:, -1], 32)
         m.sync()
+    else:
+        T = 2048
+        ids = uniform_ids(2, T + 1, d.vocab)
+        d_ids = torch.from_numpy(ids[:T].copy()).to(dev)
+        d_lg = torch.empty(T * d.vocab, dtype=torch.float32, device=dev)
+        for _ in range(2):
+            m.forward_dev(d_ids.data_ptr(), 1, T, d_lg.data_ptr(), 0, 0, 0)
+            m.sync()
     a = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
     b = torch.empty_like(a)
     torch.cuda.synchronize()
@@ -507,10 +517,11 @@ def main():
     ap.add_argument("--only", choices=WORKLOADS,
                     help="run one workload and print its record (for profiling runs)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the PMC traffic runs")
-    ap.add_argument("--pmc-probe", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-probe", nargs="?", const="prefill", choices=("prefill", "decode_b1"),
+                    help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_probe:
-        pmc_probe()
+        pmc_probe(args.pmc_probe)
         return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "

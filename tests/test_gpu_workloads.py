@@ -3,10 +3,12 @@
 tests/golden/make_fixtures.py ran the CPU oracle once on the same seeded
 weights and ids (regenerated here bit for bit by the repository's own
 generators) and stored: the per-row NLL sums of the B=8 x 2048 Zipf eval
-rows, the greedy ids of two of the 64 batched-decode sequences (1024-id
-prompt, 512 steps), and the depth-20 GQA model's last prefill row and 256
-greedy ids. Bars: logits within 2e-3 x max|logit|, NLL sums within
-2 x max|d logit| per token, greedy ids identical.
+rows, the greedy ids and per-step top-2 logit margins of all 64
+batched-decode sequences (1024-id prompts, 512 steps), and the depth-20 GQA
+model's prefill rows 0, 128, ..., 1920, 2047 and 256 greedy ids. Bars:
+logits within 2e-3 x max|logit|, NLL sums within 2 x max|d logit| per
+token, greedy ids identical (on the fp32 cache; the bf16 cache is reported
+against the same ids with the margin of each first flip).
 """
 import json
 import os
@@ -63,22 +65,70 @@ def test_eval_rows_b8_t2048():
     m.close()
 
 
-def test_decode_b64_prompt1024_steps512():
-    """Batched greedy decode: 64 sequences, 1024-id prompts, 512 steps."""
+def b64_run(bf16):
     g = fixture("decode_b64_d12")
     d, B, P, n = D12, g["B"], g["P"], g["steps"]
     prompts = uniform_ids(g["seed"], B * P, d.vocab).reshape(B, P)
     m = model(d, g["weights_seed"], P + n)
-    kv = m.kv(B, P + n)
+    kv = m.kv(B, P + n, bf16=bf16)
     kv.step_multi(prompts[:, :-1], want_logits=False)
     ids = kv.decode_greedy(prompts[:, -1], n)[0]
-    for b, rec in g["sequences"].items():
-        got = ids[:, int(b)]
-        first = int(np.argmax(got != np.array(rec["ids"]))) if not np.array_equal(got, rec["ids"]) else -1
-        print(f"sequence {b}: first mismatch {first}, oracle min top-2 margin {rec['min_top2_margin']:.3g}")
-        assert np.array_equal(got, np.array(rec["ids"], dtype=np.int32))
     kv.close()
     m.close()
+    return ids.T  # [B, n]
+
+
+def first_flips(got, ref):
+    out = {}
+    for b in range(ref.shape[0]):
+        diff = np.nonzero(got[b] != ref[b])[0]
+        if diff.size:
+            out[b] = int(diff[0])
+    return out
+
+
+# Top-2 logit margin below which two fp32 evaluations of the same logits in
+# different summation orders can rank the two ids either way: the engine's
+# logits sit within ~5e-6 x max|logit| of the oracle's (|logit| < 20 here),
+# and the reference itself accepts 1e-4 between two GEMM orders
+# (test_linear_blas, src/test/test_kernels.f90:2156-2177).
+FP32_TIE = 1e-4
+
+
+def test_decode_b64_prompt1024_steps512():
+    """Batched greedy decode: 64 sequences, 1024-id prompts, 512 steps, every
+    sequence's ids against the oracle's (fp32 cache). A sequence may leave
+    the oracle's stream only at a step whose oracle top-2 margin is an fp32
+    tie (below FP32_TIE); every such flip is printed."""
+    ref = np.load(os.path.join(GOLD, "decode_b64_d12_ids.npy"))
+    marg = np.load(os.path.join(GOLD, "decode_b64_d12_margins.npy"))
+    got = b64_run(False)
+    flips = first_flips(got, ref)
+    print(f"fp32 cache: {64 - len(flips)} of 64 sequences identical over 512 steps;",
+          "first flips (seq: step, oracle margin):",
+          {b: (t, float(marg[b, t])) for b, t in flips.items()},
+          "smallest oracle margin", float(marg.min()))
+    assert len(flips) <= 2
+    for b, t in flips.items():
+        assert marg[b, t] < FP32_TIE, (b, t, float(marg[b, t]))
+
+
+def test_decode_b64_bf16_cache_vs_oracle():
+    """The same workload on the bf16 cache the workload states: sequences
+    whose ids differ from the fp32 oracle's are reported with the step and
+    the oracle's top-2 margin there; a flip must sit at a step whose margin
+    is below 2 x the logit error that the bf16 cache alone causes at depth 12
+    (measured at < 5e-3 x max|logit| by the kv16 tests; 0.05 absolute here)."""
+    ref = np.load(os.path.join(GOLD, "decode_b64_d12_ids.npy"))
+    marg = np.load(os.path.join(GOLD, "decode_b64_d12_margins.npy"))
+    got = b64_run(True)
+    flips = first_flips(got, ref)
+    same = 64 - len(flips)
+    print(f"bf16 cache: {same} of 64 sequences identical over 512 steps;",
+          "first flips (seq: step, oracle margin):",
+          {b: (t, round(float(marg[b, t]), 5)) for b, t in flips.items()})
+    for b, t in flips.items():
+        assert marg[b, t] < 0.05, (b, t, float(marg[b, t]))
 
 
 def test_gqa20_prefill2048_decode256():
@@ -88,10 +138,16 @@ def test_gqa20_prefill2048_decode256():
     prompt = uniform_ids(g["seed"], P, d.vocab)
     m = model(d, g["weights_seed"], P + n)
     lg, _ = m.forward(prompt, 1, P)
+    lg = lg.reshape(P, d.vocab)
     last = np.load(os.path.join(GOLD, "gqa20_prefill_last.npy"))
-    rel = float(np.abs(lg.reshape(P, d.vocab)[-1].astype(np.float64) - last).max() / np.abs(last).max())
+    rel = float(np.abs(lg[-1].astype(np.float64) - last).max() / np.abs(last).max())
     print("gqa20 last prefill row rel err", rel)
     assert rel < TOL
+    rows = np.load(os.path.join(GOLD, "gqa20_prefill_rows.npy"))
+    idx = list(range(0, P, 128)) + [P - 1]
+    relr = float(np.abs(lg[idx].astype(np.float64) - rows).max() / np.abs(rows).max())
+    print(f"gqa20 prefill rows {idx[0]}..{idx[-1]} (every 128th + last) rel err", relr)
+    assert relr < TOL
     kv = m.kv(1, P + n)
     kv.step_multi(prompt[None, :-1], want_logits=False)
     ids = kv.decode_greedy(prompt[None, -1:], n)[0][:, 0]
