@@ -219,16 +219,17 @@ def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, profile, prompts=No
         out["roofline"] = roofline(tm["decode_fused"], float(sum(step_bytes)), "hbm",
                                    "decode_fused", profile)
     else:
-        kind = dominant(tm)
-        if kind == "attn_decode":
-            # per launch (one layer): n+1 cached positions read per sequence
-            alg = sum(B * kvl * (L0 + i + 1) for i in range(n_steps)) * d.n_layer
-        else:
-            alg = tm[kind][3]  # GEMV: weights once + activations, 2 N K + 4 M (K + N)
-        out["roofline"] = roofline(tm[kind], float(alg), "hbm", kind, profile)
-        if kind == "attn_decode" and tm["gemm"][0]:
-            out["roofline_linears"] = roofline(tm["gemm"], float(tm["gemm"][3]), "hbm", "gemm",
-                                               profile)
+        # attention: per launch (one layer) n+1 cached positions read per
+        # sequence; linears: weights once + activations, 2 N K + 4 M (K + N)
+        att = float(sum(B * kvl * (L0 + i + 1) for i in range(n_steps)) * d.n_layer)
+        lin = "gemm" if tm["gemm"][0] else "gemv"
+        if B > 1:  # the KV reads bound the batched step; the linears beside them
+            out["roofline"] = roofline(tm["attn_decode"], att, "hbm", "attn_decode", profile)
+            out["roofline_linears"] = roofline(tm[lin], float(tm[lin][3]), "hbm", lin, profile)
+        else:  # one sequence: the weight stream bounds the step
+            out["roofline"] = roofline(tm[lin], float(tm[lin][3]), "hbm", lin, profile)
+            out["roofline_attention"] = roofline(tm["attn_decode"], att, "hbm", "attn_decode",
+                                                 profile)
     kv.close()
     return out
 
