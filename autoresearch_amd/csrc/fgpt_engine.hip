@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <atomic>
 #include <map>
 #include <mutex>
@@ -98,6 +99,12 @@ struct fg_model {
   uint32_t* fused_err = nullptr;
   uint32_t fused_ep = 1;
   bool fused_on = true;  // fg_set_option(FG_OPT_FUSED_DECODE)
+  // FG_OPT_FORWARD_F16: the fp16 copy of the GEMM weights (the bf16 arena's
+  // layout, each value times w16_scale, a power of 2; wte unused), made on
+  // first use; w16_inv = 1 / w16_scale; wmax = max |w| of those weights
+  bool fwd_f16 = false;
+  uint16_t* w16 = nullptr;
+  float w16_scale = 1.f, w16_inv = 1.f, wmax = 0.f;
   std::string fused_why = "not set up";
 };
 
@@ -325,6 +332,14 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
   RCCHK(to_bf16_exact(st[7], V * D, tail, "lm_head"));
   RCCHK(to_bf16_exact(st[0], V * D, tail + V * D, "wte"));
   w.bytes = n_total * sizeof(bf16_t);
+  float wmax = 0.f;  // over every GEMM weight (the layers and lm_head)
+  for (size_t i = 0; i < w.layer_stride * d.L + V * D; ++i) {
+    uint32_t u = (uint32_t)(h[i] & 0x7FFF) << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    wmax = std::max(wmax, f);
+  }
+  m->wmax = wmax;
   HIPCHK(hipMalloc((void**)&w.base, w.bytes));
   HIPCHK(hipMemcpy(w.base, h.data(), w.bytes, hipMemcpyHostToDevice));
   w.lm = w.base + w.layer_stride * d.L;
@@ -459,6 +474,7 @@ struct PassOpts {
   bool rows_single = false;  // every row as a single cached step (see layer_stack)
   const int32_t* d_rows = nullptr;  // rows_single: rows live, read on the device
   bool kv16 = false;      // the cache holds bf16 elements
+  bool f16 = false;       // single-term fp16 MFMA pass where the MFMA path runs (> 128 rows)
 };
 
 // One pass over rows = B*T token rows: embedding of ids, the layer stack,
@@ -478,6 +494,9 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   Work& ws = ws_in ? *ws_in : m->ws;
   const int rows = B * T;
   const bool gm = !o.rows_single && use_gemm(d, rows);
+  // the single-term fp16 pass: MFMA GEMMs of more than 128 rows (no split K)
+  const bool f16 = o.f16 && gm && rows > 128 && m->w16;
+  auto W = [&](const bf16_t* p) { return f16 ? m->w16 + (p - m->w.base) : p; };
   const int pos_host = o.pos_host < 0 ? pos0 : o.pos_host;
   const bool embed = o.embed;
   // causal (query, key) pairs per (sequence, head) and the attention traffic
@@ -492,7 +511,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   if (embed)  // (else x already holds the embedded rows)
     timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
       launch_embed_norm(s, d, m->w.wte, ids, rows, ws.x, gm ? ws.xs : nullptr, xplane,
-                        gm ? ws.ssq : nullptr, o.d_rows);
+                        gm ? ws.ssq : nullptr, o.d_rows, f16);
     });
   int nt = 1;  // partial sums of squares per row of the current residual
   for (int l = 0; l < d.L; ++l) {
@@ -522,7 +541,9 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
       a.kv_plane = (int64_t)B * npos * d.kvd();
     }
     a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
-    a.w = m->w.qkv(l); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
+    a.f16 = f16 ? 1 : 0;
+    a.wscale = m->w16_inv;
+    a.w = W(m->w.qkv(l)); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
     linear(m, s, GV_QKV, a, d_pos, gm);
     a.qs = nullptr;
     a.ks = a.vt = nullptr;
@@ -542,23 +563,23 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
         });
       timed(m, s, FG_K_ATTN_CHUNK, at_flops, at_bytes, [&] {
         launch_attn_mfma(s, d, m->qs, m->ks, m->vt, B, T, npos, pos0, aplane,
-                         (int64_t)B * npos * d.kvd(), m->attn_part, ws.ao, aos, aplane);
+                         (int64_t)B * npos * d.kvd(), m->attn_part, ws.ao, aos, aplane, f16);
       });
     }
     // x += attn_out Wproj^T (GEMM path: also the split x and its row sums)
     a.x = ws.ao; a.xs = ws.aos; a.xs_plane = aplane; a.ssq_n = 0;
-    a.w = m->w.proj(l); a.N = d.D; a.K = d.qd(); a.norm = 0; a.y = ws.x;
+    a.w = W(m->w.proj(l)); a.N = d.D; a.K = d.qd(); a.norm = 0; a.y = ws.x;
     a.ys = ws.xs; a.ys_plane = xplane; a.ssq_out = ws.ssq;
     linear(m, s, GV_RESID, a, d_pos, gm);
     nt = nt_resid;
     // h = relu(rmsnorm(x) Wfc^T)^2
     a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
-    a.w = m->w.fc(l); a.N = d.dff; a.K = d.D; a.norm = 1; a.y = ws.h;
+    a.w = W(m->w.fc(l)); a.N = d.dff; a.K = d.D; a.norm = 1; a.y = ws.h;
     a.ys = ws.hs; a.ys_plane = hplane; a.ssq_out = nullptr;
     linear(m, s, GV_RELU2, a, d_pos, gm);
     // x += h Wproj2^T
     a.x = ws.h; a.xs = ws.hs; a.xs_plane = hplane; a.ssq_n = 0;
-    a.w = m->w.proj2(l); a.N = d.D; a.K = d.dff; a.norm = 0; a.y = ws.x;
+    a.w = W(m->w.proj2(l)); a.N = d.D; a.K = d.dff; a.norm = 0; a.y = ws.x;
     a.ys = ws.xs; a.ys_plane = xplane; a.ssq_out = ws.ssq;
     linear(m, s, GV_RESID, a, d_pos, gm);
     nt = gemm_ssq_parts(rows, d.D, d.dff);
@@ -566,7 +587,9 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   GemvArgs a = base_args(m, ws);
   a.M = rows; a.T = T; a.d_M = o.d_rows;
   a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
-  a.w = m->w.lm; a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
+  a.f16 = f16 ? 1 : 0;
+  a.wscale = m->w16_inv;
+  a.w = W(m->w.lm); a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
   linear(m, s, GV_STORE, a, d_pos, gm);
 }
 
@@ -588,7 +611,9 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   RCCHK(ensure_attn(m, B, T, 0));
   float* logits = d_logits ? d_logits : m->ws.logits;
   const double vb = (double)rows * m->d.V * 4;
-  layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, nullptr, logits);
+  PassOpts o;
+  o.f16 = m->fwd_f16;
+  layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, nullptr, logits, o);
   if (d_tgt && d_nll)
     timed(m, s, FG_K_OTHER, 0, vb, [&] { launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll); });
   HIPCHK(hipGetLastError());
@@ -657,6 +682,7 @@ extern "C" int32_t fg_model_destroy(fg_model* m) {
   if (m->samp) (void)hipFree(m->samp);
   if (m->w.base) (void)hipFree(m->w.base);
   if (m->fused_w) (void)hipFree(m->fused_w);
+  if (m->w16) (void)hipFree(m->w16);
   if (m->fused_slots) (void)hipFree(m->fused_slots);
   if (m->fused_err) (void)hipFree(m->fused_err);
   if (m->d_cos) (void)hipFree(m->d_cos);
@@ -1587,17 +1613,51 @@ extern "C" int32_t fg_decode_sample(fg_model* m, fg_kv* kv, int32_t* ids, int32_
   return FG_OK;
 }
 
+namespace {
+
+// The fp16 copy of the GEMM weights for FG_OPT_FORWARD_F16: every bf16
+// weight times 2^k, k the largest integer <= 15 with max|w| 2^k <= 32768,
+// so the copy holds each weight exactly unless it is below ~2^-(24+k-7)
+// (a bf16 has 8 significant bits; fp16 resolves 2^-24).
+int32_t ensure_w16(fg_model* m) {
+  if (m->w16) return FG_OK;
+  int k = 15;
+  while (k > -15 && m->wmax * std::ldexp(1.0f, k) > 32768.f) --k;
+  if (m->wmax * std::ldexp(1.0f, k) > 32768.f)
+    return seterr(FG_EARG, "weights up to %g exceed what fp16 holds", (double)m->wmax);
+  const size_t n = m->w.layer_stride * m->d.L + (size_t)m->d.V * m->d.D;  // layers + lm_head
+  HIPCHK(hipMalloc((void**)&m->w16, m->w.bytes));  // (the arena's size: offsets stay valid)
+  m->w16_scale = std::ldexp(1.0f, k);
+  m->w16_inv = std::ldexp(1.0f, -k);
+  launch_to_f16(m->stream, m->w.base, m->w16, (int64_t)n, m->w16_scale);
+  HIPCHK(hipStreamSynchronize(m->stream));
+  return FG_OK;
+}
+
+}  // namespace
+
 extern "C" int32_t fg_set_option(fg_model* m, int32_t key, int32_t value) {
   if (!m) return seterr(FG_EARG, "NULL argument");
-  if (key != FG_OPT_FUSED_DECODE) return seterr(FG_EARG, "unknown option %d", key);
+  if (key != FG_OPT_FUSED_DECODE && key != FG_OPT_FORWARD_F16)
+    return seterr(FG_EARG, "unknown option %d", key);
   GUARD(m);
-  m->fused_on = value != 0;
+  if (key == FG_OPT_FUSED_DECODE) {
+    m->fused_on = value != 0;
+  } else {
+    if (value) RCCHK(ensure_w16(m));
+    m->fwd_f16 = value != 0;
+  }
   return FG_OK;
 }
 
 extern "C" int32_t fg_get_option(fg_model* m, int32_t key, int32_t* value, char* why,
                                  int32_t len) {
   if (!m || !value) return seterr(FG_EARG, "NULL argument");
+  if (key == FG_OPT_FORWARD_F16) {
+    *value = m->fwd_f16 ? 1 : 0;
+    if (why && len > 0) why[0] = '\0';
+    return FG_OK;
+  }
   if (key != FG_OPT_FUSED_DECODE) return seterr(FG_EARG, "unknown option %d", key);
   *value = (m->fused_on && m->fused_w) ? 1 : 0;
   if (why && len > 0) {
@@ -1656,7 +1716,7 @@ extern "C" int32_t fg_timing_read(fg_model* m, int32_t kind, int64_t* launches, 
 
 extern "C" int32_t fg_model_bytes(const fg_model* m, int64_t* weight_bytes, int64_t* work_bytes) {
   if (!m) return seterr(FG_EARG, "NULL argument");
-  if (weight_bytes) *weight_bytes = (int64_t)m->w.bytes;
+  if (weight_bytes) *weight_bytes = (int64_t)m->w.bytes * (m->w16 ? 2 : 1);  // + the fp16 copy
   if (work_bytes) *work_bytes = m->work_bytes;
   return FG_OK;
 }

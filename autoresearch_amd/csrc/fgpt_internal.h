@@ -101,9 +101,12 @@ struct KVCacheDev {
 // x[r] = rmsnorm(wte[ids[r]]); when xs is set, also the split copy of x
 // (hi plane, lo plane `plane` elements later) and ssq[r] = sum_k x[r][k]^2.
 // d_rows (nullable): rows live this launch, read on the device.
+// dst[i] = fp16(bf16 src[i] * scale) (scale a power of 2), i < n.
+void launch_to_f16(hipStream_t s, const bf16_t* src, uint16_t* dst, int64_t n, float scale);
+
 void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
                        int64_t rows, float* x, uint16_t* xs = nullptr, int64_t plane = 0,
-                       float* ssq = nullptr, const int32_t* d_rows = nullptr);
+                       float* ssq = nullptr, const int32_t* d_rows = nullptr, bool f16 = false);
 
 // GEMV family for M <= GEMV_MAX_ROWS token rows, fp32 activations x bf16
 // weights (the MFMA GEMM shares the argument block).
@@ -153,6 +156,11 @@ struct GemvArgs {
   // applies the norm and the epilogue (RESID then writes one ssq partial per
   // row and 512 columns). Sized by gemm_splitk_floats.
   float* part;
+  // single-term fp16 pass (MFMA GEMM only, more than 128 rows): A is one fp16
+  // plane (xs), W the fp16 copy of the weights scaled by 1 / wscale (a power
+  // of 2), the outputs' operand planes fp16 too
+  int f16;
+  float wscale;
 };
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 
@@ -176,7 +184,7 @@ int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0);
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
                       int64_t kv_plane, float* scratch, float* y, uint16_t* ys = nullptr,
-                      int64_t ys_plane = 0);
+                      int64_t ys_plane = 0, bool f16 = false);
 // Fill the hi/lo key/value planes for cache positions [0, n) from the cache
 // of one layer ([B][maxT][KH*hd], fp32, or bf16 with kv16: lo planes zero).
 void launch_split_cache(hipStream_t s, const Dims& d, const void* kc, const void* vc, bool kv16,

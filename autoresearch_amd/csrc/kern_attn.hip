@@ -39,6 +39,7 @@
 namespace fgpt {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 namespace {
@@ -93,24 +94,25 @@ __device__ __forceinline__ void split8(const float* v, bf16x8_t& h, bf16x8_t& l)
 
 // four consecutive output dims (d % 4 == 0): fp32, or the bf16 hi/lo planes
 // the next GEMM reads, one 8-byte store per plane
-template <int HD>
+template <int HD, bool P16>
 __device__ __forceinline__ void store_out(const AttnArgs& p, int64_t yo, int d, const float (&v)[4]) {
   if (p.ys) {
-    split_bf16x4(v, p.ys + yo + d, p.ys_plane);
+    put4<P16>(v, p.ys + yo + d, p.ys_plane);
   } else {
     *(float4*)(p.y + yo + d) = make_float4(v[0], v[1], v[2], v[3]);
   }
 }
 
-template <int HD>
+template <int HD, bool P16>
 __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
   constexpr int NS = HD / 16;          // k-steps over the head dim
   constexpr int ND = HD / 32;          // 32-row blocks of O^T
   constexpr int RBK = HD * 2;          // bytes per K row in LDS
-  constexpr int REG = SK * RBK;        // bytes per region (K hi, K lo, V^T hi, V^T lo)
-  constexpr int STAGE = 4 * REG;
+  constexpr int REG = SK * RBK;        // bytes per region (K hi, K lo, V^T hi, V^T lo; P16: K, V^T)
+  constexpr int NKR = P16 ? 1 : 2;     // K regions (then as many V^T regions)
+  constexpr int STAGE = 2 * NKR * REG;
   constexpr int GPR = REG / 1024;      // 1 KB DMA groups per region
-  constexpr int GPW = 4 * GPR / 8;     // groups per wavefront per stage
+  constexpr int GPW = 2 * NKR * GPR / 8;  // groups per wavefront per stage
   constexpr int PSTR = QB * (HD + 2);  // floats per scratch item: O, then (max, sum)
   static_assert(GPR >= 8 && GPR % 8 == 0, "region / wavefront mismatch");
   extern __shared__ __attribute__((aligned(1024))) uint8_t lds[];
@@ -145,13 +147,13 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
   const int wq0 = p.pos0 + tq0 + qg * 32;
   const int wq1 = p.pos0 + min(tq0 + qg * 32 + 32, p.T) - 1;
 
-  bf16x8_t qh[NS], ql[NS];
+  bf16x8_t qh[NS], ql[NS];  // (P16: qh holds fp16 bits, ql is unused)
   {
     const uint16_t* qp = p.qs + ((int64_t)bh * p.T + (tok ? t : 0)) * HD + 8 * g;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       uint4 vh = *(const uint4*)(qp + 16 * s);
-      uint4 vl = *(const uint4*)(qp + 16 * s + p.q_plane);
+      uint4 vl = P16 ? make_uint4(0, 0, 0, 0) : *(const uint4*)(qp + 16 * s + p.q_plane);
       if (!tok) vh = vl = make_uint4(0, 0, 0, 0);
       qh[s] = __builtin_bit_cast(bf16x8_t, vh);
       ql[s] = __builtin_bit_cast(bf16x8_t, vl);
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
 #pragma unroll
   for (int q = 0; q < GPW; ++q) {
     const int region = 8 * q / GPR, gi = (wv + 8 * q) % GPR;
-    if (region < 2) {  // K rows: 1024 / RBK rows per group
+    if (region < NKR) {  // K rows: 1024 / RBK rows per group
       const int row = gi * (1024 / RBK) + lane / (HD / 8), slot = lane % (HD / 8);
       koff[q] = 32 * (row >> 5) + tile_key(row & 31);
       src[q] = p.ks + (region ? p.kv_plane : 0) + bk * p.npos * HD + kslot<HD>(row, slot) * 8;
@@ -181,7 +183,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
     for (int q = 0; q < GPW; ++q) {
       const int region = 8 * q / GPR;
       const uint16_t* g0 =
-          region < 2 ? src[q] + (int64_t)min(k0 + koff[q], p.nvalid - 1) * HD : src[q] + k0;
+          region < NKR ? src[q] + (int64_t)min(k0 + koff[q], p.nvalid - 1) * HD : src[q] + k0;
       dma16(g0, lds0 + stg * STAGE + 8 * q * 1024);
     }
   };
@@ -213,10 +215,15 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
       for (int s = 0; s < NS; ++s) {
         const int off = row * RBK + kslot<HD>(row, 2 * s + g) * 16;
         const bf16x8_t ah = *(const bf16x8_t*)(S + off);
-        const bf16x8_t al = *(const bf16x8_t*)(S + REG + off);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[s], sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[s], sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[s], sc, 0, 0, 0);
+        if constexpr (P16) {
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, ah),
+                                                     __builtin_bit_cast(f16x8_t, qh[s]), sc, 0, 0, 0);
+        } else {
+          const bf16x8_t al = *(const bf16x8_t*)(S + REG + off);
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, qh[s], sc, 0, 0, 0);
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, qh[s], sc, 0, 0, 0);
+          sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ql[s], sc, 0, 0, 0);
+        }
       }
     }
     // accumulator r of this lane is key kt0 + 16(r/8) + 8g + (r%8); mask
@@ -259,17 +266,30 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = sc[8 * s + e];
-      bf16x8_t bh8, bl8;
-      split8(pv, bh8, bl8);
+      if constexpr (P16) {
+        f16x8_t p8;
 #pragma unroll
-      for (int i = 0; i < ND; ++i) {
-        const int d = 32 * i + qi;
-        const int off = 2 * REG + d * 128 + vslot(d, 4 * kp + 2 * s + g) * 16;
-        const bf16x8_t avh = *(const bf16x8_t*)(S + off);
-        const bf16x8_t avl = *(const bf16x8_t*)(S + REG + off);
-        o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avh, bh8, o[i], 0, 0, 0);
-        o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avl, bh8, o[i], 0, 0, 0);
-        o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avh, bl8, o[i], 0, 0, 0);
+        for (int e = 0; e < 8; ++e) p8[e] = (_Float16)pv[e];
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+          const int d = 32 * i + qi;
+          const int off = NKR * REG + d * 128 + vslot(d, 4 * kp + 2 * s + g) * 16;
+          const f16x8_t av = *(const f16x8_t*)(S + off);
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, p8, o[i], 0, 0, 0);
+        }
+      } else {
+        bf16x8_t bh8, bl8;
+        split8(pv, bh8, bl8);
+#pragma unroll
+        for (int i = 0; i < ND; ++i) {
+          const int d = 32 * i + qi;
+          const int off = NKR * REG + d * 128 + vslot(d, 4 * kp + 2 * s + g) * 16;
+          const bf16x8_t avh = *(const bf16x8_t*)(S + off);
+          const bf16x8_t avl = *(const bf16x8_t*)(S + REG + off);
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avh, bh8, o[i], 0, 0, 0);
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avl, bh8, o[i], 0, 0, 0);
+          o[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(avh, bl8, o[i], 0, 0, 0);
+        }
       }
     }
   }
@@ -305,7 +325,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               v[e] = (o[i][4 * r4 + e] * a0 + xo[(i * 16 + 4 * r4 + e) * 64 + lane] * a1) * inv;
-            store_out<HD>(p, yo, 32 * i + 8 * r4 + 4 * g, v);
+            store_out<HD, P16>(p, yo, 32 * i + 8 * r4 + 4 * g, v);
           }
       }
     } else {
@@ -329,7 +349,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
 // Query blocks that span several key chunks: combine the chunks' partial
 // (O, max, sum) in chunk order. One workgroup per (sequence*head, block,
 // 32-query quarter); a thread owns 4 dims of 4 queries.
-template <int HD>
+template <int HD, bool P16>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
   constexpr int PSTR = QB * (HD + 2), D4 = HD / 4;
   const int bh = blockIdx.x % p.nbh, rest = blockIdx.x / p.nbh;
@@ -380,7 +400,7 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
     }
     const float inv = 1.0f / l;
     const float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
-    store_out<HD>(p, ((int64_t)b * p.T + tt) * yrow + h * HD, d, v);
+    store_out<HD, P16>(p, ((int64_t)b * p.T + tt) * yrow + h * HD, d, v);
   }
 }
 
@@ -426,18 +446,32 @@ int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0) {
   return (int64_t)B * d.H * attn_items_per_head(T, pos0) * QB * (d.hd + 2);
 }
 
+// LDS of a chunk attention launch: two stages, or the key-parity merge
+// buffer after the loop (4 query groups x (O^T + max and sum)) if larger
+template <int HD, bool P16>
+constexpr int attn_lds() {
+  constexpr int stages = 2 * 2 * (P16 ? 1 : 2) * SK * HD * 2;
+  constexpr int merge = 4 * (HD / 32 * 16 * 64 + 128) * 4;
+  return stages > merge ? stages : merge;
+}
+
+template <int HD, bool P16>
+void launch_attn_hd(hipStream_t s, const AttnArgs& p, dim3 grid, dim3 mgrid, bool split) {
+  constexpr int lds = attn_lds<HD, P16>();
+  static bool lds_set = false;
+  if (!lds_set) {
+    (void)hipFuncSetAttribute((const void*)k_attn_mfma<HD, P16>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    lds_set = true;
+  }
+  FG_LAUNCH((k_attn_mfma<HD, P16>), grid, dim3(512), lds, s, p);
+  if (split) FG_LAUNCH((k_attn_merge<HD, P16>), mgrid, dim3(256), 0, s, p);
+}
+
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
                       int64_t kv_plane, float* scratch, float* y, uint16_t* ys,
-                      int64_t ys_plane) {
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)k_attn_mfma<128>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
-    (void)hipFuncSetAttribute((const void*)k_attn_mfma<64>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
-    lds_set = true;
-  }
+                      int64_t ys_plane, bool f16) {
   AttnArgs p;
   p.qs = qs;
   p.ks = ks;
@@ -461,11 +495,11 @@ void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const ui
   const bool split = p.iph > p.nqb;  // some query block spans several chunks
   const dim3 mgrid((unsigned)(p.nbh * p.nqb * 4));
   if (d.hd == 128) {
-    FG_LAUNCH(k_attn_mfma<128>, grid, dim3(512), 2 * 4 * SK * 256, s, p);
-    if (split) FG_LAUNCH(k_attn_merge<128>, mgrid, dim3(256), 0, s, p);
+    if (f16) launch_attn_hd<128, true>(s, p, grid, mgrid, split);
+    else launch_attn_hd<128, false>(s, p, grid, mgrid, split);
   } else {
-    FG_LAUNCH(k_attn_mfma<64>, grid, dim3(512), 2 * 4 * SK * 128, s, p);
-    if (split) FG_LAUNCH(k_attn_merge<64>, mgrid, dim3(256), 0, s, p);
+    if (f16) launch_attn_hd<64, true>(s, p, grid, mgrid, split);
+    else launch_attn_hd<64, false>(s, p, grid, mgrid, split);
   }
 }
 

@@ -32,6 +32,11 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
+// fp16 bits of v, round to nearest even (v_cvt_f16_f32).
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
 // Unpack 8 bf16 held in a uint4 (little-endian pairs) to floats.
 __device__ __forceinline__ void unpack8(const uint4 v, float* f) {
   f[0] = __uint_as_float(v.x << 16);

@@ -13,6 +13,8 @@
 //   per-position NLL        src/app/eval_bpb.f90:165-181
 #include <float.h>
 
+#include <algorithm>
+
 #include "fgpt_internal.h"
 #include "kern_common.h"
 #include "kern_epi.h"
@@ -51,6 +53,9 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // gpt_forward copies back into the residual (fortran_gpt.f90:136-142).
 // An id outside [0, V) (possible only through the device-pointer entry
 // point, the host ones validate) yields a NaN row instead of a wild read.
+// xs (nullable) takes the split copy of x (bf16 hi, lo `plane` later) or,
+// for a single-term fp16 pass (P16), one fp16 plane.
+template <bool P16>
 __global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ wte,
                                                     const int32_t* __restrict__ ids, int D, int V,
                                                     float eps, float* __restrict__ x,
@@ -78,7 +83,7 @@ __global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ w
   for (int k = threadIdx.x; k < D; k += 256) {
     const float v = bf16_to_f32(row[k]) * inv;
     x[r * D + k] = v;
-    if (xs) split_bf16(v, xs + r * D + k, plane);
+    if (xs) put1<P16>(v, xs + r * D + k, plane);
     s2 += v * v;
   }
   if (ssq) {
@@ -87,12 +92,29 @@ __global__ __launch_bounds__(256) void k_embed_norm(const bf16_t* __restrict__ w
   }
 }
 
+__global__ __launch_bounds__(256) void k_to_f16(const bf16_t* __restrict__ src,
+                                                uint16_t* __restrict__ dst, int64_t n,
+                                                float scale) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    dst[i] = f32_to_f16_rne(bf16_to_f32(src[i]) * scale);
+}
+
+void launch_to_f16(hipStream_t s, const bf16_t* src, uint16_t* dst, int64_t n, float scale) {
+  if (n <= 0) return;
+  const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+  FG_LAUNCH(k_to_f16, dim3((unsigned)blocks), dim3(256), 0, s, src, dst, n, scale);
+}
+
 void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
                        int64_t rows, float* x, uint16_t* xs, int64_t plane, float* ssq,
-                       const int32_t* d_rows) {
+                       const int32_t* d_rows, bool f16) {
   if (rows <= 0) return;
-  FG_LAUNCH(k_embed_norm, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V, d.eps,
-                     x, xs, plane, ssq, d_rows);
+  if (f16)
+    FG_LAUNCH(k_embed_norm<true>, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V,
+              d.eps, x, xs, plane, ssq, d_rows);
+  else
+    FG_LAUNCH(k_embed_norm<false>, dim3((unsigned)rows), dim3(256), 0, s, wte, ids, d.D, d.V,
+              d.eps, x, xs, plane, ssq, d_rows);
 }
 
 // ------------------------------------------------------------ epilogues

@@ -7,8 +7,9 @@
 // (src/lib/fortran_kv.f90:112-116): fp32, or bf16 (RNE) when a.kv16, in
 // which case the split planes carry the rounded value (lo plane zero), so a
 // chunk's attention sees what later steps read from the cache. When the split pointers are set
-// (chunk attention follows), q, k and v are also written as bf16 hi/lo
-// planes in the layouts the MFMA attention kernel reads:
+// (chunk attention follows), q, k and v are also written as operand planes
+// (bf16 hi/lo, or one fp16 plane for a single-term pass) in the layouts the
+// MFMA attention kernel reads:
 //   qs [B][H][T][hd], ks [B][KH][npos][hd], vt [B][KH][hd][npos]
 // (hi plane first, lo plane `*_plane` elements later).
 #pragma once
@@ -85,6 +86,34 @@ __device__ __forceinline__ float kv_val(const GemvArgs& a, float v) {
   return a.kv16 ? bf16_to_f32(f32_to_bf16_rne(v)) : v;
 }
 
+// Operand planes of the MFMA kernels: a value goes in as bf16 hi at p and
+// bf16 lo at p + plane (the split format, ~16 significant bits), or, for a
+// single-term fp16 pass (P16), as one fp16 at p.
+template <bool P16>
+__device__ __forceinline__ void put1(float v, uint16_t* p, int64_t plane) {
+  if constexpr (P16)
+    p[0] = f32_to_f16_rne(v);
+  else
+    split_bf16(v, p, plane);
+}
+template <bool P16, bool NT = false>
+__device__ __forceinline__ void put2(float v0, float v1, uint16_t* p, int64_t plane) {
+  if constexpr (P16)
+    store_v<NT>(reinterpret_cast<uint32_t*>(p),
+                (uint32_t)f32_to_f16_rne(v0) | ((uint32_t)f32_to_f16_rne(v1) << 16));
+  else
+    split_bf16x2<NT>(v0, v1, p, plane);
+}
+template <bool P16, bool NT = false>
+__device__ __forceinline__ void put4(const float (&v)[4], uint16_t* p, int64_t plane) {
+  if constexpr (P16)
+    store_v<NT>(reinterpret_cast<u32x2_t*>(p),
+                u32x2_t{(uint32_t)f32_to_f16_rne(v[0]) | ((uint32_t)f32_to_f16_rne(v[1]) << 16),
+                        (uint32_t)f32_to_f16_rne(v[2]) | ((uint32_t)f32_to_f16_rne(v[3]) << 16)});
+  else
+    split_bf16x4<NT>(v, p, plane);
+}
+
 // RoPE coefficients of stored column pair r for token row m (q and k
 // columns; v columns take none).
 __device__ __forceinline__ void qkv_pair_coeffs(const GemvArgs& a, int m, int pos0, int r,
@@ -99,6 +128,7 @@ __device__ __forceinline__ void qkv_pair_coeffs(const GemvArgs& a, int m, int po
 }
 
 // qkv_pair_epilogue with the pair's RoPE coefficients already loaded.
+template <bool P16 = false>
 __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos0, int r,
                                                float x1, float x2, float cs, float sn) {
   const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
@@ -112,8 +142,8 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
     if (isq) {
       if (a.qs) {
         uint16_t* p = a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd;
-        split_bf16(y1, p + j, a.q_plane);
-        split_bf16(y2, p + j + hd / 2, a.q_plane);
+        put1<P16>(y1, p + j, a.q_plane);
+        put1<P16>(y2, p + j + hd / 2, a.q_plane);
       } else {
         float* q = a.y + (int64_t)m * qd + head * hd;
         q[j] = y1;
@@ -127,8 +157,8 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
       }
       if (a.ks) {
         uint16_t* p = a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd;
-        split_bf16(kv_val(a, y1), p + j, a.kv_plane);
-        split_bf16(kv_val(a, y2), p + j + hd / 2, a.kv_plane);
+        put1<P16>(kv_val(a, y1), p + j, a.kv_plane);
+        put1<P16>(kv_val(a, y2), p + j + hd / 2, a.kv_plane);
       }
     }
   } else {
@@ -141,8 +171,8 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
     }
     if (a.vt) {
       uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
-      split_bf16(kv_val(a, x1), p + (int64_t)j * a.npos, a.kv_plane);
-      split_bf16(kv_val(a, x2), p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
+      put1<P16>(kv_val(a, x1), p + (int64_t)j * a.npos, a.kv_plane);
+      put1<P16>(kv_val(a, x2), p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
     }
   }
 }
@@ -151,7 +181,7 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
 // head and dims j .. j+3 with j % 4 == 0) of token row m, x the eight
 // values, cs/sn the four pairs' RoPE coefficients: the arithmetic of
 // qkv_pair_store, with each plane's four dims written by one wide store.
-template <bool NT = false>
+template <bool NT = false, bool P16 = false>
 __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos0, int r8,
                                                const float (&x)[8], const float4& cs,
                                                const float4& sn) {
@@ -172,8 +202,8 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
     if (isq) {
       if (a.qs) {
         uint16_t* p = a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd;
-        split_bf16x4<NT>(y1, p + j, a.q_plane);
-        split_bf16x4<NT>(y2, p + j + hd / 2, a.q_plane);
+        put4<P16, NT>(y1, p + j, a.q_plane);
+        put4<P16, NT>(y2, p + j + hd / 2, a.q_plane);
       } else {
         float* q = a.y + (int64_t)m * qd + head * hd;
         *reinterpret_cast<float4*>(q + j) = make_float4(y1[0], y1[1], y1[2], y1[3]);
@@ -194,8 +224,8 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
             y2[i] = kv_val(a, y2[i]);
           }
         }
-        split_bf16x4<NT>(y1, p + j, a.kv_plane);
-        split_bf16x4<NT>(y2, p + j + hd / 2, a.kv_plane);
+        put4<P16, NT>(y1, p + j, a.kv_plane);
+        put4<P16, NT>(y2, p + j + hd / 2, a.kv_plane);
       }
     }
   } else {
@@ -210,18 +240,19 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         uint16_t* p = a.vt + ((int64_t)b * a.KH + head) * hd * a.npos + pos;
-        split_bf16(kv_val(a, x[2 * i]), p + (int64_t)(j + i) * a.npos, a.kv_plane);
-        split_bf16(kv_val(a, x[2 * i + 1]), p + (int64_t)(j + i + hd / 2) * a.npos, a.kv_plane);
+        put1<P16>(kv_val(a, x[2 * i]), p + (int64_t)(j + i) * a.npos, a.kv_plane);
+        put1<P16>(kv_val(a, x[2 * i + 1]), p + (int64_t)(j + i + hd / 2) * a.npos, a.kv_plane);
       }
     }
   }
 }
 
+template <bool P16 = false>
 __device__ __forceinline__ void qkv_pair_epilogue(const GemvArgs& a, int m, int pos0, int r,
                                                   float x1, float x2) {
   float cs = 0.f, sn = 0.f;
   qkv_pair_coeffs(a, m, pos0, r, cs, sn);
-  qkv_pair_store(a, m, pos0, r, x1, x2, cs, sn);
+  qkv_pair_store<P16>(a, m, pos0, r, x1, x2, cs, sn);
 }
 
 // One element of a rotation pair, for producers that hold one column per
@@ -229,6 +260,7 @@ __device__ __forceinline__ void qkv_pair_epilogue(const GemvArgs& a, int m, int 
 // dim j, r odd: dim j + hd/2, j = (r % hd) / 2), `own` its value and `other`
 // the value of the pair's other column. Same arithmetic and destinations as
 // qkv_pair_epilogue.
+template <bool P16 = false>
 __device__ __forceinline__ void qkv_elem_epilogue(const GemvArgs& a, int m, int pos0, int r,
                                                   float own, float other) {
   const int hd = a.hd, qd = a.H * hd, kd = a.KH * hd;
@@ -244,13 +276,13 @@ __device__ __forceinline__ void qkv_elem_epilogue(const GemvArgs& a, int m, int 
     const float yv = odd ? x1 * (-sn) + x2 * cs : x1 * cs + x2 * sn;
     if (isq) {
       if (a.qs)
-        split_bf16(yv, a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd + dim, a.q_plane);
+        put1<P16>(yv, a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd + dim, a.q_plane);
       else
         a.y[(int64_t)m * qd + head * hd + dim] = yv;
     } else {
       if (a.kc) kv_put(a, a.kc, ((int64_t)b * a.maxT + pos) * kd + head * hd + dim, yv);
       if (a.ks)
-        split_bf16(kv_val(a, yv), a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd + dim,
+        put1<P16>(kv_val(a, yv), a.ks + (((int64_t)b * a.KH + head) * a.npos + pos) * hd + dim,
                    a.kv_plane);
     }
   } else {
@@ -258,7 +290,7 @@ __device__ __forceinline__ void qkv_elem_epilogue(const GemvArgs& a, int m, int 
     const int head = base / hd, j = (base % hd) >> 1, dim = odd ? j + hd / 2 : j;
     if (a.vc) kv_put(a, a.vc, ((int64_t)b * a.maxT + pos) * kd + head * hd + dim, own);
     if (a.vt)
-      split_bf16(kv_val(a, own), a.vt + (((int64_t)b * a.KH + head) * hd + dim) * a.npos + pos,
+      put1<P16>(kv_val(a, own), a.vt + (((int64_t)b * a.KH + head) * hd + dim) * a.npos + pos,
                  a.kv_plane);
   }
 }

@@ -40,7 +40,18 @@ namespace fgpt {
 constexpr bool NT_RELU2 = true, NT_RESID = true, NT_QKV = false;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// One 32x32x16 MFMA step: bf16 operands, or (P16) fp16 ones.
+template <bool P16>
+__device__ __forceinline__ f32x16_t mma16(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+  if constexpr (P16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
 
 namespace {
 
@@ -69,7 +80,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 // rows (positions), so v^T gets one wide store per dim. Rows that do not
 // form an aligned run of four positions of one sequence take the per-pair
 // path. Every item's RoPE coefficients are loaded before any item stores.
-template <int BN, int NT>
+template <int BN, int NT, bool P16>
 __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* stage,
                                               const float* sinv, int m0, int n0, int q,
                                               bool rows_fast, int pos0) {
@@ -100,7 +111,7 @@ __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* st
       const float sc = a.norm ? sinv[ml] : 1.f;
       const float x[8] = {lo.x * sc, lo.y * sc, lo.z * sc, lo.w * sc,
                           hi.x * sc, hi.y * sc, hi.z * sc, hi.w * sc};
-      qkv_quad_store<NT_QKV>(a, m, pos0, n0 + pc, x, c4[k], s4[k]);
+      qkv_quad_store<NT_QKV, P16>(a, m, pos0, n0 + pc, x, c4[k], s4[k]);
     }
     return;
   }
@@ -127,8 +138,8 @@ __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* st
           x2[i] = kv_val(a, x2[i]);
         }
       }
-      split_bf16x4<NT_QKV>(x1, p + (int64_t)j * a.npos, a.kv_plane);
-      split_bf16x4<NT_QKV>(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
+      put4<P16, NT_QKV>(x1, p + (int64_t)j * a.npos, a.kv_plane);
+      put4<P16, NT_QKV>(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
       if (a.vc) {
         const int kd = a.KH * hd;
 #pragma unroll
@@ -141,7 +152,7 @@ __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* st
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (mb + i < M) qkv_pair_epilogue(a, mb + i, pos0, n, x1[i], x2[i]);
+        if (mb + i < M) qkv_pair_epilogue<P16>(a, mb + i, pos0, n, x1[i], x2[i]);
     }
   }
 }
@@ -151,7 +162,7 @@ __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* st
 // every SIMD two wavefronts of its own still keeps them all busy. The
 // groups' partial sums meet in the LDS staging buffer in a fixed order
 // (KG - 1 first, 0 last), so the result does not depend on timing.
-template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST, int KG = 1>
+template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST, int KG = 1, bool P16 = false>
 __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
                                                              const int32_t* __restrict__ d_pos) {
   constexpr int NWT = NWM * NWN, NW = NWT * KG, NT = 64 * NW;
@@ -159,7 +170,8 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
   // a stage: A hi rows, A lo rows, W rows of RB bytes each, loaded 1 KB
   // (1024 / RB rows) per wavefront instruction
   constexpr int RB = 2 * BK, CPR = BK / 8, RPG = 1024 / RB;
-  constexpr int ROWS = 2 * BM + BN;
+  constexpr int AP = P16 ? 1 : 2;  // operand planes of A (hi and lo, or one fp16)
+  constexpr int ROWS = AP * BM + BN;
   constexpr int GROUPS = ROWS / RPG;         // 1 KB load groups per stage
   // groups per wavefront per stage; when NW does not divide GROUPS, the
   // spare slots repeat the last group (the same bytes to the same place)
@@ -197,12 +209,12 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
     const int g = min(wid + NW * q, GROUPS - 1);
     const int r = RPG * g + lane / CPR, slot = lane % CPR;
     const int c = swz<BK>(r, slot);
-    if (r < 2 * BM) {  // A hi (r < BM) or A lo
+    if (r < AP * BM) {  // A hi (r < BM) or A lo
       const int ar = r < BM ? r : r - BM;
       const int row = min(m0 + ar, M - 1);  // rows past M are never stored
       src[q] = a.xs + (r < BM ? 0 : a.xs_plane) + (int64_t)row * K + kbeg + c * 8;
     } else {
-      src[q] = a.w + (int64_t)(n0 + r - 2 * BM) * K + kbeg + c * 8;
+      src[q] = a.w + (int64_t)(n0 + r - AP * BM) * K + kbeg + c * 8;
     }
   }
 
@@ -259,23 +271,23 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
       for (int i = 0; i < WM; ++i) {
         const int r = (wm * WM + i) * 32 + (lane & 31);
         ah[i] = *(const bf16x8_t*)(stg + r * RB + swz<BK>(r, c) * 16);
-        al[i] = *(const bf16x8_t*)(stg + (BM + r) * RB + swz<BK>(BM + r, c) * 16);
+        if constexpr (!P16) al[i] = *(const bf16x8_t*)(stg + (BM + r) * RB + swz<BK>(BM + r, c) * 16);
       }
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
-        const int r = 2 * BM + (wn * WN + j) * 32 + (lane & 31);
+        const int r = AP * BM + (wn * WN + j) * 32 + (lane & 31);
         bw[j] = *(const bf16x8_t*)(stg + r * RB + swz<BK>(r, c) * 16);
       }
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bw[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < WN; ++j) acc[i][j] = mma16<P16>(ah[i], bw[j], acc[i][j]);
+      if constexpr (!P16) {
 #pragma unroll
-      for (int i = 0; i < WM; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bw[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < WN; ++j) acc[i][j] = mma16<false>(al[i], bw[j], acc[i][j]);
+      }
     }
   };
   // prologue: slices 0 .. NST-2 in flight; then each step waits for its
@@ -331,7 +343,9 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
 #pragma unroll
           for (int rg = 0; rg < 16; ++rg) {
             const int r = 8 * (rg >> 2) + 4 * (lane >> 5) + (rg & 3);
-            reg[((rb & 1) * 32 + r) * SSTR + (wn * WN + j) * 32 + (lane & 31)] = acc[i][j][rg];
+            // (P16: the weights were stored scaled by 1 / wscale, a power of 2)
+            reg[((rb & 1) * 32 + r) * SSTR + (wn * WN + j) * 32 + (lane & 31)] =
+                P16 ? acc[i][j][rg] * a.wscale : acc[i][j][rg];
           }
       }
       __syncthreads();
@@ -357,7 +371,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
     // wavefront, with BN = 64 half of one (reductions stay in the wave)
     if constexpr (EPI == GV_QKV) {
       if (!a.part) {
-        qkv_tile_pass<BN, NT>(a, stage, sinv, m0, n0, q, rows_fast, pos0);
+        qkv_tile_pass<BN, NT, P16>(a, stage, sinv, m0, n0, q, rows_fast, pos0);
         __syncthreads();
         continue;
       }
@@ -381,7 +395,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
         v1 *= sinv[ml];
       }
       if (EPI == GV_QKV) {
-        if (live) qkv_pair_epilogue(a, m, pos0, n, v0, v1);
+        if (live) qkv_pair_epilogue<P16>(a, m, pos0, n, v0, v1);
       } else if (EPI == GV_RESID) {
         float2 o = make_float2(0.f, 0.f);
         float* y = a.y + (int64_t)(live ? m : 0) * a.N + n;
@@ -390,7 +404,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
           o.x += v0;
           o.y += v1;
           store_v<NT_RESID>(reinterpret_cast<f32x2_t*>(y), f32x2_t{o.x, o.y});
-          split_bf16x2<NT_RESID>(o.x, o.y, a.ys + (int64_t)m * a.N + n, a.ys_plane);
+          put2<P16, NT_RESID>(o.x, o.y, a.ys + (int64_t)m * a.N + n, a.ys_plane);
         }
         // the row's sum of squares over this tile
         const float sq0 = o.x * o.x + o.y * o.y;
@@ -403,7 +417,7 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
       } else if (EPI == GV_RELU2) {
         if (live) {
           const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
-          split_bf16x2<NT_RELU2>(t0 * t0, t1 * t1, a.ys + (int64_t)m * a.N + n, a.ys_plane);
+          put2<P16, NT_RELU2>(t0 * t0, t1 * t1, a.ys + (int64_t)m * a.N + n, a.ys_plane);
         }
       } else {
         if (live) *reinterpret_cast<float2*>(a.y + (int64_t)m * a.N + n) = make_float2(v0, v1);
@@ -442,44 +456,46 @@ struct Frag {
   bf16x8_t h[WM], l[WM], w[WN];
 };
 
-template <int BM, int WM, int WN>
+template <int BM, int WM, int WN, bool P16>
 __device__ __forceinline__ void frag_load(Frag<WM, WN>& f, const uint8_t* stg, int kk, int wm,
                                           int wn, int lane) {
+  constexpr int AP = P16 ? 1 : 2;
   const int c = 2 * kk + (lane >> 5);  // logical chunk of this half-wave
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
     const int r = (wm * WM + i) * 32 + (lane & 31);
     f.h[i] = *(const bf16x8_t*)(stg + r * 64 + swz<32>(r, c) * 16);
-    f.l[i] = *(const bf16x8_t*)(stg + (BM + r) * 64 + swz<32>(BM + r, c) * 16);
+    if constexpr (!P16) f.l[i] = *(const bf16x8_t*)(stg + (BM + r) * 64 + swz<32>(BM + r, c) * 16);
   }
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
-    const int r = 2 * BM + (wn * WN + j) * 32 + (lane & 31);
+    const int r = AP * BM + (wn * WN + j) * 32 + (lane & 31);
     f.w[j] = *(const bf16x8_t*)(stg + r * 64 + swz<32>(r, c) * 16);
   }
 }
 
-template <int WM, int WN>
+template <int WM, int WN, bool P16>
 __device__ __forceinline__ void frag_mma(const Frag<WM, WN>& f, f32x16_t (&acc)[WM][WN]) {
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < WN; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.h[i], f.w[j], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < WN; ++j) acc[i][j] = mma16<P16>(f.h[i], f.w[j], acc[i][j]);
+  if constexpr (!P16) {
 #pragma unroll
-  for (int i = 0; i < WM; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < WN; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.l[i], f.w[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < WN; ++j) acc[i][j] = mma16<false>(f.l[i], f.w[j], acc[i][j]);
+  }
 }
 
-template <int EPI, int NWM, int NWN, int WM, int WN, int NST>
+template <int EPI, int NWM, int NWN, int WM, int WN, int NST, bool P16 = false>
 __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
                                                          const int32_t* __restrict__ d_pos) {
   constexpr int BK = 32, RPG = 16;
   constexpr int BM = NWM * WM * 32, BN = NWN * WN * 32;
   constexpr int NW = NWM * NWN, NT = 64 * NW;
-  constexpr int ROWS = 2 * BM + BN, GROUPS = ROWS / RPG, GPW = GROUPS / NW;
+  constexpr int AP = P16 ? 1 : 2;
+  constexpr int ROWS = AP * BM + BN, GROUPS = ROWS / RPG, GPW = GROUPS / NW;
   static_assert(GROUPS % NW == 0, "tile / wave grid mismatch");
   constexpr int STAGE_BYTES = ROWS * 64;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
@@ -500,12 +516,12 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
     const int g = wid + NW * q;
     const int r = RPG * g + (lane >> 2), slot = lane & 3;
     const int c = swz<32>(r, slot);
-    if (r < 2 * BM) {
+    if (r < AP * BM) {
       const int ar = r < BM ? r : r - BM;
       const int row = min(m0 + ar, M - 1);  // rows past M are never stored
       src[q] = a.xs + (r < BM ? 0 : a.xs_plane) + (int64_t)row * K + c * 8;
     } else {
-      src[q] = a.w + (int64_t)(n0 + r - 2 * BM) * K + c * 8;
+      src[q] = a.w + (int64_t)(n0 + r - AP * BM) * K + c * 8;
     }
   }
 
@@ -533,14 +549,14 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
         stage_sync<(NST - 2) * GPW>();
         fill((si + NST - 1) % NST, min((kt + si + NST - 1) * BK, klast));
         const uint8_t* stg = smem + si * STAGE_BYTES;
-        frag_load<BM>(f0, stg, 0, wm, wn, lane);
-        if (kt + si > 0) frag_mma(f1, acc);  // second half of the previous slice
-        frag_load<BM>(f1, stg, 1, wm, wn, lane);
-        frag_mma(f0, acc);
+        frag_load<BM, WM, WN, P16>(f0, stg, 0, wm, wn, lane);
+        if (kt + si > 0) frag_mma<WM, WN, P16>(f1, acc);  // second half of the previous slice
+        frag_load<BM, WM, WN, P16>(f1, stg, 1, wm, wn, lane);
+        frag_mma<WM, WN, P16>(f0, acc);
       }
     }
   }
-  frag_mma(f1, acc);
+  frag_mma<WM, WN, P16>(f1, acc);
   wait_vmcnt<0>();
 
   if (a.norm) {
@@ -568,7 +584,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int rl = rb + 8 * (r >> 2) + (r & 3);
-        v[r] = a.norm ? acc[i][j][r] * sinv[rl] : acc[i][j][r];
+        const float u = P16 ? acc[i][j][r] * a.wscale : acc[i][j][r];
+        v[r] = a.norm ? u * sinv[rl] : u;
       }
       if (EPI == GV_QKV) {
         const bool vblock = cb >= (a.H + a.KH) * a.hd;  // a 32-column block never straddles
@@ -583,22 +600,15 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
             const int head = base / a.hd, j2 = (base % a.hd) >> 1;
             const int dim = (n & 1) ? j2 + a.hd / 2 : j2;
             const int b = m / a.T;
-            uint16_t hb[4], lb[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              hb[e] = f32_to_bf16_rne(v[4 * rq + e]);
-              lb[e] = f32_to_bf16_rne(v[4 * rq + e] - bf16_to_f32(hb[e]));
-            }
             uint16_t* p = a.vt + (((int64_t)b * a.KH + head) * a.hd + dim) * a.npos + pos;
-            *(uint2*)p = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
-            *(uint2*)(p + a.kv_plane) =
-                make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
+            const float w4[4] = {v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]};
+            put4<P16>(w4, p, a.kv_plane);
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float own = v[4 * rq + e];
               const float other = __shfl_xor(own, 1, 64);
-              if (m + e < M) qkv_elem_epilogue(a, m + e, pos0, n, own, other);
+              if (m + e < M) qkv_elem_epilogue<P16>(a, m + e, pos0, n, own, other);
             }
           }
         }
@@ -611,11 +621,11 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
           if (EPI == GV_RESID) {
             const float x = a.y[o] + v[r];
             a.y[o] = x;
-            split_bf16(x, a.ys + o, a.ys_plane);
+            put1<P16>(x, a.ys + o, a.ys_plane);
             ssq[r] += x * x;
           } else if (EPI == GV_RELU2) {
             const float t = v[r] < 0.f ? 0.f : v[r];
-            split_bf16(t * t, a.ys + o, a.ys_plane);
+            put1<P16>(t * t, a.ys + o, a.ys_plane);
           } else {
             __builtin_nontemporal_store(v[r], a.y + o);  // logits: read once, later
           }
@@ -637,26 +647,26 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
   }
 }
 
-template <int EPI, int NWM, int NWN, int WM, int WN, int NST>
+template <int EPI, int NWM, int NWN, int WM, int WN, int NST, bool P16>
 void launch_cfg2(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr int BM = NWM * WM * 32, BN = NWN * WN * 32;
-  constexpr size_t lds = (size_t)NST * (2 * BM + BN) * 64;
+  constexpr size_t lds = (size_t)NST * ((P16 ? 1 : 2) * BM + BN) * 64;
   static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)k_gemm2<EPI, NWM, NWN, WM, WN, NST>,
+    (void)hipFuncSetAttribute((const void*)k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr = true;
   }
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
-  FG_LAUNCH((k_gemm2<EPI, NWM, NWN, WM, WN, NST>), g, dim3(64 * NWM * NWN), lds, s, a,
+  FG_LAUNCH((k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16>), g, dim3(64 * NWM * NWN), lds, s, a,
                      d_pos);
 }
 
-template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST, int KG = 1>
+template <int EPI, int BM, int BN, int NWM, int NWN, int BK, int NST, int KG, bool P16>
 void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr bool sq_lds = EPI == GV_RESID && BN != 64 && BN != 128;
-  constexpr size_t pipe = (size_t)NST * (2 * BM + BN) * 2 * BK;
+  constexpr size_t pipe = (size_t)NST * ((P16 ? 1 : 2) * BM + BN) * 2 * BK;
   constexpr size_t epi =
       (size_t)KG * 64 * (BN + 4) * 4 + (sq_lds ? (size_t)64 * (BN / 2 + 1) * 4 : 0);
   constexpr size_t lds = pipe > epi ? pipe : epi;
@@ -664,12 +674,12 @@ void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG>,
+    (void)hipFuncSetAttribute((const void*)k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG, P16>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     attr = true;
   }
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
-  FG_LAUNCH((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG>), g, dim3(64 * NWM * NWN * KG),
+  FG_LAUNCH((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG, P16>), g, dim3(64 * NWM * NWN * KG),
                      lds, s, a, d_pos);
 }
 
@@ -789,9 +799,11 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
 // epilogue (k_gemm2) serves the plain stores of RELU2 and lm_head, with
 // 128x256 tiles (wave 64x128) when there are >= 1.5 blocks per CU.
 
-template <int EPI>
-void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
-  const int sp = a.part ? splitk_count(a.M, a.N, a.K) : 1;
+// The single-term fp16 kernels (a.f16) serve passes of more than
+// SPLITK_MAX_M rows only, so they never split K.
+template <int EPI, bool P16>
+void launch_tile_p(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  const int sp = a.part && !P16 ? splitk_count(a.M, a.N, a.K) : 1;
   if (sp > 1) {
     constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
     const dim3 g(a.N / 64, (unsigned)((a.M + 63) / 64), (unsigned)sp);
@@ -810,38 +822,46 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
     const int64_t ncu = cu_count();
     if (a.N % 192 == 0 && a.K % 64 == 0 && mt128 * (a.N / 128) > ncu &&
         mt128 * (a.N / 192) <= ncu) {
-      launch_cfg<EPI, 128, 192, 4, 2, 64, 2>(s, b, d_pos);
+      launch_cfg<EPI, 128, 192, 4, 2, 64, 2, 1, P16>(s, b, d_pos);
       return;
     }
   }
   if (a.N % 256 == 0 && ((EPI == GV_STORE && mt128 * (a.N / 256) >= 384) ||
                          (EPI == GV_RELU2 && mt128 * (a.N / 256) >= 768))) {
-    launch_cfg2<EPI, 2, 2, 2, 4, 2>(s, b, d_pos);
+    launch_cfg2<EPI, 2, 2, 2, 4, 2, P16>(s, b, d_pos);
     return;
   }
   const bool big = a.N % 128 == 0 && mt128 * (a.N / 128) >= 256;
   if (big && (EPI == GV_RELU2 || EPI == GV_STORE)) {
-    launch_cfg2<EPI, 4, 2, 1, 2, 3>(s, b, d_pos);
+    launch_cfg2<EPI, 4, 2, 1, 2, 3, P16>(s, b, d_pos);
     return;
   }
   if constexpr (EPI == GV_RESID) {
     if (resid_k4(a.M, a.N, a.K)) {
-      launch_cfg<EPI, 64, 96, 2, 1, 64, 3, 4>(s, b, d_pos);
+      launch_cfg<EPI, 64, 96, 2, 1, 64, 3, 4, P16>(s, b, d_pos);
       return;
     }
   }
   const int bn = tile_n(a.M, a.N);
   if (bn == 128 && big)
-    launch_cfg<EPI, 128, 128, 4, 2, 32, 3>(s, b, d_pos);  // 72 KB: two blocks per CU
+    launch_cfg<EPI, 128, 128, 4, 2, 32, 3, 1, P16>(s, b, d_pos);  // 72 KB: two blocks per CU
   else if (bn == 128 && EPI == GV_RESID && a.K % 64 == 0)
     // the residual GEMMs (proj, proj2) inside the layer stack: 64-wide slices
     // (half the stage hand-overs) measured ~4 us a launch faster than 32-wide
     // ones at any depth
-    launch_cfg<EPI, 64, 128, 2, 2, 64, 3>(s, b, d_pos);
+    launch_cfg<EPI, 64, 128, 2, 2, 64, 3, 1, P16>(s, b, d_pos);
   else if (bn == 128)
-    launch_cfg<EPI, 64, 128, 2, 2, 32, 4>(s, b, d_pos);
+    launch_cfg<EPI, 64, 128, 2, 2, 32, 4, 1, P16>(s, b, d_pos);
   else
-    launch_cfg<EPI, 64, 64, 2, 2, 32, 4>(s, b, d_pos);
+    launch_cfg<EPI, 64, 64, 2, 2, 32, 4, 1, P16>(s, b, d_pos);
+}
+
+template <int EPI>
+void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  if (a.f16)
+    launch_tile_p<EPI, true>(s, a, d_pos);
+  else
+    launch_tile_p<EPI, false>(s, a, d_pos);
 }
 
 }  // namespace

@@ -40,6 +40,7 @@ EXPORTS = (
 KERNEL_KINDS = {0: "gemm", 1: "gemv", 2: "attn_chunk", 3: "attn_decode", 4: "other",
                 5: "decode_fused"}
 FG_OPT_FUSED_DECODE = 1
+FG_OPT_FORWARD_F16 = 2
 
 
 FG_KV_BF16 = 1  # fg_kv_create_ex flag: bf16 K/V cache
@@ -246,6 +247,17 @@ class Model:
         buf = C.create_string_buffer(256)
         _check(_LIB.fg_get_option(self._h, FG_OPT_FUSED_DECODE, C.byref(v), buf, 256))
         return bool(v.value), buf.value.decode(errors="replace")
+
+    def set_forward_f16(self, enable: bool):
+        """FG_OPT_FORWARD_F16: forward / eval passes of more than 128 token
+        rows as single-term fp16 MFMA work (1) or in the split bf16 format
+        (0, the default). Enabling it makes the fp16 weight copy."""
+        _check(_LIB.fg_set_option(self._h, FG_OPT_FORWARD_F16, 1 if enable else 0))
+
+    def forward_f16(self) -> bool:
+        v = C.c_int32()
+        _check(_LIB.fg_get_option(self._h, FG_OPT_FORWARD_F16, C.byref(v), None, 0))
+        return bool(v.value)
 
     def eval_bpb(self, rows, token_bytes, batch: int = 8, want_nll: bool = False) -> dict:
         """fg_eval_bpb over rows (N, T+1): per-row and total byte-weighted nats

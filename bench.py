@@ -3,9 +3,12 @@
 
 One JSON line on stdout. `value` is the prefill throughput of the depth-12
 model at B=1, T=2048 (logits [2048, 8192] plus per-token cross-entropy, ids
-and targets already resident in HBM), one "step" being one full forward.
-Beside it, each with its own roofline and the profiles/ summary it
-reproduces from: the B=1 greedy decode (16-id prompt, 32 cached steps), the
+and targets already resident in HBM), one "step" being one full forward, with
+FG_OPT_FORWARD_F16 on (one fp16 MFMA per product: activations rounded once
+to fp16, weights an exact fp16 copy; logits within ~4e-4 x max|logit| of the
+fp32 forward), the split-bf16 default (2 MFMAs per product, ~5e-6) beside it
+under "split"; the B=8 eval rows likewise. Beside it, each with its own
+roofline and the profiles/ summary it reproduces from: the B=1 greedy decode (16-id prompt, 32 cached steps), the
 B=8 x 2048 Zipf eval rows, the B=64 batched decode (1024-id prompts, 512
 steps, on the bf16 KV cache the workload states, and on the fp32 cache
 beside it), the depth-20 GQA model (2048-id prefill, 256 steps), speculative and
@@ -40,7 +43,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "decode tok/s (B=1, B=64) + prefill tok/s, depth-12; % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-MFMA_BF16_PEAK_TFS = 2516.6    # 256 CU x 2.4 GHz x 4096 bf16 flop/clk, dense
+MFMA_BF16_PEAK_TFS = 2516.6    # 256 CU x 2.4 GHz x 4096 bf16 flop/clk, dense (fp16: the same)
 SEED = 1234                    # depth-12 weights
 SEED_GQA = 4321                # depth-20 GQA weights
 # executed MFMA work per algorithmic flop: the linears multiply the exact
@@ -75,7 +78,8 @@ def prefill_flops(d, B: int, T: int) -> float:
     return B * (lin + att)
 
 
-def roofline(rec, alg_total: float, bound: str, kind: str, profile: str) -> dict:
+def roofline(rec, alg_total: float, bound: str, kind: str, profile: str,
+             mfma_exec: float = None) -> dict:
     """achieved = algorithmic bytes (or flops) per launch / mean launch time,
     the launches of one kernel kind from a pass with every launch bracketed
     by HIP events on its stream (fg_timing)."""
@@ -90,8 +94,9 @@ def roofline(rec, alg_total: float, bound: str, kind: str, profile: str) -> dict
            ("alg_flop_per_launch" if bound == "mfma" else "alg_bytes_per_launch"): per_unit,
            "achieved": achieved, "peak": peak, "unit": unit, "frac": achieved / peak,
            "traffic": None, "profile": profile}
-    if kind in MFMA_EXEC:
-        out["mfma_executed_frac"] = out["frac"] * MFMA_EXEC[kind]
+    ex = mfma_exec if mfma_exec is not None else MFMA_EXEC.get(kind)
+    if ex is not None:
+        out["mfma_executed_frac"] = out["frac"] * ex
     return out
 
 
@@ -123,10 +128,20 @@ def event_time(torch, st, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def bench_forward(m, d, torch, B, T, ids, steps, warmup, profile):
+def bench_forward(m, d, torch, B, T, ids, steps, warmup, profile, f16=False):
     """Forward of B rows of T ids with per-token NLL against ids shifted by
     one, ids/targets/logits/NLL resident in HBM, timed with HIP events on the
-    stream the engine launches on; then an fg_timing pass for the kernels."""
+    stream the engine launches on; then an fg_timing pass for the kernels.
+    f16: with FG_OPT_FORWARD_F16 on (one fp16 MFMA per product instead of
+    the split format's 2 in the linears and 3 in attention)."""
+    m.set_forward_f16(f16)
+    try:
+        return _bench_forward(m, d, torch, B, T, ids, steps, warmup, profile, f16)
+    finally:
+        m.set_forward_f16(False)
+
+
+def _bench_forward(m, d, torch, B, T, ids, steps, warmup, profile, f16):
     dev = torch.device("cuda:0")
     ids = np.asarray(ids, np.int32).reshape(B, T + 1)
     d_ids = torch.from_numpy(np.ascontiguousarray(ids[:, :T])).to(dev)
@@ -141,16 +156,19 @@ def bench_forward(m, d, torch, B, T, ids, steps, warmup, profile):
     nt = min(steps, 5)
     tm = timing_pass(m, run, nt)
     g = tm["gemm"]
-    out = {"B": B, "T": T, "ms_per_step": ms, "tok_s": B * T / (ms * 1e-3),
+    ex = {"gemm": 1.0, "attn_chunk": 1.0} if f16 else MFMA_EXEC
+    out = {"B": B, "T": T, "operands": "fp16 single-term" if f16 else "bf16 hi+lo split",
+           "ms_per_step": ms, "tok_s": B * T / (ms * 1e-3),
            "alg_gflop": prefill_flops(d, B, T) / 1e9,
            "achieved_tflops_whole": prefill_flops(d, B, T) / (ms * 1e-3) / 1e12,
            "nats_per_row": nats.tolist(), "ce_bits_mean": float(nats.sum() / (B * T) / math.log(2)),
            "kernel_ms_per_step": {k: v[1] / nt for k, v in tm.items()},
            # the GEMM launches' flops are 2 M N K each: the algorithmic count
-           "roofline": roofline(g, g[2], "mfma", "gemm", profile)}
+           "roofline": roofline(g, g[2], "mfma", "gemm", profile, ex["gemm"])}
     at = tm["attn_chunk"]
     if at[0]:
-        out["roofline_attention"] = roofline(at, at[2], "mfma", "attn_chunk", profile)
+        out["roofline_attention"] = roofline(at, at[2], "mfma", "attn_chunk", profile,
+                                             ex["attn_chunk"])
     out["whole_frac"] = out["achieved_tflops_whole"] / MFMA_BF16_PEAK_TFS
     return out
 
@@ -159,8 +177,12 @@ def bench_prefill(m, d, steps, warmup, torch):
     """Depth-12 prefill, B=1, T=2048 uniform ids: logits + per-token CE."""
     from autoresearch_amd.weights import uniform_ids
     T = 2048
-    return bench_forward(m, d, torch, 1, T, uniform_ids(2, T + 1, d.vocab), steps, warmup,
-                         "profiles/prefill_d12_T2048_kernels.md")
+    ids = uniform_ids(2, T + 1, d.vocab)
+    out = bench_forward(m, d, torch, 1, T, ids, steps, warmup,
+                        "profiles/prefill_d12_T2048_kernels.md", f16=True)
+    out["split"] = bench_forward(m, d, torch, 1, T, ids, steps, warmup,
+                                 "profiles/prefill_d12_T2048_split_kernels.md")
+    return out
 
 
 def bench_eval_b8(m, d, steps, warmup, torch):
@@ -170,8 +192,11 @@ def bench_eval_b8(m, d, steps, warmup, torch):
     B, T = 8, 2048
     rows = zipf_ids(31, B * (T + 1), d.vocab).reshape(B, T + 1)
     rows[:, 0] = BOS_ID
-    return bench_forward(m, d, torch, B, T, rows, steps, warmup,
-                         "profiles/eval_d12_B8_T2048_kernels.md")
+    out = bench_forward(m, d, torch, B, T, rows, steps, warmup,
+                        "profiles/eval_d12_B8_T2048_kernels.md", f16=True)
+    out["split"] = bench_forward(m, d, torch, B, T, rows, steps, warmup,
+                                 "profiles/eval_d12_B8_T2048_split_kernels.md")
+    return out
 
 
 def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, profile, prompts=None,
@@ -383,6 +408,7 @@ def pmc_probe(workload: str = "prefill"):
         ids = uniform_ids(2, T + 1, d.vocab)
         d_ids = torch.from_numpy(ids[:T].copy()).to(dev)
         d_lg = torch.empty(T * d.vocab, dtype=torch.float32, device=dev)
+        m.set_forward_f16(True)  # the configuration the prefill line is quoted on
         for _ in range(2):
             m.forward_dev(d_ids.data_ptr(), 1, T, d_lg.data_ptr(), 0, 0, 0)
             m.sync()
@@ -589,7 +615,7 @@ def main():
     line = {
         "metric": METRIC, "value": pre["tok_s"], "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": pre["ms_per_step"],
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic (seeded N(0,0.02) bf16-exact weights, uniform / Zipf ids)",
         "config": {"workload": "depth-12 prefill, B=1, T=2048: fp32 logits [2048,8192] + "
                                "per-token CE", "global_batch": 1, "seq_len": 2048,

@@ -260,18 +260,30 @@ int32_t fg_sample(fg_model *m, const float *logits, int32_t V, const int32_t *ge
 int32_t fg_decode_sample(fg_model *m, fg_kv *kv, int32_t *ids, int32_t n_known, int32_t n_total,
                          const fg_sample_cfg *cfg, int64_t *state);
 
-/* Handle options. FG_OPT_FUSED_DECODE: 1 (the default) lets
- * fg_decode_greedy run a B=1 loop whose positions stay below 128 as ONE
- * persistent launch (all layers, lm_head and the argmax of every step; the
- * weights stream through LDS one layer ahead, activations pass between
- * workgroups through epoch-tagged slots), when the dims fit its work split
- * (head_dim 128, n_head <= 8 = n_kv_head, d_model % 32 == 0, d_ff % 512 ==
- * 0, vocab % 256 == 0) and the device has 256 CUs with workgroup b of a
- * cooperative launch on XCD b % 8; 0 keeps the captured per-kernel steps.
- * Both paths compute the same functions of the same inputs; their fp32 sums
- * run in different orders. No counterpart in the reference (it has one
- * CPU path). */
-enum { FG_OPT_FUSED_DECODE = 1 };
+/* Handle options (no counterpart in the reference, which has one CPU path).
+ *
+ * FG_OPT_FUSED_DECODE: 1 (the default) lets fg_decode_greedy run a B=1 loop
+ * on an fp32 cache whose positions stay below 128 as ONE persistent launch
+ * (all layers, lm_head and the argmax of every step; the weights stream
+ * through LDS one layer ahead, activations pass between workgroups through
+ * epoch-tagged slots), for the model shapes the library compiles it for
+ * (head_dim 128, d_ff = 4 d_model: d_model 768 with 6 heads and vocab 8192,
+ * d_model 256 with 2 heads and vocab 1024) on a device of 256 CUs in 8 XCDs
+ * that allows cooperative launches; 0 keeps the captured per-kernel steps.
+ * Both paths compute the same functions of the same inputs; their fp32
+ * sums run in different orders.
+ *
+ * FG_OPT_FORWARD_F16: 1 runs fg_forward / fg_forward_dev / fg_eval_bpb
+ * passes of more than 128 token rows as single-term fp16 MFMA work: one
+ * fp16 operand plane for the activations instead of the bf16 hi/lo pair,
+ * weights from an fp16 copy (each bf16 weight times a power of 2, exact for
+ * every weight above ~2^-31 x that scale's headroom), one MFMA per product
+ * instead of 2 (linears) or 3 (attention). Logits move by ~4e-4 x max|logit|
+ * instead of ~5e-6; passes that fill a KV cache (fg_step_multi) keep the
+ * split format. 0 (the default) is the split format everywhere. Enabling it
+ * makes the fp16 copy (the weight arena's size again) and fails with
+ * FG_EARG when the weights exceed the fp16 range. */
+enum { FG_OPT_FUSED_DECODE = 1, FG_OPT_FORWARD_F16 = 2 };
 int32_t fg_set_option(fg_model *m, int32_t key, int32_t value);
 /* *value = the option's effective value (for FG_OPT_FUSED_DECODE: 1 when
  * the persistent decode is set up and enabled); why (nullable, len bytes)
