@@ -12,6 +12,7 @@ module fgpt_c
   integer(c_int32_t), parameter, public :: FG_OK = 0, FG_EARG = -1, FG_EDIMS = -2, &
       FG_EWEIGHT = -3, FG_EHIP = -4, FG_EFULL = -5, FG_EROPE = -6, FG_ENODEV = -7, &
       FG_EBUSY = -8, FG_EARCH = -9
+  integer(c_int32_t), parameter, public :: FG_OPT_FUSED_DECODE = 1, FG_OPT_FORWARD_F16 = 2
 
   type, bind(C), public :: fg_dims
     integer(c_int32_t) :: n_layer, d_model, n_head, n_kv_head, head_dim, vocab_size
@@ -39,7 +40,7 @@ module fgpt_c
       fg_model_destroy, &
       fg_set_rope, fg_forward, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
       fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_eval_bpb, fg_rows_npy, &
-      fg_decode_spec, fg_spec_accept, fg_spec_draft, fg_sample, fg_decode_sample, &
+      fg_decode_spec, fg_spec_accept, fg_spec_draft, fg_sample, fg_decode_sample, fg_set_option, &
       fg_error_message
 
   interface
@@ -224,6 +225,12 @@ module fgpt_c
     integer(c_int32_t) function fg_sync(m) bind(C, name="fg_sync")
       import :: c_int32_t, c_ptr
       type(c_ptr), value :: m
+    end function
+
+    integer(c_int32_t) function fg_set_option(m, key, value) bind(C, name="fg_set_option")
+      import :: c_int32_t, c_ptr
+      type(c_ptr), value :: m
+      integer(c_int32_t), value :: key, value
     end function
   end interface
 

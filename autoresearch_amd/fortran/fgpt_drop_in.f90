@@ -23,6 +23,11 @@
 !    the positions being computed), as the reference uses them.
 !  - Errors stop the program with the engine's message, the reference's
 !    loud-failure convention (print + exit, or error stop).
+!  - fgpt_forward_f16(.true.) lets gpt_forward passes of more than 128 rows
+!    run as single-term fp16 MFMA work (FG_OPT_FORWARD_F16: logits within
+!    ~4e-4 x max|logit| instead of ~5e-6, ~1.4x faster at 2048 tokens) for
+!    callers whose forwards no decode follows (eval_bpb); gpt_step and
+!    gpt_step_multi are unaffected. Off unless asked for.
 module fgpt_drop_in_mod
   use, intrinsic :: iso_c_binding
   use, intrinsic :: iso_fortran_env, only: error_unit
@@ -30,7 +35,7 @@ module fgpt_drop_in_mod
   implicit none
   private
   public :: gpt_forward, gpt_step, gpt_step_multi, load_gpt_weights, fgpt_release, &
-      fgpt_handles, accept_prefix, lookup_draft, sample_next
+      fgpt_handles, accept_prefix, lookup_draft, sample_next, fgpt_forward_f16
 
   ! engine models by (weight array addresses, dims, eps) and device caches
   ! by (address of the caller's cache_k, model, B, maxT)
@@ -52,6 +57,8 @@ module fgpt_drop_in_mod
   type(c_ptr), save :: g_model = c_null_ptr
   type(c_ptr), save :: g_kv = c_null_ptr
   integer, save :: g_imodel = 0
+  ! fgpt_forward_f16: applied to every bound model and to those bound later
+  logical, save :: g_fwd_f16 = .false.
 
 contains
 
@@ -115,7 +122,27 @@ contains
     g_models(free)%eps = eps
     g_imodel = free
     g_model = g_models(free)%h
+    if (g_fwd_f16) then
+      rc = fg_set_option(g_model, FG_OPT_FORWARD_F16, 1_c_int32_t)
+      if (rc /= FG_OK) call die('fgpt: forward_f16', rc)
+    end if
   end subroutine bind_model
+
+  ! Single-term fp16 gpt_forward passes (see the header) on or off, for the
+  ! models bound now and later.
+  subroutine fgpt_forward_f16(on)
+    logical, intent(in) :: on
+    integer(c_int32_t) :: rc, v
+    integer :: i
+    g_fwd_f16 = on
+    v = merge(1_c_int32_t, 0_c_int32_t, on)
+    do i = 1, NMODELS
+      if (c_associated(g_models(i)%h)) then
+        rc = fg_set_option(g_models(i)%h, FG_OPT_FORWARD_F16, v)
+        if (rc /= FG_OK) call die('fgpt: forward_f16', rc)
+      end if
+    end do
+  end subroutine fgpt_forward_f16
 
   ! Bind the device cache of the caller's cache (its address) for the
   ! current model, B sequences of maxt positions; it becomes g_kv.

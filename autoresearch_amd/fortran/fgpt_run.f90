@@ -39,7 +39,7 @@
 !
 ! Usage:
 !   fgpt_run greedy WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [PCHUNK] [host|device]
-!   fgpt_run eval   WDIR L D H KH HD V ROWS_FILE B T OUT_FILE
+!   fgpt_run eval   WDIR L D H KH HD V ROWS_FILE B T OUT_FILE [f16]
 !   fgpt_run bpb    WDIR L D H KH HD V ROWS_NPY TOKEN_BYTES [BATCH] [NLL_OUT]
 !   fgpt_run selftest
 !   fgpt_run spec   WDIR L D H KH HD V IDS_FILE NGEN OUT_FILE [K] [MATCH] [PROBE] [MIN_ACC]
@@ -325,6 +325,8 @@ contains
     if (command_argument_count() < 12) call usage()
     wdir = sarg(2); L = iarg(3); D = iarg(4); H = iarg(5); KH = iarg(6); HD = iarg(7); V = iarg(8)
     rows_file = sarg(9); B = iarg(10); T = iarg(11); out_file = sarg(12)
+    ! f16: the single-term fp16 forward (fgpt_forward_f16), as eval_bpb may ask for it
+    if (command_argument_count() >= 13) call fgpt_forward_f16(trim(sarg(13)) == 'f16')
     call load_gpt_weights(trim(wdir), L, D, H, KH, HD, V, wte, lm, c_q, c_k, c_v, c_pr, c_fc, c_pr2)
     call read_ids(trim(rows_file), rows, n)
     if (n /= B*(T+1)) then
@@ -367,6 +369,7 @@ contains
     write (error_unit, '(A,F10.3,A,F14.1)') 'stats: forward_ms=', 1000*(t1-t0), &
         ' tok_s=', real(B*T, 8)/max(t1-t0, 1d-9)
     call fgpt_release()
+    call fgpt_forward_f16(.false.)
   end subroutine run_eval
 
   subroutine stop_rc(what, rc)

@@ -20,7 +20,7 @@ a cached position as bf16 (36 864 B per position at depth 12), 2 M N K flops
 per linear and the causal half of attention for prefill.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--skip NAME]
-                    [--only NAME] [--no-pmc]
+                    [--only NAME] [--operands both|f16|split] [--no-pmc]
 """
 from __future__ import annotations
 
@@ -173,30 +173,34 @@ def _bench_forward(m, d, torch, B, T, ids, steps, warmup, profile, f16):
     return out
 
 
-def bench_prefill(m, d, steps, warmup, torch):
-    """Depth-12 prefill, B=1, T=2048 uniform ids: logits + per-token CE."""
-    from autoresearch_amd.weights import uniform_ids
-    T = 2048
-    ids = uniform_ids(2, T + 1, d.vocab)
-    out = bench_forward(m, d, torch, 1, T, ids, steps, warmup,
-                        "profiles/prefill_d12_T2048_kernels.md", f16=True)
-    out["split"] = bench_forward(m, d, torch, 1, T, ids, steps, warmup,
-                                 "profiles/prefill_d12_T2048_split_kernels.md")
+def forward_pair(m, d, torch, B, T, ids, steps, warmup, name, operands):
+    """The fp16 single-term record with the split one under "split"
+    (operands "both"), or one of them alone ("f16", "split": profiling runs)."""
+    run = lambda f16, prof: bench_forward(m, d, torch, B, T, ids, steps, warmup, prof, f16=f16)
+    if operands == "split":
+        return run(False, f"profiles/{name}_split_kernels.md")
+    out = run(True, f"profiles/{name}_kernels.md")
+    if operands == "both":
+        out["split"] = run(False, f"profiles/{name}_split_kernels.md")
     return out
 
 
-def bench_eval_b8(m, d, steps, warmup, torch):
+def bench_prefill(m, d, steps, warmup, torch, operands="both"):
+    """Depth-12 prefill, B=1, T=2048 uniform ids: logits + per-token CE."""
+    from autoresearch_amd.weights import uniform_ids
+    T = 2048
+    return forward_pair(m, d, torch, 1, T, uniform_ids(2, T + 1, d.vocab), steps, warmup,
+                        "prefill_d12_T2048", operands)
+
+
+def bench_eval_b8(m, d, steps, warmup, torch, operands="both"):
     """bpb-style evaluation: B=8 independent rows of T=2048 Zipf(1.1) ids
     with the BOS id at position 0, summed NLL in nats per row."""
     from autoresearch_amd.weights import BOS_ID, zipf_ids
     B, T = 8, 2048
     rows = zipf_ids(31, B * (T + 1), d.vocab).reshape(B, T + 1)
     rows[:, 0] = BOS_ID
-    out = bench_forward(m, d, torch, B, T, rows, steps, warmup,
-                        "profiles/eval_d12_B8_T2048_kernels.md", f16=True)
-    out["split"] = bench_forward(m, d, torch, B, T, rows, steps, warmup,
-                                 "profiles/eval_d12_B8_T2048_split_kernels.md")
-    return out
+    return forward_pair(m, d, torch, B, T, rows, steps, warmup, "eval_d12_B8_T2048", operands)
 
 
 def bench_decode(m, d, B, prompt_len, n_steps, reps, warmup, profile, prompts=None,
@@ -420,6 +424,69 @@ def pmc_probe(workload: str = "prefill"):
     print("pmc probe done", flush=True)
 
 
+def streams_probe():
+    """Two depth-12 models' fp16 forwards (B=1, T=1024 and 2048) on one
+    stream and on two streams: does a second HIP stream overlap the engine's
+    kernels? Prints one JSON line per T (ms per pair of forwards)."""
+    import torch
+    from autoresearch_amd import engine
+    from autoresearch_amd.weights import D12, seeded_weights, rope_tables, uniform_ids
+    d = D12
+    w = seeded_weights(d, SEED)
+    c, s = rope_tables(2048, d.head_dim)
+    models = []
+    for _ in range(2):
+        m = engine.Model(d, stacks=w)
+        m.set_rope(c.reshape(-1), s.reshape(-1))
+        m.set_forward_f16(True)
+        models.append(m)
+    dev = torch.device("cuda:0")
+    st = [torch.cuda.Stream(), torch.cuda.Stream()]
+    cur = torch.cuda.current_stream()
+
+    def timed(fn, n=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        for _ in range(n):
+            fn()
+        for x in st:
+            cur.wait_stream(x)
+        e1.record(cur)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    for T in (1024, 2048):
+        ids = [torch.from_numpy(uniform_ids(2 + i, T, d.vocab).astype(np.int32)).to(dev)
+               for i in range(2)]
+        lg = [torch.empty(T * d.vocab, dtype=torch.float32, device=dev) for _ in range(2)]
+
+        def fwd(i, k):
+            models[i].forward_dev(ids[i].data_ptr(), 1, T, lg[i].data_ptr(), 0, 0, st[k].cuda_stream)
+
+        def one():
+            st[0].wait_stream(cur)
+            fwd(0, 0)
+
+        def serial():
+            st[0].wait_stream(cur)
+            fwd(0, 0)
+            fwd(1, 0)
+
+        def two_streams():
+            for x in st:
+                x.wait_stream(cur)
+            fwd(0, 0)
+            fwd(1, 1)
+
+        print(json.dumps({"T": T, "one_ms": timed(one), "two_on_one_stream_ms": timed(serial),
+                          "two_on_two_streams_ms": timed(two_streams)}), flush=True)
+    for m in models:
+        m.close()
+
+
 def pmc_counter(counter: str, launches_per_forward: int):
     """Mean `counter` (KiB per dispatch) over the dominant kind's launches of
     the probe's last forward, and the reading for the calibration copy."""
@@ -541,14 +608,21 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--skip", action="append", default=[], choices=WORKLOADS,
                     help="leave a workload out of the full run")
+    ap.add_argument("--operands", choices=("both", "f16", "split"), default="both",
+                    help="prefill / eval_b8: the fp16 single-term pass, the split one, or both")
     ap.add_argument("--only", choices=WORKLOADS,
                     help="run one workload and print its record (for profiling runs)")
     ap.add_argument("--no-pmc", action="store_true", help="skip the PMC traffic runs")
     ap.add_argument("--pmc-probe", nargs="?", const="prefill", choices=("prefill", "decode_b1"),
                     help=argparse.SUPPRESS)
+    ap.add_argument("--streams-probe", action="store_true",
+                    help="time two models' forwards on one stream and on two streams")
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe(args.pmc_probe)
+        return
+    if args.streams_probe:
+        streams_probe()
         return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "
@@ -575,11 +649,11 @@ def main():
     m.set_rope(c.reshape(-1), s.reshape(-1))
 
     runs = {
-        "prefill": lambda: bench_prefill(m, d, args.steps, args.warmup, torch),
+        "prefill": lambda: bench_prefill(m, d, args.steps, args.warmup, torch, args.operands),
         "decode_b1": lambda: bench_decode(m, d, 1, 16, 32, reps=max(args.steps, 5),
                                           warmup=args.warmup,
                                           profile="profiles/decode_d12_B1_fused.md"),
-        "eval_b8": lambda: bench_eval_b8(m, d, max(3, args.steps // 4), 1, torch),
+        "eval_b8": lambda: bench_eval_b8(m, d, max(3, args.steps // 4), 1, torch, args.operands),
         "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0,
                                            profile="profiles/decode_d12_B64_kernels.md",
                                            kv_bf16=True),

@@ -131,6 +131,33 @@ def test_fortran_eval_rows(tmp_path):
 
 
 @pytest.mark.gpu
+def test_fortran_eval_rows_f16(tmp_path):
+    """fgpt_forward_f16(.true.): the same rows through single-term fp16
+    gpt_forward passes (288 rows), within the contract's bar."""
+    d = SMALL
+    w = seeded_weights(d, 22)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=128)
+    B, T = 3, 96
+    rows = zipf_ids(5, B * (T + 1), d.vocab).reshape(B, T + 1)
+    rows[:, 0] = BOS_ID % d.vocab
+    np.savetxt(tmp_path / "rows.txt", rows.reshape(-1), fmt="%d")
+    args = ["eval", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"), str(B), str(T)]
+    r = run(args + [str(tmp_path / "nll16.txt"), "f16"])
+    print(r.stderr)
+    assert r.returncode == 0
+    r32 = run(args + [str(tmp_path / "nll.txt")])
+    assert r32.returncode == 0
+    got, split = np.loadtxt(tmp_path / "nll16.txt"), np.loadtxt(tmp_path / "nll.txt")
+    c, s = O.rope_tables(T, d.head_dim)
+    for b in range(B):
+        lg = O.gpt_forward(rows[b, :T], c, s, w, d, 1, T)
+        ref = float(O.nll(lg.reshape(T, -1), rows[b, 1:], d.vocab).astype(np.float64).sum())
+        assert abs(got[b] - ref) < 2 * 2e-3 * np.abs(lg).max() * T
+        assert abs(got[b] - ref) < 1e-3 * T
+    assert not np.array_equal(got, split)  # the option reached the engine
+
+
+@pytest.mark.gpu
 def test_fortran_arch_mismatch_stops(tmp_path):
     d = SMALL
     w = seeded_weights(d, 23)
