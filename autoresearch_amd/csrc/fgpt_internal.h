@@ -181,6 +181,8 @@ int64_t gemm_splitk_floats(int64_t M, int N, int K);
 // their partial results go through `scratch` (attn_scratch_floats floats)
 // and a merge kernel on the same stream.
 int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0);
+// Compute units of the current device (cached per device).
+int cu_count();
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
                       int64_t kv_plane, float* scratch, float* y, uint16_t* ys = nullptr,

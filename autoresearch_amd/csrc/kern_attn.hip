@@ -16,8 +16,11 @@
 // passes; the result differs from it only by rounding.
 //
 // Work split: a workgroup (8 wavefronts: 4 query groups x 2 key parities)
-// takes 128 queries against one chunk of at most 512 keys, so a T=2048
-// prefill gives ~40 items per head instead of 16 uneven query blocks. K and
+// takes 128 queries against one chunk of at most ck keys, so a T=2048
+// prefill gives ~40 items per head instead of 16 uneven query blocks at
+// ck = 512. ck is chosen per launch (attn_chunk_keys): the longest chunk
+// that still leaves two items per CU, since splitting costs the merge
+// (B=1 T=2048: 512; eight such rows: no split). K and
 // V^T tiles (64 keys per step) stream memory -> LDS by global_load_lds into
 // two XOR-swizzled buffers, the next step loading while the current one is
 // consumed. When a query block spans several chunks, each item leaves its
@@ -45,7 +48,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 namespace {
 
 constexpr int QB = 128;  // queries per workgroup (4 groups of 32 MFMA columns)
-constexpr int CK = 512;  // keys per work item
+constexpr int CK_MIN = 512;  // shortest key chunk of a work item (sizes the scratch)
 constexpr int SK = 64;   // keys per pipeline step (two 32-key tiles)
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -57,6 +60,7 @@ struct AttnArgs {
   int nbh;  // B * H
   int nqb;  // query blocks per (sequence, head)
   int iph;  // work items per (sequence, head)
+  int ck;   // keys per chunk (a multiple of CK_MIN)
   int64_t q_plane, kv_plane;
   float* y;
   uint16_t* ys;
@@ -65,10 +69,10 @@ struct AttnArgs {
 };
 
 // key chunks of query block j (queries j*QB .. j*QB+QB-1)
-__host__ __device__ inline int chunk_count(int j, int T, int pos0, int nvalid) {
+__host__ __device__ inline int chunk_count(int j, int T, int pos0, int nvalid, int ck) {
   const int tl = (j + 1) * QB < T ? (j + 1) * QB : T;
   const int kend = nvalid < pos0 + tl ? nvalid : pos0 + tl;
-  return (kend + CK - 1) / CK;
+  return (kend + ck - 1) / ck;
 }
 
 // key offset held by row i of a 32-key tile: bits 2 and 3 swapped
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
   const int bh = blockIdx.x % p.nbh;
   int it = blockIdx.x / p.nbh, j = p.nqb - 1, base = 0, nch;
   for (;;) {
-    nch = chunk_count(j, p.T, p.pos0, p.nvalid);
+    nch = chunk_count(j, p.T, p.pos0, p.nvalid, p.ck);
     if (it < nch) break;
     it -= nch;
     base += nch;
@@ -136,7 +140,7 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
   const int64_t bk = (int64_t)b * p.KH + kvh;
   const int tq0 = j * QB;
   const int kend = min(p.nvalid, p.pos0 + min(tq0 + QB, p.T));
-  const int kbeg = c * CK, kstop = min(kend, kbeg + CK);
+  const int kbeg = c * p.ck, kstop = min(kend, kbeg + p.ck);
   const int nsteps = (kstop - kbeg + SK - 1) / SK;
 
   const int t = tq0 + qg * 32 + qi;  // this lane's query (column)
@@ -354,10 +358,10 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
   constexpr int PSTR = QB * (HD + 2), D4 = HD / 4;
   const int bh = blockIdx.x % p.nbh, rest = blockIdx.x / p.nbh;
   const int j = p.nqb - 1 - rest / 4, quarter = rest % 4;  // heaviest blocks first
-  const int nch = chunk_count(j, p.T, p.pos0, p.nvalid);
+  const int nch = chunk_count(j, p.T, p.pos0, p.nvalid, p.ck);
   if (nch == 1) return;  // written by the attention kernel itself
   int base = 0;
-  for (int i = p.nqb - 1; i > j; --i) base += chunk_count(i, p.T, p.pos0, p.nvalid);
+  for (int i = p.nqb - 1; i > j; --i) base += chunk_count(i, p.T, p.pos0, p.nvalid, p.ck);
   const int b = bh / p.H, h = bh % p.H;
   const int64_t yrow = (int64_t)p.H * HD;
   const float* P0 = p.part + ((int64_t)bh * p.iph + base) * PSTR;
@@ -435,15 +439,30 @@ __global__ __launch_bounds__(256) void k_split_cache(const KT* __restrict__ kc,
 
 }  // namespace
 
-int attn_items_per_head(int T, int pos0) {
+int attn_items_per_head(int T, int pos0, int ck) {
   const int nqb = (T + QB - 1) / QB, nvalid = pos0 + T;
   int n = 0;
-  for (int j = 0; j < nqb; ++j) n += chunk_count(j, T, pos0, nvalid);
+  for (int j = 0; j < nqb; ++j) n += chunk_count(j, T, pos0, nvalid, ck);
   return n;
 }
 
+// Keys per chunk: the longest of 512, 1024, 2048, ... (the last one covering
+// every key, no split) whose items still number at least two per CU, else
+// 512. A split query block costs its partials' round trip through memory and
+// the merge; fewer, longer items cost nothing while every CU still has two.
+int attn_chunk_keys(int BH, int T, int pos0) {
+  const int64_t want = 2 * (int64_t)cu_count();
+  int best = CK_MIN;
+  for (int ck = CK_MIN;; ck *= 2) {
+    if ((int64_t)BH * attn_items_per_head(T, pos0, ck) >= want) best = ck;
+    if (ck >= pos0 + T) break;
+  }
+  return best;
+}
+
 int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0) {
-  return (int64_t)B * d.H * attn_items_per_head(T, pos0) * QB * (d.hd + 2);
+  // sized for the shortest chunks (the most items)
+  return (int64_t)B * d.H * attn_items_per_head(T, pos0, CK_MIN) * QB * (d.hd + 2);
 }
 
 // LDS of a chunk attention launch: two stages, or the key-parity merge
@@ -484,7 +503,8 @@ void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const ui
   p.pos0 = pos0;
   p.nbh = B * d.H;
   p.nqb = (T + QB - 1) / QB;
-  p.iph = attn_items_per_head(T, pos0);
+  p.ck = attn_chunk_keys(p.nbh, T, pos0);
+  p.iph = attn_items_per_head(T, pos0, p.ck);
   p.q_plane = q_plane;
   p.kv_plane = kv_plane;
   p.y = y;

@@ -683,21 +683,6 @@ void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
                      lds, s, a, d_pos);
 }
 
-// Compute units of the current device (tile counts are weighed against it).
-int cu_count() {
-  static int n[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (n[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        v <= 0)
-      v = 256;
-    n[dev] = v;
-  }
-  return n[dev];
-}
-
 // 128 wide while that still leaves half the CUs a block (the wider tile
 // reads the A panel half as often), else 64 wide
 int tile_n(int64_t M, int N) {
@@ -803,6 +788,17 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
 // SPLITK_MAX_M rows only, so they never split K.
 template <int EPI, bool P16>
 void launch_tile_p(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
+  if constexpr (P16 && (EPI == GV_RELU2 || EPI == GV_STORE)) {
+    // single-term fc and lm_head over more than 4096 rows: 256x256 tiles (8
+    // wavefronts of 128x64; one fp16 A plane leaves room for them), 4 % of
+    // the GEMM time faster than 128x256 over 8 x 2048 rows in the layer stack
+    if (a.M > 4096 && a.N % 256 == 0) {
+      GemvArgs b = a;
+      b.part = nullptr;
+      launch_cfg2<EPI, 2, 4, 4, 2, 3, P16>(s, b, d_pos);
+      return;
+    }
+  }
   const int sp = a.part && !P16 ? splitk_count(a.M, a.N, a.K) : 1;
   if (sp > 1) {
     constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
@@ -865,6 +861,21 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 }
 
 }  // namespace
+
+// Compute units of the current device (tile counts are weighed against it).
+int cu_count() {
+  static int n[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (n[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    n[dev] = v;
+  }
+  return n[dev];
+}
 
 // RESID on k_gemm: one sum-of-squares partial per row and N tile; split-K
 // RESID (given split-K scratch): one per row and 512 columns.
