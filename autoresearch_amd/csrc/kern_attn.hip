@@ -352,26 +352,31 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
 
 // Query blocks that span several key chunks: combine the chunks' partial
 // (O, max, sum) in chunk order. One workgroup per (sequence*head, block,
-// 32-query quarter); a thread owns 4 dims of 4 queries.
+// group of 1024/HD queries); a thread owns 4 dims of one query. Up to 8 chunks
+// (keys < 4096 at 512 a chunk) take one round trip: every chunk's (max,
+// sum) and O are loaded at once, the maximum is taken over the loaded
+// values, then the weighted sums; longer blocks take the maximum in a pass
+// of its own first. The arithmetic is the same either way.
+template <int HD>
+constexpr int merge_queries() { return 1024 / HD; }  // per workgroup: 256 threads x 4 dims
+
 template <int HD, bool P16>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
-  constexpr int PSTR = QB * (HD + 2), D4 = HD / 4;
+  constexpr int PSTR = QB * (HD + 2), D4 = HD / 4, MQ = merge_queries<HD>();
+  static_assert(MQ * D4 == 256 && QB % MQ == 0, "one item per thread");
   const int bh = blockIdx.x % p.nbh, rest = blockIdx.x / p.nbh;
-  const int j = p.nqb - 1 - rest / 4, quarter = rest % 4;  // heaviest blocks first
+  const int j = p.nqb - 1 - rest / (QB / MQ), part = rest % (QB / MQ);  // heaviest blocks first
   const int nch = chunk_count(j, p.T, p.pos0, p.nvalid, p.ck);
   if (nch == 1) return;  // written by the attention kernel itself
+  const int q = part * MQ + threadIdx.x / D4, d = 4 * (threadIdx.x % D4), tt = j * QB + q;
+  if (tt >= p.T) return;
   int base = 0;
   for (int i = p.nqb - 1; i > j; --i) base += chunk_count(i, p.T, p.pos0, p.nvalid, p.ck);
   const int b = bh / p.H, h = bh % p.H;
   const int64_t yrow = (int64_t)p.H * HD;
   const float* P0 = p.part + ((int64_t)bh * p.iph + base) * PSTR;
-  // chunks are read 8 at a time, all loads of a group in flight together
-#pragma unroll
-  for (int u = 0; u < 32 * D4 / 256; ++u) {
-    const int e = threadIdx.x + 256 * u;
-    const int q = quarter * 32 + e / D4, d = 4 * (e % D4), tt = j * QB + q;
-    if (tt >= p.T) continue;
-    float m = -FLT_MAX;
+  float m = -FLT_MAX;
+  if (nch > 8) {
     for (int k0 = 0; k0 < nch; k0 += 8) {
       float mk[8];
 #pragma unroll
@@ -380,32 +385,36 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnArgs p) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) m = fmaxf(m, mk[k]);
     }
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    float l = 0.f;
-    for (int k0 = 0; k0 < nch; k0 += 8) {
-      float2 ml[8];
-      float4 ov[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const bool ok = k0 + k < nch;
-        ml[k] = ok ? *(const float2*)(P0 + (k0 + k) * PSTR + QB * HD + 2 * q) : make_float2(-FLT_MAX, 0.f);
-        ov[k] = ok ? *(const float4*)(P0 + (k0 + k) * PSTR + q * HD + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (k0 + k >= nch) break;
-        const float w = exp2f(ml[k].x - m);
-        l += w * ml[k].y;
-        acc.x += w * ov[k].x;
-        acc.y += w * ov[k].y;
-        acc.z += w * ov[k].z;
-        acc.w += w * ov[k].w;
-      }
-    }
-    const float inv = 1.0f / l;
-    const float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
-    store_out<HD, P16>(p, ((int64_t)b * p.T + tt) * yrow + h * HD, d, v);
   }
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float l = 0.f;
+  for (int k0 = 0; k0 < nch; k0 += 8) {
+    float2 ml[8];
+    float4 ov[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool ok = k0 + k < nch;
+      ml[k] = ok ? *(const float2*)(P0 + (k0 + k) * PSTR + QB * HD + 2 * q) : make_float2(-FLT_MAX, 0.f);
+      ov[k] = ok ? *(const float4*)(P0 + (k0 + k) * PSTR + q * HD + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (nch <= 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m = fmaxf(m, ml[k].x);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      if (k0 + k >= nch) break;
+      const float w = exp2f(ml[k].x - m);
+      l += w * ml[k].y;
+      acc.x += w * ov[k].x;
+      acc.y += w * ov[k].y;
+      acc.z += w * ov[k].z;
+      acc.w += w * ov[k].w;
+    }
+  }
+  const float inv = 1.0f / l;
+  const float v[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+  store_out<HD, P16>(p, ((int64_t)b * p.T + tt) * yrow + h * HD, d, v);
 }
 
 // Cache positions [0, n) of one layer, [B][maxT][KH*hd] -> hi/lo planes
@@ -475,7 +484,7 @@ constexpr int attn_lds() {
 }
 
 template <int HD, bool P16>
-void launch_attn_hd(hipStream_t s, const AttnArgs& p, dim3 grid, dim3 mgrid, bool split) {
+void launch_attn_hd(hipStream_t s, const AttnArgs& p, dim3 grid, bool split) {
   constexpr int lds = attn_lds<HD, P16>();
   static bool lds_set = false;
   if (!lds_set) {
@@ -484,6 +493,7 @@ void launch_attn_hd(hipStream_t s, const AttnArgs& p, dim3 grid, dim3 mgrid, boo
     lds_set = true;
   }
   FG_LAUNCH((k_attn_mfma<HD, P16>), grid, dim3(512), lds, s, p);
+  const dim3 mgrid((unsigned)(p.nbh * p.nqb * (QB / merge_queries<HD>())));
   if (split) FG_LAUNCH((k_attn_merge<HD, P16>), mgrid, dim3(256), 0, s, p);
 }
 
@@ -513,13 +523,12 @@ void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const ui
   p.part = scratch;
   const dim3 grid((unsigned)(p.nbh * p.iph));
   const bool split = p.iph > p.nqb;  // some query block spans several chunks
-  const dim3 mgrid((unsigned)(p.nbh * p.nqb * 4));
   if (d.hd == 128) {
-    if (f16) launch_attn_hd<128, true>(s, p, grid, mgrid, split);
-    else launch_attn_hd<128, false>(s, p, grid, mgrid, split);
+    if (f16) launch_attn_hd<128, true>(s, p, grid, split);
+    else launch_attn_hd<128, false>(s, p, grid, split);
   } else {
-    if (f16) launch_attn_hd<64, true>(s, p, grid, mgrid, split);
-    else launch_attn_hd<64, false>(s, p, grid, mgrid, split);
+    if (f16) launch_attn_hd<64, true>(s, p, grid, split);
+    else launch_attn_hd<64, false>(s, p, grid, split);
   }
 }
 
