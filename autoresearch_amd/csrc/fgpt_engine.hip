@@ -350,7 +350,7 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
 void free_work(fg_model* m) {
   Work& ws = m->ws;
   void* ptrs[] = {ws.x, ws.q, ws.ao, ws.h, ws.logits, ws.ids, ws.tgt, ws.nll, ws.stat, ws.amax,
-                  ws.xs, ws.aos, ws.hs, ws.ssq, ws.part, m->qs};
+                  ws.xs, ws.aos, ws.hs, ws.ssq, ws.part, ws.nllp, m->qs};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   ws = Work();
@@ -385,6 +385,7 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
   RCCHK(alloc((void**)&ws.aos, rows * d.qd() * 2 * 2));
   RCCHK(alloc((void**)&ws.hs, rows * d.dff * 2 * 2));
   RCCHK(alloc((void**)&ws.ssq, rows * (d.D / 64) * 4));
+  if (d.V % 256 == 0) RCCHK(alloc((void**)&ws.nllp, rows * (d.V / 64) * 2 * 4));
   // split-K partials of the small-M GEMMs: the largest any row count up to
   // `rows` needs over the five GEMM shapes
   int64_t part = 0;
@@ -475,6 +476,7 @@ struct PassOpts {
   const int32_t* d_rows = nullptr;  // rows_single: rows live, read on the device
   bool kv16 = false;      // the cache holds bf16 elements
   bool f16 = false;       // single-term fp16 MFMA pass where the MFMA path runs (> 128 rows)
+  float* nll_part = nullptr;  // lm_head writes the cross-entropy's partials here (GEMM path)
 };
 
 // One pass over rows = B*T token rows: embedding of ids, the layer stack,
@@ -590,6 +592,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   a.f16 = f16 ? 1 : 0;
   a.wscale = m->w16_inv;
   a.w = W(m->w.lm); a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
+  a.nll_part = gm ? o.nll_part : nullptr;
   linear(m, s, GV_STORE, a, d_pos, gm);
 }
 
@@ -613,8 +616,17 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   const double vb = (double)rows * m->d.V * 4;
   PassOpts o;
   o.f16 = m->fwd_f16;
+  // the cross-entropy from lm_head's log-sum-exp partials where the GEMM
+  // writes them (no second pass over the logits), else from the logits
+  const bool nll_parts = d_tgt && d_nll && m->ws.nllp && use_gemm(m->d, rows) &&
+                         gemm_store_nll(rows, m->d.V);
+  if (nll_parts) o.nll_part = m->ws.nllp;
   layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, nullptr, logits, o);
-  if (d_tgt && d_nll)
+  if (nll_parts)
+    timed(m, s, FG_K_OTHER, 0, (double)rows * (m->d.V / 64) * 8 + rows * 12, [&] {
+      launch_nll_parts(s, logits, m->ws.nllp, d_tgt, rows, m->d.V, d_nll);
+    });
+  else if (d_tgt && d_nll)
     timed(m, s, FG_K_OTHER, 0, vb, [&] { launch_nll(s, logits, d_tgt, rows, m->d.V, d_nll); });
   HIPCHK(hipGetLastError());
   return FG_OK;

@@ -122,6 +122,20 @@ __device__ __forceinline__ float half_sum(float v) {
   return (threadIdx.x & 32) ? c + d : a + b;
 }
 
+// Maximum across each half-wavefront, in half_sum's pattern.
+__device__ __forceinline__ float half_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  const int iv = __builtin_bit_cast(int, v);
+  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+  return (threadIdx.x & 32) ? fmaxf(c, d) : fmaxf(a, b);
+}
+
 // Maximum across the 64 lanes, in wave_sum's pattern.
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));

@@ -950,6 +950,37 @@ __global__ __launch_bounds__(256) void k_nll(const float* __restrict__ logits,
   if (threadIdx.x == 0) out[row] = (t >= 0 && t < V) ? (m + logf(s)) - l[t] : __builtin_nanf("");
 }
 
+// The per-row nll of src/app/eval_bpb.f90:165-181 from lm_head's
+// log-sum-exp partials (one (max, sum of exp(logit - max)) per 64-column
+// group, written by the GEMM's epilogue): one wavefront per row, the row
+// maximum and the rescaled sums reduced in a fixed order.
+__global__ __launch_bounds__(256) void k_nll_parts(const float* __restrict__ logits,
+                                                   const float* __restrict__ parts,
+                                                   const int32_t* __restrict__ tgt, int64_t rows,
+                                                   int V, float* __restrict__ out) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // (whole wavefronts)
+  const int lane = threadIdx.x & 63, ng = V / 64;
+  const float2* P = reinterpret_cast<const float2*>(parts) + row * ng;
+  float m = -FLT_MAX;
+  for (int g = lane; g < ng; g += 64) m = fmaxf(m, P[g].x);
+  m = wave_max(m);
+  float sum = 0.f;
+  for (int g = lane; g < ng; g += 64) sum += P[g].y * expf(P[g].x - m);
+  sum = wave_sum(sum);
+  if (lane == 0) {
+    const int t = tgt[row];
+    out[row] = (t >= 0 && t < V) ? (m + logf(sum)) - logits[row * V + t] : __builtin_nanf("");
+  }
+}
+
+void launch_nll_parts(hipStream_t s, const float* logits, const float* parts, const int32_t* tgt,
+                      int64_t rows, int V, float* out) {
+  if (rows <= 0) return;
+  FG_LAUNCH(k_nll_parts, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, logits, parts, tgt,
+            rows, V, out);
+}
+
 // Byte-weighted sums of one eval row (scripts/eval_driver.py:174-190,
 // src/app/bpb_agg.f90:130-152): nats = sum of nll[t] over positions whose
 // target has a nonzero byte length, bytes = sum of those lengths. One block

@@ -632,6 +632,33 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
         }
       }
     }
+    if constexpr (EPI == GV_STORE) {
+      if (a.nll_part) {
+        // the cross-entropy's log-sum-exp, per row and 64-column group
+        // (blocks 2q and 2q+1 of this wavefront): the group maximum over
+        // the half-wavefront's 32 lanes, then the sum of exp(v - max); the
+        // values are the logits just stored, bit for bit
+        static_assert(WN % 2 == 0, "64-column groups");
+        const int ng = a.N / 64;
+#pragma unroll
+        for (int q = 0; q < WN / 2; ++q) {
+          const int grp = (n0 + (wn * WN + 2 * q) * 32) / 64;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rl = rb + 8 * (r >> 2) + (r & 3);
+            const float u0 = P16 ? acc[i][2 * q][r] * a.wscale : acc[i][2 * q][r];
+            const float u1 = P16 ? acc[i][2 * q + 1][r] * a.wscale : acc[i][2 * q + 1][r];
+            const float v0 = a.norm ? u0 * sinv[rl] : u0, v1 = a.norm ? u1 * sinv[rl] : u1;
+            const float mx = half_max(fmaxf(v0, v1));
+            const float sm = half_sum(expf(v0 - mx) + expf(v1 - mx));
+            const int m = m0 + rl;
+            if (cl == 0 && m < M)
+              *reinterpret_cast<float2*>(a.nll_part + ((int64_t)m * ng + grp) * 2) =
+                  make_float2(mx, sm);
+          }
+        }
+      }
+    }
     if (EPI == GV_RESID) {
       // per-row partial over this wavefront's WN*32 columns
       const int nparts = a.N / (WN * 32), part = (n0 + wn * WN * 32) / (WN * 32);
@@ -799,6 +826,16 @@ void launch_tile_p(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
       return;
     }
   }
+  if constexpr (EPI == GV_STORE) {
+    // lm_head with the cross-entropy's partials: a register-epilogue tiling
+    // (the only one that writes them; gemm_store_nll guarantees the shape)
+    if (a.nll_part) {
+      GemvArgs b = a;
+      b.part = nullptr;
+      launch_cfg2<EPI, 2, 2, 2, 4, 2, P16>(s, b, d_pos);
+      return;
+    }
+  }
   const int sp = a.part && !P16 ? splitk_count(a.M, a.N, a.K) : 1;
   if (sp > 1) {
     constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
@@ -884,6 +921,10 @@ int cu_count() {
 
 // RESID on k_gemm: one sum-of-squares partial per row and N tile; split-K
 // RESID (given split-K scratch): one per row and 512 columns.
+// (up to 4096 rows: beyond, the 256x256 tiles hold 64 rows a lane, and the
+// partials' reductions in the epilogue cost more than a pass over the logits)
+bool gemm_store_nll(int64_t M, int N) { return M > SPLITK_MAX_M && M <= 4096 && N % 256 == 0; }
+
 int gemm_ssq_parts(int64_t M, int N, int K) {
   if (splitk_count(M, N, K) == 1 && resid_k4(M, N, K)) return N / 96;
   return splitk_count(M, N, K) > 1 ? (N + RED_COLS - 1) / RED_COLS : N / tile_n(M, N);
