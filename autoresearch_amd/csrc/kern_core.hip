@@ -297,6 +297,7 @@ struct DecArgs {
   const void* kc;  // [B][maxT][KH*hd], fp32 or bf16
   const void* vc;
   int H, KH, maxT, nchunk;
+  int iters;             // DPC-position blocks per workgroup (k_attn_dec_loop), else 1
   const int32_t* d_len;  // cache length before the step (first query at *d_len), or null
   int len_imm;           // cache length including the first query, if d_len is null
   int qpr;               // query rows per sequence: row j sees one position more than j-1
@@ -474,6 +475,152 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
   }
 }
 
+// k_attn_dec over a.iters consecutive blocks of DPC positions per
+// workgroup, for batches with rows x KV heads enough to fill the chip
+// without splitting the positions finely (at B=64 one workgroup takes a
+// whole sequence and head, and no merge follows). Each wavefront keeps an
+// online softmax of its own positions across the blocks (running maximum,
+// sum and O, rescaled when the maximum moves); the four wavefronts' results
+// meet at the end, each rescaled to the workgroup maximum, and leave as
+// k_attn_dec's do (the output, or a partial for k_attn_dec_merge). While a
+// block's scores are formed its V rows load, and the next block's K rows
+// load while its V rows are weighed.
+template <int HD, int DPC, int GH, class KT>
+__global__ __launch_bounds__(256) void k_attn_dec_loop(DecArgs a) {
+  constexpr int LPP = HD / 8;        // lanes per cached row
+  constexpr int PPW = 64 / LPP;      // rows per wavefront load
+  constexpr int IT = DPC / 4 / PPW;  // loads per lane and tensor per block
+  static_assert(LPP == 8 || LPP == 16, "head dim 64 or 128");
+  __shared__ float red[3][4][GH];
+  __shared__ float so[4 * PPW][GH][HD];
+  const int G = a.H / a.KH, ng = G / GH;
+  const int gi = blockIdx.x, c = blockIdx.y;
+  const int row = gi / (a.KH * ng), kvh = (gi / ng) % a.KH, h0 = kvh * G + (gi % ng) * GH;
+  if (a.d_rows && row >= *a.d_rows) return;
+  const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + row % a.qpr;
+  const int span = DPC * a.iters;
+  const int p0 = c * span;
+  if (p0 >= len) return;
+  const int nch = (len + span - 1) / span;
+  const int nblk = min(a.iters, (len - p0 + DPC - 1) / DPC);  // blocks with positions < len
+  const int b = row / a.qpr;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int sub = lane / LPP, dl = lane % LPP;
+  const int64_t kd = (int64_t)a.KH * HD;
+  const KT* K = (const KT*)a.kc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
+  const KT* V = (const KT*)a.vc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
+  auto pos = [&](int blk, int i) { return p0 + blk * DPC + wv * (DPC / 4) + i * PPW + sub; };
+  Row8<KT> kr[IT], vr[IT];
+#pragma unroll
+  for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(0, i), len - 1) * kd);
+  float qv[GH][8];
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    const float* qp = a.q + ((int64_t)row * a.H + h0 + j) * HD + 8 * dl;
+    const float4 u = *(const float4*)qp, w = *(const float4*)(qp + 4);
+    qv[j][0] = u.x; qv[j][1] = u.y; qv[j][2] = u.z; qv[j][3] = u.w;
+    qv[j][4] = w.x; qv[j][5] = w.y; qv[j][6] = w.z; qv[j][7] = w.w;
+  }
+  const float scale = 1.0f / sqrtf((float)HD);
+  float m[GH], l[GH], o[GH][8];
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    m[j] = -FLT_MAX;
+    l[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[j][e] = 0.f;
+  }
+  for (int blk = 0; blk < nblk; ++blk) {
+#pragma unroll
+    for (int i = 0; i < IT; ++i) vr[i].load(V + min(pos(blk, i), len - 1) * kd);
+    float sc[GH][IT], mx[GH];
+#pragma unroll
+    for (int j = 0; j < GH; ++j) mx[j] = -FLT_MAX;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      float x[8];
+      kr[i].get(x);
+      const int p = pos(blk, i);
+#pragma unroll
+      for (int j = 0; j < GH; ++j) {
+        float v = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v += qv[j][e] * x[e];
+        v = row_sum<LPP>(v);
+        sc[j][i] = p < len ? v * scale : -INFINITY;
+        mx[j] = fmaxf(mx[j], sc[j][i]);
+      }
+    }
+    if (blk + 1 < nblk) {
+#pragma unroll
+      for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(blk + 1, i), len - 1) * kd);
+    }
+#pragma unroll
+    for (int j = 0; j < GH; ++j) {
+      const float mn = fmaxf(m[j], wave_max(mx[j]));  // (finite: block 0 of a chunk has p0 < len)
+      const float alpha = expf(m[j] - mn);
+      m[j] = mn;
+      l[j] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[j][e] *= alpha;
+    }
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      float x[8];
+      vr[i].get(x);
+#pragma unroll
+      for (int j = 0; j < GH; ++j) {
+        const float w = expf(sc[j][i] - m[j]);
+        l[j] += w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[j][e] += w * x[e];
+      }
+    }
+  }
+  // the four wavefronts' maxima, then each wavefront's O and row sums
+  // rescaled to the workgroup's
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < GH; ++j) red[0][wv][j] = m[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < GH; ++j) {
+    const float mw = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
+    const float f = expf(m[j] - mw);
+    float4* dst = (float4*)&so[wv * PPW + sub][j][8 * dl];
+    dst[0] = make_float4(o[j][0] * f, o[j][1] * f, o[j][2] * f, o[j][3] * f);
+    dst[1] = make_float4(o[j][4] * f, o[j][5] * f, o[j][6] * f, o[j][7] * f);
+    const int iv = __builtin_bit_cast(int, l[j]);
+    float t = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+#pragma unroll
+    for (int r = 1; r < PPW; ++r)
+      t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, r * LPP));
+    if (lane == 0) red[1][wv][j] = t * f;
+    if (lane == 0) red[2][wv][j] = mw;
+  }
+  __syncthreads();
+  for (int q4 = tid; q4 < GH * HD / 4; q4 += 256) {
+    const int j = q4 / (HD / 4), d = 4 * (q4 % (HD / 4));
+    float4 t = *(const float4*)&so[0][j][d];
+#pragma unroll
+    for (int r = 1; r < 4 * PPW; ++r) {
+      const float4 u = *(const float4*)&so[r][j][d];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    const float lj = (red[1][0][j] + red[1][1][j]) + (red[1][2][j] + red[1][3][j]);
+    const int64_t bh = (int64_t)row * a.H + h0 + j;
+    if (nch == 1) {
+      const float inv = 1.0f / lj;
+      dec_store<HD>(a, bh * HD, d, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
+    } else {
+      float* P = a.part + (bh * a.nchunk + c) * (HD + 2);
+      *(float4*)(P + d) = t;
+      if (d == 0) *(float2*)(P + HD) = make_float2(red[2][0][j], lj);
+    }
+  }
+}
+
 // Combine the chunks of a multi-chunk step: the maximum over chunks, then
 // 256/(hd/8) chunk groups (group g takes chunks g, g + NG, ..., ascending)
 // whose weighted partial sums are added in group order. Every chunk's loads
@@ -565,6 +712,13 @@ template <int HD, int DPC, class KT>
 void launch_dec_gh(hipStream_t s, const DecArgs& a, int rows, int gh) {
   const int ng = a.H / a.KH / gh;
   const dim3 grid((unsigned)(rows * a.KH * ng), (unsigned)a.nchunk);
+  if (a.iters > 1) {  // (DPC 128 only: dec_group's options for it)
+    if (gh == 2)
+      FG_LAUNCH((k_attn_dec_loop<HD, DPC, 2, KT>), grid, dim3(256), 0, s, a);
+    else
+      FG_LAUNCH((k_attn_dec_loop<HD, DPC, 1, KT>), grid, dim3(256), 0, s, a);
+    return;
+  }
   switch (gh) {
     case 5:
       if constexpr (DPC == 64) { FG_LAUNCH((k_attn_dec<HD, DPC, 5, KT>), grid, dim3(256), 0, s, a); return; }
@@ -585,7 +739,8 @@ void launch_dec_hd(hipStream_t s, const DecArgs& a, int rows, int dpc, int gh) {
   else
     launch_dec_gh<HD, DPC_MIN, KT>(s, a, rows, gh);
   if (a.nchunk > 1)
-    FG_LAUNCH((k_attn_dec_merge<HD>), dim3((unsigned)(rows * a.H)), dim3(256), 0, s, a, dpc);
+    FG_LAUNCH((k_attn_dec_merge<HD>), dim3((unsigned)(rows * a.H)), dim3(256), 0, s, a,
+              dpc * a.iters);
 }
 
 }  // namespace
@@ -605,7 +760,24 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   // the last query row
   const int dpc = B * d.H >= 192 ? 128 : DPC_MIN;
   const int live = d_len ? maxT : len + qpr - 1;
-  a.nchunk = (live + dpc - 1) / dpc;
+  const int rows = B * qpr;
+  const int gh = dec_group(d.H / d.KH, dpc);
+  // blocks of dpc positions per workgroup (k_attn_dec_loop: fewer chunks to
+  // merge): as many as keep 1.5 workgroups per CU on a bf16 cache (B=64: a
+  // sequence and head each, no merge; 1.8 % of the step faster than one
+  // block), 6 on an fp32 one (its workgroups hold twice the bytes in flight
+  // and half the occupancy; 1.2 %), else one
+  const int nblk = (live + dpc - 1) / dpc, wg_rows = rows * d.KH * (d.H / d.KH / gh);
+  const int64_t want2 = (kv16 ? 3 : 12) * (int64_t)cu_count();  // twice the workgroups wanted
+  int iters = 1;
+  if (dpc == 128)
+    for (int it = nblk; it > 1; --it)
+      if ((int64_t)wg_rows * ((nblk + it - 1) / it) * 2 >= want2) {
+        iters = it;
+        break;
+      }
+  a.iters = iters;
+  a.nchunk = (live + dpc * iters - 1) / (dpc * iters);
   a.d_len = d_len;
   a.len_imm = len;
   a.qpr = qpr;
@@ -614,8 +786,6 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.ys = ys;
   a.ys_plane = ys_plane;
   a.part = scratch;
-  const int rows = B * qpr;
-  const int gh = dec_group(d.H / d.KH, dpc);
   if (d.hd == 128) {
     if (kv16) launch_dec_hd<128, uint16_t>(s, a, rows, dpc, gh);
     else launch_dec_hd<128, float>(s, a, rows, dpc, gh);
