@@ -385,7 +385,7 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
   RCCHK(alloc((void**)&ws.aos, rows * d.qd() * 2 * 2));
   RCCHK(alloc((void**)&ws.hs, rows * d.dff * 2 * 2));
   RCCHK(alloc((void**)&ws.ssq, rows * (d.D / 64) * 4));
-  if (d.V % 256 == 0) RCCHK(alloc((void**)&ws.nllp, rows * (d.V / 64) * 2 * 4));
+  if (d.V % 256 == 0) RCCHK(alloc((void**)&ws.nllp, rows * (d.V / NLL_GROUP_COLS) * 2 * 4));
   // split-K partials of the small-M GEMMs: the largest any row count up to
   // `rows` needs over the five GEMM shapes
   int64_t part = 0;
@@ -623,7 +623,7 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   if (nll_parts) o.nll_part = m->ws.nllp;
   layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, nullptr, logits, o);
   if (nll_parts)
-    timed(m, s, FG_K_OTHER, 0, (double)rows * (m->d.V / 64) * 8 + rows * 12, [&] {
+    timed(m, s, FG_K_OTHER, 0, (double)rows * (m->d.V / NLL_GROUP_COLS) * 8 + rows * 12, [&] {
       launch_nll_parts(s, logits, m->ws.nllp, d_tgt, rows, m->d.V, d_nll);
     });
   else if (d_tgt && d_nll)

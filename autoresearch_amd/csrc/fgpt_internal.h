@@ -66,6 +66,10 @@ __host__ __device__ inline int pair_dim(int s, int hd) {
   return (s & 1) ? (hd / 2 + (s >> 1)) : (s >> 1);
 }
 
+// Columns of one log-sum-exp partial of lm_head's cross-entropy epilogue
+// (one wavefront row of the 128x256 register-epilogue tile).
+constexpr int NLL_GROUP_COLS = 128;
+
 // Activation workspace for up to `rows` token rows.
 struct Work {
   int64_t rows = 0;
@@ -87,7 +91,7 @@ struct Work {
   uint16_t* hs = nullptr;   // relu2(fc) [rows][4D]
   float* ssq = nullptr;
   float* part = nullptr;    // split-K partial sums of the small-M GEMMs
-  float* nllp = nullptr;    // lm_head's per-row log-sum-exp partials [rows][V/64][2]
+  float* nllp = nullptr;    // lm_head's log-sum-exp partials [rows][V/NLL_GROUP_COLS][2]
 };
 
 struct KVCacheDev {
@@ -163,9 +167,9 @@ struct GemvArgs {
   int f16;
   float wscale;
   // lm_head with the cross-entropy to follow (STORE only, nullable): per row
-  // and 64-column group, the group's maximum logit and sum of exp(logit -
-  // maximum), [M][N/64][2]; the GEMM then runs where it can write them
-  // (gemm_store_nll says when)
+  // and NLL_GROUP_COLS-column group, the group's maximum logit and sum of
+  // exp(logit - maximum), [M][N/NLL_GROUP_COLS][2]; the GEMM then runs where
+  // it can write them (gemm_store_nll says when)
   float* nll_part;
 };
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
@@ -239,12 +243,12 @@ void launch_bpb_rows(hipStream_t s, const float* nll, const int32_t* tgt, int ro
 // Per-row nll = logsumexp - logit[tgt].
 void launch_nll(hipStream_t s, const float* logits, const int32_t* tgt, int64_t rows, int V,
                 float* out);
-// The same from lm_head's per-row partials (GemvArgs::nll_part, V/64 groups
-// a row) and the target's logit.
+// The same from lm_head's per-row partials (GemvArgs::nll_part,
+// V/NLL_GROUP_COLS groups a row) and the target's logit.
 void launch_nll_parts(hipStream_t s, const float* logits, const float* parts, const int32_t* tgt,
                       int64_t rows, int V, float* out);
 // Whether an lm_head GEMM of M rows over a vocabulary of N writes the
-// log-sum-exp partials when asked (129 to 4096 rows, N a multiple of 256).
+// log-sum-exp partials when asked (1025 to 4096 rows, N a multiple of 256).
 bool gemm_store_nll(int64_t M, int N);
 
 // ---- greedy speculative decoding

@@ -1121,8 +1121,8 @@ __global__ __launch_bounds__(256) void k_nll(const float* __restrict__ logits,
 }
 
 // The per-row nll of src/app/eval_bpb.f90:165-181 from lm_head's
-// log-sum-exp partials (one (max, sum of exp(logit - max)) per 64-column
-// group, written by the GEMM's epilogue): one wavefront per row, the row
+// log-sum-exp partials (one (max, sum of exp(logit - max)) per
+// NLL_GROUP_COLS-column group, written by the GEMM's epilogue): one wavefront per row, the row
 // maximum and the rescaled sums reduced in a fixed order.
 __global__ __launch_bounds__(256) void k_nll_parts(const float* __restrict__ logits,
                                                    const float* __restrict__ parts,
@@ -1130,7 +1130,7 @@ __global__ __launch_bounds__(256) void k_nll_parts(const float* __restrict__ log
                                                    int V, float* __restrict__ out) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // (whole wavefronts)
-  const int lane = threadIdx.x & 63, ng = V / 64;
+  const int lane = threadIdx.x & 63, ng = V / NLL_GROUP_COLS;
   const float2* P = reinterpret_cast<const float2*>(parts) + row * ng;
   float m = -FLT_MAX;
   for (int g = lane; g < ng; g += 64) m = fmaxf(m, P[g].x);

@@ -633,28 +633,43 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
       }
     }
     if constexpr (EPI == GV_STORE) {
-      if (a.nll_part) {
-        // the cross-entropy's log-sum-exp, per row and 64-column group
-        // (blocks 2q and 2q+1 of this wavefront): the group maximum over
-        // the half-wavefront's 32 lanes, then the sum of exp(v - max); the
-        // values are the logits just stored, bit for bit
-        static_assert(WN % 2 == 0, "64-column groups");
-        const int ng = a.N / 64;
+      // the cross-entropy's log-sum-exp, per row and NLL_GROUP_COLS-column
+      // group (GB adjacent 32-column blocks of this wavefront): the group
+      // maximum over the lane's GB values and the half-wavefront's 32 lanes,
+      // then the sum of exp(v - max) (the hardware exp2 of (v - max) log2 e:
+      // its relative error, a few ulp, is far below the tolerance of the
+      // nll); the values are the logits just stored, bit for bit. Only
+      // tilings whose wavefront row holds whole groups generate it; the
+      // launcher picks one of those when nll_part is set.
+      constexpr int GB = NLL_GROUP_COLS / 32;
+      if constexpr (WN % GB == 0) {
+        if (a.nll_part) {
+          const int ng = a.N / NLL_GROUP_COLS;
 #pragma unroll
-        for (int q = 0; q < WN / 2; ++q) {
-          const int grp = (n0 + (wn * WN + 2 * q) * 32) / 64;
+          for (int q = 0; q < WN / GB; ++q) {
+            const int grp = (n0 + (wn * WN + GB * q) * 32) / NLL_GROUP_COLS;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rl = rb + 8 * (r >> 2) + (r & 3);
-            const float u0 = P16 ? acc[i][2 * q][r] * a.wscale : acc[i][2 * q][r];
-            const float u1 = P16 ? acc[i][2 * q + 1][r] * a.wscale : acc[i][2 * q + 1][r];
-            const float v0 = a.norm ? u0 * sinv[rl] : u0, v1 = a.norm ? u1 * sinv[rl] : u1;
-            const float mx = half_max(fmaxf(v0, v1));
-            const float sm = half_sum(expf(v0 - mx) + expf(v1 - mx));
-            const int m = m0 + rl;
-            if (cl == 0 && m < M)
-              *reinterpret_cast<float2*>(a.nll_part + ((int64_t)m * ng + grp) * 2) =
-                  make_float2(mx, sm);
+            for (int r = 0; r < 16; ++r) {
+              const int rl = rb + 8 * (r >> 2) + (r & 3);
+              float v[GB];
+#pragma unroll
+              for (int g = 0; g < GB; ++g) {
+                const float u = P16 ? acc[i][GB * q + g][r] * a.wscale : acc[i][GB * q + g][r];
+                v[g] = a.norm ? u * sinv[rl] : u;
+              }
+              float mx = v[0];
+#pragma unroll
+              for (int g = 1; g < GB; ++g) mx = fmaxf(mx, v[g]);
+              mx = half_max(mx);
+              float e = 0.f;
+#pragma unroll
+              for (int g = 0; g < GB; ++g) e += __expf(v[g] - mx);
+              const float sm = half_sum(e);
+              const int m = m0 + rl;
+              if (cl == 0 && m < M)
+                *reinterpret_cast<float2*>(a.nll_part + ((int64_t)m * ng + grp) * 2) =
+                    make_float2(mx, sm);
+            }
           }
         }
       }
@@ -919,12 +934,15 @@ int cu_count() {
   return n[dev];
 }
 
+// lm_head writes the log-sum-exp partials over 1025 to 4096 rows. Measured
+// against the separate pass over the logits on the depth-12 forward: 10-30
+// us faster per pass at 2048 and 4096 rows, 10 us slower at 1024 (the pass
+// over 128 MB of logits is short there); beyond 4096 rows the 256x256 tiles
+// hold 64 rows a lane and the epilogue's reductions cost more than the pass.
+bool gemm_store_nll(int64_t M, int N) { return M > 1024 && M <= 4096 && N % 256 == 0; }
+
 // RESID on k_gemm: one sum-of-squares partial per row and N tile; split-K
 // RESID (given split-K scratch): one per row and 512 columns.
-// (up to 4096 rows: beyond, the 256x256 tiles hold 64 rows a lane, and the
-// partials' reductions in the epilogue cost more than a pass over the logits)
-bool gemm_store_nll(int64_t M, int N) { return M > SPLITK_MAX_M && M <= 4096 && N % 256 == 0; }
-
 int gemm_ssq_parts(int64_t M, int N, int K) {
   if (splitk_count(M, N, K) == 1 && resid_k4(M, N, K)) return N / 96;
   return splitk_count(M, N, K) > 1 ? (N + RED_COLS - 1) / RED_COLS : N / tile_n(M, N);

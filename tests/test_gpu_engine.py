@@ -53,7 +53,7 @@ def d12():
 
 
 @pytest.mark.parametrize("d", [SMALL, SMALL_MHA], ids=["gqa", "mha"])
-@pytest.mark.parametrize("B,T", [(1, 1), (1, 4), (2, 3), (2, 37), (3, 130)])
+@pytest.mark.parametrize("B,T", [(1, 1), (1, 4), (2, 3), (2, 37), (3, 130), (3, 500)])
 def test_forward_small_vs_oracle(d, B, T):
     w = seeded_weights(d, 7)
     ids = uniform_ids(B * 100 + T, B * T, d.vocab)

@@ -129,7 +129,7 @@ def test_eval_rows_b8_t2048_f16():
 
 
 @pytest.mark.parametrize("d", [SMALL, SMALL_MHA], ids=["gqa", "mha"])
-@pytest.mark.parametrize("B,T", [(1, 100), (2, 64), (3, 130), (1, 300), (2, 257)])
+@pytest.mark.parametrize("B,T", [(1, 100), (2, 64), (3, 130), (1, 300), (2, 257), (3, 500)])
 def test_forward_small_f16(d, B, T):
     """Small models: above 128 rows within the bar, at or below 128 rows the
     split format's exact bits."""
