@@ -822,12 +822,40 @@ __global__ __launch_bounds__(256) void k_argmax(const float* __restrict__ logits
   float* cp = (d_len && lgs_out) ? lgs_out + slot * V : nullptr;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int j = threadIdx.x; j < V; j += 256) {
-    const float v = l[j];
-    if (cp) cp[j] = v;
+  auto take = [&](float v, int j) {
     if (v > bv) {
       bv = v;
       bi = j;
+    }
+  };
+  if ((V & 3) == 0 && ((reinterpret_cast<uintptr_t>(l) | reinterpret_cast<uintptr_t>(cp)) & 15) == 0) {
+    // 16-byte loads, eight in flight per thread before any compare; each
+    // thread still sees its indices in increasing order
+    const float4* l4 = reinterpret_cast<const float4*>(l);
+    float4* c4 = reinterpret_cast<float4*>(cp);
+    const int V4 = V >> 2;
+    for (int j0 = threadIdx.x; j0 < V4; j0 += 256 * 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        v[u] = j0 + 256 * u < V4 ? l4[j0 + 256 * u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + 256 * u;
+        if (j < V4) {
+          if (c4) c4[j] = v[u];
+          take(v[u].x, 4 * j);
+          take(v[u].y, 4 * j + 1);
+          take(v[u].z, 4 * j + 2);
+          take(v[u].w, 4 * j + 3);
+        }
+      }
+    }
+  } else {
+    for (int j = threadIdx.x; j < V; j += 256) {
+      const float v = l[j];
+      if (cp) cp[j] = v;
+      take(v, j);
     }
   }
 #pragma unroll

@@ -258,6 +258,51 @@ def test_batched_decode_rows_independent(B):
     m.close()
 
 
+@pytest.mark.parametrize("d,B,mode", [(SMALL, 1, "step"), (SMALL, 6, "step"),
+                                      (SMALL_MHA, 1, "decode"), (SMALL_MHA, 6, "decode")],
+                         ids=["step-b1", "step-b6", "fused-b1", "loop-b6"])
+def test_argmax_ties_take_the_first_index(d, B, mode):
+    """Exact ties in the logits: lm_head rows copied from sequence 0's winner
+    give the same bits at every copy (the same dot product). The step's id
+    must be the lowest tied index, as sample_token's strict > scan returns
+    it, on every argmax the step can run (per-row kernel, single-block tail,
+    the persistent loop's two-level exchange)."""
+    w = seeded_weights(d, 31)
+    P = 5
+    prompts = uniform_ids(5, B * P, d.vocab).reshape(B, P)
+    c, s = tables(d, P + 1)
+
+    def run(weights):
+        m = engine.Model(d, stacks=weights)
+        m.set_rope(c, s)
+        kv = m.kv(B, P + 1)
+        kv.step_multi(prompts[:, :-1], want_logits=False)
+        if mode == "step":
+            lg, nxt = kv.step(prompts[:, -1])
+        else:
+            ids, lgs = kv.decode_greedy(prompts[:, -1], 1, want_logits=True)
+            lg, nxt = lgs[0], ids[0]
+        kv.close()
+        m.close()
+        return lg, nxt
+
+    _, nxt0 = run(w)
+    r = int(nxt0[0])
+    lm = w["lm_head"].reshape(d.vocab, d.d_model).copy()
+    copies = sorted({(r + k) % d.vocab for k in (-1, 1, 4, 129, 258)} - {r})
+    for t in copies:
+        lm[t] = lm[r]
+    w2 = dict(w, lm_head=lm.reshape(-1))
+    lg, nxt = run(w2)
+    row = lg[0]
+    tied = np.flatnonzero(row == row.max())
+    record("argmax_ties", mode=mode, B=B, winner=r, tied=tied.tolist(), got=int(nxt[0]))
+    assert len(tied) >= len(copies)  # the copies reproduce the winner's bits
+    assert nxt[0] == tied[0]
+    for b in range(B):
+        assert nxt[b] == int(np.argmax(lg[b]))  # numpy's argmax: the first maximum
+
+
 def test_errors_are_loud():
     d = SMALL
     w = seeded_weights(d, 14)
