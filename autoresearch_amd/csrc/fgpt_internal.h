@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <string>
 
 #include "../../include/fgpt.h"
@@ -193,6 +194,17 @@ int64_t gemm_splitk_floats(int64_t M, int N, int K);
 int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0);
 // Compute units of the current device (cached per device).
 int cu_count();
+// Raise kernel fn's dynamic LDS limit to `bytes` on the current device. The
+// limit is an attribute of the function on each device, so it is set once
+// per device (bit d of *done); devices past 63 set it at every launch.
+inline void raise_lds_once(const void* fn, size_t bytes, std::atomic<uint64_t>* done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  const uint64_t bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+  if (bit && (done->load(std::memory_order_acquire) & bit)) return;
+  (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+  if (bit) done->fetch_or(bit, std::memory_order_release);
+}
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
                       int64_t kv_plane, float* scratch, float* y, uint16_t* ys = nullptr,

@@ -486,12 +486,8 @@ constexpr int attn_lds() {
 template <int HD, bool P16>
 void launch_attn_hd(hipStream_t s, const AttnArgs& p, dim3 grid, bool split) {
   constexpr int lds = attn_lds<HD, P16>();
-  static bool lds_set = false;
-  if (!lds_set) {
-    (void)hipFuncSetAttribute((const void*)k_attn_mfma<HD, P16>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    lds_set = true;
-  }
+  static std::atomic<uint64_t> lds_set{0};
+  raise_lds_once((const void*)k_attn_mfma<HD, P16>, lds, &lds_set);
   FG_LAUNCH((k_attn_mfma<HD, P16>), grid, dim3(512), lds, s, p);
   const dim3 mgrid((unsigned)(p.nbh * p.nqb * (QB / merge_queries<HD>())));
   if (split) FG_LAUNCH((k_attn_merge<HD, P16>), mgrid, dim3(256), 0, s, p);

@@ -694,12 +694,8 @@ void launch_cfg2(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr int BM = NWM * WM * 32, BN = NWN * WN * 32;
   constexpr size_t lds = (size_t)NST * ((P16 ? 1 : 2) * BM + BN) * 64;
   static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void*)k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  raise_lds_once((const void*)k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16>, lds, &attr);
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
   FG_LAUNCH((k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16>), g, dim3(64 * NWM * NWN), lds, s, a,
                      d_pos);
@@ -714,12 +710,8 @@ void launch_cfg(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr size_t lds = pipe > epi ? pipe : epi;
   // gfx950: 160 KB of LDS per workgroup, the row scales (BM floats) included
   static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void*)k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG, P16>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    attr = true;
-  }
+  static std::atomic<uint64_t> attr{0};
+  raise_lds_once((const void*)k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG, P16>, lds, &attr);
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
   FG_LAUNCH((k_gemm<EPI, BM, BN, NWM, NWN, BK, NST, KG, P16>), g, dim3(64 * NWM * NWN * KG),
                      lds, s, a, d_pos);
