@@ -476,23 +476,24 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
 }
 
 // k_attn_dec over a.iters consecutive blocks of DPC positions per
-// workgroup, for batches with rows x KV heads enough to fill the chip
-// without splitting the positions finely (at B=64 one workgroup takes a
-// whole sequence and head, and no merge follows). Each wavefront keeps an
-// online softmax of its own positions across the blocks (running maximum,
-// sum and O, rescaled when the maximum moves); the four wavefronts' results
-// meet at the end, each rescaled to the workgroup maximum, and leave as
+// workgroup (NWV wavefronts, DPC / NWV positions each per block), for
+// batches with rows x KV heads enough to fill the chip without splitting
+// the positions finely (at B=64 one workgroup takes a whole sequence and
+// head, and no merge follows). Each wavefront keeps an online softmax of
+// its own positions across the blocks (running maximum, sum and O, rescaled
+// when the maximum moves); the wavefronts' results meet at the end, each
+// rescaled to the workgroup maximum, and leave as
 // k_attn_dec's do (the output, or a partial for k_attn_dec_merge). While a
 // block's scores are formed its V rows load, and the next block's K rows
 // load while its V rows are weighed.
-template <int HD, int DPC, int GH, class KT>
-__global__ __launch_bounds__(256) void k_attn_dec_loop(DecArgs a) {
+template <int HD, int DPC, int GH, class KT, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   constexpr int LPP = HD / 8;        // lanes per cached row
   constexpr int PPW = 64 / LPP;      // rows per wavefront load
-  constexpr int IT = DPC / 4 / PPW;  // loads per lane and tensor per block
+  constexpr int IT = DPC / NWV / PPW;  // loads per lane and tensor per block
   static_assert(LPP == 8 || LPP == 16, "head dim 64 or 128");
-  __shared__ float red[3][4][GH];
-  __shared__ float so[4 * PPW][GH][HD];
+  __shared__ float red[3][NWV][GH];
+  __shared__ float so[NWV * PPW][GH][HD];
   const int G = a.H / a.KH, ng = G / GH;
   const int gi = blockIdx.x, c = blockIdx.y;
   const int row = gi / (a.KH * ng), kvh = (gi / ng) % a.KH, h0 = kvh * G + (gi % ng) * GH;
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(256) void k_attn_dec_loop(DecArgs a) {
   const int64_t kd = (int64_t)a.KH * HD;
   const KT* K = (const KT*)a.kc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
   const KT* V = (const KT*)a.vc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
-  auto pos = [&](int blk, int i) { return p0 + blk * DPC + wv * (DPC / 4) + i * PPW + sub; };
+  auto pos = [&](int blk, int i) { return p0 + blk * DPC + wv * (DPC / NWV) + i * PPW + sub; };
   Row8<KT> kr[IT], vr[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(0, i), len - 1) * kd);
@@ -586,7 +587,9 @@ __global__ __launch_bounds__(256) void k_attn_dec_loop(DecArgs a) {
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < GH; ++j) {
-    const float mw = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
+    float mw = red[0][0][j];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) mw = fmaxf(mw, red[0][w][j]);
     const float f = expf(m[j] - mw);
     float4* dst = (float4*)&so[wv * PPW + sub][j][8 * dl];
     dst[0] = make_float4(o[j][0] * f, o[j][1] * f, o[j][2] * f, o[j][3] * f);
@@ -600,15 +603,17 @@ __global__ __launch_bounds__(256) void k_attn_dec_loop(DecArgs a) {
     if (lane == 0) red[2][wv][j] = mw;
   }
   __syncthreads();
-  for (int q4 = tid; q4 < GH * HD / 4; q4 += 256) {
+  for (int q4 = tid; q4 < GH * HD / 4; q4 += 64 * NWV) {
     const int j = q4 / (HD / 4), d = 4 * (q4 % (HD / 4));
     float4 t = *(const float4*)&so[0][j][d];
 #pragma unroll
-    for (int r = 1; r < 4 * PPW; ++r) {
+    for (int r = 1; r < NWV * PPW; ++r) {
       const float4 u = *(const float4*)&so[r][j][d];
       t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
     }
-    const float lj = (red[1][0][j] + red[1][1][j]) + (red[1][2][j] + red[1][3][j]);
+    float lj = red[1][0][j];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) lj += red[1][w][j];
     const int64_t bh = (int64_t)row * a.H + h0 + j;
     if (nch == 1) {
       const float inv = 1.0f / lj;
@@ -712,6 +717,21 @@ template <int HD, int DPC, class KT>
 void launch_dec_gh(hipStream_t s, const DecArgs& a, int rows, int gh) {
   const int ng = a.H / a.KH / gh;
   const dim3 grid((unsigned)(rows * a.KH * ng), (unsigned)a.nchunk);
+  if constexpr (sizeof(KT) == 2 && DPC == 128) {
+    // a bf16 cache walked in pairs of blocks: 8 wavefronts over blocks of
+    // 256 positions, the same span per workgroup (and chunk count) with
+    // twice the K/V rows in flight per workgroup (B=64: 384 workgroups,
+    // all resident at two per CU; 1.9 % of the step faster than 4 x 128)
+    if (a.iters > 1 && a.iters % 2 == 0) {
+      DecArgs b2 = a;
+      b2.iters = a.iters / 2;
+      if (gh == 2)
+        FG_LAUNCH((k_attn_dec_loop<HD, 256, 2, KT, 8>), grid, dim3(512), 0, s, b2);
+      else
+        FG_LAUNCH((k_attn_dec_loop<HD, 256, 1, KT, 8>), grid, dim3(512), 0, s, b2);
+      return;
+    }
+  }
   if (a.iters > 1) {  // (DPC 128 only: dec_group's options for it)
     if (gh == 2)
       FG_LAUNCH((k_attn_dec_loop<HD, DPC, 2, KT>), grid, dim3(256), 0, s, a);
