@@ -1656,7 +1656,15 @@ extern "C" int32_t fg_set_option(fg_model* m, int32_t key, int32_t value) {
   if (key == FG_OPT_FUSED_DECODE) {
     m->fused_on = value != 0;
   } else {
-    if (value) RCCHK(ensure_w16(m));
+    if (value) {
+      RCCHK(ensure_w16(m));
+    } else if (m->w16) {
+      // the copy goes with the option; passes queued on any stream (the
+      // device-pointer entries take the caller's) may still read it
+      HIPCHK(hipDeviceSynchronize());
+      HIPCHK(hipFree(m->w16));
+      m->w16 = nullptr;
+    }
     m->fwd_f16 = value != 0;
   }
   return FG_OK;

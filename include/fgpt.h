@@ -282,7 +282,8 @@ int32_t fg_decode_sample(fg_model *m, fg_kv *kv, int32_t *ids, int32_t n_known, 
  * instead of ~5e-6; passes that fill a KV cache (fg_step_multi) keep the
  * split format. 0 (the default) is the split format everywhere. Enabling it
  * makes the fp16 copy (the weight arena's size again) and fails with
- * FG_EARG when the weights exceed the fp16 range. */
+ * FG_EARG when the weights exceed the fp16 range; disabling it waits for
+ * the device's queued work (any stream) and frees the copy. */
 enum { FG_OPT_FUSED_DECODE = 1, FG_OPT_FORWARD_F16 = 2 };
 int32_t fg_set_option(fg_model *m, int32_t key, int32_t value);
 /* *value = the option's effective value (for FG_OPT_FUSED_DECODE: 1 when

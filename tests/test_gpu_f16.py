@@ -69,6 +69,7 @@ def test_option_round_trip(d12):
     assert wb1 == 2 * wb0  # the fp16 copy has the arena's size
     m.set_forward_f16(False)
     assert m.forward_f16() is False
+    assert m.bytes()[0] == wb0  # the copy is released with the option
     with pytest.raises(engine.FgptError):
         engine._check(engine._LIB.fg_set_option(m._h, 99, 1))
 
