@@ -444,9 +444,11 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
 }
 
 // ------------------------------------------------------------------ v2
-// Wave tile (WM x 32) x (WN x 32). The operand fragments of the next
-// 16-deep half slice are read from LDS into a second register set while
-// the MFMAs of the current one run, so LDS latency hides behind MFMA work
+// Wave tile (WM x 32) x (WN x 32), K slices of BK (32 or 64) per stage. The
+// operand fragments of the next 16-deep step are read from LDS into a
+// second register set while the MFMAs of the current one run (the last
+// step of a slice runs after the next slice's barrier), so LDS latency hides
+// behind MFMA work
 // even at one wavefront per SIMD. The epilogue works straight from the
 // accumulators: lane l of a 32x32 block holds column l % 32 of rows
 // 8(r/4) + 4(l/32) + r%4, r = 0..15, so 32 lanes store 32 consecutive
@@ -456,7 +458,7 @@ struct Frag {
   bf16x8_t h[WM], l[WM], w[WN];
 };
 
-template <int BM, int WM, int WN, bool P16>
+template <int BM, int WM, int WN, bool P16, int BK = 32>
 __device__ __forceinline__ void frag_load(Frag<WM, WN>& f, const uint8_t* stg, int kk, int wm,
                                           int wn, int lane) {
   constexpr int AP = P16 ? 1 : 2;
@@ -464,13 +466,13 @@ __device__ __forceinline__ void frag_load(Frag<WM, WN>& f, const uint8_t* stg, i
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
     const int r = (wm * WM + i) * 32 + (lane & 31);
-    f.h[i] = *(const bf16x8_t*)(stg + r * 64 + swz<32>(r, c) * 16);
-    if constexpr (!P16) f.l[i] = *(const bf16x8_t*)(stg + (BM + r) * 64 + swz<32>(BM + r, c) * 16);
+    f.h[i] = *(const bf16x8_t*)(stg + r * (2 * BK) + swz<BK>(r, c) * 16);
+    if constexpr (!P16) f.l[i] = *(const bf16x8_t*)(stg + (BM + r) * (2 * BK) + swz<BK>(BM + r, c) * 16);
   }
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
     const int r = AP * BM + (wn * WN + j) * 32 + (lane & 31);
-    f.w[j] = *(const bf16x8_t*)(stg + r * 64 + swz<32>(r, c) * 16);
+    f.w[j] = *(const bf16x8_t*)(stg + r * (2 * BK) + swz<BK>(r, c) * 16);
   }
 }
 
@@ -488,16 +490,16 @@ __device__ __forceinline__ void frag_mma(const Frag<WM, WN>& f, f32x16_t (&acc)[
   }
 }
 
-template <int EPI, int NWM, int NWN, int WM, int WN, int NST, bool P16 = false>
+template <int EPI, int NWM, int NWN, int WM, int WN, int NST, bool P16 = false, int BK = 32>
 __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
                                                          const int32_t* __restrict__ d_pos) {
-  constexpr int BK = 32, RPG = 16;
+  constexpr int RB = 2 * BK, CPR = BK / 8, RPG = 1024 / RB;
   constexpr int BM = NWM * WM * 32, BN = NWN * WN * 32;
   constexpr int NW = NWM * NWN, NT = 64 * NW;
   constexpr int AP = P16 ? 1 : 2;
   constexpr int ROWS = AP * BM + BN, GROUPS = ROWS / RPG, GPW = GROUPS / NW;
   static_assert(GROUPS % NW == 0, "tile / wave grid mismatch");
-  constexpr int STAGE_BYTES = ROWS * 64;
+  constexpr int STAGE_BYTES = ROWS * RB;
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   __shared__ float sinv[BM];
 
@@ -514,8 +516,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
 #pragma unroll
   for (int q = 0; q < GPW; ++q) {
     const int g = wid + NW * q;
-    const int r = RPG * g + (lane >> 2), slot = lane & 3;
-    const int c = swz<32>(r, slot);
+    const int r = RPG * g + lane / CPR, slot = lane % CPR;
+    const int c = swz<BK>(r, slot);
     if (r < AP * BM) {
       const int ar = r < BM ? r : r - BM;
       const int row = min(m0 + ar, M - 1);  // rows past M are never stored
@@ -549,10 +551,17 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
         stage_sync<(NST - 2) * GPW>();
         fill((si + NST - 1) % NST, min((kt + si + NST - 1) * BK, klast));
         const uint8_t* stg = smem + si * STAGE_BYTES;
-        frag_load<BM, WM, WN, P16>(f0, stg, 0, wm, wn, lane);
-        if (kt + si > 0) frag_mma<WM, WN, P16>(f1, acc);  // second half of the previous slice
-        frag_load<BM, WM, WN, P16>(f1, stg, 1, wm, wn, lane);
+        frag_load<BM, WM, WN, P16, BK>(f0, stg, 0, wm, wn, lane);
+        if (kt + si > 0) frag_mma<WM, WN, P16>(f1, acc);  // last k-step of the previous slice
+        frag_load<BM, WM, WN, P16, BK>(f1, stg, 1, wm, wn, lane);
         frag_mma<WM, WN, P16>(f0, acc);
+#pragma unroll
+        for (int kk = 2; kk < BK / 16; kk += 2) {
+          frag_load<BM, WM, WN, P16, BK>(f0, stg, kk, wm, wn, lane);
+          frag_mma<WM, WN, P16>(f1, acc);
+          frag_load<BM, WM, WN, P16, BK>(f1, stg, kk + 1, wm, wn, lane);
+          frag_mma<WM, WN, P16>(f0, acc);
+        }
       }
     }
   }
@@ -689,15 +698,15 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
   }
 }
 
-template <int EPI, int NWM, int NWN, int WM, int WN, int NST, bool P16>
+template <int EPI, int NWM, int NWN, int WM, int WN, int NST, bool P16, int BK = 32>
 void launch_cfg2(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   constexpr int BM = NWM * WM * 32, BN = NWN * WN * 32;
-  constexpr size_t lds = (size_t)NST * ((P16 ? 1 : 2) * BM + BN) * 64;
+  constexpr size_t lds = (size_t)NST * ((P16 ? 1 : 2) * BM + BN) * 2 * BK;
   static_assert(lds + BM * sizeof(float) <= 160 * 1024, "tile exceeds the LDS");
   static std::atomic<uint64_t> attr{0};
-  raise_lds_once((const void*)k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16>, lds, &attr);
+  raise_lds_once((const void*)k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16, BK>, lds, &attr);
   const dim3 g(a.N / BN, (unsigned)((a.M + BM - 1) / BM));
-  FG_LAUNCH((k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16>), g, dim3(64 * NWM * NWN), lds, s, a,
+  FG_LAUNCH((k_gemm2<EPI, NWM, NWN, WM, WN, NST, P16, BK>), g, dim3(64 * NWM * NWN), lds, s, a,
                      d_pos);
 }
 
@@ -825,11 +834,14 @@ void launch_tile_p(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   if constexpr (P16 && (EPI == GV_RELU2 || EPI == GV_STORE)) {
     // single-term fc and lm_head over more than 4096 rows: 256x256 tiles (8
     // wavefronts of 128x64; one fp16 A plane leaves room for them), 4 % of
-    // the GEMM time faster than 128x256 over 8 x 2048 rows in the layer stack
+    // the GEMM time faster than 128x256 over 8 x 2048 rows in the layer stack;
+    // two 64-wide K slices (128 KB) rather than three 32-wide ones, half the
+    // barriers per K: 0.8 % of the 8 x 2048 eval forward (identical bits; at
+    // 2048 rows the 128x256 tiles are 1.5 % slower with them)
     if (a.M > 4096 && a.N % 256 == 0) {
       GemvArgs b = a;
       b.part = nullptr;
-      launch_cfg2<EPI, 2, 4, 4, 2, 3, P16>(s, b, d_pos);
+      launch_cfg2<EPI, 2, 4, 4, 2, 2, P16, 64>(s, b, d_pos);
       return;
     }
   }
