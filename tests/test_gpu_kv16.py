@@ -106,3 +106,34 @@ def test_bf16_cache_d12_decode_vs_oracle():
         assert marg[first] < 2 * 2 * TOL * np.abs(ref_lg).max()
     kv.close()
     m.close()
+
+
+def test_batched_bf16_chunks_merged():
+    """B=96 at the small MHA dims over a 1152-position bf16 cache (9 blocks
+    of 128, 8 per workgroup) runs the looped decode attention on 8
+    wavefronts of 256-position blocks, split into two chunks per sequence
+    and head that a merge combines; the fp32 cache at the same shape runs
+    the single-block kernel over 9 chunks. Layer 0's appended rows are
+    exactly the bf16 rounding of the fp32 ones; the step's logits agree
+    within the bar, and every id matches but at near-ties."""
+    d, B, P, maxT, n = SMALL_MHA, 96, 1000, 1152, 1
+    m, c, s = model(d, 8, maxT)
+    ids = uniform_ids(23, B * P, d.vocab).reshape(B, P)
+    out = []
+    for bf in (False, True):
+        kv = m.kv(B, maxT, bf16=bf)
+        kv.step_multi(ids[:, :-1], want_logits=False)
+        nxt, lg = kv.decode_greedy(ids[:, -1], n, want_logits=True)
+        out.append((nxt, lg, kv.read()))
+        kv.close()
+    n0 = B * maxT * d.n_kv_head * d.head_dim
+    for t32, t16 in zip(out[0][2], out[1][2]):
+        assert np.array_equal(t16[:n0], bf16_round(t32[:n0]))
+    (i32, l32, _), (i16, l16, _) = out
+    e = relerr(l16, l32)
+    srt = np.sort(l32[0], -1)
+    flips = np.flatnonzero(i16[0] != i32[0])
+    record("bf16_chunks_merged", relerr=e, first_step_flips=flips.tolist())
+    assert e < TOL
+    assert np.all(srt[flips, -1] - srt[flips, -2] < 2 * TOL * np.abs(l32).max())
+    m.close()
