@@ -168,7 +168,10 @@ def sample_top_p(w, temp, topp, state):
     for i in range(1, V):
         if w[i] > m:
             m = w[i]
-    sc = np.exp(((w - m) / t).astype(np.float32)).astype(np.float32)
+    # (w - m) / t overflows to -inf for tiny temperatures, as it does in the
+    # reference's single precision; exp then gives 0
+    with np.errstate(over="ignore"):
+        sc = np.exp(((w - m) / t).astype(np.float32)).astype(np.float32)
     s = F(0.0)
     for i in range(V):
         s = F(s + sc[i])
