@@ -925,17 +925,17 @@ void launch_tile(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
 
 // Compute units of the current device (tile counts are weighed against it).
 int cu_count() {
-  static int n[64] = {0};
+  static std::atomic<int> n[64];  // 0: not looked up yet (handles on several threads)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (n[dev] == 0) {
-    int v = 0;
+  int v = n[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         v <= 0)
       v = 256;
-    n[dev] = v;
+    n[dev].store(v, std::memory_order_relaxed);
   }
-  return n[dev];
+  return v;
 }
 
 // lm_head writes the log-sum-exp partials over 1025 to 4096 rows. Measured
