@@ -401,3 +401,46 @@ def test_eval_bpb_small_vs_oracle():
     with pytest.raises(engine.FgptError):
         m.eval_bpb(rows, tb, batch=65)
     m.close()
+
+
+@pytest.mark.parametrize("B,T", [(1, 255), (1, 256), (1, 257), (2, 613)])
+def test_host_logits_staged_copy_exact(d12, B, T):
+    """Logits copied to host memory equal the device-pointer forward's bit
+    for bit: below one 8 MiB staging chunk (255 rows of 8192 fp32), exactly
+    one, one plus a row, and a ragged four-plus chunks; twice, so the second
+    call reuses the staging buffers."""
+    from .devbuf import DevBuf
+    d, w, m, c, s = d12
+    ids = uniform_ids(5 + T, B * T, d.vocab)
+    di = DevBuf(ids)
+    dl = DevBuf(np.zeros(B * T * d.vocab, np.float32))
+    try:
+        m.forward_dev(di.ptr, B, T, dl.ptr)
+        ref = dl.get()
+        for _ in range(2):
+            lg, _ = m.forward(ids, B, T)
+            assert np.array_equal(lg.reshape(-1), ref)
+    finally:
+        di.free()
+        dl.free()
+
+
+def test_decode_logits_over_staging_chunks(d12):
+    """decode_greedy's logits for 64 sequences x 8 steps (16 MiB, two
+    staging chunks) agree with per-step step_multi logits (2 MiB each, a
+    direct copy) and give the same ids."""
+    d, w, m, c, s = d12
+    B, P, n = 64, 5, 8
+    prompts = uniform_ids(31, B * P, d.vocab).reshape(B, P)
+    a, b = m.kv(B, P + n), m.kv(B, P + n)
+    a.step_multi(prompts[:, :-1], want_logits=False)
+    b.step_multi(prompts[:, :-1], want_logits=False)
+    ids, lg = a.decode_greedy(prompts[:, -1], n, want_logits=True)
+    cur = prompts[:, -1]
+    for k in range(n):
+        one, nxt = b.step_multi(cur.reshape(B, 1))
+        assert np.array_equal(nxt, ids[k])
+        assert relerr(lg[k], one.reshape(B, d.vocab)) < 1e-5
+        cur = nxt
+    a.close()
+    b.close()
