@@ -895,10 +895,11 @@ void launch_tile_p(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
     }
   }
   const int bn = tile_n(a.M, a.N);
-  if (P16 && bn == 128 && big && EPI != GV_STORE && a.M > 4096 && a.K % 64 == 0)
-    // single-term QKV and residual GEMMs over more than 4096 rows: 64-wide K
-    // slices, two stages (64 KB with one fp16 A plane): 1-3 % of the GEMM
-    // time faster than 32-wide ones over 8 x 2048 rows
+  if (P16 && bn == 128 && big && EPI != GV_STORE && a.M > 1024 && a.K % 64 == 0)
+    // single-term QKV and residual GEMMs that fill the chip with 128x128
+    // tiles: 64-wide K slices, two stages (64 KB with one fp16 A plane):
+    // 1-3 % of the GEMM time faster than 32-wide ones over 8 x 2048 rows,
+    // and the depth-12 forward 0.9 % (1 x 2048) to 1.2 % (2 x 2048) faster
     launch_cfg<EPI, 128, 128, 4, 2, 64, 2, 1, P16>(s, b, d_pos);
   else if (bn == 128 && big)
     launch_cfg<EPI, 128, 128, 4, 2, 32, 3, 1, P16>(s, b, d_pos);  // 72 KB: two blocks per CU

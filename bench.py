@@ -386,11 +386,12 @@ PMC_MATCH = ("k_gemm",)           # kernel-name fragments of that kind
 CALIB_BYTES = 256 << 20           # plain copy of known size: reads and writes this much
 
 
-def pmc_probe(workload: str = "prefill"):
+def pmc_probe(workload: str = "prefill", f16: bool = True):
     """Child of a `rocprofv3 --pmc` run: one warm-up and one measured T=2048
-    prefill (or, for decode_b1, two loops of the B=1 decode workload: 16-id
-    prompt, 32 steps), then a 256 MiB device copy whose counter reading
-    calibrates the counter against known bytes."""
+    prefill, on single-term fp16 operands (split-bf16 ones with f16=False),
+    or, for decode_b1, two loops of the B=1 decode workload (16-id prompt,
+    32 steps); then a 256 MiB device copy whose counter reading calibrates
+    the counter against known bytes."""
     import torch
     from autoresearch_amd import engine
     from autoresearch_amd.weights import D12, seeded_weights, rope_tables, uniform_ids
@@ -412,7 +413,7 @@ def pmc_probe(workload: str = "prefill"):
         ids = uniform_ids(2, T + 1, d.vocab)
         d_ids = torch.from_numpy(ids[:T].copy()).to(dev)
         d_lg = torch.empty(T * d.vocab, dtype=torch.float32, device=dev)
-        m.set_forward_f16(True)  # the configuration the prefill line is quoted on
+        m.set_forward_f16(f16)  # on: the configuration the prefill line is quoted on
         for _ in range(2):
             m.forward_dev(d_ids.data_ptr(), 1, T, d_lg.data_ptr(), 0, 0, 0)
             m.sync()
@@ -619,7 +620,7 @@ def main():
                     help="time two models' forwards on one stream and on two streams")
     args = ap.parse_args()
     if args.pmc_probe:
-        pmc_probe(args.pmc_probe)
+        pmc_probe(args.pmc_probe, f16=args.operands != "split")
         return
     if args.streams_probe:
         streams_probe()
