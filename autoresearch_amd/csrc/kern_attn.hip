@@ -489,8 +489,14 @@ void launch_attn_hd(hipStream_t s, const AttnArgs& p, dim3 grid, bool split) {
   static std::atomic<uint64_t> lds_set{0};
   raise_lds_once((const void*)k_attn_mfma<HD, P16>, lds, &lds_set);
   FG_LAUNCH((k_attn_mfma<HD, P16>), grid, dim3(512), lds, s, p);
-  const dim3 mgrid((unsigned)(p.nbh * p.nqb * (QB / merge_queries<HD>())));
-  if (split) FG_LAUNCH((k_attn_merge<HD, P16>), mgrid, dim3(256), 0, s, p);
+  if (!split) return;
+  // the merge takes query blocks from the last one down, and a block's chunk
+  // count never falls as its index grows: the grid ends before the blocks
+  // that fit in one chunk (written by the attention kernel itself)
+  int nm = 0;
+  while (nm < p.nqb && chunk_count(p.nqb - 1 - nm, p.T, p.pos0, p.nvalid, p.ck) > 1) ++nm;
+  const dim3 mgrid((unsigned)(p.nbh * nm * (QB / merge_queries<HD>())));
+  if (nm > 0) FG_LAUNCH((k_attn_merge<HD, P16>), mgrid, dim3(256), 0, s, p);
 }
 
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
