@@ -87,20 +87,9 @@ def build_seedgen() -> str:
     return out
 
 
-def build_probes() -> str:
-    """The platform probe (clock, launch floor, stream overlap): a standalone
-    program, no engine code."""
-    src = os.path.join(PKG, "probes", "platform_probe.hip")
-    exe = os.path.join(PKG, "probes", "platform_probe")
-    _run([HIPCC, *[f for f in HIP_FLAGS if f != "-fPIC"], src, "-o", exe + ".tmp"])
-    os.replace(exe + ".tmp", exe)
-    return exe
-
-
 def build(fortran: bool = True) -> None:
     build_seedgen()
     build_hip()
-    build_probes()
     if fortran and os.path.exists(os.path.join(FSRC, F_PROGRAMS[0])):
         build_fortran()
 

@@ -230,6 +230,40 @@ int32_t check_device(int* dev_out) {
   return FG_OK;
 }
 
+// Initialisation and uploads are queued on the handle's own stream, never on
+// the null stream. The handle's stream is non-blocking, so nothing orders
+// null-stream work (plain hipMemset / hipMemcpy) against it, and a plain
+// hipMemset of device memory may return before the fill has run: a clear
+// queued there can land after the handle's first kernels have written the
+// buffer. (A new fp32 KV cache is ~7 GB of clearing at the B=64 batched
+// decode shape; the split key/value planes cleared behind it were zeroed
+// again after the prompt's first QKV tiles had written them, and the
+// sequences whose rows those tiles hold left the reference's greedy ids.)
+// Every buffer the engine allocates starts zeroed through here, so no read
+// of an unwritten element can depend on what the memory held before.
+int32_t dev_zero(fg_model* m, void* p, size_t bytes) {
+  if (p && bytes) HIPCHK(hipMemsetAsync(p, 0, bytes, m->stream));
+  return FG_OK;
+}
+
+// Host -> device (or device -> device) copy on the handle's stream, complete
+// on return (the source may be released afterwards).
+int32_t dev_copy(fg_model* m, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+  if (!bytes) return FG_OK;
+  HIPCHK(hipMemcpyAsync(dst, src, bytes, kind, m->stream));
+  HIPCHK(hipStreamSynchronize(m->stream));
+  return FG_OK;
+}
+
+// Before a buffer the handle owns is freed or replaced: every stream may
+// still have work reading it (the device-pointer entry points run on the
+// caller's stream), so wait for the whole device.
+int32_t quiesce(fg_model* m) {
+  HIPCHK(hipStreamSynchronize(m->stream));
+  HIPCHK(hipDeviceSynchronize());
+  return FG_OK;
+}
+
 }  // namespace
 
 int32_t fgpt::check_dims(const fg_dims* in, Dims* d) {
@@ -294,10 +328,11 @@ int32_t setup_fused(fg_model* m, const bf16_t* host_main) {
   std::vector<bf16_t> hf((size_t)FUSED_NWG * m->fl.cu_bytes / 2);
   fused_pack(m->d, m->fl, m->w, host_main, hf.data());
   HIPCHK(hipMalloc((void**)&m->fused_w, hf.size() * 2));
-  HIPCHK(hipMemcpy(m->fused_w, hf.data(), hf.size() * 2, hipMemcpyHostToDevice));
   HIPCHK(hipMalloc((void**)&m->fused_slots, (size_t)m->fl.slots * 8));
-  HIPCHK(hipMemset(m->fused_slots, 0, (size_t)m->fl.slots * 8));
   HIPCHK(hipMalloc((void**)&m->fused_err, 4 * (1 + FUSED_NX)));
+  RCCHK(dev_zero(m, m->fused_slots, (size_t)m->fl.slots * 8));
+  RCCHK(dev_zero(m, m->fused_err, 4 * (1 + FUSED_NX)));
+  RCCHK(dev_copy(m, m->fused_w, hf.data(), hf.size() * 2, hipMemcpyHostToDevice));
   m->fused_ep = 1;
   m->fused_why = "";
   return FG_OK;
@@ -350,7 +385,7 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
   }
   m->wmax = wmax;
   HIPCHK(hipMalloc((void**)&w.base, w.bytes));
-  HIPCHK(hipMemcpy(w.base, h.data(), w.bytes, hipMemcpyHostToDevice));
+  RCCHK(dev_copy(m, w.base, h.data(), w.bytes, hipMemcpyHostToDevice));
   w.lm = w.base + w.layer_stride * d.L;
   w.wte = w.lm + V * D;
   return setup_fused(m, h.data());
@@ -468,7 +503,7 @@ int32_t copy_out(fg_model* m, void* dst, const void* src, size_t bytes, hipStrea
 
 int32_t ensure_work(fg_model* m, int64_t rows) {
   if (rows <= m->ws.rows) return FG_OK;
-  HIPCHK(hipStreamSynchronize(m->stream));
+  RCCHK(quiesce(m));
   free_work(m);
   const Dims& d = m->d;
   Work& ws = m->ws;
@@ -476,7 +511,7 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
   auto alloc = [&](void** p, int64_t bytes) -> int32_t {
     total += bytes;
     HIPCHK(hipMalloc(p, (size_t)bytes));
-    return FG_OK;
+    return dev_zero(m, *p, (size_t)bytes);
   };
   RCCHK(alloc((void**)&ws.x, rows * d.D * 4));
   RCCHK(alloc((void**)&ws.q, rows * d.qd() * 4));
@@ -504,6 +539,7 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
       part = std::max(part, gemm_splitk_floats(r, (int)sh[0], (int)sh[1]));
   }
   if (part > 0) RCCHK(alloc((void**)&ws.part, part * 4));
+  HIPCHK(hipStreamSynchronize(m->stream));  // the clears, before any caller stream's work
   ws.rows = rows;
   m->work_bytes = total;
   m->gen++;
@@ -513,7 +549,7 @@ int32_t ensure_work(fg_model* m, int64_t rows) {
 // hi/lo key and value planes for B sequences of npos (padded) positions.
 int32_t ensure_split(fg_model* m, int64_t elems) {
   if (elems <= m->split_kv_elems) return FG_OK;
-  HIPCHK(hipStreamSynchronize(m->stream));
+  RCCHK(quiesce(m));
   if (m->ks) HIPCHK(hipFree(m->ks));
   if (m->vt) HIPCHK(hipFree(m->vt));
   m->ks = m->vt = nullptr;
@@ -522,8 +558,9 @@ int32_t ensure_split(fg_model* m, int64_t elems) {
   HIPCHK(hipMalloc((void**)&m->vt, (size_t)elems * 2 * 2));
   // the attention reads whole 64-key steps: padding positions must hold
   // finite values (zero here; later only values this engine wrote)
-  HIPCHK(hipMemset(m->ks, 0, (size_t)elems * 2 * 2));
-  HIPCHK(hipMemset(m->vt, 0, (size_t)elems * 2 * 2));
+  RCCHK(dev_zero(m, m->ks, (size_t)elems * 2 * 2));
+  RCCHK(dev_zero(m, m->vt, (size_t)elems * 2 * 2));
+  HIPCHK(hipStreamSynchronize(m->stream));
   m->split_kv_elems = elems;
   m->gen++;
   return FG_OK;
@@ -533,11 +570,13 @@ int32_t ensure_split(fg_model* m, int64_t elems) {
 int32_t ensure_attn(fg_model* m, int B, int T, int pos0) {
   const int64_t floats = attn_scratch_floats(m->d, B, T, pos0);
   if (floats <= m->attn_floats) return FG_OK;
-  HIPCHK(hipStreamSynchronize(m->stream));
+  RCCHK(quiesce(m));
   if (m->attn_part) HIPCHK(hipFree(m->attn_part));
   m->attn_part = nullptr;
   m->attn_floats = 0;
   HIPCHK(hipMalloc((void**)&m->attn_part, (size_t)floats * 4));
+  RCCHK(dev_zero(m, m->attn_part, (size_t)floats * 4));
+  HIPCHK(hipStreamSynchronize(m->stream));
   m->attn_floats = floats;
   m->gen++;
   return FG_OK;
@@ -837,11 +876,14 @@ extern "C" int32_t fg_set_rope(fg_model* m, int32_t pos0, int32_t n_pos, const f
     float *nc = nullptr, *ns = nullptr;
     HIPCHK(hipMalloc((void**)&nc, (size_t)cap * half * 4));
     HIPCHK(hipMalloc((void**)&ns, (size_t)cap * half * 4));
-    HIPCHK(hipStreamSynchronize(m->stream));
+    RCCHK(quiesce(m));
+    RCCHK(dev_zero(m, nc, (size_t)cap * half * 4));
+    RCCHK(dev_zero(m, ns, (size_t)cap * half * 4));
     if (m->rope_n > 0) {
-      HIPCHK(hipMemcpy(nc, m->d_cos, (size_t)m->rope_n * half * 4, hipMemcpyDeviceToDevice));
-      HIPCHK(hipMemcpy(ns, m->d_sin, (size_t)m->rope_n * half * 4, hipMemcpyDeviceToDevice));
+      RCCHK(dev_copy(m, nc, m->d_cos, (size_t)m->rope_n * half * 4, hipMemcpyDeviceToDevice));
+      RCCHK(dev_copy(m, ns, m->d_sin, (size_t)m->rope_n * half * 4, hipMemcpyDeviceToDevice));
     }
+    HIPCHK(hipStreamSynchronize(m->stream));
     if (m->d_cos) HIPCHK(hipFree(m->d_cos));
     if (m->d_sin) HIPCHK(hipFree(m->d_sin));
     m->d_cos = nc;
@@ -849,11 +891,12 @@ extern "C" int32_t fg_set_rope(fg_model* m, int32_t pos0, int32_t n_pos, const f
     m->rope_cap = cap;
     m->gen++;
   }
-  HIPCHK(hipStreamSynchronize(m->stream));
-  HIPCHK(hipMemcpy(m->d_cos + (size_t)pos0 * half, cos_buf, (size_t)n_pos * half * 4,
-                   hipMemcpyHostToDevice));
-  HIPCHK(hipMemcpy(m->d_sin + (size_t)pos0 * half, sin_buf, (size_t)n_pos * half * 4,
-                   hipMemcpyHostToDevice));
+  // rows being replaced may still be read by queued work on any stream
+  RCCHK(quiesce(m));
+  RCCHK(dev_copy(m, m->d_cos + (size_t)pos0 * half, cos_buf, (size_t)n_pos * half * 4,
+                 hipMemcpyHostToDevice));
+  RCCHK(dev_copy(m, m->d_sin + (size_t)pos0 * half, sin_buf, (size_t)n_pos * half * 4,
+                 hipMemcpyHostToDevice));
   if (need > m->rope_n) m->rope_n = need;
   return FG_OK;
 }
@@ -992,11 +1035,19 @@ extern "C" int32_t fg_kv_create_ex(fg_model* m, int32_t B, int32_t maxT, int32_t
   if (e == hipSuccess) e = hipMalloc((void**)&kv->v, n * esz);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_len, 8);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_ids, (size_t)B * 4);
-  if (e == hipSuccess)
-    e = hipMalloc((void**)&kv->d_part, (size_t)attn_decode_scratch_floats(m->d, B, maxT) * 4);
-  if (e == hipSuccess) e = hipMemset(kv->k, 0, n * esz);  // the caller zeroes it in the reference
-  if (e == hipSuccess) e = hipMemset(kv->v, 0, n * esz);
+  const size_t part_bytes = (size_t)attn_decode_scratch_floats(m->d, B, maxT) * 4;
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_part, part_bytes);
+  // zeroed on the handle's stream, and finished before the cache is handed
+  // out (its first user may be a caller's stream); the reference's callers
+  // zero their caches too
+  if (e == hipSuccess) e = hipMemsetAsync(kv->k, 0, n * esz, m->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->v, 0, n * esz, m->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->d_len, 0, 8, m->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->d_ids, 0, (size_t)B * 4, m->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->d_part, 0, part_bytes, m->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
   if (e != hipSuccess) {
+    (void)hipStreamSynchronize(m->stream);
     if (kv->k) (void)hipFree(kv->k);
     if (kv->v) (void)hipFree(kv->v);
     if (kv->d_len) (void)hipFree(kv->d_len);
@@ -1399,6 +1450,7 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
   if (nout > kv->cap_out) {
     if (kv->d_out) HIPCHK(hipFree(kv->d_out));
     HIPCHK(hipMalloc((void**)&kv->d_out, nout * 4));
+    RCCHK(dev_zero(m, kv->d_out, (size_t)nout * 4));
     kv->cap_out = nout;
     for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
     kv->graphs.clear();
@@ -1408,6 +1460,7 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
   if (nlg > kv->cap_lgs) {
     if (kv->d_lgs) HIPCHK(hipFree(kv->d_lgs));
     HIPCHK(hipMalloc((void**)&kv->d_lgs, nlg * 4));
+    RCCHK(dev_zero(m, kv->d_lgs, (size_t)nlg * 4));
     kv->cap_lgs = nlg;
     for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
     kv->graphs.clear();
@@ -1518,12 +1571,17 @@ extern "C" int32_t fg_decode_spec(fg_model* m, fg_kv* kv, int32_t* ids, int32_t 
   const int maxr = cfg->k + 1;
   RCCHK(check_rope(m, n_total));
   RCCHK(ensure_work(m, maxr));
-  if (!kv->d_sids) HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
+  if (!kv->d_sids) {
+    HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
+    RCCHK(dev_zero(m, kv->d_sids, (size_t)kv->maxT * 4));
+  }
   if (!kv->d_sst) {
+    const size_t spb = (size_t)attn_decode_scratch_floats(m->d, GEMV_MAX_ROWS, kv->maxT) * 4;
     HIPCHK(hipMalloc((void**)&kv->d_sst, sizeof(SpecDev)));
     HIPCHK(hipHostMalloc((void**)&kv->h_sst, sizeof(SpecDev), hipHostMallocDefault));
-    HIPCHK(hipMalloc((void**)&kv->d_spart,
-                     (size_t)attn_decode_scratch_floats(m->d, GEMV_MAX_ROWS, kv->maxT) * 4));
+    HIPCHK(hipMalloc((void**)&kv->d_spart, spb));
+    RCCHK(dev_zero(m, kv->d_sst, sizeof(SpecDev)));
+    RCCHK(dev_zero(m, kv->d_spart, spb));
   }
   if (kv->graphs_gen != m->gen) {
     for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
@@ -1606,6 +1664,7 @@ extern "C" int32_t fg_sample(fg_model* m, const float* logits, int32_t V, const 
     m->samp = nullptr;
     m->samp_bytes = 0;
     HIPCHK(hipMalloc((void**)&m->samp, need));
+    RCCHK(dev_zero(m, m->samp, (size_t)need));
     m->samp_bytes = need;
   }
   int64_t* d_state = (int64_t*)m->samp;
@@ -1688,9 +1747,13 @@ extern "C" int32_t fg_decode_sample(fg_model* m, fg_kv* kv, int32_t* ids, int32_
   if (n_total == n_known) return FG_OK;
   RCCHK(check_rope(m, n_total));
   RCCHK(ensure_work(m, 1));
-  if (!kv->d_sids) HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
+  if (!kv->d_sids) {
+    HIPCHK(hipMalloc((void**)&kv->d_sids, (size_t)kv->maxT * 4));
+    RCCHK(dev_zero(m, kv->d_sids, (size_t)kv->maxT * 4));
+  }
   if (!kv->d_smp) {
     HIPCHK(hipMalloc((void**)&kv->d_smp, sizeof(SampleDev)));
+    RCCHK(dev_zero(m, kv->d_smp, sizeof(SampleDev)));
     HIPCHK(hipHostMalloc((void**)&kv->h_smp, sizeof(SampleDev), hipHostMallocDefault));
   }
   if (kv->graphs_gen != m->gen) {

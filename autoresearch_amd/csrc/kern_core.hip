@@ -305,8 +305,13 @@ struct DecArgs {
   float* y;
   uint16_t* ys;
   int64_t ys_plane;
-  float* part;  // [rows*H][nchunk][hd + 2]: O, then max and sum
+  float* part;  // [rows*H][nchunk][hd + 4]: O, then max and sum (and two unused
+                // floats, so every partial row starts 16-byte aligned)
 };
+
+// Floats per partial row of the single-query attention: O (HD), max, sum,
+// padded to a multiple of 4 so the row's float4 accesses are aligned.
+__host__ __device__ constexpr int dec_pstride(int hd) { return hd + 4; }
 
 template <int HD>
 __device__ __forceinline__ void dec_store(const DecArgs& a, int64_t o, int d, float4 v) {
@@ -465,7 +470,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
       const float inv = 1.0f / lj;
       dec_store<HD>(a, bh * HD, d, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
     } else {
-      float* P = a.part + (bh * a.nchunk + c) * (HD + 2);
+      float* P = a.part + (bh * a.nchunk + c) * dec_pstride(HD);
       *(float4*)(P + d) = t;
       if (d == 0) {
         float mj = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
@@ -619,7 +624,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
       const float inv = 1.0f / lj;
       dec_store<HD>(a, bh * HD, d, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
     } else {
-      float* P = a.part + (bh * a.nchunk + c) * (HD + 2);
+      float* P = a.part + (bh * a.nchunk + c) * dec_pstride(HD);
       *(float4*)(P + d) = t;
       if (d == 0) *(float2*)(P + HD) = make_float2(red[2][0][j], lj);
     }
@@ -641,10 +646,10 @@ __global__ __launch_bounds__(256) void k_attn_dec_merge(DecArgs a, int dpc) {
   const int len = (a.d_len ? *a.d_len + 1 : a.len_imm) + (bh / a.H) % a.qpr;
   const int nch = (len + dpc - 1) / dpc;
   if (nch == 1) return;
-  const float* P = a.part + (int64_t)bh * a.nchunk * (HD + 2);
+  const float* P = a.part + (int64_t)bh * a.nchunk * dec_pstride(HD);
   const int g = tid / LPC, dl = tid % LPC;
   float mx = -FLT_MAX;
-  for (int c = tid; c < nch; c += 256) mx = fmaxf(mx, P[(int64_t)c * (HD + 2) + HD]);
+  for (int c = tid; c < nch; c += 256) mx = fmaxf(mx, P[(int64_t)c * dec_pstride(HD) + HD]);
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, l = 0.f, m = 0.f;
   float2 ml[CPG];
   float4 ov[CPG][2];
@@ -652,7 +657,7 @@ __global__ __launch_bounds__(256) void k_attn_dec_merge(DecArgs a, int dpc) {
 #pragma unroll
     for (int k = 0; k < CPG; ++k) {
       const int c = c0 + k * NG;
-      const float* pc = P + (int64_t)(c < nch ? c : 0) * (HD + 2);
+      const float* pc = P + (int64_t)(c < nch ? c : 0) * dec_pstride(HD);
       ml[k] = *(const float2*)(pc + HD);
       ov[k][0] = *(const float4*)(pc + 8 * dl);
       ov[k][1] = *(const float4*)(pc + 8 * dl + 4);
@@ -697,7 +702,7 @@ __global__ __launch_bounds__(256) void k_attn_dec_merge(DecArgs a, int dpc) {
 int attn_decode_chunks(int maxT) { return (maxT + DPC_MIN - 1) / DPC_MIN; }
 
 int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT) {
-  return (int64_t)B * d.H * attn_decode_chunks(maxT) * (d.hd + 2);
+  return (int64_t)B * d.H * attn_decode_chunks(maxT) * dec_pstride(d.hd);
 }
 
 namespace {
