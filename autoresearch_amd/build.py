@@ -26,8 +26,10 @@ HIP_SOURCES = ["fgpt_engine.hip", "fgpt_weights.hip", "fgpt_spec.hip", "kern_cor
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function", "-Wno-unused-result"]
-F_SOURCES = ["fgpt_c.f90", "fgpt_drop_in.f90"]
+F_SOURCES = ["fgpt_c.f90", "fgpt_drop_in.f90", "fgpt_util.f90"]
 F_PROGRAMS = ["fgpt_run.f90"]
+# check programs of the drop-in (test code, built next to their sources)
+F_CHECKS = [os.path.join(ROOT, "tests", "fortran", "dropin_checks.f90")]
 
 
 def _run(cmd, cwd=None):
@@ -76,6 +78,12 @@ def build_fortran() -> str:
         _run([FLANG, "-O2", "-I", mod, os.path.join(FSRC, prog), *objs, "-L", PKG, "-lfgpt",
               "-Wl,-rpath,$ORIGIN", "-o", exe + ".tmp"])
         os.replace(exe + ".tmp", exe)
+    for src in F_CHECKS:
+        out = src[:-len(".f90")]
+        rpath = os.path.relpath(PKG, os.path.dirname(src))
+        _run([FLANG, "-O2", "-I", mod, src, *objs, "-L", PKG, "-lfgpt",
+              f"-Wl,-rpath,$ORIGIN/{rpath}", "-o", out + ".tmp"])
+        os.replace(out + ".tmp", out)
     return exe
 
 

@@ -111,6 +111,12 @@ struct fg_model {
   uint16_t* w16 = nullptr;
   float w16_scale = 1.f, w16_inv = 1.f, wmax = 0.f;
   std::string fused_why = "not set up";
+  // the single-term fp16 passes' overflow flag (device, one word): set by
+  // an epilogue whose fp16 store would round to inf (FG_ERANGE)
+  uint32_t* d_ovf = nullptr;
+  // fg_forward_pos's per-item positive-score counts (device), grown on use
+  uint32_t* d_pos = nullptr;
+  int64_t pos_cap = 0;
   // two pinned staging buffers (and their events) for large copies to the
   // caller's host memory, made on first use (copy_out)
   void* pin[2] = {nullptr, nullptr};
@@ -386,6 +392,9 @@ int32_t upload_weights(fg_model* m, const float* const st[8]) {
   m->wmax = wmax;
   HIPCHK(hipMalloc((void**)&w.base, w.bytes));
   RCCHK(dev_copy(m, w.base, h.data(), w.bytes, hipMemcpyHostToDevice));
+  HIPCHK(hipMalloc((void**)&m->d_ovf, 4));
+  RCCHK(dev_zero(m, m->d_ovf, 4));
+  HIPCHK(hipStreamSynchronize(m->stream));
   w.lm = w.base + w.layer_stride * d.L;
   w.wte = w.lm + V * D;
   return setup_fused(m, h.data());
@@ -624,6 +633,9 @@ struct PassOpts {
   bool kv16 = false;      // the cache holds bf16 elements
   bool f16 = false;       // single-term fp16 MFMA pass where the MFMA path runs (> 128 rows)
   float* nll_part = nullptr;  // lm_head writes the cross-entropy's partials here (GEMM path)
+  // (nullable) the chunk attention's positive-score counts, attn_items(...)
+  // per layer, layer after layer
+  uint32_t* pos_cnt = nullptr;
 };
 
 // One pass over rows = B*T token rows: embedding of ids, the layer stack,
@@ -656,6 +668,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   const int64_t hplane = (int64_t)rows * d.dff;
   // ssq partials per row after the attention-output RESID
   const int nt_resid = gemm_ssq_parts(rows, d.D, d.qd());
+  const int64_t pos_items = o.pos_cnt ? attn_items(d, B, T, pos0) : 0;
 
   if (embed)  // (else x already holds the embedded rows)
     timed(m, s, FG_K_OTHER, 0, (double)rows * d.D * (gm ? 10 : 6), [&] {
@@ -691,6 +704,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     }
     a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
     a.f16 = f16 ? 1 : 0;
+    a.ovf = f16 ? m->d_ovf : nullptr;
     a.wscale = m->w16_inv;
     a.w = W(m->w.qkv(l)); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
     linear(m, s, GV_QKV, a, d_pos, gm);
@@ -712,7 +726,8 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
         });
       timed(m, s, FG_K_ATTN_CHUNK, at_flops, at_bytes, [&] {
         launch_attn_mfma(s, d, m->qs, m->ks, m->vt, B, T, npos, pos0, aplane,
-                         (int64_t)B * npos * d.kvd(), m->attn_part, ws.ao, aos, aplane, f16);
+                         (int64_t)B * npos * d.kvd(), m->attn_part, ws.ao, aos, aplane, f16,
+                         o.pos_cnt ? o.pos_cnt + l * pos_items : nullptr);
       });
     }
     // x += attn_out Wproj^T (GEMM path: also the split x and its row sums)
@@ -737,6 +752,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
   a.M = rows; a.T = T; a.d_M = o.d_rows;
   a.x = ws.x; a.xs = ws.xs; a.xs_plane = xplane; a.ssq_in = ws.ssq; a.ssq_n = nt;
   a.f16 = f16 ? 1 : 0;
+  a.ovf = f16 ? m->d_ovf : nullptr;
   a.wscale = m->w16_inv;
   a.w = W(m->w.lm); a.N = d.V; a.K = d.D; a.norm = 1; a.y = logits;
   a.nll_part = gm ? o.nll_part : nullptr;
@@ -751,7 +767,8 @@ int32_t check_rope(fg_model* m, int64_t upto) {
 }
 
 int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_logits,
-                     const int32_t* d_tgt, float* d_nll, hipStream_t s) {
+                     const int32_t* d_tgt, float* d_nll, hipStream_t s,
+                     uint32_t* d_pos_cnt = nullptr) {
   if (B < 1 || T < 1) return seterr(FG_EARG, "B and T must be >= 1");
   RCCHK(check_rope(m, T));
   const int64_t rows = (int64_t)B * T;
@@ -768,6 +785,7 @@ int32_t forward_core(fg_model* m, const int32_t* d_ids, int B, int T, float* d_l
   const bool nll_parts = d_tgt && d_nll && m->ws.nllp && use_gemm(m->d, rows) &&
                          gemm_store_nll(rows, m->d.V);
   if (nll_parts) o.nll_part = m->ws.nllp;
+  o.pos_cnt = d_pos_cnt;
   layer_stack(m, s, d_ids, B, T, 0, nullptr, nullptr, nullptr, T, 0, nullptr, logits, o);
   if (nll_parts)
     timed(m, s, FG_K_OTHER, 0, (double)rows * (m->d.V / NLL_GROUP_COLS) * 8 + rows * 12, [&] {
@@ -838,6 +856,8 @@ extern "C" int32_t fg_model_destroy(fg_model* m) {
   if (m->ks) (void)hipFree(m->ks);
   if (m->vt) (void)hipFree(m->vt);
   if (m->attn_part) (void)hipFree(m->attn_part);
+  if (m->d_pos) (void)hipFree(m->d_pos);
+  if (m->d_ovf) (void)hipFree(m->d_ovf);
   if (m->samp) (void)hipFree(m->samp);
   if (m->w.base) (void)hipFree(m->w.base);
   if (m->fused_w) (void)hipFree(m->fused_w);
@@ -901,8 +921,26 @@ extern "C" int32_t fg_set_rope(fg_model* m, int32_t pos0, int32_t n_pos, const f
   return FG_OK;
 }
 
-extern "C" int32_t fg_forward(fg_model* m, const int32_t* ids, int32_t B, int32_t T,
-                              float* logits, const int32_t* targets, float* nll) {
+namespace {
+
+// After a pass queued on s: FG_ERANGE when a single-term fp16 epilogue
+// raised the overflow flag (the flag is cleared again).
+int32_t check_f16_range(fg_model* m, hipStream_t s) {
+  if (!m->fwd_f16) return FG_OK;
+  uint32_t f = 0;
+  HIPCHK(hipMemcpyAsync(&f, m->d_ovf, 4, hipMemcpyDeviceToHost, s));
+  HIPCHK(hipStreamSynchronize(s));
+  if (f == 0) return FG_OK;
+  launch_zero_u32(s, m->d_ovf, 1);
+  HIPCHK(hipStreamSynchronize(s));
+  return seterr(FG_ERANGE, "an activation of the single-term fp16 pass reached fp16's range "
+                           "limit (|x| >= 65520): results invalid; run without "
+                           "FG_OPT_FORWARD_F16");
+}
+
+// fg_forward, and with npos set attn_sgemm's positive-score statistic.
+int32_t forward_host(fg_model* m, const int32_t* ids, int32_t B, int32_t T, float* logits,
+                     const int32_t* targets, float* nll, int32_t* npos) {
   if (!m || !ids) return seterr(FG_EARG, "NULL argument");
   if (B < 1 || T < 1) return seterr(FG_EARG, "B and T must be >= 1");
   const int64_t rows = (int64_t)B * T;
@@ -917,14 +955,54 @@ extern "C" int32_t fg_forward(fg_model* m, const int32_t* ids, int32_t B, int32_
   GUARD(m);
   RCCHK(ensure_work(m, rows));
   hipStream_t s = m->stream;
+  const int64_t items = npos ? attn_items(m->d, B, T, 0) : 0;
+  if (npos && items * m->d.L > m->pos_cap) {
+    RCCHK(quiesce(m));
+    if (m->d_pos) HIPCHK(hipFree(m->d_pos));
+    m->d_pos = nullptr;
+    m->pos_cap = 0;
+    HIPCHK(hipMalloc((void**)&m->d_pos, (size_t)items * m->d.L * 4));
+    RCCHK(dev_zero(m, m->d_pos, (size_t)items * m->d.L * 4));
+    m->pos_cap = items * m->d.L;
+  }
   HIPCHK(hipMemcpyAsync(m->ws.ids, ids, rows * 4, hipMemcpyHostToDevice, s));
   if (targets) HIPCHK(hipMemcpyAsync(m->ws.tgt, targets, rows * 4, hipMemcpyHostToDevice, s));
+  if (m->fwd_f16) launch_zero_u32(s, m->d_ovf, 1);
   RCCHK(forward_core(m, m->ws.ids, B, T, m->ws.logits, targets ? m->ws.tgt : nullptr,
-                     targets ? m->ws.nll : nullptr, s));
+                     targets ? m->ws.nll : nullptr, s, npos ? m->d_pos : nullptr));
+  RCCHK(check_f16_range(m, s));
   if (logits) RCCHK(copy_out(m, logits, m->ws.logits, (size_t)rows * m->d.V * 4, s));
   if (targets && nll) HIPCHK(hipMemcpyAsync(nll, m->ws.nll, rows * 4, hipMemcpyDeviceToHost, s));
+  std::vector<uint32_t> cnt(npos ? (size_t)items * m->d.L : 0);
+  if (npos) HIPCHK(hipMemcpyAsync(cnt.data(), m->d_pos, cnt.size() * 4, hipMemcpyDeviceToHost, s));
   HIPCHK(hipStreamSynchronize(s));
+  if (npos) {
+    // item i of a layer belongs to (row * H + head) = i % (B * H); its
+    // counts are whole numbers of scores, so the sums are exact
+    const int64_t nbh = (int64_t)B * m->d.H;
+    std::vector<int64_t> sum((size_t)nbh);
+    for (int l = 0; l < m->d.L; ++l) {
+      std::fill(sum.begin(), sum.end(), 0);
+      for (int64_t i = 0; i < items; ++i) sum[i % nbh] += cnt[(size_t)l * items + i];
+      for (int64_t bh = 0; bh < nbh; ++bh) npos[l * nbh + bh] = (int32_t)sum[bh];
+    }
+  }
   return FG_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t fg_forward(fg_model* m, const int32_t* ids, int32_t B, int32_t T,
+                              float* logits, const int32_t* targets, float* nll) {
+  return forward_host(m, ids, B, T, logits, targets, nll, nullptr);
+}
+
+extern "C" int32_t fg_forward_pos(fg_model* m, const int32_t* ids, int32_t B, int32_t T,
+                                  float* logits, const int32_t* targets, float* nll,
+                                  int32_t* npos) {
+  if (!npos) return seterr(FG_EARG, "npos is NULL");
+  if (T > 65535) return seterr(FG_EARG, "T %d: the counts of T(T+1)/2 scores overflow", T);
+  return forward_host(m, ids, B, T, logits, targets, nll, npos);
 }
 
 extern "C" int32_t fg_eval_bpb(fg_model* m, const int32_t* rows, int32_t n_rows, int32_t T,
@@ -975,6 +1053,7 @@ extern "C" int32_t fg_eval_bpb(fg_model* m, const int32_t* rows, int32_t n_rows,
       const int64_t n = (int64_t)nb * T;
       HIPCHK(hipMemcpyAsync(m->ws.ids, ids.data(), n * 4, hipMemcpyHostToDevice, s));
       HIPCHK(hipMemcpyAsync(m->ws.tgt, tgt.data(), n * 4, hipMemcpyHostToDevice, s));
+      if (m->fwd_f16) launch_zero_u32(s, m->d_ovf, 1);
       RCCHK(forward_core(m, m->ws.ids, nb, T, m->ws.logits, m->ws.tgt, m->ws.nll, s));
       timed(m, s, FG_K_OTHER, 0, (double)n * 12, [&] {
         launch_bpb_rows(s, m->ws.nll, m->ws.tgt, nb, T, d_tb, d_rn, d_rb);
@@ -983,6 +1062,7 @@ extern "C" int32_t fg_eval_bpb(fg_model* m, const int32_t* rows, int32_t n_rows,
       HIPCHK(hipMemcpyAsync(rn.data(), d_rn, nb * sizeof(double), hipMemcpyDeviceToHost, s));
       HIPCHK(hipMemcpyAsync(rb.data(), d_rb, nb * sizeof(long long), hipMemcpyDeviceToHost, s));
       HIPCHK(hipStreamSynchronize(s));
+      RCCHK(check_f16_range(m, s));
       for (int b = 0; b < nb; ++b) {  // rows in order, as bpb_agg adds them
         if (row_nats) row_nats[r0 + b] = rn[b];
         if (row_bytes) row_bytes[r0 + b] = rb[b];
@@ -1864,7 +1944,7 @@ extern "C" int32_t fg_sync(fg_model* m) {
   if (!m) return seterr(FG_EARG, "NULL argument");
   GUARD(m);
   HIPCHK(hipStreamSynchronize(m->stream));
-  return FG_OK;
+  return check_f16_range(m, m->stream);
 }
 
 extern "C" int32_t fg_timing(fg_model* m, int32_t enable) {

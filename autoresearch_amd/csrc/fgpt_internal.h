@@ -109,6 +109,8 @@ struct KVCacheDev {
 // d_rows (nullable): rows live this launch, read on the device.
 // dst[i] = fp16(bf16 src[i] * scale) (scale a power of 2), i < n.
 void launch_to_f16(hipStream_t s, const bf16_t* src, uint16_t* dst, int64_t n, float scale);
+// p[0..n) = 0 by a kernel (capturable, unlike a memset node).
+void launch_zero_u32(hipStream_t s, uint32_t* p, int n);
 
 void launch_embed_norm(hipStream_t s, const Dims& d, const bf16_t* wte, const int32_t* ids,
                        int64_t rows, float* x, uint16_t* xs = nullptr, int64_t plane = 0,
@@ -172,6 +174,9 @@ struct GemvArgs {
   // exp(logit - maximum), [M][N/NLL_GROUP_COLS][2]; the GEMM then runs where
   // it can write them (gemm_store_nll says when)
   float* nll_part;
+  // single-term fp16 pass (nullable): set to 1 by any epilogue whose fp16
+  // operand store would round a value to inf (|v| >= 65520 or not finite)
+  uint32_t* ovf;
 };
 void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a);
 
@@ -205,10 +210,14 @@ inline void raise_lds_once(const void* fn, size_t bytes, std::atomic<uint64_t>* 
   (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
   if (bit) done->fetch_or(bit, std::memory_order_release);
 }
+// pos_cnt (nullable): one count per work item, attn_items(d, B, T, pos0) of
+// them, item i belonging to (sequence * H + head) = i % (B * H): how many of
+// the item's causal scores q.k are > 0 (src/lib/fortran_attn.f90:247-300).
+int64_t attn_items(const Dims& d, int B, int T, int pos0);
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
                       int64_t kv_plane, float* scratch, float* y, uint16_t* ys = nullptr,
-                      int64_t ys_plane = 0, bool f16 = false);
+                      int64_t ys_plane = 0, bool f16 = false, uint32_t* pos_cnt = nullptr);
 // Fill the hi/lo key/value planes for cache positions [0, n) from the cache
 // of one layer ([B][maxT][KH*hd], fp32, or bf16 with kv16: lo planes zero).
 void launch_split_cache(hipStream_t s, const Dims& d, const void* kc, const void* vc, bool kv16,

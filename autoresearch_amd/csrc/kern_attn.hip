@@ -66,6 +66,10 @@ struct AttnArgs {
   uint16_t* ys;
   int64_t ys_plane;
   float* part;
+  // (nullable) per work item (blockIdx.x): how many of its causal scores
+  // q.k are > 0 -- attn_sgemm's positive-score statistic
+  // (src/lib/fortran_attn.f90:247-300), counted before the softmax
+  uint32_t* pos_cnt;
 };
 
 // key chunks of query block j (queries j*QB .. j*QB+QB-1)
@@ -198,6 +202,8 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[i][r] = 0.f;
   float m_run = -FLT_MAX, l_run = 0.f;  // in the log2 domain
+  uint32_t npos = 0;  // this lane's positive causal scores (p.pos_cnt)
+  __shared__ float wpos[8];
   const float cs = LOG2E / sqrtf((float)HD);
 
   fill(0, kbeg);
@@ -237,6 +243,10 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         sc[r] = kt0 + 16 * (r >> 3) + 8 * g + (r & 7) < klim ? sc[r] : -INFINITY;
+    }
+    if (p.pos_cnt) {  // (masked scores are -inf; a query past T has q = 0, so s = 0)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) npos += sc[r] > 0.f ? 1u : 0u;
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -298,9 +308,19 @@ __global__ __launch_bounds__(512) void k_attn_mfma(AttnArgs p) {
     }
   }
 
+  if (p.pos_cnt) {  // (a wavefront's count is below 2^24: its float sum is exact)
+    const float wc = wave_sum((float)npos);
+    if (lane == 0) wpos[wv] = wc;
+  }
   // merge the two key parities of each query group through LDS (no DMA is
   // in flight: the last step issued none and waited for its own)
   __syncthreads();
+  if (p.pos_cnt && tid == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) t += wpos[w];
+    p.pos_cnt[blockIdx.x] = (uint32_t)t;
+  }
   float* xo = reinterpret_cast<float*>(lds) + qg * (ND * 16 * 64 + 128);
   if (kp == 1) {
 #pragma unroll
@@ -469,6 +489,11 @@ int attn_chunk_keys(int BH, int T, int pos0) {
   return best;
 }
 
+int64_t attn_items(const Dims& d, int B, int T, int pos0) {
+  const int nbh = B * d.H;
+  return (int64_t)nbh * attn_items_per_head(T, pos0, attn_chunk_keys(nbh, T, pos0));
+}
+
 int64_t attn_scratch_floats(const Dims& d, int B, int T, int pos0) {
   // sized for the shortest chunks (the most items)
   return (int64_t)B * d.H * attn_items_per_head(T, pos0, CK_MIN) * QB * (d.hd + 2);
@@ -502,7 +527,7 @@ void launch_attn_hd(hipStream_t s, const AttnArgs& p, dim3 grid, bool split) {
 void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const uint16_t* ks,
                       const uint16_t* vt, int B, int T, int npos, int pos0, int64_t q_plane,
                       int64_t kv_plane, float* scratch, float* y, uint16_t* ys,
-                      int64_t ys_plane, bool f16) {
+                      int64_t ys_plane, bool f16, uint32_t* pos_cnt) {
   AttnArgs p;
   p.qs = qs;
   p.ks = ks;
@@ -523,6 +548,7 @@ void launch_attn_mfma(hipStream_t s, const Dims& d, const uint16_t* qs, const ui
   p.ys = ys;
   p.ys_plane = ys_plane;
   p.part = scratch;
+  p.pos_cnt = pos_cnt;
   const dim3 grid((unsigned)(p.nbh * p.iph));
   const bool split = p.iph > p.nqb;  // some query block spans several chunks
   if (d.hd == 128) {

@@ -99,6 +99,14 @@ __global__ __launch_bounds__(256) void k_to_f16(const bf16_t* __restrict__ src,
     dst[i] = f32_to_f16_rne(bf16_to_f32(src[i]) * scale);
 }
 
+__global__ __launch_bounds__(64) void k_zero_u32(uint32_t* __restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += 64) p[i] = 0u;
+}
+
+void launch_zero_u32(hipStream_t s, uint32_t* p, int n) {
+  if (n > 0) FG_LAUNCH(k_zero_u32, dim3(1), dim3(64), 0, s, p, n);
+}
+
 void launch_to_f16(hipStream_t s, const bf16_t* src, uint16_t* dst, int64_t n, float scale) {
   if (n <= 0) return;
   const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);

@@ -114,6 +114,18 @@ __device__ __forceinline__ void put4(const float (&v)[4], uint16_t* p, int64_t p
     split_bf16x4<NT>(v, p, plane);
 }
 
+// The single-term fp16 pass stores its activations as fp16, whose largest
+// finite value is 65504: an fp32 value of magnitude 65520 or more (or one
+// that is not finite) would become inf. Such a value raises the pass's
+// overflow flag, which the host turns into an error instead of returning
+// inf / NaN logits.
+template <bool P16>
+__device__ __forceinline__ void f16_guard(const GemvArgs& a, float v) {
+  if constexpr (P16) {
+    if (!(fabsf(v) < 65520.f) && a.ovf) *a.ovf = 1u;
+  }
+}
+
 // RoPE coefficients of stored column pair r for token row m (q and k
 // columns; v columns take none).
 __device__ __forceinline__ void qkv_pair_coeffs(const GemvArgs& a, int m, int pos0, int r,
@@ -139,6 +151,8 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
     const int head = base / hd, j = (base % hd) >> 1;
     const float y1 = x1 * cs + x2 * sn;
     const float y2 = x1 * (-sn) + x2 * cs;
+    f16_guard<P16>(a, y1);
+    f16_guard<P16>(a, y2);
     if (isq) {
       if (a.qs) {
         uint16_t* p = a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd;
@@ -164,6 +178,8 @@ __device__ __forceinline__ void qkv_pair_store(const GemvArgs& a, int m, int pos
   } else {
     const int base = r - qd - kd;
     const int head = base / hd, j = (base % hd) >> 1;
+    f16_guard<P16>(a, x1);
+    f16_guard<P16>(a, x2);
     if (a.vc) {
       const int64_t v = ((int64_t)b * a.maxT + pos) * kd + head * hd;
       kv_put(a, a.vc, v + j, x1);
@@ -198,6 +214,8 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
       const float x1 = x[2 * i], x2 = x[2 * i + 1];
       y1[i] = x1 * c[i] + x2 * s[i];
       y2[i] = x1 * (-s[i]) + x2 * c[i];
+      f16_guard<P16>(a, y1[i]);
+      f16_guard<P16>(a, y2[i]);
     }
     if (isq) {
       if (a.qs) {
@@ -231,6 +249,8 @@ __device__ __forceinline__ void qkv_quad_store(const GemvArgs& a, int m, int pos
   } else {
     const int base = r8 - qd - kd;
     const int head = base / hd, j = (base % hd) >> 1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f16_guard<P16>(a, x[i]);
     if (a.vc) {
       const int64_t v = ((int64_t)b * a.maxT + pos) * kd + head * hd;
       kv_put4(a, a.vc, v + j, x[0], x[2], x[4], x[6]);
@@ -274,6 +294,7 @@ __device__ __forceinline__ void qkv_elem_epilogue(const GemvArgs& a, int m, int 
     const float sn = a.sinb[(int64_t)pos * (hd / 2) + j];
     const float x1 = odd ? other : own, x2 = odd ? own : other;
     const float yv = odd ? x1 * (-sn) + x2 * cs : x1 * cs + x2 * sn;
+    f16_guard<P16>(a, yv);
     if (isq) {
       if (a.qs)
         put1<P16>(yv, a.qs + (((int64_t)b * a.H + head) * a.T + t) * hd + dim, a.q_plane);
@@ -288,6 +309,7 @@ __device__ __forceinline__ void qkv_elem_epilogue(const GemvArgs& a, int m, int 
   } else {
     const int base = r - qd - kd;
     const int head = base / hd, j = (base % hd) >> 1, dim = odd ? j + hd / 2 : j;
+    f16_guard<P16>(a, own);
     if (a.vc) kv_put(a, a.vc, ((int64_t)b * a.maxT + pos) * kd + head * hd + dim, own);
     if (a.vt)
       put1<P16>(kv_val(a, own), a.vt + (((int64_t)b * a.KH + head) * hd + dim) * a.npos + pos,

@@ -138,6 +138,11 @@ __device__ __forceinline__ void qkv_tile_pass(const GemvArgs& a, const float* st
           x2[i] = kv_val(a, x2[i]);
         }
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f16_guard<P16>(a, x1[i]);
+        f16_guard<P16>(a, x2[i]);
+      }
       put4<P16, NT_QKV>(x1, p + (int64_t)j * a.npos, a.kv_plane);
       put4<P16, NT_QKV>(x2, p + (int64_t)(j + hd / 2) * a.npos, a.kv_plane);
       if (a.vc) {
@@ -404,6 +409,8 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
           o.x += v0;
           o.y += v1;
           store_v<NT_RESID>(reinterpret_cast<f32x2_t*>(y), f32x2_t{o.x, o.y});
+          f16_guard<P16>(a, o.x);
+          f16_guard<P16>(a, o.y);
           put2<P16, NT_RESID>(o.x, o.y, a.ys + (int64_t)m * a.N + n, a.ys_plane);
         }
         // the row's sum of squares over this tile
@@ -417,6 +424,8 @@ __global__ __launch_bounds__(64 * NWM * NWN * KG) void k_gemm(GemvArgs a,
       } else if (EPI == GV_RELU2) {
         if (live) {
           const float t0 = v0 < 0.f ? 0.f : v0, t1 = v1 < 0.f ? 0.f : v1;
+          f16_guard<P16>(a, t0 * t0);
+          f16_guard<P16>(a, t1 * t1);
           put2<P16, NT_RELU2>(t0 * t0, t1 * t1, a.ys + (int64_t)m * a.N + n, a.ys_plane);
         }
       } else {
@@ -611,6 +620,8 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
             const int b = m / a.T;
             uint16_t* p = a.vt + (((int64_t)b * a.KH + head) * a.hd + dim) * a.npos + pos;
             const float w4[4] = {v[4 * rq], v[4 * rq + 1], v[4 * rq + 2], v[4 * rq + 3]};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) f16_guard<P16>(a, w4[e]);
             put4<P16>(w4, p, a.kv_plane);
           } else {
 #pragma unroll
@@ -630,10 +641,12 @@ __global__ __launch_bounds__(64 * NWM * NWN) void k_gemm2(GemvArgs a,
           if (EPI == GV_RESID) {
             const float x = a.y[o] + v[r];
             a.y[o] = x;
+            f16_guard<P16>(a, x);
             put1<P16>(x, a.ys + o, a.ys_plane);
             ssq[r] += x * x;
           } else if (EPI == GV_RELU2) {
             const float t = v[r] < 0.f ? 0.f : v[r];
+            f16_guard<P16>(a, t * t);
             put1<P16>(t * t, a.ys + o, a.ys_plane);
           } else {
             __builtin_nontemporal_store(v[r], a.y + o);  // logits: read once, later

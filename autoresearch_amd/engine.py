@@ -23,14 +23,14 @@ LIB_PATH = os.path.join(_PKG, "libfgpt.so")
 
 FG_ERRORS = {
     -1: "FG_EARG", -2: "FG_EDIMS", -3: "FG_EWEIGHT", -4: "FG_EHIP", -5: "FG_EFULL",
-    -6: "FG_EROPE", -7: "FG_ENODEV", -8: "FG_EBUSY", -9: "FG_EARCH",
+    -6: "FG_EROPE", -7: "FG_ENODEV", -8: "FG_EBUSY", -9: "FG_EARCH", -10: "FG_ERANGE",
 }
 
 # every symbol include/fgpt.h declares
 EXPORTS = (
     "fg_version", "fg_last_error", "fg_model_create", "fg_weights_read", "fg_model_load",
     "fg_model_destroy",
-    "fg_set_rope", "fg_forward", "fg_forward_dev", "fg_kv_create", "fg_kv_create_ex", "fg_kv_destroy",
+    "fg_set_rope", "fg_forward", "fg_forward_pos", "fg_forward_dev", "fg_kv_create", "fg_kv_create_ex", "fg_kv_destroy",
     "fg_kv_len", "fg_kv_set_len", "fg_kv_read", "fg_step", "fg_step_multi",
     "fg_decode_greedy", "fg_sync", "fg_model_bytes", "fg_timing", "fg_timing_read",
     "fg_eval_bpb", "fg_rows_npy", "fg_decode_spec", "fg_spec_accept", "fg_spec_draft",
@@ -108,6 +108,7 @@ def load_library(path: str = LIB_PATH):
         "fg_model_destroy": (i32, [_vp]),
         "fg_set_rope": (i32, [_vp, i32, i32, _f, _f]),
         "fg_forward": (i32, [_vp, _i, i32, i32, _f, _i, _f]),
+        "fg_forward_pos": (i32, [_vp, _i, i32, i32, _f, _i, _f, _i]),
         "fg_forward_dev": (i32, [_vp, _vp, i32, i32, _vp, _vp, _vp, _vp]),
         "fg_kv_create": (i32, [_vp, i32, i32, C.POINTER(_vp)]),
         "fg_kv_create_ex": (i32, [_vp, i32, i32, i32, C.POINTER(_vp)]),
@@ -217,6 +218,34 @@ class Model:
         _check(_LIB.fg_forward(self._h, _ip(ids), B, T, _fp(lg), _ip(tg), _fp(nll)))
         lg = lg.reshape(B, T, self.d.vocab) if lg is not None else None
         return lg, (nll.reshape(B, T) if nll is not None else None)
+
+    def forward_pos(self, ids, B: int, T: int, want_logits: bool = True):
+        """fg_forward_pos: the forward's logits and attn_sgemm's positive-score
+        counts per layer, row and head ([L, B, H] int32)."""
+        ids = _i32(ids).reshape(-1)
+        if ids.size != B * T:
+            raise ValueError("ids must hold B*T values")
+        lg = np.empty(B * T * self.d.vocab, np.float32) if want_logits else None
+        npos = np.zeros(self.d.n_layer * B * self.d.n_head, np.int32)
+        _check(_LIB.fg_forward_pos(self._h, _ip(ids), B, T, _fp(lg), None, None, _ip(npos)))
+        lg = lg.reshape(B, T, self.d.vocab) if lg is not None else None
+        return lg, npos.reshape(self.d.n_layer, B, self.d.n_head)
+
+    @staticmethod
+    def pos_frac_accumulate(npos, T: int, pos_frac=None, pos_n=None):
+        """The reference's accumulation of the counts into pos_frac / pos_n
+        (src/lib/fortran_attn.f90:291-296): per (layer, row) in that order,
+        pos_frac[h] += npos / (T(T+1)/2) in fp32, pos_n[h] += 1."""
+        L, B, H = npos.shape
+        pf = np.zeros(H, np.float32) if pos_frac is None else pos_frac
+        pn = np.zeros(H, np.int32) if pos_n is None else pos_n
+        den = np.float32(T * (T + 1) // 2)
+        for ll in range(L):
+            for aa in range(B):
+                for bb in range(H):
+                    pf[bb] = np.float32(pf[bb] + np.float32(npos[ll, aa, bb]) / den)
+                    pn[bb] += 1
+        return pf, pn
 
     def forward_dev(self, d_ids: int, B: int, T: int, d_logits: int = 0, d_targets: int = 0,
                     d_nll: int = 0, stream: int = 0):

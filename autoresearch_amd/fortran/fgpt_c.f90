@@ -11,7 +11,7 @@ module fgpt_c
 
   integer(c_int32_t), parameter, public :: FG_OK = 0, FG_EARG = -1, FG_EDIMS = -2, &
       FG_EWEIGHT = -3, FG_EHIP = -4, FG_EFULL = -5, FG_EROPE = -6, FG_ENODEV = -7, &
-      FG_EBUSY = -8, FG_EARCH = -9
+      FG_EBUSY = -8, FG_EARCH = -9, FG_ERANGE = -10
   integer(c_int32_t), parameter, public :: FG_OPT_FUSED_DECODE = 1, FG_OPT_FORWARD_F16 = 2
 
   type, bind(C), public :: fg_dims
@@ -38,7 +38,7 @@ module fgpt_c
 
   public :: fg_version, fg_last_error, fg_model_create, fg_weights_read, fg_model_load, &
       fg_model_destroy, &
-      fg_set_rope, fg_forward, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
+      fg_set_rope, fg_forward, fg_forward_pos, fg_kv_create, fg_kv_destroy, fg_kv_len, fg_kv_set_len, &
       fg_step, fg_step_multi, fg_decode_greedy, fg_sync, fg_eval_bpb, fg_rows_npy, &
       fg_decode_spec, fg_spec_accept, fg_spec_draft, fg_sample, fg_decode_sample, fg_set_option, &
       fg_error_message
@@ -120,6 +120,18 @@ module fgpt_c
       integer(c_int32_t), value :: B, T
       real(c_float), intent(out) :: logits(*)
       type(c_ptr), value :: targets, nll
+    end function
+
+    ! fg_forward with attn_sgemm's positive-score counts, npos(n_layer*B*n_head)
+    integer(c_int32_t) function fg_forward_pos(m, ids, B, T, logits, targets, nll, npos) &
+        bind(C, name="fg_forward_pos")
+      import :: c_int32_t, c_float, c_ptr
+      type(c_ptr), value :: m
+      integer(c_int32_t), intent(in) :: ids(*)
+      integer(c_int32_t), value :: B, T
+      real(c_float), intent(out) :: logits(*)
+      type(c_ptr), value :: targets, nll
+      integer(c_int32_t), intent(out) :: npos(*)
     end function
 
     integer(c_int32_t) function fg_kv_create(m, B, maxT, out) bind(C, name="fg_kv_create")

@@ -207,11 +207,12 @@ contains
 
   ! src/lib/fortran_gpt.f90:54-199. attn_blas selects another summation
   ! order of the same attention in the reference (attn_sgemm); here there is
-  ! one attention kernel, so attn_blas alone is accepted. With attn_blas the
-  ! reference also accumulates its positive-score statistics into pos_frac
-  ! / pos_n (src/lib/fortran_attn.f90:247-300): this engine does not produce
-  ! them, so asking for them stops the program. attn_qk (QK-hop) is not part
-  ! of this path and stops it too.
+  ! one attention kernel, so attn_blas changes no result. With attn_blas the
+  ! reference also accumulates its positive-score statistic into pos_frac /
+  ! pos_n (src/lib/fortran_attn.f90:247-300): per layer, row and head, the
+  ! count of causal scores > 0 over T(T+1)/2, added in (layer, row) order;
+  ! without attn_blas they are left alone, as the reference's causal_attn
+  ! leaves them. attn_qk (QK-hop) is not part of this path and stops it.
   subroutine gpt_forward(idx, cos_buf, sin_buf, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, &
       lm_head, outp, BB, TT, vocab_size, d_model, n_head, n_kv_head, head_dim, n_layer, eps, &
       attn_blas, attn_qk, pos_frac, pos_n)
@@ -227,6 +228,9 @@ contains
         c_proj2(:), lm_head(:)
     real(c_float), intent(out) :: outp(:)
     integer(c_int32_t) :: rc
+    logical :: stats
+    integer(c_int32_t), allocatable :: npos(:)
+    integer :: il, ib, ih
 
     if (present(attn_qk)) then
       if (attn_qk) then
@@ -234,11 +238,18 @@ contains
         error stop 1
       end if
     end if
-    if (present(attn_blas)) then
-      if (attn_blas .and. (present(pos_frac) .or. present(pos_n))) then
-        write (error_unit, '(A)') 'gpt_forward: the attn_blas positive-score statistics ' // &
-            '(pos_frac / pos_n) are not produced by this engine'
+    stats = .false.
+    if (present(attn_blas)) stats = attn_blas .and. present(pos_frac)
+    if (stats) then
+      if (size(pos_frac) < n_head) then
+        write (error_unit, '(A)') 'gpt_forward: pos_frac smaller than n_head'
         error stop 1
+      end if
+      if (present(pos_n)) then
+        if (size(pos_n) < n_head) then
+          write (error_unit, '(A)') 'gpt_forward: pos_n smaller than n_head'
+          error stop 1
+        end if
       end if
     end if
     if (size(outp) < BB*TT*vocab_size .or. size(idx) < BB*TT .or. &
@@ -250,8 +261,25 @@ contains
         n_head, n_kv_head, head_dim, n_layer, eps)
     rc = fg_set_rope(g_model, 0_c_int32_t, TT, cos_buf, sin_buf)
     if (rc /= FG_OK) call die('gpt_forward: RoPE tables', rc)
-    rc = fg_forward(g_model, idx, BB, TT, outp, c_null_ptr, c_null_ptr)
+    if (.not. stats) then
+      rc = fg_forward(g_model, idx, BB, TT, outp, c_null_ptr, c_null_ptr)
+      if (rc /= FG_OK) call die('gpt_forward', rc)
+      return
+    end if
+    allocate (npos(n_layer*BB*n_head))
+    rc = fg_forward_pos(g_model, idx, BB, TT, outp, c_null_ptr, c_null_ptr, npos)
     if (rc /= FG_OK) call die('gpt_forward', rc)
+    ! the reference's order: layers (gpt_forward), then rows and heads
+    ! (attn_sgemm), one addition per (layer, row, head)
+    do il = 1, n_layer
+      do ib = 1, BB
+        do ih = 1, n_head
+          pos_frac(ih) = pos_frac(ih) + real(npos(((il-1)*BB + (ib-1))*n_head + ih), c_float) &
+              / real(TT*(TT + 1)/2, c_float)
+          if (present(pos_n)) pos_n(ih) = pos_n(ih) + 1
+        end do
+      end do
+    end do
   end subroutine gpt_forward
 
   ! src/lib/fortran_kv.f90:26-149

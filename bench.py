@@ -380,160 +380,189 @@ def bench_sample(m, d, reps, warmup, n_gen=256):
             "kernel_ms_per_step": {k: v[1] / n_gen for k, v in tm.items()}}
 
 
-# --- HBM traffic of the dominant prefill kernel kind, from PMC counters ---
-PMC_KIND = "gemm"                 # kernel kind the prefill roofline is quoted on
-PMC_MATCH = ("k_gemm",)           # kernel-name fragments of that kind
+# --- PMC counters: HBM-side traffic of each record's dominant kernel, and
+# the prefill kernels' MFMA use. Each reading comes from a child process run
+# under `rocprofv3 --pmc` before this process touches the GPU.
 CALIB_BYTES = 256 << 20           # plain copy of known size: reads and writes this much
+# (probe mode, kernel-name fragments of the kind)
+PMC_KINDS = {
+    "prefill": ("prefill", ("k_gemm",)),
+    "prefill_attn": ("prefill", ("k_attn_mfma",)),
+    "decode_b1": ("decode_b1", ("k_fused_decode",)),
+    "decode_b64": ("decode_b64", ("k_attn_dec",)),
+}
+PMC_B64_STEPS = 16                # batched-decode steps the probe runs
 
 
 def pmc_probe(workload: str = "prefill", f16: bool = True):
-    """Child of a `rocprofv3 --pmc` run: one warm-up and one measured T=2048
-    prefill, on single-term fp16 operands (split-bf16 ones with f16=False),
-    or, for decode_b1, two loops of the B=1 decode workload (16-id prompt,
-    32 steps); then a 256 MiB device copy whose counter reading calibrates
-    the counter against known bytes."""
+    """Child of a `rocprofv3 --pmc` run. prefill: one warm-up and one
+    measured T=2048 forward (single-term fp16 operands, or split-bf16 ones
+    with f16=False); decode_b1: two loops of the B=1 decode workload (16-id
+    prompt, 32 steps); decode_b64: the batched workload's 64 x 1023-id
+    prompt pass and PMC_B64_STEPS steps on the bf16 cache. Then a 256 MiB
+    device copy whose reading calibrates the counter against known bytes.
+    Every handle is closed and the device idle before the process exits."""
     import torch
     from autoresearch_amd import engine
     from autoresearch_amd.weights import D12, seeded_weights, rope_tables, uniform_ids
     d = D12
     m = engine.Model(d, stacks=seeded_weights(d, SEED))
-    c, s = rope_tables(2048, d.head_dim)
-    m.set_rope(c.reshape(-1), s.reshape(-1))
-    dev = torch.device("cuda:0")
-    if workload == "decode_b1":
-        prompts = uniform_ids(43, 16, d.vocab).reshape(1, 16)
-        kv = m.kv(1, 48)
-        kv.step_multi(prompts[:, :-1], want_logits=False)
-        for _ in range(2):
-            kv.len = 15
-            kv.decode_greedy(prompts[:, -1], 32)
+    try:
+        c, s = rope_tables(2048, d.head_dim)
+        m.set_rope(c.reshape(-1), s.reshape(-1))
+        dev = torch.device("cuda:0")
+        if workload == "decode_b1":
+            prompts = uniform_ids(43, 16, d.vocab).reshape(1, 16)
+            kv = m.kv(1, 48)
+            kv.step_multi(prompts[:, :-1], want_logits=False)
+            for _ in range(2):
+                kv.len = 15
+                kv.decode_greedy(prompts[:, -1], 32)
+            kv.close()
+        elif workload == "decode_b64":
+            B, P = 64, 1024
+            prompts = uniform_ids(42 + B, B * P, d.vocab).reshape(B, P)
+            kv = m.kv(B, P + PMC_B64_STEPS, bf16=True)
+            kv.step_multi(prompts[:, :-1], want_logits=False)
+            kv.decode_greedy(prompts[:, -1], PMC_B64_STEPS)
+            kv.close()
+        else:
+            T = 2048
+            ids = uniform_ids(2, T + 1, d.vocab)
+            d_ids = torch.from_numpy(ids[:T].copy()).to(dev)
+            d_lg = torch.empty(T * d.vocab, dtype=torch.float32, device=dev)
+            m.set_forward_f16(f16)  # on: the configuration the prefill line is quoted on
+            for _ in range(2):
+                m.forward_dev(d_ids.data_ptr(), 1, T, d_lg.data_ptr(), 0, 0, 0)
+                m.sync()
         m.sync()
-    else:
-        T = 2048
-        ids = uniform_ids(2, T + 1, d.vocab)
-        d_ids = torch.from_numpy(ids[:T].copy()).to(dev)
-        d_lg = torch.empty(T * d.vocab, dtype=torch.float32, device=dev)
-        m.set_forward_f16(f16)  # on: the configuration the prefill line is quoted on
-        for _ in range(2):
-            m.forward_dev(d_ids.data_ptr(), 1, T, d_lg.data_ptr(), 0, 0, 0)
-            m.sync()
-    a = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
-    b = torch.empty_like(a)
-    torch.cuda.synchronize()
-    b.copy_(a)
-    torch.cuda.synchronize()
+        a = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+    finally:
+        m.close()
+        torch.cuda.synchronize()
     print("pmc probe done", flush=True)
 
 
-def streams_probe():
-    """Two depth-12 models' fp16 forwards (B=1, T=1024 and 2048) on one
-    stream and on two streams: does a second HIP stream overlap the engine's
-    kernels? Prints one JSON line per T (ms per pair of forwards)."""
-    import torch
-    from autoresearch_amd import engine
-    from autoresearch_amd.weights import D12, seeded_weights, rope_tables, uniform_ids
-    d = D12
-    w = seeded_weights(d, SEED)
-    c, s = rope_tables(2048, d.head_dim)
-    models = []
-    for _ in range(2):
-        m = engine.Model(d, stacks=w)
-        m.set_rope(c.reshape(-1), s.reshape(-1))
-        m.set_forward_f16(True)
-        models.append(m)
-    dev = torch.device("cuda:0")
-    st = [torch.cuda.Stream(), torch.cuda.Stream()]
-    cur = torch.cuda.current_stream()
-
-    def timed(fn, n=20):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(cur)
-        for _ in range(n):
-            fn()
-        for x in st:
-            cur.wait_stream(x)
-        e1.record(cur)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n
-
-    for T in (1024, 2048):
-        ids = [torch.from_numpy(uniform_ids(2 + i, T, d.vocab).astype(np.int32)).to(dev)
-               for i in range(2)]
-        lg = [torch.empty(T * d.vocab, dtype=torch.float32, device=dev) for _ in range(2)]
-
-        def fwd(i, k):
-            models[i].forward_dev(ids[i].data_ptr(), 1, T, lg[i].data_ptr(), 0, 0, st[k].cuda_stream)
-
-        def one():
-            st[0].wait_stream(cur)
-            fwd(0, 0)
-
-        def serial():
-            st[0].wait_stream(cur)
-            fwd(0, 0)
-            fwd(1, 0)
-
-        def two_streams():
-            for x in st:
-                x.wait_stream(cur)
-            fwd(0, 0)
-            fwd(1, 1)
-
-        print(json.dumps({"T": T, "one_ms": timed(one), "two_on_one_stream_ms": timed(serial),
-                          "two_on_two_streams_ms": timed(two_streams)}), flush=True)
-    for m in models:
-        m.close()
-
-
-def pmc_counter(counter: str, launches_per_forward: int):
-    """Mean `counter` (KiB per dispatch) over the dominant kind's launches of
-    the probe's last forward, and the reading for the calibration copy."""
+def pmc_rows(mode: str, counters):
+    """Per-dispatch rows (kernel, counter, value) of one `rocprofv3 --pmc`
+    run of the probe, or None when the profiler is absent or gave nothing."""
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None
     with tempfile.TemporaryDirectory(dir="/tmp") as td:
-        cmd = ["timeout", "-s", "KILL", "180", exe, "--pmc", counter, "--output-format", "csv",
-               "-d", td, "-o", "run", "--", sys.executable, os.path.abspath(__file__),
-               "--pmc-probe"]
+        cmd = ["timeout", "-s", "KILL", "240", exe, "--pmc", *counters, "--output-format",
+               "csv", "-d", td, "-o", "run", "--", sys.executable, os.path.abspath(__file__),
+               "--pmc-probe", mode]
         env = dict(os.environ, TMPDIR="/tmp")
         r = subprocess.run(cmd, cwd=ROOT, env=env, stdout=subprocess.PIPE,
                            stderr=subprocess.STDOUT, text=True)
         files = glob.glob(os.path.join(td, "**", "*counter_collection.csv"), recursive=True)
         if not files or "pmc probe done" not in r.stdout:
-            log(f"bench: rocprofv3 --pmc {counter} gave no result (rc {r.returncode})")
+            log(f"bench: rocprofv3 --pmc {' '.join(counters)} ({mode}) gave no result "
+                f"(rc {r.returncode})")
             return None
-        rows = sorted(csv.DictReader(open(files[0])), key=lambda x: int(x["Dispatch_Id"]))
-    rows = [x for x in rows if x["Counter_Name"] == counter]
-    kern = [float(x["Counter_Value"]) for x in rows
-            if any(f in x["Kernel_Name"] for f in PMC_MATCH)][-launches_per_forward:]
-    copy = [float(x["Counter_Value"]) for x in rows if "copy" in x["Kernel_Name"].lower()]
-    if len(kern) < launches_per_forward or not copy:
+        return sorted(csv.DictReader(open(files[0])), key=lambda x: int(x["Dispatch_Id"]))
+
+
+def kind_values(rows, counter, frags):
+    """The counter's per-dispatch values, in dispatch order, of the kernels
+    whose names hold one of frags."""
+    return [float(x["Counter_Value"]) for x in rows
+            if x["Counter_Name"] == counter and any(f in x["Kernel_Name"] for f in frags)]
+
+
+def pmc_kind(key: str, counters, reduce_last):
+    """Mean reading per launch of the kind (over the launches reduce_last
+    picks from the kind's dispatches) for each counter, and the calibration
+    copy's reading."""
+    mode, frags = PMC_KINDS[key]
+    rows = pmc_rows(mode, counters)
+    if rows is None:
         return None
-    return sum(kern) / len(kern), copy[-1]
-
-
-def pmc_traffic(launches_per_forward: int):
-    """HBM bytes per launch of the dominant kind: FETCH_SIZE and WRITE_SIZE
-    (two runs), each scaled by bytes / reading of the calibration copy."""
     out = {}
-    for counter, key in (("FETCH_SIZE", "read"), ("WRITE_SIZE", "write")):
-        got = pmc_counter(counter, launches_per_forward)
-        if got is None:
+    for counter in counters:
+        vals = kind_values(rows, counter, frags)
+        sel = reduce_last(vals)
+        if not sel:
             return None
-        kib, calib_kib = got
-        factor = CALIB_BYTES / (calib_kib * 1024.0)
-        out[key + "_bytes"] = kib * 1024.0 * factor
-        out[key + "_calibration"] = factor
+        out[counter] = sum(sel) / len(sel)
+        out["launches"] = len(sel)
+        copy = [float(x["Counter_Value"]) for x in rows
+                if x["Counter_Name"] == counter and "copy" in x["Kernel_Name"].lower()]
+        if copy:
+            out[counter + "_copy"] = copy[-1]
+    return out
+
+
+def _last_half(vals):
+    return vals[len(vals) // 2:]
+
+
+def pmc_traffic(key: str):
+    """HBM-side bytes per launch of the kind: FETCH_SIZE and WRITE_SIZE (two
+    runs, KiB per dispatch), each scaled by bytes / reading of the 256 MiB
+    calibration copy. Prefill and B=1 decode ran their pass twice: the
+    second pass's launches; the batched decode: every launch of its steps."""
+    pick = (lambda v: v) if key == "decode_b64" else _last_half
+    out = {}
+    for counter, name in (("FETCH_SIZE", "read"), ("WRITE_SIZE", "write")):
+        got = pmc_kind(key, [counter], pick)
+        if got is None or counter + "_copy" not in got:
+            return None
+        factor = CALIB_BYTES / (got[counter + "_copy"] * 1024.0)
+        out[name + "_bytes"] = got[counter] * 1024.0 * factor
+        out[name + "_calibration"] = factor
+        out["launches"] = got["launches"]
     out["bytes"] = out["read_bytes"] + out["write_bytes"]
     return out
+
+
+# MfmaUtil is the profiler's derived metric: the MFMA busy cycles summed over
+# the SIMDs / (the busiest XCC's GRBM_GUI_ACTIVE x the SIMD count), in %
+MFMA_COUNTERS = ["MfmaUtil", "SQ_INSTS_VALU_MFMA_MOPS_F16"]
+
+
+def pmc_mfma(key: str):
+    """MFMA use of the kind over the second forward: the profiler's MfmaUtil
+    per dispatch (as a fraction), and the executed fp16 MFMA flops per launch
+    (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512)."""
+    got = pmc_kind(key, MFMA_COUNTERS, _last_half)
+    if got is None:
+        return None
+    return {"launches": got["launches"], "mfma_util": got["MfmaUtil"] / 100.0,
+            "mfma_f16_flop_per_launch": got["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512.0}
 
 
 CPU_LOOP = ("naive loop order of the reference's non-BLAS path (fortran_linear / causal_attn: "
             "each output a sequential fp32 sum, OpenMP over outputs), not OpenBLAS sgemm_; "
             "weights transposed once before the timed region")
+
+
+def cpu_facts() -> dict:
+    """The host the CPU baseline runs on: model name, logical CPUs, the CPUs
+    this process may use, and physical cores (lscpu's sockets x cores)."""
+    out = {"logical_cpus": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    out["model"] = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        r = subprocess.run(["lscpu"], stdout=subprocess.PIPE, stderr=subprocess.DEVNULL,
+                           text=True, timeout=10)
+        kv = dict(l.split(":", 1) for l in r.stdout.splitlines() if ":" in l)
+        cps, sock = int(kv["Core(s) per socket"].strip()), int(kv["Socket(s)"].strip())
+        out["physical_cores"] = cps * sock
+    except Exception:
+        pass
+    return out
 
 
 def cpu_baseline(d, w, budget_s: float = 12.0) -> dict:
@@ -597,8 +626,84 @@ def cpu_decode_baseline(d, w, c, s, budget_s: float = 6.0) -> dict:
             "first_ids": ids[:8]}
 
 
+def cpu_child():
+    """--cpu-child: the CPU baselines in a process of their own, so the
+    oracle's OpenMP runtime starts with the settings the reference measured
+    best (OMP_PROC_BIND=close, OMP_DYNAMIC=FALSE: set by the parent) and no
+    GPU runtime beside it. Prints one JSON line."""
+    from autoresearch_amd.weights import D12, seeded_weights, rope_tables
+    d = D12
+    w = seeded_weights(d, SEED)
+    c, s = rope_tables(2304, d.head_dim)
+    out = cpu_baseline(d, w)
+    out["decode_b1"] = cpu_decode_baseline(d, w, c.reshape(-1), s.reshape(-1))
+    print("CPU " + json.dumps(out), flush=True)
+
+
+def run_cpu_baseline() -> dict:
+    facts = cpu_facts()
+    env = dict(os.environ, OMP_PROC_BIND="close", OMP_DYNAMIC="FALSE")
+    if "OMP_NUM_THREADS" not in env:
+        env["OMP_NUM_THREADS"] = str(facts.get("usable_cpus", os.cpu_count()))
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-child"], cwd=ROOT,
+                       env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                       timeout=600)
+    line = [l for l in r.stdout.splitlines() if l.startswith("CPU ")]
+    if r.returncode != 0 or not line:
+        log("bench: CPU baseline child failed", r.stderr[-2000:])
+        return None
+    out = json.loads(line[-1][4:])
+    out["host"] = {**facts, "OMP_NUM_THREADS": env["OMP_NUM_THREADS"],
+                   "OMP_PROC_BIND": "close", "OMP_DYNAMIC": "FALSE"}
+    return out
+
+
 WORKLOADS = ("prefill", "decode_b1", "eval_b8", "decode_b64", "decode_b64_fp32kv", "gqa20",
              "decode_spec", "decode_sample")
+
+# what the final line keeps of a roofline record (the full records go to stderr)
+ROOF_KEYS = ("bound", "kernel_kind", "avg_launch_us", "achieved", "peak", "unit", "frac",
+             "traffic", "mfma_executed_frac", "mfma_util")
+
+
+def sig(v, n=5):
+    """v to n significant digits (the line's figures; full ones on stderr)."""
+    return float(f"{v:.{n}g}") if isinstance(v, float) and math.isfinite(v) else v
+
+
+def brief_roof(r):
+    if not r:
+        return r
+    return {k: sig(v) for k, v in r.items() if k in ROOF_KEYS}
+
+
+def brief(rec):
+    """The figures of a workload record that the one-line summary keeps:
+    throughput, step time, the rooflines (without per-launch detail), whole
+    fractions; nested records likewise; per-row arrays and per-kernel
+    breakdowns stay in the full record on stderr."""
+    if not isinstance(rec, dict):
+        return rec
+    out = {}
+    for k, v in rec.items():
+        if k.startswith("roofline"):
+            out[k] = brief_roof(v)
+        elif isinstance(v, dict) and k in ("split", "prefill", "decode"):
+            out[k] = brief(v)
+        elif isinstance(v, (int, float, str, bool)) and k not in ("first_ids",):
+            out[k] = sig(v)
+    return out
+
+
+def profiles_of(rec, prefix="", out=None):
+    """record path -> the profiles/ summary each of its rooflines reproduces from."""
+    out = {} if out is None else out
+    for k, v in (rec or {}).items():
+        if k.startswith("roofline") and isinstance(v, dict) and v.get("profile"):
+            out.setdefault(v["profile"], []).append(prefix + k)
+        elif isinstance(v, dict) and k in ("split", "prefill", "decode"):
+            profiles_of(v, prefix + k + ".", out)
+    return out
 
 
 def main():
@@ -613,17 +718,17 @@ def main():
                     help="prefill / eval_b8: the fp16 single-term pass, the split one, or both")
     ap.add_argument("--only", choices=WORKLOADS,
                     help="run one workload and print its record (for profiling runs)")
-    ap.add_argument("--no-pmc", action="store_true", help="skip the PMC traffic runs")
-    ap.add_argument("--pmc-probe", nargs="?", const="prefill", choices=("prefill", "decode_b1"),
-                    help=argparse.SUPPRESS)
-    ap.add_argument("--streams-probe", action="store_true",
-                    help="time two models' forwards on one stream and on two streams")
+    ap.add_argument("--no-pmc", action="store_true", help="skip the PMC counter runs")
+    ap.add_argument("--detail", metavar="FILE", help="also write the full records to FILE")
+    ap.add_argument("--pmc-probe", nargs="?", const="prefill",
+                    choices=("prefill", "decode_b1", "decode_b64"), help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.pmc_probe:
         pmc_probe(args.pmc_probe, f16=args.operands != "split")
         return
-    if args.streams_probe:
-        streams_probe()
+    if args.cpu_child:
+        cpu_child()
         return
     if args.gpus != 1:
         print(f"bench.py: this engine runs on one GPU; --gpus {args.gpus} is not supported "
@@ -631,12 +736,15 @@ def main():
         sys.exit(2)
 
     # the counter runs go first, before this process touches the GPU
-    traffic = None
+    pmc = {}
     if not args.only and not args.no_pmc:
-        log("bench: PMC traffic runs (FETCH_SIZE, WRITE_SIZE)")
-        from autoresearch_amd.weights import D12 as _d
-        traffic = pmc_traffic(4 * _d.n_layer + 1)
-        log("bench: traffic", json.dumps(traffic))
+        log("bench: PMC runs (FETCH_SIZE, WRITE_SIZE; MFMA busy cycles)")
+        for key in ("prefill", "decode_b1", "decode_b64"):
+            pmc[key] = pmc_traffic(key)
+            log(f"bench: traffic {key}", json.dumps(pmc[key]))
+        for key in ("prefill", "prefill_attn"):
+            pmc["mfma_" + key] = pmc_mfma(key)
+            log(f"bench: mfma {key}", json.dumps(pmc["mfma_" + key]))
 
     import torch
     from autoresearch_amd import engine
@@ -646,47 +754,81 @@ def main():
     log("bench: generating seeded depth-12 weights")
     w = seeded_weights(d, SEED)
     m = engine.Model(d, stacks=w)
-    c, s = rope_tables(2304, d.head_dim)
-    m.set_rope(c.reshape(-1), s.reshape(-1))
+    try:
+        c, s = rope_tables(2304, d.head_dim)
+        m.set_rope(c.reshape(-1), s.reshape(-1))
+        runs = {
+            "prefill": lambda: bench_prefill(m, d, args.steps, args.warmup, torch, args.operands),
+            "decode_b1": lambda: bench_decode(m, d, 1, 16, 32, reps=max(args.steps, 5),
+                                              warmup=args.warmup,
+                                              profile="profiles/decode_d12_B1_fused.md"),
+            "eval_b8": lambda: bench_eval_b8(m, d, max(3, args.steps // 4), 1, torch,
+                                             args.operands),
+            "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0,
+                                               profile="profiles/decode_d12_B64_kernels.md",
+                                               kv_bf16=True),
+            "decode_b64_fp32kv": lambda: bench_decode(
+                m, d, 64, 1024, 512, reps=1, warmup=0,
+                profile="profiles/decode_d12_B64_fp32kv_kernels.md"),
+            "gqa20": lambda: bench_gqa20(args.steps, 1, torch),
+            "decode_spec": lambda: bench_spec(m, d, reps=3, warmup=1),
+            "decode_sample": lambda: bench_sample(m, d, reps=3, warmup=1),
+        }
+        if args.only:
+            print(json.dumps({"only": args.only, **runs[args.only]()}), flush=True)
+            return
+        rec = {}
+        for name in WORKLOADS:
+            if name in args.skip:
+                rec[name] = None
+                continue
+            log(f"bench: {name}")
+            rec[name] = runs[name]()
+            log(f"bench: {name}", json.dumps(rec[name]))
+    finally:
+        m.close()
+        torch.cuda.synchronize()
 
-    runs = {
-        "prefill": lambda: bench_prefill(m, d, args.steps, args.warmup, torch, args.operands),
-        "decode_b1": lambda: bench_decode(m, d, 1, 16, 32, reps=max(args.steps, 5),
-                                          warmup=args.warmup,
-                                          profile="profiles/decode_d12_B1_fused.md"),
-        "eval_b8": lambda: bench_eval_b8(m, d, max(3, args.steps // 4), 1, torch, args.operands),
-        "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0,
-                                           profile="profiles/decode_d12_B64_kernels.md",
-                                           kv_bf16=True),
-        "decode_b64_fp32kv": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0,
-                                                  profile="profiles/decode_d12_B64_fp32kv_kernels.md"),
-        "gqa20": lambda: bench_gqa20(args.steps, 1, torch),
-        "decode_spec": lambda: bench_spec(m, d, reps=3, warmup=1),
-        "decode_sample": lambda: bench_sample(m, d, reps=3, warmup=1),
-    }
-    if args.only:
-        print(json.dumps({"only": args.only, **runs[args.only]()}), flush=True)
-        return
-
-    rec = {}
-    for name in WORKLOADS:
-        if name in args.skip:
-            rec[name] = None
-            continue
-        log(f"bench: {name}")
-        rec[name] = runs[name]()
-        log(f"bench: {name}", json.dumps(rec[name]))
-    pre = rec["prefill"]
     cpu = None
     if not args.no_cpu:
-        log("bench: CPU oracle baseline")
-        cpu = cpu_baseline(d, w)
-        cpu["decode_b1"] = cpu_decode_baseline(d, w, c.reshape(-1), s.reshape(-1))
+        log("bench: CPU oracle baseline (child process)")
+        cpu = run_cpu_baseline()
         log("bench: cpu", json.dumps(cpu))
 
-    if traffic is not None and pre["roofline"]["kernel_kind"] == PMC_KIND:
-        pre["roofline"]["traffic"] = traffic["bytes"]
-        pre["roofline"]["traffic_detail"] = traffic
+    # counter readings into the records they belong to
+    pre = rec["prefill"]
+    attach = (("prefill", "roofline", "prefill", "gemm"),
+              ("decode_b1", "roofline", "decode_b1", "decode_fused"),
+              ("decode_b64", "roofline", "decode_b64", "attn_decode"))
+    for key, field, name, kind in attach:
+        t = pmc.get(key)
+        r = rec.get(name)
+        if t and r and r.get(field, {}).get("kernel_kind") == kind:
+            if key == "decode_b64":
+                # the probed launches' own algorithmic bytes (the probe runs
+                # the first PMC_B64_STEPS steps after the 1023-id prompts)
+                kvl = kv_pos_bytes(d) // d.n_layer
+                t["alg_bytes_per_launch"] = 64 * kvl * float(
+                    np.mean([1023 + i + 1 for i in range(PMC_B64_STEPS)]))
+            r[field]["traffic"] = t["bytes"]
+            r[field]["traffic_detail"] = t
+    for key, field in (("mfma_prefill", "roofline"), ("mfma_prefill_attn", "roofline_attention")):
+        mf = pmc.get(key)
+        if mf and pre and pre.get(field):
+            pre[field]["mfma_util"] = mf["mfma_util"]
+            pre[field]["mfma_counters"] = mf
+    if args.detail:
+        with open(args.detail, "w") as f:
+            json.dump({"records": rec, "pmc": pmc, "cpu_baseline": cpu}, f, indent=1)
+
+    def roof_line(r):
+        out = brief_roof(r)
+        if r and r.get("traffic_detail"):
+            out["traffic"] = round(r["traffic_detail"]["bytes"])
+        if r and r.get("mfma_counters"):
+            out["mfma_util"] = sig(r["mfma_counters"]["mfma_util"])
+        return out
+
     line = {
         "metric": METRIC, "value": pre["tok_s"], "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": pre["ms_per_step"],
@@ -695,11 +837,24 @@ def main():
         "config": {"workload": "depth-12 prefill, B=1, T=2048: fp32 logits [2048,8192] + "
                                "per-token CE", "global_batch": 1, "seq_len": 2048,
                    "parallelism": "single GPU"},
-        "roofline": pre["roofline"],
-        "cpu_baseline": cpu,
-        **rec,
+        "roofline": roof_line(pre["roofline"]),
+        "cpu_baseline": None if cpu is None else {
+            k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
     }
-    print(json.dumps(line), flush=True)
+    if cpu is not None:
+        line["cpu_baseline"]["host"] = cpu["host"]
+        line["cpu_baseline"]["decode_b1"] = {k: cpu["decode_b1"][k] for k in ("value", "unit")}
+    profs = {}
+    for name in WORKLOADS:
+        line[name] = brief(rec[name]) if rec[name] is not None else None
+        if rec[name] is not None:
+            for k, v in rec[name].items():
+                if k.startswith("roofline") and isinstance(v, dict):
+                    line[name][k] = roof_line(v)
+            for path, keys in profiles_of(rec[name], name + ".").items():
+                profs.setdefault(path, []).extend(keys)
+    line["profiles"] = profs
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

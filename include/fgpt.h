@@ -39,9 +39,12 @@ enum {
   FG_EROPE = -6,    /* RoPE table row not set for a position in use        */
   FG_ENODEV = -7,   /* no usable gfx950 device                             */
   FG_EBUSY = -8,    /* handle in use by another thread                     */
-  FG_EARCH = -9     /* arch.txt or safetensors arch.* metadata disagrees with the
+  FG_EARCH = -9,    /* arch.txt or safetensors arch.* metadata disagrees with the
                        dims or with itself (fortran_arch.f90:238-246,
                        load_weights.f90:533-590,799-821) */
+  FG_ERANGE = -10   /* FG_OPT_FORWARD_F16: an activation reached fp16's range
+                       limit (|x| >= 65520 rounds to inf); the results of that
+                       pass are not valid -- run it without the option */
 };
 
 typedef struct fg_model fg_model;
@@ -100,6 +103,17 @@ int32_t fg_set_rope(fg_model *m, int32_t pos0, int32_t n_pos, const float *cos_b
  * (src/app/eval_bpb.f90:165-181). RoPE rows 0..T-1 must be set. */
 int32_t fg_forward(fg_model *m, const int32_t *ids, int32_t B, int32_t T, float *logits,
                    const int32_t *targets, float *nll);
+
+/* fg_forward with attn_sgemm's positive-score statistic (gpt_forward's
+ * optional pos_frac / pos_n with attn_blas, src/lib/fortran_attn.f90:
+ * 247-300): npos (n_layer*B*n_head, host; layer-major, then row, then head)
+ * receives, per layer, row and head, how many of the T(T+1)/2 causal scores
+ * q.k/sqrt(head_dim) are > 0, counted before the softmax as the reference
+ * counts them before its cap and relu. The reference's accumulation,
+ * pos_frac(h) += npos / (T(T+1)/2) and pos_n(h) += 1 over (layer, row) in
+ * that order, is the caller's (the Fortran drop-in does it). T <= 65535. */
+int32_t fg_forward_pos(fg_model *m, const int32_t *ids, int32_t B, int32_t T, float *logits,
+                       const int32_t *targets, float *nll, int32_t *npos);
 
 /* eval_bpb on the device (src/app/eval_bpb.f90:97-181 with the byte
  * weighting of scripts/eval_driver.py:174-190 / src/app/bpb_agg.f90:130-155):
@@ -291,7 +305,12 @@ int32_t fg_set_option(fg_model *m, int32_t key, int32_t value);
  * receives the reason when it is not available. */
 int32_t fg_get_option(fg_model *m, int32_t key, int32_t *value, char *why, int32_t len);
 
-/* Block until the handle's queued work is done. */
+/* Block until the handle's queued work is done. Returns FG_ERANGE (once)
+ * when a single-term fp16 pass queued through fg_forward_dev since the last
+ * report overflowed fp16 (FG_OPT_FORWARD_F16; a pass on a caller stream is
+ * covered once that stream has been synchronised). The host-buffer entry
+ * points (fg_forward, fg_forward_pos, fg_eval_bpb) report their own pass's
+ * overflow as their return code. */
 int32_t fg_sync(fg_model *m);
 
 /* Kernel timing, the device-side counterpart of chat_text --stats

@@ -289,6 +289,40 @@ void or_attn_chunk(const float *q, const float *K, const float *V, float *y,
   }
 }
 
+/* src/lib/fortran_attn.f90:247-300 (attn_sgemm's statistic, counted in its
+ * causal loop :249-254 before the cap and the softmax): per (b, h), npos =
+ * the number of scores s = (q . k) * scale, key t' <= query t, that are
+ * > 0 (strict). The score is the dot product in attn_row's order. namb
+ * (nullable) receives, per (b, h), how many of those scores have
+ * |q . k| <= rel_tol * sum_d |q_d k_d|: their sign is within rounding and
+ * can differ in another summation order. */
+void or_attn_pos_count(const float *q, const float *k, int32_t B, int32_t T,
+                       int32_t H, int32_t KH, int32_t D, float rel_tol,
+                       int32_t *npos, int32_t *namb) {
+  float scale = 1.0f / sqrtf((float)D);
+  int32_t rep = H / KH;
+#pragma omp parallel for collapse(2) schedule(dynamic, 1)
+  for (int32_t a = 0; a < B; ++a)
+    for (int32_t h = 0; h < H; ++h) {
+      int32_t kb = h / rep, np = 0, na = 0;
+      for (int32_t t = 0; t < T; ++t) {
+        const float *qr = q + (((int64_t)a * T + t) * H + h) * D;
+        for (int32_t j = 0; j <= t; ++j) {
+          const float *kr = k + (((int64_t)a * T + j) * KH + kb) * D;
+          float acc = 0.0f, mag = 0.0f;
+          for (int32_t d = 0; d < D; ++d) {
+            acc = acc + qr[d] * kr[d];
+            mag = mag + fabsf(qr[d] * kr[d]);
+          }
+          if (acc * scale > 0.0f) ++np;
+          if (fabsf(acc) <= rel_tol * mag) ++na;
+        }
+      }
+      npos[a * H + h] = np;
+      if (namb) namb[a * H + h] = na;
+    }
+}
+
 /* src/lib/fortran_attn.f90:697-710: x = max(0, x)^2 in place */
 void or_relu2(float *x, int64_t N) {
 #pragma omp parallel for schedule(static)
@@ -304,13 +338,16 @@ static void add_into(float *dst, const float *src, int64_t n) {
   for (int64_t i = 0; i < n; ++i) dst[i] = dst[i] + src[i];
 }
 
-/* src/lib/fortran_gpt.f90:54-199 (default causal_attn path). */
-void or_gpt_forward(const int32_t *idx, const float *cosb, const float *sinb,
-                    const float *wte, const float *c_q, const float *c_k,
-                    const float *c_v, const float *c_proj, const float *c_fc,
-                    const float *c_proj2, const float *lm_head, float *outp,
-                    int32_t B, int32_t T, int32_t V, int32_t D, int32_t H,
-                    int32_t KH, int32_t HD, int32_t L, float eps) {
+/* src/lib/fortran_gpt.f90:54-199 (default causal_attn path); with npos set,
+ * each layer's attention inputs also give or_attn_pos_count's counts
+ * (npos / namb [L][B][H]). */
+static void forward_body(const int32_t *idx, const float *cosb, const float *sinb,
+                         const float *wte, const float *c_q, const float *c_k,
+                         const float *c_v, const float *c_proj, const float *c_fc,
+                         const float *c_proj2, const float *lm_head, float *outp,
+                         int32_t B, int32_t T, int32_t V, int32_t D, int32_t H,
+                         int32_t KH, int32_t HD, int32_t L, float eps,
+                         float rel_tol, int32_t *npos, int32_t *namb) {
   int64_t bt = (int64_t)B * T;
   int32_t dff = 4 * D, hdd = H * HD, kvd = KH * HD;
   int64_t qsz = (int64_t)hdd * D, ksz = (int64_t)kvd * D, psz = (int64_t)D * hdd;
@@ -331,6 +368,9 @@ void or_gpt_forward(const int32_t *idx, const float *cosb, const float *sinb,
     or_linear(xn, c_v + l * ksz, v, bt, D, kvd);
     or_rope(q, cosb, sinb, qr, B, T, H, HD);
     or_rope(k, cosb, sinb, kr, B, T, KH, HD);
+    if (npos)
+      or_attn_pos_count(qr, kr, B, T, H, KH, HD, rel_tol, npos + (int64_t)l * B * H,
+                        namb ? namb + (int64_t)l * B * H : NULL);
     or_causal_attn(qr, kr, v, ao, B, T, H, KH, HD);
     or_linear(ao, c_proj + l * psz, sub, bt, D, D);
     add_into(emd, sub, bt * D);
@@ -344,6 +384,27 @@ void or_gpt_forward(const int32_t *idx, const float *cosb, const float *sinb,
   or_linear(xn, lm_head, outp, bt, D, V);                    /* :192 */
   free(emd); free(xn); free(sub); free(ao); free(q); free(qr);
   free(k); free(kr); free(v); free(mlp);
+}
+
+void or_gpt_forward(const int32_t *idx, const float *cosb, const float *sinb,
+                    const float *wte, const float *c_q, const float *c_k,
+                    const float *c_v, const float *c_proj, const float *c_fc,
+                    const float *c_proj2, const float *lm_head, float *outp,
+                    int32_t B, int32_t T, int32_t V, int32_t D, int32_t H,
+                    int32_t KH, int32_t HD, int32_t L, float eps) {
+  forward_body(idx, cosb, sinb, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, outp,
+               B, T, V, D, H, KH, HD, L, eps, 0.0f, NULL, NULL);
+}
+
+void or_gpt_forward_pos(const int32_t *idx, const float *cosb, const float *sinb,
+                        const float *wte, const float *c_q, const float *c_k,
+                        const float *c_v, const float *c_proj, const float *c_fc,
+                        const float *c_proj2, const float *lm_head, float *outp,
+                        int32_t B, int32_t T, int32_t V, int32_t D, int32_t H,
+                        int32_t KH, int32_t HD, int32_t L, float eps, float rel_tol,
+                        int32_t *npos, int32_t *namb) {
+  forward_body(idx, cosb, sinb, wte, c_q, c_k, c_v, c_proj, c_fc, c_proj2, lm_head, outp,
+               B, T, V, D, H, KH, HD, L, eps, rel_tol, npos, namb);
 }
 
 /* Shared body of gpt_step / gpt_step_multi (src/lib/fortran_kv.f90:80-147

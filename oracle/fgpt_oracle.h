@@ -46,6 +46,12 @@ void or_attn_step(const float *q, const float *K, const float *V, float *y,
 void or_attn_chunk(const float *q, const float *K, const float *V, float *y,
                    int32_t B, int32_t H, int32_t KH, int32_t D,
                    int32_t TC_PREV, int32_t TB);
+/* src/lib/fortran_attn.f90:247-300: attn_sgemm's positive-score count per
+ * (b, h) over the causal scores (q . k) * scale > 0; namb (nullable): how
+ * many have |q . k| <= rel_tol * sum |q_d k_d| (sign within rounding). */
+void or_attn_pos_count(const float *q, const float *k, int32_t B, int32_t T,
+                       int32_t H, int32_t KH, int32_t D, float rel_tol,
+                       int32_t *npos, int32_t *namb);
 /* src/lib/fortran_attn.f90:697-710 */
 void or_relu2(float *x, int64_t N);
 
@@ -57,6 +63,16 @@ void or_gpt_forward(const int32_t *idx, const float *cosb, const float *sinb,
                     int32_t B, int32_t T, int32_t V, int32_t D, int32_t H,
                     int32_t KH, int32_t HD, int32_t L, float eps);
 
+/* or_gpt_forward plus each layer's or_attn_pos_count (npos, namb:
+ * [L][B][H]), the statistic gpt_forward collects with attn_blas and
+ * pos_frac (src/lib/fortran_gpt.f90:160-162). */
+void or_gpt_forward_pos(const int32_t *idx, const float *cosb, const float *sinb,
+                        const float *wte, const float *c_q, const float *c_k,
+                        const float *c_v, const float *c_proj, const float *c_fc,
+                        const float *c_proj2, const float *lm_head, float *outp,
+                        int32_t B, int32_t T, int32_t V, int32_t D, int32_t H,
+                        int32_t KH, int32_t HD, int32_t L, float eps, float rel_tol,
+                        int32_t *npos, int32_t *namb);
 /* src/lib/fortran_kv.f90:26-149. Returns 0, or 1 when the cache is full
  * (the reference prints and exits). */
 int32_t or_gpt_step(const int32_t *idx1, const float *cos1, const float *sin1,

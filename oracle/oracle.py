@@ -43,6 +43,8 @@ def lib():
             "or_attn_step": (None, [_f, _f, _f, _f, i32, i32, i32, i32, i32]),
             "or_attn_chunk": (None, [_f, _f, _f, _f, i32, i32, i32, i32, i32, i32]),
             "or_relu2": (None, [_f, i64]),
+            "or_attn_pos_count": (None, [_f, _f, i32, i32, i32, i32, i32, f32, _i, _i]),
+            "or_gpt_forward_pos": (None, [_i, _f, _f] + [_f] * 8 + [_f] + [i32] * 8 + [f32, f32, _i, _i]),
             "or_gpt_forward": (None, [_i, _f, _f] + [_f] * 8 + [_f] + [i32] * 8 + [f32]),
             "or_gpt_step": (i32, [_i, _f, _f] + [_f] * 8 + [_f, _f, _i, i32, _f] + [i32] * 7 + [f32]),
             "or_gpt_step_multi": (i32, [_i, _f, _f] + [_f] * 8 + [_f, _f, _i, i32, _f] + [i32] * 8 + [f32]),
@@ -169,6 +171,29 @@ def gpt_forward(ids, cosb, sinb, w: dict, d, B: int, T: int) -> np.ndarray:
     ws = {n: f32(w[n]) for n in w}
     lib().or_gpt_forward(ip(ids), fp(cosb), fp(sinb), *_w(ws), fp(out), B, T, *_dims(d), d.eps)
     return out.reshape(B, T, d.vocab)
+
+
+def attn_pos_count(q, k, B: int, T: int, H: int, KH: int, D: int, rel_tol: float = 1e-4):
+    """attn_sgemm's positive-score count per (b, h) (npos) and how many of
+    the scores sit within rel_tol of zero relative to sum |q_d k_d| (namb)."""
+    npos = np.zeros(B * H, np.int32)
+    namb = np.zeros(B * H, np.int32)
+    lib().or_attn_pos_count(fp(f32(q)), fp(f32(k)), B, T, H, KH, D, rel_tol, ip(npos), ip(namb))
+    return npos.reshape(B, H), namb.reshape(B, H)
+
+
+def gpt_forward_pos(ids, cosb, sinb, w: dict, d, B: int, T: int, rel_tol: float = 1e-4):
+    """gpt_forward's logits with each layer's positive-score counts
+    (npos, namb: [L, B, H])."""
+    ids, cosb, sinb = i32(ids), f32(cosb), f32(sinb)
+    out = np.empty(B * T * d.vocab, dtype=np.float32)
+    npos = np.zeros(d.n_layer * B * d.n_head, np.int32)
+    namb = np.zeros_like(npos)
+    ws = {n: f32(w[n]) for n in w}
+    lib().or_gpt_forward_pos(ip(ids), fp(cosb), fp(sinb), *_w(ws), fp(out), B, T, *_dims(d),
+                             d.eps, rel_tol, ip(npos), ip(namb))
+    sh = (d.n_layer, B, d.n_head)
+    return out.reshape(B, T, d.vocab), npos.reshape(sh), namb.reshape(sh)
 
 
 class KVCache:

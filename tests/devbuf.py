@@ -25,6 +25,10 @@ class DevBuf:
     def put(self, arr):
         a = np.ascontiguousarray(arr, dtype=self.dtype)
         assert DevBuf.hip.hipMemcpy(self.p, a.ctypes.data_as(C.c_void_p), C.c_size_t(self.nbytes), 1) == 0
+        # a pageable hipMemcpy may return before its DMA lands, and the null
+        # stream it runs on is not ordered against the engine's non-blocking
+        # stream: wait for the device before the buffer is handed over
+        assert DevBuf.hip.hipDeviceSynchronize() == 0
 
     def get(self):
         out = np.empty(self.nbytes // self.dtype.itemsize, self.dtype)

@@ -1,6 +1,7 @@
 """The Fortran host layer: the iso_c_binding module, the drop-in
-gpt_forward / gpt_step / gpt_step_multi and the ids-in/ids-out harness
-(autoresearch_amd/fgpt_run), checked against the CPU oracle."""
+gpt_forward / gpt_step / gpt_step_multi, the ids-in/ids-out harness
+(autoresearch_amd/fgpt_run) and the drop-in check program
+(tests/fortran/dropin_checks), checked against the CPU oracle."""
 import os
 import subprocess
 
@@ -13,6 +14,7 @@ from oracle import oracle as O
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "autoresearch_amd", "fgpt_run")
+CHECKS = os.path.join(ROOT, "tests", "fortran", "dropin_checks")
 SMALL = Dims(n_layer=2, d_model=128, n_head=2, n_kv_head=1, head_dim=64, vocab=512)
 
 
@@ -24,12 +26,17 @@ def run(args, timeout=300):
     return subprocess.run([EXE, *args], capture_output=True, text=True, timeout=timeout)
 
 
+def run_checks(args, timeout=300):
+    return subprocess.run([CHECKS, *args], capture_output=True, text=True, timeout=timeout)
+
+
 def test_harness_built_and_fails_loudly_without_device():
     import torch
     assert os.path.exists(EXE), "build() must compile the Fortran harness"
+    assert os.path.exists(CHECKS), "build() must compile the drop-in check program"
     if torch.cuda.is_available():
         pytest.skip("a GPU is visible")
-    r = run(["selftest"], timeout=60)
+    r = run_checks(["selftest"], timeout=60)
     assert r.returncode != 0
     assert "no HIP device" in r.stderr or "gfx950" in r.stderr
 
@@ -37,13 +44,56 @@ def test_harness_built_and_fails_loudly_without_device():
 def test_harness_usage_error():
     r = run(["nonsense"], timeout=30)
     assert r.returncode == 2 and "usage" in r.stderr
+    r = run_checks(["nonsense"], timeout=30)
+    assert r.returncode == 2 and "usage" in r.stderr
 
 
 @pytest.mark.gpu
 def test_fortran_selftest_steps_equal_forward():
-    r = run(["selftest"], timeout=120)
+    r = run_checks(["selftest"], timeout=120)
     print(r.stdout, r.stderr)
     assert r.returncode == 0 and "selftest: ok" in r.stdout
+
+
+@pytest.mark.gpu
+def test_fortran_posfrac_attn_blas(tmp_path):
+    """eval_bpb --attn blas through the drop-in: gpt_forward with attn_blas
+    and pos_frac / pos_n, called twice into the same accumulators and then
+    once without attn_blas (which leaves them alone). pos_n must count one
+    addition per (call, layer, row); pos_frac must equal the reference's
+    accumulation (src/lib/fortran_attn.f90:291-296, fp32, (layer, row)
+    order) of the CPU oracle's positive-score counts on the same inputs,
+    within the counts whose score sits within rounding of zero."""
+    d = SMALL
+    w = seeded_weights(d, 61)
+    write_npy_dir(str(tmp_path / "w"), d, w, ctx=160)
+    B, T, ncall = 2, 96, 2
+    rows = uniform_ids(62, B * T, d.vocab)
+    np.savetxt(tmp_path / "rows.txt", rows[None, :], fmt="%d")
+    r = run_checks(["posfrac", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"),
+                    str(B), str(T), str(ncall), str(tmp_path / "pf.txt")])
+    print(r.stdout, r.stderr)
+    assert r.returncode == 0, r.stdout + r.stderr
+    got = np.loadtxt(tmp_path / "pf.txt").reshape(d.n_head, 2)
+    c, s = O.rope_tables(T, d.head_dim)
+    _, npos, namb = O.gpt_forward_pos(rows, c, s, w, d, B, T)
+    assert np.array_equal(got[:, 1], np.full(d.n_head, ncall * d.n_layer * B))
+    den = np.float32(T * (T + 1) // 2)
+    pf = np.zeros(d.n_head, np.float32)
+    lo = np.zeros(d.n_head, np.float32)
+    hi = np.zeros(d.n_head, np.float32)
+    for _ in range(ncall):
+        for ll in range(d.n_layer):
+            for aa in range(B):
+                for hh in range(d.n_head):
+                    n, a = npos[ll, aa, hh], namb[ll, aa, hh]
+                    pf[hh] = np.float32(pf[hh] + np.float32(n) / den)
+                    lo[hh] = np.float32(lo[hh] + np.float32(n - a) / den)
+                    hi[hh] = np.float32(hi[hh] + np.float32(n + a) / den)
+    print("pos_frac", got[:, 0], "oracle", pf, "ambiguous scores", int(namb.sum()))
+    assert np.all(got[:, 0] >= lo * (1 - 1e-6)) and np.all(got[:, 0] <= hi * (1 + 1e-6))
+    if namb.sum() == 0:
+        assert np.array_equal(got[:, 0].astype(np.float32), pf)
 
 
 def oracle_greedy(d, w, prompt, ngen):
@@ -241,7 +291,7 @@ def test_fortran_specbench_trunc_drafter(tmp_path):
     ids = uniform_ids(47, 40, d.vocab)
     np.savetxt(tmp_path / "rows.txt", ids[None, :], fmt="%d")
     npre, ngen = 33, 48
-    r = run(["specbench", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"),
+    r = run_checks(["specbench", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"),
              str(npre), str(ngen), str(tmp_path / "o.txt"), "4", "1"])
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stdout + r.stderr
@@ -259,7 +309,7 @@ def test_fortran_specbench_depth12(tmp_path):
     write_npy_dir(str(tmp_path / "w"), d, w)
     ids = uniform_ids(48, 70, d.vocab)
     np.savetxt(tmp_path / "rows.txt", ids[None, :], fmt="%d")
-    r = run(["specbench", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"), "64",
+    r = run_checks(["specbench", str(tmp_path / "w"), *dims_args(d), str(tmp_path / "rows.txt"), "64",
              "32", str(tmp_path / "o.txt")])
     print(r.stdout, r.stderr)
     assert r.returncode == 0, r.stdout + r.stderr

@@ -71,6 +71,34 @@ def test_forward_small_vs_oracle(d, B, T):
     m.close()
 
 
+@pytest.mark.parametrize("d,B,T,f16", [(SMALL, 2, 37, False), (SMALL, 3, 500, False),
+                                       (SMALL_MHA, 1, 700, False), (SMALL, 2, 300, True)],
+                         ids=["gqa-2x37", "gqa-3x500", "mha-1x700", "gqa-2x300-f16"])
+def test_forward_pos_counts_vs_oracle(d, B, T, f16):
+    """attn_sgemm's positive-score statistic (fg_forward_pos): per layer, row
+    and head, the engine's count of causal scores > 0 against the oracle's
+    count from its fp32 scores, within the scores whose sign sits within
+    rounding (|q.k| <= tol * sum |q_d k_d|: 1e-4 for the split operands'
+    ~16 significant bits, 2e-3 for single-term fp16's 11). The logits are
+    fg_forward's, bit for bit (the count changes no arithmetic)."""
+    w = seeded_weights(d, 8)
+    ids = uniform_ids(B * 7 + T, B * T, d.vocab)
+    c, s = tables(d, T)
+    m = engine.Model(d, stacks=w)
+    m.set_rope(c, s)
+    m.set_forward_f16(f16)
+    lg, npos = m.forward_pos(ids, B, T)
+    lg0, _ = m.forward(ids, B, T)
+    assert np.array_equal(lg, lg0)
+    _, ref, amb = O.gpt_forward_pos(ids, c, s, w, d, B, T, rel_tol=2e-3 if f16 else 1e-4)
+    diff = np.abs(npos.astype(np.int64) - ref)
+    record("forward_pos_counts", dims=str(d), B=B, T=T, f16=f16, total=int(ref.sum()),
+           max_diff=int(diff.max()), ambiguous=int(amb.sum()),
+           frac_positive=float(ref.sum() / (d.n_layer * B * d.n_head * T * (T + 1) / 2)))
+    assert np.all(diff <= amb)
+    m.close()
+
+
 def test_forward_d12_vs_oracle(d12):
     d, w, m, c, s = d12
     T = 256

@@ -197,3 +197,49 @@ def test_gqa20_prefill2048_f16_rows():
     assert e < TOL
     assert bounded
     m.close()
+
+
+def test_f16_overflow_is_an_error():
+    """An activation beyond fp16's range fails the pass with FG_ERANGE
+    instead of returning inf / NaN logits. c_fc scaled by 2^10 (still
+    bf16-exact) puts relu^2 of the fc outputs far above 65504: fg_forward,
+    fg_eval_bpb and a device-pointer pass (reported at the next fg_sync)
+    refuse with the option on; the split path computes the same rows with
+    finite logits, and the flag does not outlive its report."""
+    from tests.devbuf import DevBuf
+    d = SMALL
+    w = seeded_weights(d, 9)
+    w["c_fc"] = (w["c_fc"] * np.float32(1024.0)).astype(np.float32)
+    B, T = 2, 200
+    ids = uniform_ids(10, B * T, d.vocab)
+    c, s = tables(d, T)
+    m = engine.Model(d, stacks=w)
+    m.set_rope(c, s)
+    lg, _ = m.forward(ids, B, T)
+    assert np.isfinite(lg).all()
+    m.set_forward_f16(True)
+    with pytest.raises(engine.FgptError) as e:
+        m.forward(ids, B, T)
+    assert e.value.code == -10 and "fp16" in str(e.value)
+    rows = np.concatenate([ids.reshape(B, T), ids.reshape(B, T)[:, :1]], axis=1)
+    with pytest.raises(engine.FgptError) as e:
+        m.eval_bpb(rows, np.ones(d.vocab, np.int32), batch=B)
+    assert e.value.code == -10
+    d_ids = DevBuf(ids.astype(np.int32))
+    d_lg = DevBuf(np.zeros(B * T * d.vocab, np.float32))
+    m.forward_dev(d_ids.ptr, B, T, d_lg.ptr)
+    with pytest.raises(engine.FgptError) as e:
+        m.sync()
+    assert e.value.code == -10
+    m.sync()  # reported once
+    d_ids.free()
+    d_lg.free()
+    # the same weights without the scale pass on the fp16 path
+    m.close()
+    w["c_fc"] = (w["c_fc"] / np.float32(1024.0)).astype(np.float32)
+    m = engine.Model(d, stacks=w)
+    m.set_rope(c, s)
+    m.set_forward_f16(True)
+    lg16, _ = m.forward(ids, B, T)
+    assert np.isfinite(lg16).all()
+    m.close()

@@ -26,6 +26,11 @@ What fixes each oracle routine (reference = 14NGiestas/autoresearch):
   or_gpt_step_multi chunked == per-token == forward (:1466-1550); cache-full
                     and TB<1 errors (src/lib/fortran_kv.f90:74-77,209-216)
   or_nll            float64 logsumexp - logit[target]
+  or_attn_pos_count closed forms (scores all > 0, all < 0, exactly 0 on some
+                    rows: the strict >), the GQA head -> kv head mapping,
+                    float64 counts on random inputs
+  or_gpt_forward_pos  logits bit-equal to or_gpt_forward; per-layer counts
+                    equal to the float64 forward's (tests/np_ref.py)
   or_frand_fill     input generator only (no parity claim): range and
                     determinism
 """
@@ -264,3 +269,61 @@ def test_nll_vs_logsumexp():
     out = O.nll(lg, tg, 300)
     ref = np_ref.nll(lg, tg)
     assert np.max(np.abs(out - ref)) < 1e-5
+
+
+def test_attn_pos_count_closed_forms():
+    """attn_sgemm's positive-score count (src/lib/fortran_attn.f90:249-254):
+    q = k with positive entries makes every causal score > 0 (T(T+1)/2 per
+    row and head), q = -k none; query rows of zeros give scores of exactly
+    0, which the strict > does not count."""
+    B, T, H, D = 2, 7, 2, 4
+    k = np.full((B, T, H, D), 0.5, np.float32)
+    n, _ = O.attn_pos_count(k, k, B, T, H, H, D)
+    assert np.all(n == T * (T + 1) // 2)
+    n, _ = O.attn_pos_count(-k, k, B, T, H, H, D)
+    assert np.all(n == 0)
+    q = k.copy()
+    q[:, 1::2] = 0.0  # odd query positions: scores exactly 0
+    n, amb = O.attn_pos_count(q, k, B, T, H, H, D)
+    assert np.all(n == sum(t + 1 for t in range(0, T, 2)))
+    assert np.all(amb == sum(t + 1 for t in range(1, T, 2)))  # the zeros sit at 0
+
+
+def test_attn_pos_count_gqa_mapping():
+    """Query head h reads kv head h / (H/KH) (src/lib/fortran_attn.f90:226):
+    with kv head 0 positive and kv head 1 negative, heads 0-1 count every
+    score and heads 2-3 none."""
+    B, T, H, KH, D = 1, 5, 4, 2, 4
+    q = np.ones((B, T, H, D), np.float32)
+    k = np.ones((B, T, KH, D), np.float32)
+    k[:, :, 1] = -1.0
+    n, _ = O.attn_pos_count(q, k, B, T, H, KH, D)
+    assert n.tolist() == [[T * (T + 1) // 2] * 2 + [0, 0]]
+
+
+def test_attn_pos_count_random_vs_float64():
+    rng = np.random.default_rng(3)
+    B, T, H, KH, D = 2, 33, 4, 2, 16
+    q = rng.standard_normal((B, T, H, D)).astype(np.float32)
+    k = rng.standard_normal((B, T, KH, D)).astype(np.float32)
+    n, amb = O.attn_pos_count(q, k, B, T, H, KH, D)
+    kk = np.repeat(k.astype(np.float64), H // KH, axis=2)
+    s = np.einsum("bqhd,bkhd->bhqk", q.astype(np.float64), kk)
+    causal = np.tril(np.ones((T, T), bool))
+    ref = ((s > 0) & causal).sum(axis=(2, 3))
+    assert np.all(np.abs(n - ref) <= amb)
+    assert 0 < n.min() and n.max() < T * (T + 1) // 2
+
+
+@pytest.mark.parametrize("d", [TINY, TINY_GQA])
+def test_gpt_forward_pos_vs_float64(d):
+    w = frand_weights(d, 19)
+    B, T = 2, 9
+    ids = uniform_ids(4, B * T, d.vocab)
+    c, s = O.rope_tables(T, d.head_dim)
+    lg, npos, namb = O.gpt_forward_pos(ids, c, s, w, d, B, T)
+    assert np.array_equal(lg, O.gpt_forward(ids, c, s, w, d, B, T))
+    ref, closest = np_ref.pos_counts(ids, c, s, w, d, B, T)
+    assert np.all(np.abs(npos - ref) <= namb)
+    assert closest > 1e-4 or namb.sum() > 0
+    assert npos.shape == (d.n_layer, B, d.n_head)
