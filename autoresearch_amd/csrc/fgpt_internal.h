@@ -328,7 +328,14 @@ void launch_sample_step(hipStream_t s, SampleDev* sd, const float* logits, int V
 constexpr int FUSED_NWG = 256;  // workgroups (CUs)
 constexpr int FUSED_NX = 8;     // XCDs
 constexpr int FUSED_NC = 32;    // workgroups per XCD
-constexpr int FUSED_MAX_LEN = 128;  // attention positions a step may see
+constexpr int FUSED_MAX_LEN = 2048;  // attention positions a step may see
+// From this many positions on, a head's attention is split over
+// FUSED_SPLIT_WG workgroups of its XCD (each takes every FUSED_SPLIT_WG-th
+// position) and their partial results meet in one more hand-over within the
+// XCD; below it every workgroup of the XCD computes the whole attention of
+// the head itself.
+constexpr int FUSED_SPLIT_MIN = 128;
+constexpr int FUSED_SPLIT_WG = 8;
 
 struct FusedLayout {
   bool ok = false;
@@ -339,7 +346,7 @@ struct FusedLayout {
   int64_t cu_bytes;         // bytes of one workgroup's region of the fused arena
   int64_t lds_bytes;        // dynamic LDS of the kernel
   int64_t slots;            // exchange slots (8 bytes each)
-  int64_t off_ql, off_pp, off_xl, off_hl, off_p2, off_lm;  // slot offsets
+  int64_t off_ql, off_pp, off_xl, off_hl, off_p2, off_lm, off_ap;  // slot offsets
 };
 // The layout for dims d; ok = false (with the reason in *why) when the
 // fused kernel does not serve them.

@@ -29,10 +29,12 @@
 // launch has its own epoch and the host advances the base across launches,
 // so a stale slot is never taken. Every poll is bounded: past the bound the
 // workgroup raises the error flag and all workgroups leave, so the grid
-// always drains. Per layer: q/k/v within the XCD, c_proj partials across,
-// the updated residual within, the fc block within, c_proj2 partials
-// across, the residual within; the step ends with the lm_head argmax
-// candidates of all 256 workgroups.
+// always drains. Per layer: q/k/v within the XCD, (from FUSED_SPLIT_MIN
+// positions on) the attention partials of the XCD's workgroups within,
+// c_proj partials across, the updated residual within, the fc block
+// within, c_proj2 partials across, the residual within; the step ends with
+// the lm_head argmax candidates of all 256 workgroups, one hand-over
+// across.
 //
 // Arithmetic per output element: rmsnorm0 (src/lib/fortran_rmsnorm.f90:
 // 40-60) as a scale of the dot products, fp32 accumulation of bf16 weights
@@ -208,7 +210,8 @@ struct FusedShape {
   static constexpr int64_t OFF_HL = OFF_XL + 2 * FUSED_NX * D;
   static constexpr int64_t OFF_P2 = OFF_HL + 2 * FUSED_NX * HN;
   static constexpr int64_t OFF_LM = OFF_P2 + 2 * FUSED_NX * D;
-  static constexpr int64_t SLOTS = OFF_LM + 2 * FUSED_NWG * 2 + 2 * FUSED_NX * 2;
+  static constexpr int64_t OFF_AP = OFF_LM + 2 * FUSED_NWG * 2;  // (the argmax candidates)
+  static constexpr int64_t SLOTS = OFF_AP + 2 * FUSED_NX * FUSED_SPLIT_WG * (HD + 2);
 };
 // The shapes the persistent decode is built for: depth-12's (d_model 768,
 // 6 heads, vocab 8192) and a small one the tests run.
@@ -253,8 +256,11 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
   constexpr int NP = QLN / 64;           // rotation pairs per workgroup (6)
   constexpr int LPP = HD / 4;            // lanes per cached row in the attention
   constexpr int NG = 4 * (64 / LPP);     // position groups
-  constexpr int PPG = FUSED_MAX_LEN / NG;  // positions per group, at most
+  // positions per group, at most: below FUSED_SPLIT_MIN, or (split) of
+  // this workgroup's every FUSED_SPLIT_WG-th position
+  constexpr int PPG = std::max(FUSED_SPLIT_MIN / NG, FUSED_MAX_LEN / (FUSED_SPLIT_WG * NG));
   constexpr int AST = HD + 4;            // floats per group record: o, m, l
+  constexpr int APS = HD + 2;            // slots per workgroup attention partial: o, m, l
   constexpr int AB = 8;                  // attention positions per batch
   static_assert(LPP == 32 && NP == 6, "the work split is laid out for head_dim 128");
   constexpr int D = Sh::D, H = Sh::H, V = Sh::V, KD = Sh::H * HD;
@@ -275,6 +281,11 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
   int* stop = ired + 8;         // nonzero: leave (a hand-over failed)
   int* place = stop + 1;        // this workgroup's XCD and its index there
   float* rope = (float*)(place + 2);  // cos, sin of the step's position [2][HD/2]
+  // split attention: the XCD's workgroup partials [FUSED_SPLIT_WG][AST], at the
+  // first 16-byte boundary past rope (an offset from lds, so LDS accesses)
+  constexpr int64_t ROPE_END = 2 * Sh::WBUF + 4 * ((int64_t)D + HN + QLN + NG * AST + 4 * 8 * 64 +
+                                                   8 + 8 + 1 + 2 + HD);
+  float* apart = (float*)(lds + (ROPE_END + 15) / 16 * 16);
   uint32_t* err = a.err;
   const int E = 8 * L + 8;      // epochs per step
   const int total = a.n_steps * (L + 1);  // pseudo-layers of the launch
@@ -420,16 +431,25 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
           mark(s, l, 1);
         }
         // attention of head g over positions 0..pos: group grp (half a
-        // wave) takes positions grp, grp+NG, ...; the current position's k
-        // and v come from the hand-over, earlier ones from the cache. The
-        // first batch's cache rows are requested before the wait for q/k/v.
+        // wave) takes positions grp, grp+NG, ... -- or, from FUSED_SPLIT_MIN
+        // positions on, workgroup c < FUSED_SPLIT_WG takes only the
+        // positions c, c + FUSED_SPLIT_WG, ... (group grp: c +
+        // FUSED_SPLIT_WG (grp + NG i)), the others none, and the partial
+        // results are merged after one more hand-over. The current
+        // position's k and v come from the hand-over, earlier ones from the
+        // cache. The first batch's cache rows are requested before the wait
+        // for q/k/v.
+        const bool split = pos >= FUSED_SPLIT_MIN;  // (uniform)
+        const bool attend = !split || c < FUSED_SPLIT_WG;
         const int grp = wv * 2 + (lane >> 5), dl = lane & 31;
+        const int pb = split ? c : 0, ps = split ? FUSED_SPLIT_WG : 1;
+        auto posof = [&](int i) { return pb + ps * (grp + NG * i); };
         float4 kr[AB], vr[AB];
         if (comp) {
 #pragma unroll
           for (int i = 0; i < AB; ++i) {
-            const int p = grp + NG * i;
-            if (p < pos) {
+            const int p = posof(i);
+            if (attend && p < pos) {
               kr[i] = *(const float4*)(kc + (int64_t)p * KD + 4 * dl);
               vr[i] = *(const float4*)(vc + (int64_t)p * KD + 4 * dl);
             }
@@ -439,15 +459,16 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
         lds_barrier();  // B1
         mark(s, l, 2);
         if (*stop) goto done;
-        if (comp) {
+        if (comp && attend) {
           const float4 q4 = *(const float4*)(qkv_lds + 4 * dl);
           const float scale = 1.0f / sqrtf((float)HD);
           float m = -INFINITY, lsum = 0.f;
           float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-          for (int i0 = 0; i0 < PPG && grp + NG * i0 <= pos; i0 += AB) {
+#pragma unroll 1
+          for (int i0 = 0; i0 < PPG && posof(i0) <= pos; i0 += AB) {
 #pragma unroll
             for (int i = 0; i < AB; ++i) {
-              const int p = grp + NG * (i0 + i);
+              const int p = posof(i0 + i);
               if (p >= pos) {
                 kr[i] = *(const float4*)(qkv_lds + HD + 4 * dl);
                 vr[i] = *(const float4*)(qkv_lds + 2 * HD + 4 * dl);
@@ -463,7 +484,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
 #pragma unroll
             for (int i = 0; i < AB; ++i) {
               const float dp = q4.x * kr[i].x + q4.y * kr[i].y + q4.z * kr[i].z + q4.w * kr[i].w;
-              sc[i] = grp + NG * (i0 + i) <= pos ? half_sum(dp) * scale : -INFINITY;
+              sc[i] = posof(i0 + i) <= pos ? half_sum(dp) * scale : -INFINITY;
               mb = fmaxf(mb, sc[i]);
             }
             const float mn = fmaxf(m, mb), al = __expf(m - mn);
@@ -491,13 +512,12 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
         }
         lds_barrier();  // B2
         mark(s, l, 3);
-        // c_proj partial of head g over this workgroup's C output columns:
-        // wave w takes outputs w, w+4, ...
-        if (comp) {
-          float mx = -INFINITY;
+        // the groups' records merged in group order: this lane's head dims
+        // 2*lane, 2*lane+1 (o0, o1, unnormalised), the maximum and the sum
+        float mx = -INFINITY, ls = 0.f, o0 = 0.f, o1 = 0.f;
+        if (comp && attend) {
 #pragma unroll
           for (int q = 0; q < NG; ++q) mx = fmaxf(mx, att[q * AST + HD]);
-          float ls = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll
           for (int q = 0; q < NG; ++q) {
             const float w = __expf(att[q * AST + HD] - mx);
@@ -505,6 +525,53 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
             o0 += att[q * AST + 2 * lane] * w;
             o1 += att[q * AST + 2 * lane + 1] * w;
           }
+        }
+        if (split) {
+          // this workgroup's partial to the XCD (wave 0), then every
+          // workgroup merges the FUSED_SPLIT_WG partials in workgroup order
+          uint64_t* AP = S + Sh::OFF_AP + (int64_t)(par * 8 + g) * FUSED_SPLIT_WG * APS;
+          if (wv == 0 && attend) {
+            slot_put_xcd(AP + (int64_t)c * APS + 2 * lane, o0, ep + 6);
+            slot_put_xcd(AP + (int64_t)c * APS + 2 * lane + 1, o1, ep + 6);
+            if (lane == 0) {
+              slot_put_xcd(AP + (int64_t)c * APS + HD, mx, ep + 6);
+              slot_put_xcd(AP + (int64_t)c * APS + HD + 1, ls, ep + 6);
+            }
+          }
+          if (comp) {
+            // slot j = w * APS + e of the FUSED_SPLIT_WG x APS lands at
+            // apart[w * AST + e]
+            constexpr int NJ = (FUSED_SPLIT_WG * APS + 255) / 256;
+            float v[NJ];
+            const int cnt = (FUSED_SPLIT_WG * APS - tid + 255) / 256;
+            if (!slots_wait<NJ>(AP + tid, 256, cnt, ep + 6, v, err)) *stop = 1;
+#pragma unroll
+            for (int i = 0; i < NJ; ++i)
+              if (i < cnt) {
+                const int j = tid + 256 * i;
+                apart[(j / APS) * AST + j % APS] = v[i];
+              }
+          }
+          lds_barrier();  // B2s
+          mark(s, l, 12);
+          if (*stop) goto done;
+          mx = -INFINITY;
+          ls = o0 = o1 = 0.f;
+          if (comp) {
+#pragma unroll
+            for (int w = 0; w < FUSED_SPLIT_WG; ++w) mx = fmaxf(mx, apart[w * AST + HD]);
+#pragma unroll
+            for (int w = 0; w < FUSED_SPLIT_WG; ++w) {
+              const float e = __expf(apart[w * AST + HD] - mx);
+              ls += apart[w * AST + HD + 1] * e;
+              o0 += apart[w * AST + 2 * lane] * e;
+              o1 += apart[w * AST + 2 * lane + 1] * e;
+            }
+          }
+        }
+        // c_proj partial of head g over this workgroup's C output columns:
+        // wave w takes outputs w, w+4, ...
+        if (comp) {
           const float il = 1.0f / ls;
           const float ao0 = o0 * il, ao1 = o1 * il;  // head dims 2*lane, 2*lane+1
           for (int j0 = wv; j0 < C; j0 += 32) {
@@ -596,10 +663,8 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       const int G = s * (L + 1) + L;
       const uint8_t* W = lds + (G & 1) * Sh::WBUF;
       const uint32_t ep = a.ep_base + (uint32_t)(s * E + 8 * L);
-      // argmax candidates: per workgroup within its XCD [2][8][32][2], then
-      // per XCD across [2][8][2]
-      uint64_t* LMX = S + Sh::OFF_LM + ((int64_t)(s & 1) * FUSED_NX + g) * FUSED_NC * 2;
-      uint64_t* LMG = S + Sh::OFF_LM + 2 * FUSED_NWG * 2 + (int64_t)(s & 1) * FUSED_NX * 2;
+      // argmax candidates of the 256 workgroups, [2][256][2] (value, index)
+      uint64_t* LMC = S + Sh::OFF_LM + (int64_t)(s & 1) * FUSED_NWG * 2;
       if (comp) {
         const float inv = 1.0f / sqrtf(sumsq<D>(x_lds, lane) / (float)D + eps);
         float bv = -INFINITY;
@@ -634,50 +699,29 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       }
       lds_barrier();  // B5
       if (loader && G + 1 < total) issue(G + 1, 1);
-      // the first-max argmax over all 256 candidates in two hand-overs: the
-      // 32 candidates of this XCD (every workgroup of it reduces them
-      // alike), then the 8 XCD winners (wave 0 only)
+      // the first-max argmax over all 256 candidates in one hand-over
+      // across XCDs: every workgroup publishes its candidate and reads all
+      // 256 (wave 0, four per lane), reducing them alike
       if (wv == 0) {
         if (lane == 0) {
           float v = red[0];
           int i = ired[0];
           for (int w = 1; w < 4; ++w) amax_take(v, i, red[w], ired[w]);
-          slot_put_xcd(LMX + 2 * c, v, ep);
-          slot_put_xcd(LMX + 2 * c + 1, __int_as_float(i), ep);
+          slot_put_dev(LMC + 2 * b, v, ep);
+          slot_put_dev(LMC + 2 * b + 1, __int_as_float(i), ep);
         }
-        float cv[2];
+        float cv[4], ci[4];
         float bv = -INFINITY;
         int bi = 0x7fffffff;
-        if (lane < FUSED_NC) {
-          if (slots_wait<2>(LMX + 2 * lane, 1, 2, ep, cv, err)) {
-            bv = cv[0];
-            bi = __float_as_int(cv[1]);
-          } else {
-            *stop = 1;
-          }
+        if (slots_wait<4>(LMC + 2 * lane, 128, 4, ep, cv, err) &&
+            slots_wait<4>(LMC + 2 * lane + 1, 128, 4, ep, ci, err)) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) amax_take(bv, bi, cv[k], __float_as_int(ci[k]));
+        } else {
+          *stop = 1;
         }
 #pragma unroll
-        for (int o = 16; o > 0; o >>= 1) {
-          const float v2 = __shfl_xor(bv, o, 64);
-          const int i2 = __shfl_xor(bi, o, 64);
-          amax_take(bv, bi, v2, i2);
-        }
-        if (lane == 0 && c == 0) {
-          slot_put_dev(LMG + 2 * g, bv, ep + 1);
-          slot_put_dev(LMG + 2 * g + 1, __int_as_float(bi), ep + 1);
-        }
-        bv = -INFINITY;
-        bi = 0x7fffffff;
-        if (lane < FUSED_NX && !*stop) {
-          if (slots_wait<2>(LMG + 2 * lane, 1, 2, ep + 1, cv, err)) {
-            bv = cv[0];
-            bi = __float_as_int(cv[1]);
-          } else {
-            *stop = 1;
-          }
-        }
-#pragma unroll
-        for (int o = 4; o > 0; o >>= 1) {
+        for (int o = 32; o > 0; o >>= 1) {
           const float v2 = __shfl_xor(bv, o, 64);
           const int i2 = __shfl_xor(bi, o, 64);
           amax_take(bv, bi, v2, i2);
@@ -741,7 +785,9 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
   // place, rope (floats / ints)
   const int64_t act = 4 * ((int64_t)d.D + f.HN + 3 * FUSED_HD + NG * (FUSED_HD + 4) + 4 * 8 * 64 +
                            8 + 8 + 1 + 2 + FUSED_HD);
-  f.lds_bytes = 2 * f.wbuf + act;
+  // then the split attention's partials [FUSED_SPLIT_WG][hd + 4] on a
+  // 16-byte boundary
+  f.lds_bytes = (2 * f.wbuf + act + 15) / 16 * 16 + 4 * (int64_t)FUSED_SPLIT_WG * (FUSED_HD + 4);
   if (f.lds_bytes > 160 * 1024) return no("weight slices do not fit twice in LDS");
   f.off_ql = 0;
   f.off_pp = f.off_ql + 2 * FUSED_NX * 3 * (int64_t)d.hd;
@@ -749,7 +795,8 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
   f.off_hl = f.off_xl + 2 * FUSED_NX * (int64_t)d.D;
   f.off_p2 = f.off_hl + 2 * FUSED_NX * (int64_t)f.HN;
   f.off_lm = f.off_p2 + 2 * FUSED_NX * (int64_t)d.D;
-  f.slots = f.off_lm + 2 * FUSED_NWG * 2 + 2 * FUSED_NX * 2;
+  f.off_ap = f.off_lm + 2 * FUSED_NWG * 2;
+  f.slots = f.off_ap + 2 * FUSED_NX * FUSED_SPLIT_WG * (int64_t)(d.hd + 2);
   f.ok = true;
   return f;
 }
@@ -796,7 +843,7 @@ uint32_t fused_epochs(const Dims& d, int n_steps) { return (uint32_t)n_steps * (
 template <class Sh>
 static hipError_t launch_shape(hipStream_t s, const FusedLayout& f, const FusedArgs& a) {
   if (f.slice != Sh::SLICE || f.lmb != Sh::LMB || f.wbuf != Sh::WBUF || f.wf != Sh::WF ||
-      f.off_lm != Sh::OFF_LM || f.slots != Sh::SLOTS)
+      f.off_lm != Sh::OFF_LM || f.off_ap != Sh::OFF_AP || f.slots != Sh::SLOTS)
     return hipErrorInvalidValue;  // (host and device layouts disagree)
   const void* k = a.trace ? (const void*)k_fused_decode<Sh, true> : (const void*)k_fused_decode<Sh, false>;
   hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)f.lds_bytes);

@@ -366,7 +366,11 @@ contains
     allocate (ids(ntot), plain(max(ngen, 1)), lg(64*V))
     ids(1:nprompt) = prompt(1:nprompt)
 
-    ! plain greedy on its own cache (spec_bench's run_plain)
+    ! plain greedy on its own cache (spec_bench's run_plain): the per-kernel
+    ! steps, whose arithmetic the verification pass repeats row by row (the
+    ! persistent loop sums in another order)
+    rc = fg_set_option(model, FG_OPT_FUSED_DECODE, 0_c_int32_t)
+    if (rc /= FG_OK) call stop_rc('fg_set_option', rc)
     call prefill(kv2)
     t0 = now()
     if (ngen > 0) then

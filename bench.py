@@ -334,7 +334,15 @@ def bench_spec(m, d, reps, warmup, k=8, match=2, probe=8, min_acc=0.5):
             out = fn()
         return out, (time.perf_counter() - t0) / reps
 
-    g, t_g = timed(lambda: kv.decode_greedy(prompt[-1:], n_gen)[0][:, 0])
+    # plain greedy as per-kernel steps (the arithmetic the verification pass
+    # repeats row by row, so the streams must be equal), and the persistent
+    # loop beside it
+    m.set_fused_decode(False)
+    try:
+        g, t_g = timed(lambda: kv.decode_greedy(prompt[-1:], n_gen)[0][:, 0])
+    finally:
+        m.set_fused_decode(True)
+    gf, t_f = timed(lambda: kv.decode_greedy(prompt[-1:], n_gen)[0][:, 0])
     (sp, st), t_s = timed(lambda: kv.decode_spec(prompt, n_gen, k=k, match=match, probe=probe,
                                                  min_acc=min_acc))
     kv.close()
@@ -342,6 +350,8 @@ def bench_spec(m, d, reps, warmup, k=8, match=2, probe=8, min_acc=0.5):
         raise RuntimeError("speculative stream differs from the greedy stream")
     return {"prompt": int(prompt.size), "gen": n_gen, "k": k, "match": match,
             "greedy_tok_s": n_gen / t_g, "spec_tok_s": n_gen / t_s, "speedup": t_g / t_s,
+            "persistent_greedy_tok_s": n_gen / t_f,
+            "persistent_stream_equal": bool(np.array_equal(gf, g)),
             "stats": st, "streams_equal": True}
 
 
@@ -367,7 +377,11 @@ def bench_sample(m, d, reps, warmup, n_gen=256):
             out = fn()
         return out, (time.perf_counter() - t0) / reps
 
-    _, t_g = timed(lambda: kv.decode_greedy(prompt[-1:], n_gen))
+    m.set_fused_decode(False)  # the per-kernel steps sampling is built on
+    try:
+        _, t_g = timed(lambda: kv.decode_greedy(prompt[-1:], n_gen))
+    finally:
+        m.set_fused_decode(True)
     (ids, _), t_s = timed(lambda: kv.decode_sample(prompt, n_gen, seed=12345, **cfg))
     m.timing(True)
     kv.len = L0
@@ -658,12 +672,15 @@ def run_cpu_baseline() -> dict:
     return out
 
 
-WORKLOADS = ("prefill", "decode_b1", "eval_b8", "decode_b64", "decode_b64_fp32kv", "gqa20",
-             "decode_spec", "decode_sample")
+WORKLOADS = ("prefill", "decode_b1", "decode_b1_ctx1k", "eval_b8", "decode_b64",
+             "decode_b64_fp32kv", "gqa20", "decode_spec", "decode_sample")
 
 # what the final line keeps of a roofline record (the full records go to stderr)
 ROOF_KEYS = ("bound", "kernel_kind", "avg_launch_us", "achieved", "peak", "unit", "frac",
              "traffic", "mfma_executed_frac", "mfma_util")
+# (the workload records leave out peak and unit: the line's "peaks" holds
+# them, per bound)
+ROOF_KEYS_NESTED = tuple(k for k in ROOF_KEYS if k not in ("peak", "unit"))
 
 
 def sig(v, n=5):
@@ -671,10 +688,10 @@ def sig(v, n=5):
     return float(f"{v:.{n}g}") if isinstance(v, float) and math.isfinite(v) else v
 
 
-def brief_roof(r):
+def brief_roof(r, keys=ROOF_KEYS_NESTED):
     if not r:
         return r
-    return {k: sig(v) for k, v in r.items() if k in ROOF_KEYS}
+    return {k: sig(v) for k, v in r.items() if k in keys}
 
 
 def brief(rec):
@@ -762,6 +779,10 @@ def main():
             "decode_b1": lambda: bench_decode(m, d, 1, 16, 32, reps=max(args.steps, 5),
                                               warmup=args.warmup,
                                               profile="profiles/decode_d12_B1_fused.md"),
+            # the B=1 loop at chat_text's context: a 1032-id prompt, 64 steps
+            "decode_b1_ctx1k": lambda: bench_decode(
+                m, d, 1, 1032, 64, reps=max(args.steps // 4, 3), warmup=1,
+                profile="profiles/decode_d12_B1_ctx1k_fused.md"),
             "eval_b8": lambda: bench_eval_b8(m, d, max(3, args.steps // 4), 1, torch,
                                              args.operands),
             "decode_b64": lambda: bench_decode(m, d, 64, 1024, 512, reps=1, warmup=0,
@@ -821,8 +842,8 @@ def main():
         with open(args.detail, "w") as f:
             json.dump({"records": rec, "pmc": pmc, "cpu_baseline": cpu}, f, indent=1)
 
-    def roof_line(r):
-        out = brief_roof(r)
+    def roof_line(r, keys=ROOF_KEYS_NESTED):
+        out = brief_roof(r, keys)
         if r and r.get("traffic_detail"):
             out["traffic"] = round(r["traffic_detail"]["bytes"])
         if r and r.get("mfma_counters"):
@@ -837,7 +858,8 @@ def main():
         "config": {"workload": "depth-12 prefill, B=1, T=2048: fp32 logits [2048,8192] + "
                                "per-token CE", "global_batch": 1, "seq_len": 2048,
                    "parallelism": "single GPU"},
-        "roofline": roof_line(pre["roofline"]),
+        "roofline": roof_line(pre["roofline"], ROOF_KEYS),
+        "peaks": {"hbm": [HBM_PEAK_GBS, "GB/s"], "mfma": [MFMA_BF16_PEAK_TFS, "TFLOP/s"]},
         "cpu_baseline": None if cpu is None else {
             k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
     }

@@ -130,28 +130,70 @@ def test_fused_replay_and_chained_calls(d12):
     kv.close()
 
 
-def test_fused_small_mha_to_max_length():
-    """Small MHA dims (d_model 256, 2 heads of 128): the loop runs up to the
-    128 positions it serves, then a call past them takes the per-kernel
-    path; both against the oracle."""
+def test_fused_small_mha_across_split():
+    """Small MHA dims (d_model 256, 2 heads of 128): one persistent call
+    through the positions below FUSED_SPLIT_MIN (128: each workgroup of a
+    head's XCD runs the whole attention) and on past it (the attention split
+    over 8 workgroups, partials merged after one more hand-over), against
+    the oracle and the per-kernel path."""
     d = SMALL_MHA
-    w, m, c, s = setup(d, 21, 160)
+    w, m, c, s = setup(d, 21, 200)
     on, why = m.fused_decode()
     assert on, why
     prompt = uniform_ids(5, 7, d.vocab)
-    n = 150
-    ref_ids, ref_lg = O.greedy_decode(prompt, w, d, n, c, s, maxT=160)
-    kv = m.kv(1, 160)
+    n = 180
+    ref_ids, ref_lg = O.greedy_decode(prompt, w, d, n, c, s, maxT=200)
+    kv = m.kv(1, 200)
     kv.step_multi(prompt[:-1], want_logits=False)
-    i1, l1 = kv.decode_greedy(prompt[-1:], 122, want_logits=True)   # positions 6..127
-    i2, l2 = kv.decode_greedy(i1[-1], n - 122, want_logits=True)     # 128.. : per-kernel
-    ids = np.concatenate([i1, i2])[:, 0]
-    lg = np.concatenate([l1, l2])[:, 0]
-    print("small mha: ids equal", np.array_equal(ids, ref_ids), "relerr", relerr(lg, ref_lg))
-    assert np.array_equal(ids, ref_ids)
-    assert relerr(lg, ref_lg) < TOL
+    ids, lg = kv.decode_greedy(prompt[-1:], n, want_logits=True)   # positions 6..185
+    e = relerr(lg[:, 0], ref_lg)
+    print("small mha across the split: ids equal", np.array_equal(ids[:, 0], ref_ids), "relerr", e)
+    assert np.array_equal(ids[:, 0], ref_ids)
+    assert e < TOL
+    m.set_fused_decode(False)
+    try:
+        kv.len = 6
+        ids_g, lg_g = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    finally:
+        m.set_fused_decode(True)
+    assert np.array_equal(ids, ids_g)
+    print("vs per-kernel path: logits relerr", relerr(lg, lg_g))
+    assert relerr(lg, lg_g) < 1e-5
     kv.close()
     m.close()
+
+
+def test_fused_d12_long_context_vs_oracle(d12):
+    """chat_text's context length: a 1032-id prompt (cached by one chunked
+    pass), then 40 greedy steps at positions 1031..1070 in one persistent
+    call (the split attention), against the oracle (ids identical, logits
+    within the bar) and the per-kernel path; a replay is bit for bit the
+    same."""
+    d, w, m, c, s = d12
+    P, n, maxT = 1032, 40, 1080
+    prompt = uniform_ids(77, P, d.vocab)
+    ref_ids, ref_lg = O.greedy_decode(prompt, w, d, n, c, s, maxT=maxT, prefill_multi=True)
+    kv = m.kv(1, maxT)
+    kv.step_multi(prompt[:-1], want_logits=False)
+    ids, lg = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    e = relerr(lg[:, 0], ref_lg)
+    srt = np.sort(ref_lg, -1)
+    print("fused d12 at 1031..1070: ids equal", np.array_equal(ids[:, 0], ref_ids), "relerr", e,
+          "min oracle top-2 margin", float((srt[:, -1] - srt[:, -2]).min()))
+    assert np.array_equal(ids[:, 0], ref_ids)
+    assert e < TOL
+    kv.len = P - 1
+    ids2, lg2 = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    assert np.array_equal(ids, ids2) and np.array_equal(lg, lg2)
+    m.set_fused_decode(False)
+    try:
+        kv.len = P - 1
+        ids_g, lg_g = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    finally:
+        m.set_fused_decode(True)
+    assert np.array_equal(ids, ids_g)
+    assert relerr(lg, lg_g) < 1e-5
+    kv.close()
 
 
 def test_fused_not_for_unsupported_dims():
