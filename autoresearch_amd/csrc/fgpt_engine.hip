@@ -137,6 +137,9 @@ struct fg_kv {
   int64_t cap_out = 0;
   float* d_lgs = nullptr;    // [cap_lgs] per-step logits of fg_decode_greedy
   float* d_part = nullptr;   // per-chunk partials of the single-query attention
+  // its arrival counters, max(B, GEMV_MAX_ROWS) * H, zero between launches
+  // (every row count this cache is stepped with: greedy, sampling, spec)
+  uint32_t* d_dcnt = nullptr;
   int64_t cap_lgs = 0;
   // greedy speculative decoding (fg_decode_spec): the loop's device state
   // and its pinned host mirror, the sequence's ids [maxT], and the
@@ -636,6 +639,9 @@ struct PassOpts {
   // (nullable) the chunk attention's positive-score counts, attn_items(...)
   // per layer, layer after layer
   uint32_t* pos_cnt = nullptr;
+  // (nullable) the single-query attention's arrival counters
+  // (attn_decode_counters(d, rows) of them, zero between launches)
+  uint32_t* dec_cnt = nullptr;
 };
 
 // One pass over rows = B*T token rows: embedding of ids, the layer stack,
@@ -714,7 +720,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     if (one) {
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
         launch_attn_decode_pos(s, d, ws.q, lk, lv, o.kv16, B, maxT, d_pos, pos0 + 1, dec_part,
-                               ws.ao, aos,
+                               o.dec_cnt, ws.ao, aos,
                                aplane, T, o.d_rows);
       });
     } else {
@@ -1117,6 +1123,8 @@ extern "C" int32_t fg_kv_create_ex(fg_model* m, int32_t B, int32_t maxT, int32_t
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_ids, (size_t)B * 4);
   const size_t part_bytes = (size_t)attn_decode_scratch_floats(m->d, B, maxT) * 4;
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_part, part_bytes);
+  const size_t cnt_bytes = (size_t)attn_decode_counters(m->d, std::max(B, GEMV_MAX_ROWS)) * 4;
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_dcnt, cnt_bytes);
   // zeroed on the handle's stream, and finished before the cache is handed
   // out (its first user may be a caller's stream); the reference's callers
   // zero their caches too
@@ -1125,6 +1133,7 @@ extern "C" int32_t fg_kv_create_ex(fg_model* m, int32_t B, int32_t maxT, int32_t
   if (e == hipSuccess) e = hipMemsetAsync(kv->d_len, 0, 8, m->stream);
   if (e == hipSuccess) e = hipMemsetAsync(kv->d_ids, 0, (size_t)B * 4, m->stream);
   if (e == hipSuccess) e = hipMemsetAsync(kv->d_part, 0, part_bytes, m->stream);
+  if (e == hipSuccess) e = hipMemsetAsync(kv->d_dcnt, 0, cnt_bytes, m->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
   if (e != hipSuccess) {
     (void)hipStreamSynchronize(m->stream);
@@ -1133,6 +1142,7 @@ extern "C" int32_t fg_kv_create_ex(fg_model* m, int32_t B, int32_t maxT, int32_t
     if (kv->d_len) (void)hipFree(kv->d_len);
     if (kv->d_ids) (void)hipFree(kv->d_ids);
     if (kv->d_part) (void)hipFree(kv->d_part);
+    if (kv->d_dcnt) (void)hipFree(kv->d_dcnt);
     delete kv;
     return seterr(FG_EHIP, "KV cache allocation (%zu bytes): %s", 2 * n * esz,
                   hipGetErrorString(e));
@@ -1147,7 +1157,7 @@ extern "C" int32_t fg_kv_destroy(fg_kv* kv) {
   (void)hipStreamSynchronize(kv->m->stream);
   for (auto& g : kv->graphs) (void)hipGraphExecDestroy(g.second);
   void* ptrs[] = {kv->k,     kv->v,      kv->d_len, kv->d_ids,   kv->d_out,  kv->d_lgs,
-                  kv->d_part, kv->d_sst, kv->d_sids, kv->d_spart, kv->d_smp};
+                  kv->d_part, kv->d_sst, kv->d_sids, kv->d_spart, kv->d_smp, kv->d_dcnt};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   if (kv->h_sst) (void)hipHostFree(kv->h_sst);
@@ -1226,6 +1236,7 @@ int32_t kv_pass(fg_model* m, fg_kv* kv, const int32_t* h_ids, int TB, float* log
   const int64_t lstride = (int64_t)B * kv->maxT * m->d.kvd();
   PassOpts o;
   o.kv16 = kv->kv16;
+  o.dec_cnt = kv->d_dcnt;
   layer_stack(m, s, m->ws.ids, B, TB, kv->len, nullptr, kv->k, kv->v, kv->maxT, lstride,
               kv->d_part, m->ws.logits, o);
   HIPCHK(hipGetLastError());
@@ -1259,6 +1270,7 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
     PassOpts o;
     o.pos_host = pos_host;
     o.kv16 = kv->kv16;
+    o.dec_cnt = kv->d_dcnt;
     layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
                 kv->d_part, m->ws.logits, o);
     timed(m, s, FG_K_OTHER, 0, (double)B * m->d.V * 4 * (with_logits ? 2 : 1), [&] {
@@ -1273,6 +1285,7 @@ void greedy_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, bool with_logit
     o.pos_host = pos_host;
     o.embed = false;
     o.kv16 = kv->kv16;
+    o.dec_cnt = kv->d_dcnt;
     layer_stack(m, s, kv->d_ids, B, 1, 0, kv->d_len, kv->k, kv->v, kv->maxT, lstride,
                 kv->d_part, m->ws.logits, o);
     timed(m, s, FG_K_OTHER, 0, (double)B * (m->d.V * 4 * (with_logits ? 2 : 1) + 6 * m->d.D),
@@ -1430,6 +1443,7 @@ extern "C" int32_t fg_step(fg_model* m, fg_kv* kv, const int32_t* ids, float* lo
 // allocates. Its device address is taken once per device with
 // hipGetSymbolAddress; host code uses only that address, never the name.
 constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
+constexpr size_t NOALLOC_CNT_BYTES = 4096;  // at the start: attention arrival counters
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 constexpr int NOALLOC_MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
@@ -1473,26 +1487,30 @@ extern "C" int32_t fg_step_dev_noalloc(fg_model* m, fg_kv* kv, const int32_t* d_
   if (kv->len + 1 > kv->maxT)
     return seterr(FG_EFULL, "cache full (raise maxT): len %d + 1 > %d", kv->len, kv->maxT);
   RCCHK(check_rope(m, kv->len + 1));
+  // [arrival counters][activations][attention partials]: the counters sit
+  // at a fixed place nothing else writes, so they stay zero between calls
   const size_t act = align256((size_t)B * (d.D + 2 * d.qd() + d.dff) * 4);
   const size_t part = (size_t)attn_decode_scratch_floats(d, B, kv->maxT) * 4;
-  if (act + part > NOALLOC_SCRATCH_BYTES)
+  if (NOALLOC_CNT_BYTES + act + part > NOALLOC_SCRATCH_BYTES)
     return seterr(FG_EARG, "this step needs %zu bytes of scratch (B=%d, maxT=%d), above the %zu "
                            "the library holds",
-                  act + part, B, kv->maxT, NOALLOC_SCRATCH_BYTES);
+                  NOALLOC_CNT_BYTES + act + part, B, kv->maxT, NOALLOC_SCRATCH_BYTES);
   uint8_t* sp = nullptr;
   RCCHK(scratch_on(m->device, &sp));
   Work w;
   w.rows = B;
-  w.x = (float*)sp;
+  w.x = (float*)(sp + NOALLOC_CNT_BYTES);
   w.q = w.x + (size_t)B * d.D;
   w.ao = w.q + (size_t)B * d.qd();
   w.h = w.ao + (size_t)B * d.qd();
-  float* dec_part = (float*)(sp + act);
+  float* dec_part = (float*)(sp + NOALLOC_CNT_BYTES + act);
   hipStream_t s = stream ? (hipStream_t)stream : m->stream;
   const bool tm = m->timing;  // (timing records events: not on this path)
   m->timing = false;
   PassOpts o;
   o.kv16 = kv->kv16;
+  // (beyond the counters' room the attention merges in a kernel of its own)
+  if ((size_t)attn_decode_counters(d, B) * 4 <= NOALLOC_CNT_BYTES) o.dec_cnt = (uint32_t*)sp;
   layer_stack(m, s, d_ids, B, 1, kv->len, nullptr, kv->k, kv->v, kv->maxT,
               (int64_t)B * kv->maxT * d.kvd(), dec_part, d_logits, o, &w);
   if (d_next) launch_argmax(s, d_logits, B, d.V, d_next);
@@ -1587,6 +1605,7 @@ void spec_round_launches(fg_model* m, fg_kv* kv, hipStream_t s, int maxr, int po
   o.rows_single = true;
   o.d_rows = &st->rows;
   o.kv16 = kv->kv16;
+  o.dec_cnt = kv->d_dcnt;
   layer_stack(m, s, st->inp, 1, maxr, 0, &st->len, kv->k, kv->v, kv->maxT,
               (int64_t)kv->maxT * m->d.kvd(), kv->d_spart, m->ws.logits, o);
   timed(m, s, FG_K_OTHER, 0, (double)maxr * m->d.V * 4, [&] {
@@ -1772,6 +1791,7 @@ void sample_step_launches(fg_model* m, fg_kv* kv, hipStream_t s, int pos_host) {
   PassOpts o;
   o.pos_host = pos_host;
   o.kv16 = kv->kv16;
+  o.dec_cnt = kv->d_dcnt;
   layer_stack(m, s, sd->inp, 1, 1, 0, &sd->len, kv->k, kv->v, kv->maxT,
               (int64_t)kv->maxT * m->d.kvd(), kv->d_part, m->ws.logits, o);
   timed(m, s, FG_K_OTHER, 0, (double)m->d.V * 4, [&] {

@@ -234,13 +234,17 @@ void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_
 // consecutive single steps in one launch. d_len (nullable) holds the cache
 // length before the step (the first query is at *d_len), else len is the
 // length including the first query. scratch: attn_decode_scratch_floats(d,
-// B*qpr, maxT) floats (a multi-chunk step also launches a merge kernel).
-// d_rows (nullable): query rows live this launch (of B*qpr), on the device.
+// B*qpr, maxT) floats. cnt (nullable): attn_decode_counters(d, B*qpr)
+// arrival counters, zero before the first launch and left zero by every
+// launch; with them a multi-chunk step merges its chunks in the same launch,
+// else a merge kernel follows. d_rows (nullable): query rows live this
+// launch (of B*qpr), on the device.
 int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT);
+inline int64_t attn_decode_counters(const Dims& d, int rows) { return (int64_t)rows * d.H; }
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const void* kc,
                             const void* vc, bool kv16, int B, int maxT, const int32_t* d_len,
-                            int len, float* scratch, float* y, uint16_t* ys = nullptr,
-                            int64_t ys_plane = 0, int qpr = 1,
+                            int len, float* scratch, uint32_t* cnt, float* y,
+                            uint16_t* ys = nullptr, int64_t ys_plane = 0, int qpr = 1,
                             const int32_t* d_rows = nullptr);
 // argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +
 // row] (and the logits row into lgs_out at that slot, when set), then

@@ -155,7 +155,17 @@ __device__ __forceinline__ void single_store(const GemvArgs& a, int m, int r, fl
 // over the chunks they read. Each (token row, weight row) result is the same
 // sequence of operations whatever M is, so a row's value does not depend on
 // how many rows share the launch.
-template <int M, int EPI, int R>
+// 8-term dot product, one multiply then seven fused multiply-adds in index
+// order, spelled out so that every instantiation (any M, any U) rounds alike
+// whatever contraction the compiler would choose for a sum of products.
+__device__ __forceinline__ float dot8(const float (&u)[8], const float (&v)[8]) {
+  float t = u[0] * v[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) t = fmaf(u[e], v[e], t);
+  return t;
+}
+
+template <int M, int EPI, int R, int U>
 __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int pos0) {
   const int K = a.K, lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int nunits = (a.N + R - 1) / R, nch = K >> 3;
@@ -177,21 +187,40 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int pos0) {
         if (EPI == GV_RESID && R * u + r < a.N) e0[r][m] = a.y[(int64_t)m * a.N + R * u + r];
       }
     }
-#pragma unroll 2
-    for (int c = lane; c < nch; c += 64) {
-      float f[R][8];
+    // U chunks per lane in flight: every load of a round goes out before the
+    // first is used (a 5120-long row is 10 chunks a lane: one round at U = 10
+    // instead of five dependent pairs); the chunks are summed in ascending
+    // order whatever U is
+    for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+      uint4 wv[U][R];
+      float4 xa[U][M], xb[U][M];
 #pragma unroll
-      for (int r = 0; r < R; ++r) unpack8(*(const uint4*)(wr[r] + c * 8), f[r]);
+      for (int i = 0; i < U; ++i) {
+        const int c = c0 + 64 * i;
+        if (c < nch) {
 #pragma unroll
-      for (int m = 0; m < M; ++m) {
-        const float4 xa = *(const float4*)(a.x + (int64_t)m * K + c * 8);
-        const float4 xb = *(const float4*)(a.x + (int64_t)m * K + c * 8 + 4);
-        ss[m] += xa.x * xa.x + xa.y * xa.y + xa.z * xa.z + xa.w * xa.w + xb.x * xb.x +
-                 xb.y * xb.y + xb.z * xb.z + xb.w * xb.w;
+          for (int r = 0; r < R; ++r) wv[i][r] = *(const uint4*)(wr[r] + c * 8);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          acc[r][m] += f[r][0] * xa.x + f[r][1] * xa.y + f[r][2] * xa.z + f[r][3] * xa.w +
-                       f[r][4] * xb.x + f[r][5] * xb.y + f[r][6] * xb.z + f[r][7] * xb.w;
+          for (int m = 0; m < M; ++m) {
+            xa[i][m] = *(const float4*)(a.x + (int64_t)m * K + c * 8);
+            xb[i][m] = *(const float4*)(a.x + (int64_t)m * K + c * 8 + 4);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < U; ++i) {
+        if (c0 + 64 * i >= nch) break;
+        float f[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) unpack8(wv[i][r], f[r]);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const float4 p = xa[i][m], q = xb[i][m];
+          const float xv[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+          ss[m] += dot8(xv, xv);
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[r][m] += dot8(f[r], xv);
+        }
       }
     }
 #pragma unroll
@@ -219,16 +248,25 @@ __device__ __forceinline__ void gemv_rows(const GemvArgs& a, int pos0) {
   }
 }
 
-template <int M, int EPI, int R>
+template <int M, int EPI, int R, int U>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a, const int32_t* __restrict__ d_pos) {
-  gemv_rows<M, EPI, R>(a, d_pos ? *d_pos : a.pos0);
+  gemv_rows<M, EPI, R, U>(a, d_pos ? *d_pos : a.pos0);
 }
+
+// Chunks in flight per lane: rows of up to 4 chunks a lane (K <= 2048) in
+// one round; longer rows (the MLP's second matrix) in rounds of 10 for one
+// token row, fewer as x's registers grow with M. k_gemv and k_gemv_live
+// pick U alike (gemv_long), so a row's arithmetic is the same code in both.
+template <int M, bool LONG> constexpr int gemv_u() {
+  return LONG ? (M == 1 ? 10 : M == 2 ? 5 : 2) : (M <= 2 ? 4 : 2);
+}
+inline bool gemv_long(int K) { return K > 64 * 8 * 4; }
 
 // Up to 16 rows, the live count *a.d_M read on the device (a captured pass
 // whose row count changes between replays). blockIdx.y picks a group of up
 // to four rows; each group runs the exact 1-4 row body of k_gemv on its
 // rows (offset x, y and positions), groups past the live count exit.
-template <int EPI>
+template <int EPI, bool LONG>
 __global__ __launch_bounds__(256) void k_gemv_live(GemvArgs a, const int32_t* __restrict__ d_pos) {
   constexpr int R = EPI == GV_QKV ? 2 : 1;
   const int g0 = blockIdx.y * 4, ml = *a.d_M - g0;
@@ -236,10 +274,10 @@ __global__ __launch_bounds__(256) void k_gemv_live(GemvArgs a, const int32_t* __
   const int pos0 = (d_pos ? *d_pos : a.pos0) + g0;
   a.x += (int64_t)g0 * a.K;
   a.y += (int64_t)g0 * (EPI == GV_QKV ? a.H * a.hd : a.N);
-  if (ml == 1) gemv_rows<1, EPI, R>(a, pos0);
-  else if (ml == 2) gemv_rows<2, EPI, R>(a, pos0);
-  else if (ml == 3) gemv_rows<3, EPI, R>(a, pos0);
-  else gemv_rows<4, EPI, R>(a, pos0);
+  if (ml == 1) gemv_rows<1, EPI, R, gemv_u<1, LONG>()>(a, pos0);
+  else if (ml == 2) gemv_rows<2, EPI, R, gemv_u<2, LONG>()>(a, pos0);
+  else if (ml == 3) gemv_rows<3, EPI, R, gemv_u<3, LONG>()>(a, pos0);
+  else gemv_rows<4, EPI, R, gemv_u<4, LONG>()>(a, pos0);
 }
 
 template <int M, int EPI, int R>
@@ -247,7 +285,11 @@ static void gemv_grid(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   const int nunits = (a.N + R - 1) / R;
   int grid = (nunits + 3) / 4;
   if (grid > 2048) grid = 2048;
-  FG_LAUNCH((k_gemv<M, EPI, R>), dim3(grid), dim3(256), 0, s, a, d_pos);
+  constexpr int US = gemv_u<M, false>(), UL = gemv_u<M, true>();
+  if (US != UL && gemv_long(a.K))
+    FG_LAUNCH((k_gemv<M, EPI, R, UL>), dim3(grid), dim3(256), 0, s, a, d_pos);
+  else
+    FG_LAUNCH((k_gemv<M, EPI, R, US>), dim3(grid), dim3(256), 0, s, a, d_pos);
 }
 
 template <int EPI>
@@ -256,7 +298,10 @@ static void gemv_m(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   if (a.d_M) {  // a.M = the most rows the launch can be given
     int grid = (a.N / R + 3) / 4;
     if (grid > 2048) grid = 2048;
-    FG_LAUNCH((k_gemv_live<EPI>), dim3(grid, (a.M + 3) / 4), dim3(256), 0, s, a, d_pos);
+    if (gemv_long(a.K))
+      FG_LAUNCH((k_gemv_live<EPI, true>), dim3(grid, (a.M + 3) / 4), dim3(256), 0, s, a, d_pos);
+    else
+      FG_LAUNCH((k_gemv_live<EPI, false>), dim3(grid, (a.M + 3) / 4), dim3(256), 0, s, a, d_pos);
   } else if (a.M <= 1) {
     gemv_grid<1, EPI, R>(s, a, d_pos);
   } else if (a.M == 2) {
@@ -299,6 +344,7 @@ void launch_gemv(hipStream_t s, GemvEpi epi, const GemvArgs& a) {
 // decoded alone, sums alike). The cache holds fp32 (the reference's) or
 // bf16 elements (KT).
 constexpr int DPC_MIN = 64;
+constexpr int DEC_FOLD_MAX_CHUNKS = 8;  // chunks up to which a launch merges its own
 
 struct DecArgs {
   const float* q;  // [rows][H][hd]
@@ -315,6 +361,8 @@ struct DecArgs {
   int64_t ys_plane;
   float* part;  // [rows*H][nchunk][hd + 4]: O, then max and sum (and two unused
                 // floats, so every partial row starts 16-byte aligned)
+  uint32_t* cnt;  // (nullable) arrival counters, one per head group, zero
+                  // between launches: k_attn_dec merges its own chunks
 };
 
 // Floats per partial row of the single-query attention: O (HD), max, sum,
@@ -362,6 +410,85 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
+// A partial's pair of floats, written through to memory (agent scope), and
+// read back the same way by the merging workgroup.
+__device__ __forceinline__ void part_put(float* p, float x, float y) {
+  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+  __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 part_get(const float* p) {
+  const uint64_t v = __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+
+// The merge of nch chunk partials of GH heads, run by the workgroup that
+// arrived last. 256 / (HD/8) lane groups, NGH per head: group k of head j
+// takes chunks k, k + NGH, ... ascending with a running maximum (old sums
+// rescaled when it moves); the NGH groups of a head then meet at their
+// common maximum, in group order. sO: NG x HD floats of LDS, gml: the
+// groups' maxima and sums.
+template <int HD, int GH>
+__device__ void dec_fold_merge(const DecArgs& a, int row, int h0, int nch, float* sO,
+                               float (*gml)[256 / (HD / 8)]) {
+  constexpr int LPC = HD / 8, NG = 256 / LPC, NGH = NG / GH, CPG = 4;
+  const int tid = threadIdx.x, g = tid / LPC, dl = tid % LPC;
+  const int j = g / NGH, k = g % NGH;
+  const bool act = j < GH && k < nch;
+  float m = -FLT_MAX, l = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (act) {
+    const float* P = a.part + ((int64_t)row * a.H + h0 + j) * a.nchunk * dec_pstride(HD);
+    for (int c0 = k; c0 < nch; c0 += NGH * CPG) {
+      float2 ml[CPG], ov[CPG][4];
+#pragma unroll
+      for (int i = 0; i < CPG; ++i) {  // this round's loads go out together
+        const int c = min(c0 + i * NGH, nch - 1);
+        const float* pc = P + (int64_t)c * dec_pstride(HD);
+        ml[i] = part_get(pc + HD);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[i][e] = part_get(pc + 8 * dl + 2 * e);
+      }
+#pragma unroll
+      for (int i = 0; i < CPG; ++i) {
+        if (c0 + i * NGH >= nch) break;
+        const float mn = fmaxf(m, ml[i].x);
+        const float s0 = expf(m - mn), w = expf(ml[i].x - mn);
+        l = l * s0 + w * ml[i].y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[2 * e] = o[2 * e] * s0 + w * ov[i][e].x;
+          o[2 * e + 1] = o[2 * e + 1] * s0 + w * ov[i][e].y;
+        }
+        m = mn;
+      }
+    }
+  }
+  *(float4*)&sO[g * HD + 8 * dl] = make_float4(o[0], o[1], o[2], o[3]);
+  *(float4*)&sO[g * HD + 8 * dl + 4] = make_float4(o[4], o[5], o[6], o[7]);
+  if (dl == 0) {
+    gml[0][g] = m;
+    gml[1][g] = l;
+  }
+  __syncthreads();
+  for (int q4 = tid; q4 < GH * HD / 4; q4 += 256) {
+    const int jj = q4 / (HD / 4), d = 4 * (q4 % (HD / 4)), g0 = jj * NGH;
+    const int ngr = min(NGH, nch);
+    float mx = gml[0][g0];
+    for (int i = 1; i < ngr; ++i) mx = fmaxf(mx, gml[0][g0 + i]);
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+    float L = 0.f;
+    for (int i = 0; i < ngr; ++i) {
+      const float w = expf(gml[0][g0 + i] - mx);
+      const float4 u = *(const float4*)&sO[(g0 + i) * HD + d];
+      t.x += w * u.x; t.y += w * u.y; t.z += w * u.z; t.w += w * u.w;
+      L += w * gml[1][g0 + i];
+    }
+    const float inv = 1.0f / L;
+    dec_store<HD>(a, ((int64_t)row * a.H + h0 + jj) * HD, d,
+                  make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
+  }
+}
+
 template <int HD, int DPC, int GH, class KT>
 __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
   constexpr int LPP = HD / 8;        // lanes per cached row
@@ -370,6 +497,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
   static_assert(LPP == 8 || LPP == 16, "head dim 64 or 128");
   __shared__ float red[2][4][GH];
   __shared__ float so[4 * PPW][GH][HD];
+  __shared__ float gml[2][256 / LPP];
   const int G = a.H / a.KH, ng = G / GH;
   const int gi = blockIdx.x, c = blockIdx.y;
   const int row = gi / (a.KH * ng), kvh = (gi / ng) % a.KH, h0 = kvh * G + (gi % ng) * GH;
@@ -463,6 +591,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
     if (lane == 0) red[1][wv][j] = t;
   }
   __syncthreads();
+  const bool fold = a.cnt && nch > 1;
   // O of each head: the 4*PPW row partials summed in a fixed order
   for (int q4 = tid; q4 < GH * HD / 4; q4 += 256) {
     const int j = q4 / (HD / 4), d = 4 * (q4 % (HD / 4));
@@ -479,13 +608,31 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
       dec_store<HD>(a, bh * HD, d, make_float4(t.x * inv, t.y * inv, t.z * inv, t.w * inv));
     } else {
       float* P = a.part + (bh * a.nchunk + c) * dec_pstride(HD);
-      *(float4*)(P + d) = t;
-      if (d == 0) {
-        float mj = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
-        *(float2*)(P + HD) = make_float2(mj, lj);
+      const float mj = fmaxf(fmaxf(red[0][0][j], red[0][1][j]), fmaxf(red[0][2][j], red[0][3][j]));
+      if (fold) {  // written through to memory: the merging workgroup may sit on another XCD
+        part_put(P + d, t.x, t.y);
+        part_put(P + d + 2, t.z, t.w);
+        if (d == 0) part_put(P + HD, mj, lj);
+      } else {
+        *(float4*)(P + d) = t;
+        if (d == 0) *(float2*)(P + HD) = make_float2(mj, lj);
       }
     }
   }
+  if (!fold) return;
+  // Arrival: each lane's partial stores are complete before the workgroup
+  // is counted; the last of the nch chunk workgroups merges them.
+  __shared__ uint32_t last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(a.cnt + gi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (uint32_t)(nch - 1);
+  __syncthreads();
+  if (!last) return;
+  if (tid == 0)  // every chunk has arrived: ready for the next launch
+    __hip_atomic_store(a.cnt + gi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  dec_fold_merge<HD, GH>(a, row, h0, nch, &so[0][0][0], gml);
 }
 
 // k_attn_dec over a.iters consecutive blocks of DPC positions per
@@ -771,7 +918,7 @@ void launch_dec_hd(hipStream_t s, const DecArgs& a, int rows, int dpc, int gh) {
     launch_dec_gh<HD, 128, KT>(s, a, rows, gh);
   else
     launch_dec_gh<HD, DPC_MIN, KT>(s, a, rows, gh);
-  if (a.nchunk > 1)
+  if (a.nchunk > 1 && !(a.cnt && a.iters == 1))  // k_attn_dec with counters merges itself
     FG_LAUNCH((k_attn_dec_merge<HD>), dim3((unsigned)(rows * a.H)), dim3(256), 0, s, a,
               dpc * a.iters);
 }
@@ -780,8 +927,8 @@ void launch_dec_hd(hipStream_t s, const DecArgs& a, int rows, int dpc, int gh) {
 
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const void* kc,
                             const void* vc, bool kv16, int B, int maxT, const int32_t* d_len,
-                            int len, float* scratch, float* y, uint16_t* ys, int64_t ys_plane,
-                            int qpr, const int32_t* d_rows) {
+                            int len, float* scratch, uint32_t* cnt, float* y, uint16_t* ys,
+                            int64_t ys_plane, int qpr, const int32_t* d_rows) {
   DecArgs a;
   a.q = q;
   a.kc = kc;
@@ -794,7 +941,8 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   const int dpc = B * d.H >= 192 ? 128 : DPC_MIN;
   const int live = d_len ? maxT : len + qpr - 1;
   const int rows = B * qpr;
-  const int gh = dec_group(d.H / d.KH, dpc);
+  const int G = d.H / d.KH;
+  const int gh = dec_group(G, dpc);
   // blocks of dpc positions per workgroup (k_attn_dec_loop: fewer chunks to
   // merge): as many as keep 1.5 workgroups per CU on a bf16 cache (B=64: a
   // sequence and head each, no merge; 1.8 % of the step faster than one
@@ -819,6 +967,13 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.ys = ys;
   a.ys_plane = ys_plane;
   a.part = scratch;
+  // The in-launch merge costs the chunk workgroups a write-through, an
+  // agent-scope count and the last one's reads, a chain of device-scope
+  // round trips that beats a merge launch only for a few chunks (B=1, 2 KV
+  // heads x 5, 36 chunks of 64: 6.2 + 3.2 us as two launches, 11.8 us as
+  // one; at up to 6 chunks one launch is the faster)
+  if (a.nchunk > DEC_FOLD_MAX_CHUNKS) cnt = nullptr;
+  a.cnt = cnt;
   if (d.hd == 128) {
     if (kv16) launch_dec_hd<128, uint16_t>(s, a, rows, dpc, gh);
     else launch_dec_hd<128, float>(s, a, rows, dpc, gh);
