@@ -415,20 +415,38 @@ void free_work(fg_model* m) {
 }
 
 // Host threads that copy out of pinned staging memory, shared by every
-// handle: a copy is split over the workers and the calling thread. One copy
-// at a time; the workers are made on first use (again in a forked child,
-// which has none of its parent's threads) and live until the process ends.
+// handle of the process: a copy is split over the workers and the calling
+// thread, one copy at a time (handles copying large outputs at once take
+// turns). A forked child gets a pool object of its own, with new mutexes,
+// condition variables and workers: what it inherited (locks possibly held by
+// parent threads that do not exist in the child) is never touched again.
 class CopyPool {
  public:
   static void copy(void* dst, const void* src, size_t n) {
-    // never destroyed: the detached workers wait on its members until exit
-    static CopyPool* pool = new CopyPool;
+    CopyPool* pool = instance();
     std::lock_guard<std::mutex> one(pool->job_mu_);
     pool->run_job(static_cast<char*>(dst), static_cast<const char*>(src), n);
   }
 
  private:
+  explicit CopyPool(pid_t pid) : pid_(pid) {}
+  // The pool of this process, made on first use and again after a fork.
+  // Objects are never destroyed: detached workers wait on their members
+  // until exit, and a parent's object is left as the fork found it.
+  static CopyPool* instance() {
+    static std::atomic<CopyPool*> cur{nullptr};
+    const pid_t me = getpid();
+    CopyPool* p = cur.load(std::memory_order_acquire);
+    while (!p || p->pid_ != me) {
+      CopyPool* fresh = new CopyPool(me);  // (no threads until its first job)
+      if (cur.compare_exchange_strong(p, fresh, std::memory_order_acq_rel)) return fresh;
+      delete fresh;  // another thread of this process made one first: p holds it now
+    }
+    return p;
+  }
+
   static constexpr int kWorkers = 7;
+  const pid_t pid_;
   std::mutex job_mu_, mu_;
   std::condition_variable go_, done_;
   char* dst_ = nullptr;
@@ -436,7 +454,7 @@ class CopyPool {
   size_t n_ = 0, step_ = 0;
   uint64_t gen_ = 0;
   int pending_ = 0, nw_ = 0;  // nw_: workers running (fewer if the system refused threads)
-  pid_t pid_ = 0;
+  bool started_ = false;
 
   void part(int i) {
     const size_t b = (size_t)i * step_;
@@ -455,9 +473,8 @@ class CopyPool {
     }
   }
   void run_job(char* dst, const char* src, size_t n) {
-    if (pid_ != getpid()) {  // (first use, or a forked child)
-      pid_ = getpid();
-      nw_ = 0;
+    if (!started_) {
+      started_ = true;
       try {
         for (; nw_ < kWorkers; ++nw_) std::thread([this, i = nw_, g = gen_] { worker(i, g); }).detach();
       } catch (const std::system_error&) {
@@ -1446,8 +1463,17 @@ constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)4 << 20;
 constexpr size_t NOALLOC_CNT_BYTES = 4096;  // at the start: attention arrival counters
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 constexpr int NOALLOC_MAX_DEVICES = 64;
-static std::mutex g_scratch_mu;
+static std::mutex g_scratch_mu;  // also held while a call enqueues its work
 static uint8_t* g_scratch_ptr[NOALLOC_MAX_DEVICES];
+// The last uncaptured call on each device's array: its stream and an event
+// recorded after its work, so that a call on another stream while that work
+// is queued or running is refused (FG_EBUSY) instead of racing on the array.
+struct ScratchUse {
+  hipEvent_t ev = nullptr;
+  hipStream_t last = nullptr;
+  bool pending = false;
+};
+static ScratchUse g_scratch_use[NOALLOC_MAX_DEVICES];
 
 namespace {
 
@@ -1461,6 +1487,10 @@ int32_t scratch_on(int dev, uint8_t** out) {
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return seterr(FG_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    hipEvent_t ev = nullptr;
+    const hipError_t e2 = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e2 != hipSuccess) return seterr(FG_EHIP, "hipEventCreate: %s", hipGetErrorString(e2));
+    g_scratch_use[dev].ev = ev;
     g_scratch_ptr[dev] = (uint8_t*)p;
   }
   *out = g_scratch_ptr[dev];
@@ -1505,6 +1535,22 @@ extern "C" int32_t fg_step_dev_noalloc(fg_model* m, fg_kv* kv, const int32_t* d_
   w.h = w.ao + (size_t)B * d.qd();
   float* dec_part = (float*)(sp + NOALLOC_CNT_BYTES + act);
   hipStream_t s = stream ? (hipStream_t)stream : m->stream;
+  // Calls under graph capture are not tracked (their replays are ordered
+  // by the caller); an uncaptured call waits for no one: it is refused if
+  // another stream's call may still be using the array.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIPCHK(hipStreamIsCapturing(s, &cap));
+  const bool track = cap == hipStreamCaptureStatusNone;
+  std::lock_guard<std::mutex> use_lk(g_scratch_mu);
+  ScratchUse& use = g_scratch_use[m->device];
+  if (track && use.pending && use.last != s) {
+    const hipError_t q = hipEventQuery(use.ev);
+    if (q == hipErrorNotReady)
+      return seterr(FG_EBUSY, "the no-allocation scratch of device %d is in use by a call on "
+                              "another stream that has not finished",
+                    m->device);
+    if (q != hipSuccess) return seterr(FG_EHIP, "hipEventQuery: %s", hipGetErrorString(q));
+  }
   const bool tm = m->timing;  // (timing records events: not on this path)
   m->timing = false;
   PassOpts o;
@@ -1516,6 +1562,11 @@ extern "C" int32_t fg_step_dev_noalloc(fg_model* m, fg_kv* kv, const int32_t* d_
   if (d_next) launch_argmax(s, d_logits, B, d.V, d_next);
   m->timing = tm;
   HIPCHK(hipGetLastError());
+  if (track) {
+    HIPCHK(hipEventRecord(use.ev, s));
+    use.last = s;
+    use.pending = true;
+  }
   kv->len += 1;
   kv->filled = std::max(kv->filled, kv->len);
   return FG_OK;

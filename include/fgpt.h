@@ -177,9 +177,14 @@ int32_t fg_step(fg_model *m, fg_kv *kv, const int32_t *ids, float *logits, int32
  * The kv's B must take the single-row path (B <= 4 at depth-12's dims;
  * FG_EARG otherwise). The step's activations and attention partials live
  * in one 4 MiB device array the library holds per GPU (FG_EARG when B and
- * maxT need more); every call on a GPU shares it, so calls that overlap on
- * one GPU race. Nothing in it needs clearing: each kernel writes what it
- * reads later. Invalid ids are not checked on the host (they embed to NaN). */
+ * maxT need more); every call on a GPU shares it. A call on another stream
+ * while an earlier call's work may still be queued or running fails with
+ * FG_EBUSY (calls on one stream are ordered by it); calls made under graph
+ * capture are not tracked, and ordering their replays against other calls
+ * on the GPU is the caller's part. The array needs no clearing: each kernel
+ * writes what it reads later, and the attention's arrival counters at its
+ * start are zero when the library loads and left zero by every launch.
+ * Invalid ids are not checked on the host (they embed to NaN). */
 int32_t fg_step_dev_noalloc(fg_model *m, fg_kv *kv, const int32_t *d_ids, float *d_logits,
                             int32_t *d_next, void *stream);
 

@@ -2,7 +2,10 @@
 the library's own per-GPU device array) against fg_step, through the C ABI,
 on twin caches filled by the same prefill: the same kernels on the same
 inputs, so logits, next ids and the cache rows written must be identical.
-Two calls in a row, the second with fewer sequences, then the refusals.
+Two calls in a row, the second with fewer sequences, one whose attention
+spans several chunks (merged in the launch, with the arrival counters at
+the array's start), then the refusals: sizes beyond the array, and a call
+on a second stream while the first stream's call may still be running.
 """
 import ctypes as C
 
@@ -20,7 +23,7 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture(scope="module")
 def d12():
     m = engine.Model(D12, stacks=seeded_weights(D12, 1234))
-    c, s = rope_tables(64, D12.head_dim)
+    c, s = rope_tables(320, D12.head_dim)
     m.set_rope(c.reshape(-1), s.reshape(-1))
     yield D12, m
     m.close()
@@ -58,6 +61,48 @@ def test_noalloc_step_equals_step_then_smaller(d12):
     d, m = d12
     noalloc_vs_step(d, m, B=4, P=9, seed=3)
     noalloc_vs_step(d, m, B=2, P=5, seed=4)
+    # 300 cached positions: five 64-position chunks per head, merged by the
+    # last chunk workgroup to arrive; then a short one again (counters left
+    # zero by the previous launches)
+    noalloc_vs_step(d, m, B=2, P=300, seed=5)
+    noalloc_vs_step(d, m, B=1, P=7, seed=6)
+
+
+def test_noalloc_second_stream_refused_while_busy(d12):
+    """A call on stream B while stream A's call may still run fails with
+    FG_EBUSY and leaves the cache alone; once A has finished, B may call."""
+    d, m = d12
+    P = 9
+    kv = m.kv(1, P + 2)
+    kv.step_multi(uniform_ids(7, P, d.vocab)[None, :-1], want_logits=False)
+    d_ids = DevBuf(np.array([5], np.int32))
+    d_lg = DevBuf(np.zeros(d.vocab, np.float32))
+    hip = DevBuf.hip
+    sa, sb, big = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    assert hip.hipStreamCreateWithFlags(C.byref(sa), 1) == 0
+    assert hip.hipStreamCreateWithFlags(C.byref(sb), 1) == 0
+    nbig = 8 << 30
+    assert hip.hipMalloc(C.byref(big), C.c_size_t(nbig)) == 0
+    try:
+        # ~1.5 ms of fill ahead of A's step keeps it queued while B calls
+        assert hip.hipMemsetAsync(big, 0, C.c_size_t(nbig), sa) == 0
+        kv.step_dev_noalloc(d_ids.ptr, d_lg.ptr, stream=sa.value)
+        with pytest.raises(engine.FgptError, match="another stream"):
+            kv.step_dev_noalloc(d_ids.ptr, d_lg.ptr, stream=sb.value)
+        assert kv.len == P
+        assert hip.hipStreamSynchronize(sa) == 0
+        kv.step_dev_noalloc(d_ids.ptr, d_lg.ptr, stream=sb.value)
+        assert hip.hipStreamSynchronize(sb) == 0
+        assert kv.len == P + 1
+    finally:
+        hip.hipStreamSynchronize(sa)
+        hip.hipStreamSynchronize(sb)
+        hip.hipFree(big)
+        hip.hipStreamDestroy(sa)
+        hip.hipStreamDestroy(sb)
+        kv.close()
+        d_ids.free()
+        d_lg.free()
 
 
 def test_noalloc_refusals(d12):
