@@ -406,14 +406,18 @@ PMC_KINDS = {
     "decode_b64": ("decode_b64", ("k_attn_dec",)),
 }
 PMC_B64_STEPS = 16                # batched-decode steps the probe runs
+# the probe's prompt length: its 16 steps attend over 1272..1287 positions,
+# 1279.5 on average, the mean of the timed 512 steps after 1023-id prompts
+PMC_B64_PROMPT = 1272
 
 
 def pmc_probe(workload: str = "prefill", f16: bool = True):
     """Child of a `rocprofv3 --pmc` run. prefill: one warm-up and one
     measured T=2048 forward (single-term fp16 operands, or split-bf16 ones
     with f16=False); decode_b1: two loops of the B=1 decode workload (16-id
-    prompt, 32 steps); decode_b64: the batched workload's 64 x 1023-id
-    prompt pass and PMC_B64_STEPS steps on the bf16 cache. Then a 256 MiB
+    prompt, 32 steps); decode_b64: 64 sequences prefilled to
+    PMC_B64_PROMPT - 1 positions, then PMC_B64_STEPS steps on the bf16 cache
+    (the timed workload's mean context). Then a 256 MiB
     device copy whose reading calibrates the counter against known bytes.
     Every handle is closed and the device idle before the process exits."""
     import torch
@@ -434,7 +438,7 @@ def pmc_probe(workload: str = "prefill", f16: bool = True):
                 kv.decode_greedy(prompts[:, -1], 32)
             kv.close()
         elif workload == "decode_b64":
-            B, P = 64, 1024
+            B, P = 64, PMC_B64_PROMPT
             prompts = uniform_ids(42 + B, B * P, d.vocab).reshape(B, P)
             kv = m.kv(B, P + PMC_B64_STEPS, bf16=True)
             kv.step_multi(prompts[:, :-1], want_logits=False)
@@ -826,11 +830,11 @@ def main():
         r = rec.get(name)
         if t and r and r.get(field, {}).get("kernel_kind") == kind:
             if key == "decode_b64":
-                # the probed launches' own algorithmic bytes (the probe runs
-                # the first PMC_B64_STEPS steps after the 1023-id prompts)
+                # the probed launches' own algorithmic bytes (PMC_B64_STEPS
+                # steps after PMC_B64_PROMPT - 1 prefilled positions)
                 kvl = kv_pos_bytes(d) // d.n_layer
                 t["alg_bytes_per_launch"] = 64 * kvl * float(
-                    np.mean([1023 + i + 1 for i in range(PMC_B64_STEPS)]))
+                    np.mean([PMC_B64_PROMPT - 1 + i + 1 for i in range(PMC_B64_STEPS)]))
             r[field]["traffic"] = t["bytes"]
             r[field]["traffic_detail"] = t
     for key, field in (("mfma_prefill", "roofline"), ("mfma_prefill_attn", "roofline_attention")):
