@@ -339,7 +339,7 @@ constexpr int FUSED_MAX_LEN = 2048;  // attention positions a step may see
 // XCD; below it every workgroup of the XCD computes the whole attention of
 // the head itself.
 constexpr int FUSED_SPLIT_MIN = 128;
-constexpr int FUSED_SPLIT_WG = 8;
+constexpr int FUSED_SPLIT_WG = 16;  // (1 032 positions: 13.4 us a layer; 8 workgroups 14.6)
 
 struct FusedLayout {
   bool ok = false;
