@@ -756,6 +756,16 @@ bool resid_k4(int64_t M, int N, int K) {
   return K % 64 == 0 && N % 96 == 0 && mt64 * (N / 128) < ncu && t96 <= ncu && 2 * t96 > ncu;
 }
 
+// The residual GEMMs where 64x128 tiles spill into a second round over the
+// CUs and 64x160 tiles fill one (the depth-20 model's d_model 1280 at 2047
+// rows: 320 tiles of 64x128, 256 of 64x160): K split over 2 wavefront
+// groups of two (the staged tiles of four groups would not fit the LDS).
+bool resid_160(int64_t M, int N, int K) {
+  const int64_t mt64 = (M + 63) / 64, ncu = cu_count(), t160 = mt64 * (N / 160);
+  return K % 64 == 0 && N % 160 == 0 && mt64 * (N / 128) > ncu && t160 <= ncu &&
+         2 * t160 > ncu;
+}
+
 // Small M (batched decode, short chunks): too few output tiles to fill the
 // chip, so K is split over blockIdx.z as well: 64x64 tiles, enough splits
 // for ~256 blocks, each split a whole number of 32-wide slices.
@@ -906,8 +916,21 @@ void launch_tile_p(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
       launch_cfg<EPI, 64, 96, 2, 1, 64, 3, 4, P16>(s, b, d_pos);
       return;
     }
+    if (resid_160(a.M, a.N, a.K)) {
+      launch_cfg<EPI, 64, 160, 2, 1, 64, 3, 2, P16>(s, b, d_pos);
+      return;
+    }
   }
   const int bn = tile_n(a.M, a.N);
+  if constexpr (EPI == GV_QKV) {
+    // 128x128 tiles where they fit in one round and 64x128 ones would need
+    // two (the depth-20 model at 2047 rows: 224 tiles against 448)
+    const int64_t ncu = cu_count(), t128 = mt128 * (a.N / 128);
+    if (bn == 128 && !big && t128 <= ncu && 2 * t128 > ncu) {
+      launch_cfg<EPI, 128, 128, 4, 2, 32, 3, 1, P16>(s, b, d_pos);
+      return;
+    }
+  }
   if (P16 && bn == 128 && big && EPI != GV_STORE && a.M > 1024 && a.K % 64 == 0)
     // single-term QKV and residual GEMMs that fill the chip with 128x128
     // tiles: 64-wide K slices, two stages (64 KB with one fp16 A plane):
@@ -963,6 +986,7 @@ bool gemm_store_nll(int64_t M, int N) { return M > 1024 && M <= 4096 && N % 256 
 // RESID (given split-K scratch): one per row and 512 columns.
 int gemm_ssq_parts(int64_t M, int N, int K) {
   if (splitk_count(M, N, K) == 1 && resid_k4(M, N, K)) return N / 96;
+  if (splitk_count(M, N, K) == 1 && resid_160(M, N, K)) return N / 160;
   return splitk_count(M, N, K) > 1 ? (N + RED_COLS - 1) / RED_COLS : N / tile_n(M, N);
 }
 
