@@ -1103,12 +1103,22 @@ __global__ __launch_bounds__(1024) void k_greedy_tail(const float* __restrict__ 
     float* cp = lgs_out ? lgs_out + (slot * rows + r) * V : nullptr;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int j = tid; j < V; j += 1024) {
-      const float v = l[j];
-      if (cp) cp[j] = v;
-      if (v > bv) {
-        bv = v;
-        bi = j;
+    // eight values a thread in flight at once (one round trip for V <= 8192),
+    // then scanned in index order
+    for (int j0 = tid; j0 < V; j0 += 8 * 1024) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = j0 + 1024 * u < V ? l[j0 + 1024 * u] : -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + 1024 * u;
+        if (j < V) {
+          if (cp) cp[j] = v[u];
+          if (v[u] > bv) {
+            bv = v[u];
+            bi = j;
+          }
+        }
       }
     }
 #pragma unroll
@@ -1226,12 +1236,16 @@ __global__ __launch_bounds__(1024) void k_spec_commit(SpecDev* __restrict__ st,
     const float* l = logits + (int64_t)r * V;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int j = tid; j < V; j += 1024) {
-      const float v = l[j];
-      if (v > bv) {
-        bv = v;
-        bi = j;
-      }
+    for (int j0 = tid; j0 < V; j0 += 8 * 1024) {  // eight loads in flight, then in index order
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = j0 + 1024 * u < V ? l[j0 + 1024 * u] : -INFINITY;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (v[u] > bv) {  // (padding is -inf: never taken)
+          bv = v[u];
+          bi = j0 + 1024 * u;
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax_merge(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
