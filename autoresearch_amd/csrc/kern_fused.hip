@@ -58,6 +58,10 @@ namespace {
 constexpr int FUSED_HD = 128;            // head dim this kernel is built for
 constexpr int FUSED_THREADS = 320;       // 4 compute waves + 1 loader wave
 constexpr long FUSED_MAX_SPIN = 1l << 20;  // polls before a hand-over is given up
+// copies of the lm_head argmax candidates, each read by 256 / FUSED_LMC
+// workgroups (the lm_head pseudo-layer: one copy read by all 256 5.4 us,
+// 8 copies 4.6, 16 4.9, 64 5.3: more copies cost more write-through stores)
+constexpr int FUSED_LMC = 8;
 
 __device__ __forceinline__ uint64_t slot_pack(float v, uint32_t ep) {
   return ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v);
@@ -210,7 +214,8 @@ struct FusedShape {
   static constexpr int64_t OFF_HL = OFF_XL + 2 * FUSED_NX * D;
   static constexpr int64_t OFF_P2 = OFF_HL + 2 * FUSED_NX * HN;
   static constexpr int64_t OFF_LM = OFF_P2 + 2 * FUSED_NX * D;
-  static constexpr int64_t OFF_AP = OFF_LM + 2 * FUSED_NWG * 2;  // (the argmax candidates)
+  // (the argmax candidates: two step parities x FUSED_LMC copies)
+  static constexpr int64_t OFF_AP = OFF_LM + 2 * FUSED_LMC * 2 * FUSED_NWG;
   static constexpr int64_t SLOTS = OFF_AP + 2 * FUSED_NX * FUSED_SPLIT_WG * (HD + 2);
 };
 // The shapes the persistent decode is built for: depth-12's (d_model 768,
@@ -664,7 +669,7 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       const uint8_t* W = lds + (G & 1) * Sh::WBUF;
       const uint32_t ep = a.ep_base + (uint32_t)(s * E + 8 * L);
       // argmax candidates of the 256 workgroups, [2][256][2] (value, index)
-      uint64_t* LMC = S + Sh::OFF_LM + (int64_t)(s & 1) * FUSED_NWG * 2;
+      uint64_t* LMC = S + Sh::OFF_LM + (int64_t)(s & 1) * FUSED_LMC * 2 * FUSED_NWG;
       if (comp) {
         const float inv = 1.0f / sqrtf(sumsq<D>(x_lds, lane) / (float)D + eps);
         float bv = -INFINITY;
@@ -700,23 +705,28 @@ __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
       lds_barrier();  // B5
       if (loader && G + 1 < total) issue(G + 1, 1);
       // the first-max argmax over all 256 candidates in one hand-over
-      // across XCDs: every workgroup publishes its candidate and reads all
-      // 256 (wave 0, four per lane), reducing them alike
+      // across XCDs: every workgroup publishes its candidate (value in
+      // slot b, index in slot 256 + b) into FUSED_LMC copies (lane k of
+      // wave 0 writes copy k), and reads all 256 from copy b % FUSED_LMC
+      // (wave 0: four candidates a lane, values and indices in one wait),
+      // so the 256 readers are spread over FUSED_LMC regions; every
+      // workgroup reduces them alike
       if (wv == 0) {
-        if (lane == 0) {
+        if (lane < FUSED_LMC) {
           float v = red[0];
           int i = ired[0];
           for (int w = 1; w < 4; ++w) amax_take(v, i, red[w], ired[w]);
-          slot_put_dev(LMC + 2 * b, v, ep);
-          slot_put_dev(LMC + 2 * b + 1, __int_as_float(i), ep);
+          uint64_t* cp = LMC + (int64_t)lane * 2 * FUSED_NWG;
+          slot_put_dev(cp + b, v, ep);
+          slot_put_dev(cp + FUSED_NWG + b, __int_as_float(i), ep);
         }
-        float cv[4], ci[4];
+        float cv[8];  // candidates lane + 64 k: values (k < 4), then their indices
         float bv = -INFINITY;
         int bi = 0x7fffffff;
-        if (slots_wait<4>(LMC + 2 * lane, 128, 4, ep, cv, err) &&
-            slots_wait<4>(LMC + 2 * lane + 1, 128, 4, ep, ci, err)) {
+        if (slots_wait<8>(LMC + (int64_t)(b % FUSED_LMC) * 2 * FUSED_NWG + lane, 64, 8, ep, cv,
+                          err)) {
 #pragma unroll
-          for (int k = 0; k < 4; ++k) amax_take(bv, bi, cv[k], __float_as_int(ci[k]));
+          for (int k = 0; k < 4; ++k) amax_take(bv, bi, cv[k], __float_as_int(cv[4 + k]));
         } else {
           *stop = 1;
         }
@@ -795,7 +805,7 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
   f.off_hl = f.off_xl + 2 * FUSED_NX * (int64_t)d.D;
   f.off_p2 = f.off_hl + 2 * FUSED_NX * (int64_t)f.HN;
   f.off_lm = f.off_p2 + 2 * FUSED_NX * (int64_t)d.D;
-  f.off_ap = f.off_lm + 2 * FUSED_NWG * 2;
+  f.off_ap = f.off_lm + 2 * FUSED_LMC * 2 * (int64_t)FUSED_NWG;
   f.slots = f.off_ap + 2 * FUSED_NX * FUSED_SPLIT_WG * (int64_t)(d.hd + 2);
   f.ok = true;
   return f;
