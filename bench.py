@@ -722,6 +722,8 @@ def profiles_of(rec, prefix="", out=None):
     for k, v in (rec or {}).items():
         if k.startswith("roofline") and isinstance(v, dict) and v.get("profile"):
             out.setdefault(v["profile"], []).append(prefix + k)
+            if v.get("traffic_profile"):
+                out.setdefault(v["traffic_profile"], []).append(prefix + k + ".traffic")
         elif isinstance(v, dict) and k in ("split", "prefill", "decode"):
             profiles_of(v, prefix + k + ".", out)
     return out
@@ -825,6 +827,9 @@ def main():
     attach = (("prefill", "roofline", "prefill", "gemm"),
               ("decode_b1", "roofline", "decode_b1", "decode_fused"),
               ("decode_b64", "roofline", "decode_b64", "attn_decode"))
+    traffic_profiles = {"prefill": "profiles/prefill_d12_T2048_traffic.md",
+                        "decode_b1": "profiles/decode_d12_B1_traffic.md",
+                        "decode_b64": "profiles/decode_d12_B64_traffic.md"}
     for key, field, name, kind in attach:
         t = pmc.get(key)
         r = rec.get(name)
@@ -837,6 +842,7 @@ def main():
                     np.mean([PMC_B64_PROMPT - 1 + i + 1 for i in range(PMC_B64_STEPS)]))
             r[field]["traffic"] = t["bytes"]
             r[field]["traffic_detail"] = t
+            r[field]["traffic_profile"] = traffic_profiles[key]
     for key, field in (("mfma_prefill", "roofline"), ("mfma_prefill_attn", "roofline_attention")):
         mf = pmc.get(key)
         if mf and pre and pre.get(field):
