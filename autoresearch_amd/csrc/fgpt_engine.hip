@@ -730,7 +730,33 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
     a.ovf = f16 ? m->d_ovf : nullptr;
     a.wscale = m->w16_inv;
     a.w = W(m->w.qkv(l)); a.N = d.nqkv(); a.K = d.D; a.norm = 1; a.y = ws.q;
-    linear(m, s, GV_QKV, a, d_pos, gm);
+    // Batched cached steps (split-K GEMM, one query row per sequence): the
+    // decode attention finishes the QKV's split-K sums itself (row norm,
+    // RoPE, the k/v append) in place of the reduce launch
+    QkvFold qf;
+    bool fold = false;
+    if (one && gm && T == 1 && !o.d_rows && !f16 &&
+        attn_decode_takes_qkv(d, B, maxT, d_pos != nullptr, pos0 + 1, o.kv16)) {
+      int sp = 0;
+      const double M = a.M, N = a.N, K = a.K;  // (linear()'s units)
+      timed(m, s, FG_K_GEMM, 2.0 * M * N * K, N * K * 2 + M * K * 4 + M * N * 4, [&] {
+        sp = launch_gemm_partials(s, GV_QKV, a, d_pos);
+      });
+      if (sp > 0) {
+        fold = true;
+        qf.part = a.part;
+        qf.splits = sp;
+        qf.rows = rows;
+        qf.N = a.N;
+        qf.K = a.K;
+        qf.ssq_n = a.ssq_n;
+        qf.ssq_in = a.ssq_in;
+        qf.eps = a.eps;
+        qf.cosb = a.cosb;
+        qf.sinb = a.sinb;
+      }
+    }
+    if (!fold) linear(m, s, GV_QKV, a, d_pos, gm);
     a.qs = nullptr;
     a.ks = a.vt = nullptr;
     uint16_t* aos = gm ? ws.aos : nullptr;
@@ -738,7 +764,7 @@ void layer_stack(fg_model* m, hipStream_t s, const int32_t* ids, int B, int T, i
       timed(m, s, FG_K_ATTN_DECODE, at_flops, at_bytes, [&] {
         launch_attn_decode_pos(s, d, ws.q, lk, lv, o.kv16, B, maxT, d_pos, pos0 + 1, dec_part,
                                o.dec_cnt, ws.ao, aos,
-                               aplane, T, o.d_rows);
+                               aplane, T, o.d_rows, fold ? &qf : nullptr);
       });
     } else {
       if (pos0 > 0)  // earlier cache positions enter the chunk's key planes

@@ -241,11 +241,29 @@ void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_
 // launch (of B*qpr), on the device.
 int64_t attn_decode_scratch_floats(const Dims& d, int B, int maxT);
 inline int64_t attn_decode_counters(const Dims& d, int rows) { return (int64_t)rows * d.H; }
+// The QKV GEMM's split-K partial sums, left for the single-query attention
+// to finish (sum in split order, row norm, RoPE, the k/v append) instead of
+// a reduce launch: part [splits][rows][N], N = (H + 2 KH) hd in the stored
+// column order; the norm from ssq_in [rows][ssq_n] over K inputs.
+struct QkvFold {
+  const float* part = nullptr;
+  int splits = 0, rows = 0, N = 0, K = 0, ssq_n = 0;
+  const float* ssq_in = nullptr;
+  float eps = 0.f;
+  const float* cosb = nullptr;
+  const float* sinb = nullptr;
+};
+// Whether launch_attn_decode_pos for one query row per sequence (no
+// d_rows; replayed: d_len set) runs the kernel that takes a QkvFold.
+bool attn_decode_takes_qkv(const Dims& d, int B, int maxT, bool replayed, int len, bool kv16);
+// The split-K GEMM alone (no reduce): its partial sums into a.part. Returns
+// the split count, or 0 (nothing launched) when this GEMM is not split.
+int launch_gemm_partials(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos);
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const void* kc,
                             const void* vc, bool kv16, int B, int maxT, const int32_t* d_len,
                             int len, float* scratch, uint32_t* cnt, float* y,
                             uint16_t* ys = nullptr, int64_t ys_plane = 0, int qpr = 1,
-                            const int32_t* d_rows = nullptr);
+                            const int32_t* d_rows = nullptr, const QkvFold* qf = nullptr);
 // argmax into out; with d_len/d_len0 set, also into out2[(len-len0)*rows +
 // row] (and the logits row into lgs_out at that slot, when set), then
 // *d_len += 1.

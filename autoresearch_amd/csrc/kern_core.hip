@@ -14,6 +14,8 @@
 #include <float.h>
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 #include "fgpt_internal.h"
 #include "kern_common.h"
@@ -363,6 +365,8 @@ struct DecArgs {
                 // floats, so every partial row starts 16-byte aligned)
   uint32_t* cnt;  // (nullable) arrival counters, one per head group, zero
                   // between launches: k_attn_dec merges its own chunks
+  int fold;       // k_attn_dec_loop: q, k, v from qf's split-K sums (qpr == 1)
+  QkvFold qf;
 };
 
 // Floats per partial row of the single-query attention: O (HD), max, sum,
@@ -635,6 +639,138 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
   dec_fold_merge<HD, GH>(a, row, h0, nch, &so[0][0][0], gml);
 }
 
+// The QKV projection's tail for one query row, done by the attention that
+// consumes it (a batched cached step whose QKV GEMM split K): the split
+// partial sums added in split order, eight at a time, the row's rmsnorm
+// scale, RoPE at position pos, as k_splitk_reduce and the QKV epilogue have
+// it (stored column pair 2i, 2i+1 of a head holds dims i and i + hd/2).
+// Thread t takes item t: pair t of the GH query heads h0.., then, with kv
+// set, pair t - GH*HD/2 of the KV head's k and then v (at most (GH+2)*HD/2
+// items, no more than the workgroup's threads). fold_load issues every load
+// the item needs at once (the first eight splits, four of the row's
+// sum-of-squares partials, the RoPE pair), ahead of the kernel's first K
+// rows; fold_pin, after those, marks where the values must have arrived;
+// fold_finish adds them (and any further splits and partials), and leaves q
+// in sq and the new k and v (their cached values: bf16-rounded for a bf16
+// cache) in skv, and with put set also in the cache at pos.
+struct FoldIn {
+  float2 pv[8];
+  float ss[4];
+  float cs, sn;
+};
+
+template <int HD, int GH>
+__device__ __forceinline__ int fold_col(const DecArgs& a, int h0, int kvh, bool kv, int& grp,
+                                        int& i) {
+  constexpr int NP = HD / 2;  // rotation pairs per head
+  const int it = threadIdx.x;
+  grp = it / NP;  // q heads 0..GH-1, then k, then v
+  i = it % NP;
+  if (it >= (GH + (kv ? 2 : 0)) * NP) return -1;
+  return grp < GH ? (h0 + grp) * HD + 2 * i
+                  : a.H * HD + (grp - GH) * a.KH * HD + kvh * HD + 2 * i;
+}
+
+// (Every load goes out, from a clamped and valid address; the unused
+// values are dropped later: conditional loads would become branches that
+// each wait for their load.)
+template <int HD, int GH>
+__device__ __forceinline__ void fold_load(const DecArgs& a, int row, int h0, int kvh, bool kv,
+                                          int pos, FoldIn& in) {
+  const QkvFold& f = a.qf;
+  int grp, i;
+  const int n = fold_col<HD, GH>(a, h0, kvh, kv, grp, i);
+  const float* P = f.part + (int64_t)row * f.N + max(n, 0);
+  const int64_t stride = (int64_t)f.rows * f.N;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    in.pv[k] = *reinterpret_cast<const float2*>(P + min(k, f.splits - 1) * stride);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) in.ss[t] = f.ssq_in[(int64_t)row * f.ssq_n + min(t, f.ssq_n - 1)];
+  const int64_t at = (int64_t)pos * (HD / 2) + i;
+  in.cs = f.cosb[at];
+  in.sn = f.sinb[at];
+}
+
+__device__ __forceinline__ void fold_pin(FoldIn& in) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(in.pv[k].x), "+v"(in.pv[k].y) : : "memory");
+  asm volatile("" : "+v"(in.ss[0]), "+v"(in.ss[1]), "+v"(in.ss[2]), "+v"(in.ss[3]),
+               "+v"(in.cs), "+v"(in.sn) : : "memory");
+}
+
+template <int HD, int GH, class KT>
+__device__ void fold_finish(const DecArgs& a, int row, int h0, int kvh, int pos, bool kv,
+                            bool put, const FoldIn& in, float (*sq)[HD], float (*skv)[HD]) {
+  const QkvFold& f = a.qf;
+  constexpr int NP = HD / 2;
+  int grp, i;
+  const int n = fold_col<HD, GH>(a, h0, kvh, kv, grp, i);
+  if (n < 0) return;
+  float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {  // split order (a zero adds nothing)
+    const float2 x = k < f.splits ? in.pv[k] : make_float2(0.f, 0.f);
+    v0 += x.x;
+    v1 += x.y;
+  }
+  const float* P = f.part + (int64_t)row * f.N + n;
+  const int64_t stride = (int64_t)f.rows * f.N;
+  for (int s0 = 8; s0 < f.splits; s0 += 8) {
+    float2 pv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      pv[k] = s0 + k < f.splits ? *reinterpret_cast<const float2*>(P + (s0 + k) * stride)
+                                : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      v0 += pv[k].x;
+      v1 += pv[k].y;
+    }
+  }
+  float ssum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    if (t < f.ssq_n) ssum += in.ss[t];
+  for (int t = 4; t < f.ssq_n; ++t) ssum += f.ssq_in[(int64_t)row * f.ssq_n + t];
+  const float inv = 1.0f / sqrtf(ssum / (float)f.K + f.eps);
+  v0 *= inv;
+  v1 *= inv;
+  float y1 = v0, y2 = v1;
+  if (grp <= GH) {  // q and k: rotated
+    const float cs = in.cs, sn = in.sn;
+    y1 = v0 * cs + v1 * sn;
+    y2 = v0 * (-sn) + v1 * cs;
+  }
+  if (grp < GH) {
+    sq[grp][i] = y1;
+    sq[grp][i + NP] = y2;
+    return;
+  }
+  const int t = grp - GH;  // 0: k, 1: v
+  // (row = sequence: one query row each; the cache operands are read-only
+  // to every other kernel of the launch)
+  const int64_t at = (int64_t)(row * a.maxT + pos) * a.KH * HD + kvh * HD;
+  if constexpr (sizeof(KT) == 2) {
+    const uint16_t h1 = f32_to_bf16_rne(y1), h2 = f32_to_bf16_rne(y2);
+    skv[t][i] = bf16_to_f32(h1);
+    skv[t][i + NP] = bf16_to_f32(h2);
+    if (put) {
+      uint16_t* c = (uint16_t*)(t ? a.vc : a.kc) + at;
+      c[i] = h1;
+      c[i + NP] = h2;
+    }
+  } else {
+    skv[t][i] = y1;
+    skv[t][i + NP] = y2;
+    if (put) {
+      float* c = (float*)(t ? a.vc : a.kc) + at;
+      c[i] = y1;
+      c[i + NP] = y2;
+    }
+  }
+}
+
 // k_attn_dec over a.iters consecutive blocks of DPC positions per
 // workgroup (NWV wavefronts, DPC / NWV positions each per block), for
 // batches with rows x KV heads enough to fill the chip without splitting
@@ -646,7 +782,7 @@ __global__ __launch_bounds__(256) void k_attn_dec(DecArgs a) {
 // k_attn_dec's do (the output, or a partial for k_attn_dec_merge). While a
 // block's scores are formed its V rows load, and the next block's K rows
 // load while its V rows are weighed.
-template <int HD, int DPC, int GH, class KT, int NWV = 4>
+template <int HD, int DPC, int GH, class KT, int NWV = 4, bool FOLD = false>
 __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   constexpr int LPP = HD / 8;        // lanes per cached row
   constexpr int PPW = 64 / LPP;      // rows per wavefront load
@@ -654,6 +790,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   static_assert(LPP == 8 || LPP == 16, "head dim 64 or 128");
   __shared__ float red[3][NWV][GH];
   __shared__ float so[NWV * PPW][GH][HD];
+  __shared__ float sq[FOLD ? GH : 1][HD], skv[FOLD ? 2 : 1][HD];  // (FOLD) q; new k, v
   const int G = a.H / a.KH, ng = G / GH;
   const int gi = blockIdx.x, c = blockIdx.y;
   const int row = gi / (a.KH * ng), kvh = (gi / ng) % a.KH, h0 = kvh * G + (gi % ng) * GH;
@@ -663,7 +800,12 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   const int p0 = c * span;
   if (p0 >= len) return;
   const int nch = (len + span - 1) / span;
-  const int nblk = min(a.iters, (len - p0 + DPC - 1) / DPC);  // blocks with positions < len
+  // With FOLD the new position len-1 is not in the cache yet: the cached
+  // positions stop at lenc, and the last chunk adds the new one from skv.
+  const int lenc = FOLD ? len - 1 : len;
+  const int plast = max(lenc - 1, 0);  // (loads past lenc repeat a cached row)
+  const int nblk = min(a.iters, (lenc - p0 + DPC - 1) / DPC);  // blocks with positions < lenc
+  const bool last = c == nch - 1;
   const int b = row / a.qpr;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int sub = lane / LPP, dl = lane % LPP;
@@ -672,15 +814,32 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   const KT* V = (const KT*)a.vc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
   auto pos = [&](int blk, int i) { return p0 + blk * DPC + wv * (DPC / NWV) + i * PPW + sub; };
   Row8<KT> kr[IT], vr[IT];
+  FoldIn fin;
+  if constexpr (FOLD) {
+    fold_load<HD, GH>(a, row, h0, kvh, last, len - 1, fin);
+    asm volatile("" ::: "memory");  // (those loads go out before the K rows')
+  }
 #pragma unroll
-  for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(0, i), len - 1) * kd);
+  for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(0, i), plast) * kd);
   float qv[GH][8];
+  if constexpr (FOLD) {
+    fold_pin(fin);
+    fold_finish<HD, GH, KT>(a, row, h0, kvh, len - 1, last, last && gi % ng == 0, fin, sq, skv);
+    __syncthreads();
 #pragma unroll
-  for (int j = 0; j < GH; ++j) {
-    const float* qp = a.q + ((int64_t)row * a.H + h0 + j) * HD + 8 * dl;
-    const float4 u = *(const float4*)qp, w = *(const float4*)(qp + 4);
-    qv[j][0] = u.x; qv[j][1] = u.y; qv[j][2] = u.z; qv[j][3] = u.w;
-    qv[j][4] = w.x; qv[j][5] = w.y; qv[j][6] = w.z; qv[j][7] = w.w;
+    for (int j = 0; j < GH; ++j) {
+      const float4 u = *(const float4*)&sq[j][8 * dl], w = *(const float4*)&sq[j][8 * dl + 4];
+      qv[j][0] = u.x; qv[j][1] = u.y; qv[j][2] = u.z; qv[j][3] = u.w;
+      qv[j][4] = w.x; qv[j][5] = w.y; qv[j][6] = w.z; qv[j][7] = w.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < GH; ++j) {
+      const float* qp = a.q + ((int64_t)row * a.H + h0 + j) * HD + 8 * dl;
+      const float4 u = *(const float4*)qp, w = *(const float4*)(qp + 4);
+      qv[j][0] = u.x; qv[j][1] = u.y; qv[j][2] = u.z; qv[j][3] = u.w;
+      qv[j][4] = w.x; qv[j][5] = w.y; qv[j][6] = w.z; qv[j][7] = w.w;
+    }
   }
   const float scale = 1.0f / sqrtf((float)HD);
   float m[GH], l[GH], o[GH][8];
@@ -693,7 +852,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   }
   for (int blk = 0; blk < nblk; ++blk) {
 #pragma unroll
-    for (int i = 0; i < IT; ++i) vr[i].load(V + min(pos(blk, i), len - 1) * kd);
+    for (int i = 0; i < IT; ++i) vr[i].load(V + min(pos(blk, i), plast) * kd);
     float sc[GH][IT], mx[GH];
 #pragma unroll
     for (int j = 0; j < GH; ++j) mx[j] = -FLT_MAX;
@@ -708,17 +867,17 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v += qv[j][e] * x[e];
         v = row_sum<LPP>(v);
-        sc[j][i] = p < len ? v * scale : -INFINITY;
+        sc[j][i] = p < lenc ? v * scale : -INFINITY;
         mx[j] = fmaxf(mx[j], sc[j][i]);
       }
     }
     if (blk + 1 < nblk) {
 #pragma unroll
-      for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(blk + 1, i), len - 1) * kd);
+      for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(blk + 1, i), plast) * kd);
     }
 #pragma unroll
     for (int j = 0; j < GH; ++j) {
-      const float mn = fmaxf(m[j], wave_max(mx[j]));  // (finite: block 0 of a chunk has p0 < len)
+      const float mn = fmaxf(m[j], wave_max(mx[j]));  // (>= -FLT_MAX: finite)
       const float alpha = expf(m[j] - mn);
       m[j] = mn;
       l[j] *= alpha;
@@ -738,8 +897,35 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
       }
     }
   }
-  // the four wavefronts' maxima, then each wavefront's O and row sums
-  // rescaled to the workgroup's
+  if (FOLD && last && wv == 0) {  // the new position, one row of wavefront 0
+    float kx[8], vx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kx[e] = skv[0][8 * dl + e];
+      vx[e] = skv[1][8 * dl + e];
+    }
+#pragma unroll
+    for (int j = 0; j < GH; ++j) {
+      float v = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v += qv[j][e] * kx[e];
+      const float sc = row_sum<LPP>(v) * scale;
+      const float mn = fmaxf(m[j], sc);
+      const float alpha = expf(m[j] - mn);
+      m[j] = mn;
+      l[j] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[j][e] *= alpha;
+      if (sub == 0) {
+        const float w = expf(sc - mn);
+        l[j] += w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[j][e] += w * vx[e];
+      }
+    }
+  }
+  // the wavefronts' maxima, then each wavefront's O and row sums rescaled
+  // to the workgroup's
   if (lane == 0) {
 #pragma unroll
     for (int j = 0; j < GH; ++j) red[0][wv][j] = m[j];
@@ -885,14 +1071,30 @@ void launch_dec_gh(hipStream_t s, const DecArgs& a, int rows, int gh) {
     if (a.iters > 1 && a.iters % 2 == 0) {
       DecArgs b2 = a;
       b2.iters = a.iters / 2;
-      if (gh == 2)
-        FG_LAUNCH((k_attn_dec_loop<HD, 256, 2, KT, 8>), grid, dim3(512), 0, s, b2);
-      else
-        FG_LAUNCH((k_attn_dec_loop<HD, 256, 1, KT, 8>), grid, dim3(512), 0, s, b2);
+      if (a.fold) {
+        if (gh == 2)
+          FG_LAUNCH((k_attn_dec_loop<HD, 256, 2, KT, 8, true>), grid, dim3(512), 0, s, b2);
+        else
+          FG_LAUNCH((k_attn_dec_loop<HD, 256, 1, KT, 8, true>), grid, dim3(512), 0, s, b2);
+      } else {
+        if (gh == 2)
+          FG_LAUNCH((k_attn_dec_loop<HD, 256, 2, KT, 8>), grid, dim3(512), 0, s, b2);
+        else
+          FG_LAUNCH((k_attn_dec_loop<HD, 256, 1, KT, 8>), grid, dim3(512), 0, s, b2);
+      }
       return;
     }
   }
   if (a.iters > 1) {  // (DPC 128 only: dec_group's options for it)
+    if constexpr (DPC == 128) {
+      if (a.fold) {
+        if (gh == 2)
+          FG_LAUNCH((k_attn_dec_loop<HD, DPC, 2, KT, 4, true>), grid, dim3(256), 0, s, a);
+        else
+          FG_LAUNCH((k_attn_dec_loop<HD, DPC, 1, KT, 4, true>), grid, dim3(256), 0, s, a);
+        return;
+      }
+    }
     if (gh == 2)
       FG_LAUNCH((k_attn_dec_loop<HD, DPC, 2, KT>), grid, dim3(256), 0, s, a);
     else
@@ -925,10 +1127,48 @@ void launch_dec_hd(hipStream_t s, const DecArgs& a, int rows, int dpc, int gh) {
 
 }  // namespace
 
+namespace {
+
+// Positions per chunk, head group and blocks per workgroup of a launch.
+struct DecPlan {
+  int dpc, gh, iters, live;
+};
+DecPlan dec_plan(const Dims& d, int B, int maxT, bool replayed, int len, int qpr, bool kv16) {
+  DecPlan p;
+  // chunks that can be live: all of maxT for a replayed step, else those of
+  // the last query row
+  p.dpc = B * d.H >= 192 ? 128 : DPC_MIN;
+  p.live = replayed ? maxT : len + qpr - 1;
+  const int rows = B * qpr;
+  p.gh = dec_group(d.H / d.KH, p.dpc);
+  // blocks of dpc positions per workgroup (k_attn_dec_loop: fewer chunks to
+  // merge): as many as keep 1.5 workgroups per CU on a bf16 cache (B=64: a
+  // sequence and head each, no merge; 1.8 % of the step faster than one
+  // block), 6 on an fp32 one (its workgroups hold twice the bytes in flight
+  // and half the occupancy; 1.2 %), else one
+  const int nblk = (p.live + p.dpc - 1) / p.dpc, wg_rows = rows * d.KH * (d.H / d.KH / p.gh);
+  const int64_t want2 = (kv16 ? 3 : 12) * (int64_t)cu_count();  // twice the workgroups wanted
+  p.iters = 1;
+  if (p.dpc == 128)
+    for (int it = nblk; it > 1; --it)
+      if ((int64_t)wg_rows * ((nblk + it - 1) / it) * 2 >= want2) {
+        p.iters = it;
+        break;
+      }
+  return p;
+}
+
+}  // namespace
+
+bool attn_decode_takes_qkv(const Dims& d, int B, int maxT, bool replayed, int len, bool kv16) {
+  return dec_plan(d, B, maxT, replayed, len, 1, kv16).iters > 1;  // k_attn_dec_loop
+}
+
 void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const void* kc,
                             const void* vc, bool kv16, int B, int maxT, const int32_t* d_len,
                             int len, float* scratch, uint32_t* cnt, float* y, uint16_t* ys,
-                            int64_t ys_plane, int qpr, const int32_t* d_rows) {
+                            int64_t ys_plane, int qpr, const int32_t* d_rows,
+                            const QkvFold* qf) {
   DecArgs a;
   a.q = q;
   a.kc = kc;
@@ -936,27 +1176,17 @@ void launch_attn_decode_pos(hipStream_t s, const Dims& d, const float* q, const 
   a.H = d.H;
   a.KH = d.KH;
   a.maxT = maxT;
-  // chunks that can be live: all of maxT for a replayed step, else those of
-  // the last query row
-  const int dpc = B * d.H >= 192 ? 128 : DPC_MIN;
-  const int live = d_len ? maxT : len + qpr - 1;
+  const DecPlan pl = dec_plan(d, B, maxT, d_len != nullptr, len, qpr, kv16);
+  const int dpc = pl.dpc, live = pl.live, gh = pl.gh, iters = pl.iters;
   const int rows = B * qpr;
-  const int G = d.H / d.KH;
-  const int gh = dec_group(G, dpc);
-  // blocks of dpc positions per workgroup (k_attn_dec_loop: fewer chunks to
-  // merge): as many as keep 1.5 workgroups per CU on a bf16 cache (B=64: a
-  // sequence and head each, no merge; 1.8 % of the step faster than one
-  // block), 6 on an fp32 one (its workgroups hold twice the bytes in flight
-  // and half the occupancy; 1.2 %), else one
-  const int nblk = (live + dpc - 1) / dpc, wg_rows = rows * d.KH * (d.H / d.KH / gh);
-  const int64_t want2 = (kv16 ? 3 : 12) * (int64_t)cu_count();  // twice the workgroups wanted
-  int iters = 1;
-  if (dpc == 128)
-    for (int it = nblk; it > 1; --it)
-      if ((int64_t)wg_rows * ((nblk + it - 1) / it) * 2 >= want2) {
-        iters = it;
-        break;
-      }
+  // a caller passes qf only where attn_decode_takes_qkv holds for the same
+  // arguments; the QKV's sums would go unfinished otherwise
+  if (qf && (iters <= 1 || qpr != 1 || d_rows)) {
+    std::fprintf(stderr, "fgpt: internal error: QKV fold for a launch that cannot take it\n");
+    std::abort();
+  }
+  a.fold = qf ? 1 : 0;
+  if (qf) a.qf = *qf;
   a.iters = iters;
   a.nchunk = (live + dpc * iters - 1) / (dpc * iters);
   a.d_len = d_len;

@@ -845,6 +845,15 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemvArgs a, int splits,
   }
 }
 
+// The K-split partial sums of a small-M GEMM into a.part (64x64 tiles,
+// blockIdx.z the split).
+template <int EPI>
+void launch_splitk_parts(hipStream_t s, const GemvArgs& a, int sp, const int32_t* d_pos) {
+  constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
+  const dim3 g(a.N / 64, (unsigned)((a.M + 63) / 64), (unsigned)sp);
+  FG_LAUNCH((k_gemm<EPI, 64, 64, 2, 2, 32, 4>), g, dim3(256), lds, s, a, d_pos);
+}
+
 // Tile choice. The LDS-staged epilogue (k_gemm) serves QKV and RESID,
 // whose outputs are scattered or need per-row reductions; the register
 // epilogue (k_gemm2) serves the plain stores of RELU2 and lm_head, with
@@ -880,9 +889,7 @@ void launch_tile_p(hipStream_t s, const GemvArgs& a, const int32_t* d_pos) {
   }
   const int sp = a.part && !P16 ? splitk_count(a.M, a.N, a.K) : 1;
   if (sp > 1) {
-    constexpr size_t lds = (size_t)4 * (2 * 64 + 64) * 64;
-    const dim3 g(a.N / 64, (unsigned)((a.M + 63) / 64), (unsigned)sp);
-    FG_LAUNCH((k_gemm<EPI, 64, 64, 2, 2, 32, 4>), g, dim3(256), lds, s, a, d_pos);
+    launch_splitk_parts<EPI>(s, a, sp, d_pos);
     const dim3 rg((unsigned)a.M, (unsigned)((a.N + RED_COLS - 1) / RED_COLS));
     FG_LAUNCH((k_splitk_reduce<EPI>), rg, dim3(256), 0, s, a, sp, d_pos);
     return;
@@ -1002,6 +1009,18 @@ void launch_gemm_pos(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_
     case GV_RELU2: launch_tile<GV_RELU2>(s, a, d_pos); break;
     default: launch_tile<GV_STORE>(s, a, d_pos); break;
   }
+}
+
+int launch_gemm_partials(hipStream_t s, GemvEpi epi, const GemvArgs& a, const int32_t* d_pos) {
+  const int sp = a.part && !a.f16 ? splitk_count(a.M, a.N, a.K) : 1;
+  if (sp <= 1) return 0;
+  switch (epi) {  // (the kernel writes raw partials whatever the epilogue)
+    case GV_QKV: launch_splitk_parts<GV_QKV>(s, a, sp, d_pos); break;
+    case GV_RESID: launch_splitk_parts<GV_RESID>(s, a, sp, d_pos); break;
+    case GV_RELU2: launch_splitk_parts<GV_RELU2>(s, a, sp, d_pos); break;
+    default: launch_splitk_parts<GV_STORE>(s, a, sp, d_pos); break;
+  }
+  return sp;
 }
 
 void launch_gemm(hipStream_t s, GemvEpi epi, const GemvArgs& a) {
