@@ -137,3 +137,61 @@ def test_batched_bf16_chunks_merged():
     assert e < TOL
     assert np.all(srt[flips, -1] - srt[flips, -2] < 2 * TOL * np.abs(l32).max())
     m.close()
+
+
+def test_batched_qkv_fold_gqa_vs_single_rows():
+    """B=40 sequences of the 5:1 GQA shape (5 query heads over one KV head,
+    head_dim 128) on a bf16 cache, 400-id prompts: 200 (sequence, head)
+    rows take the looped decode attention (3 blocks of 128 positions per
+    workgroup, 2 chunks and a merge), which also finishes the QKV's split-K
+    sums (five workgroups per KV head fold the query, one of them appends
+    k/v). One plain step and two graph-replayed steps, against each
+    sequence decoded alone (single-row GEMV path, no fold): the appended
+    layer-0 rows within one bf16 unit (the two paths sum the projection in
+    different orders; elements near zero within 1e-5 of the row's largest),
+    the logits within the bar, ids equal but at near-ties."""
+    d, B, P, n = GQA5, 40, 400, 2
+    maxT = P + 1 + n
+    m, _, _ = model(d, 11, maxT)
+    prompts = uniform_ids(29, B * P, d.vocab).reshape(B, P)
+    kv = m.kv(B, maxT, bf16=True)
+    kv.step_multi(prompts[:, :-1], want_logits=False)
+    lg0, nxt = kv.step(prompts[:, -1])
+    ids, lg = kv.decode_greedy(nxt, n, want_logits=True)
+    kb, vb = kv.read()
+    kv.close()
+    got_ids = np.vstack([nxt[None, :], ids])              # [n+1, B]
+    got_lg = np.concatenate([lg0[None], lg])               # [n+1, B, V]
+    kvd = d.n_kv_head * d.head_dim
+    worst, flips = 0.0, []
+    for b in range(B):
+        one = m.kv(1, maxT, bf16=True)
+        one.step_multi(prompts[b:b + 1, :-1], want_logits=False)
+        l1, x1 = one.step(prompts[b, -1:])
+        i1, l2 = one.decode_greedy(x1, n, want_logits=True)
+        k1, v1 = one.read()
+        one.close()
+        ref_ids = np.concatenate([x1, i1[:, 0]])
+        ref_lg = np.concatenate([l1, l2[:, 0]])
+        diff = np.flatnonzero(got_ids[:, b] != ref_ids)
+        first = int(diff[0]) if diff.size else n + 1
+        if first <= n:
+            srt = np.sort(ref_lg[first])
+            flips.append((b, first, float(srt[-1] - srt[-2])))
+        # steps t <= first see the same context in both runs: their logits,
+        # and the layer-0 rows they append at position P-1+t
+        for t in range(min(first, n) + 1):
+            worst = max(worst, relerr(got_lg[t, b], ref_lg[t]))
+            p = P - 1 + t
+            for big, small in ((kb, k1), (vb, v1)):
+                a = big[(b * maxT + p) * kvd:(b * maxT + p + 1) * kvd]
+                r = small[p * kvd:(p + 1) * kvd]
+                # one bf16 unit of the element, plus the fp32 summation-order
+                # difference of the projection (elements near zero)
+                bar = 2.0 ** -7 * np.abs(r) + 1e-5 * np.abs(r).max()
+                assert np.all(np.abs(a - r) <= bar), (b, p, float(np.abs(a - r).max()))
+    record("qkv_fold_gqa5_b40", relerr=worst, flips=flips)
+    assert worst < TOL
+    for b, t, marg in flips:
+        assert marg < 2 * TOL * np.abs(got_lg).max(), (b, t, marg)
+    m.close()
