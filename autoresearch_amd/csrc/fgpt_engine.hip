@@ -1153,6 +1153,10 @@ extern "C" int32_t fg_kv_create_ex(fg_model* m, int32_t B, int32_t maxT, int32_t
   if (flags & ~FG_KV_BF16) return seterr(FG_EARG, "unknown cache flags 0x%x", flags);
   // the largest cache this build is tested with
   if (maxT > 16000) return seterr(FG_EARG, "maxT %d above the 16000 this build supports", maxT);
+  // the decode attention addresses a sequence's cache rows with 32-bit offsets
+  if ((int64_t)maxT * m->d.kvd() * ((flags & FG_KV_BF16) ? 2 : 4) >= ((int64_t)1 << 31))
+    return seterr(FG_EARG, "a sequence's cache (maxT %d x %d values) exceeds 2 GiB", maxT,
+                  m->d.kvd());
   GUARD(m);
   fg_kv* kv = new fg_kv();
   kv->m = m;

@@ -810,8 +810,16 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int sub = lane / LPP, dl = lane % LPP;
   const int64_t kd = (int64_t)a.KH * HD;
-  const KT* K = (const KT*)a.kc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
-  const KT* V = (const KT*)a.vc + (int64_t)b * a.maxT * kd + kvh * HD + 8 * dl;
+  // cached rows: the sequence's head base (workgroup-uniform) plus a 32-bit
+  // byte offset, row x row bytes as a 24-bit multiply (rows and row bytes
+  // below 2^24, a sequence's cache below 2^31 bytes: the cache's creation
+  // checks it)
+  const char* Kb = (const char*)((const KT*)a.kc + (int64_t)b * a.maxT * kd + kvh * HD);
+  const char* Vb = (const char*)((const KT*)a.vc + (int64_t)b * a.maxT * kd + kvh * HD);
+  const uint32_t rowb = (uint32_t)kd * sizeof(KT), laneb = 8 * dl * sizeof(KT);
+  auto rowp = [&](const char* base, int p) {
+    return (const KT*)(base + (__umul24((uint32_t)min(p, plast), rowb) + laneb));
+  };
   auto pos = [&](int blk, int i) { return p0 + blk * DPC + wv * (DPC / NWV) + i * PPW + sub; };
   Row8<KT> kr[IT], vr[IT];
   FoldIn fin;
@@ -820,7 +828,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
     asm volatile("" ::: "memory");  // (those loads go out before the K rows')
   }
 #pragma unroll
-  for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(0, i), plast) * kd);
+  for (int i = 0; i < IT; ++i) kr[i].load(rowp(Kb, pos(0, i)));
   float qv[GH][8];
   if constexpr (FOLD) {
     fold_pin(fin);
@@ -841,7 +849,9 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
       qv[j][4] = w.x; qv[j][5] = w.y; qv[j][6] = w.z; qv[j][7] = w.w;
     }
   }
-  const float scale = 1.0f / sqrtf((float)HD);
+  // scores in log2 units (scale x log2(e)): each weight is one v_exp_f32 of
+  // a difference; the maximum handed to the merge is converted back
+  const float scale = 1.44269504088896341f / sqrtf((float)HD);
   float m[GH], l[GH], o[GH][8];
 #pragma unroll
   for (int j = 0; j < GH; ++j) {
@@ -852,7 +862,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   }
   for (int blk = 0; blk < nblk; ++blk) {
 #pragma unroll
-    for (int i = 0; i < IT; ++i) vr[i].load(V + min(pos(blk, i), plast) * kd);
+    for (int i = 0; i < IT; ++i) vr[i].load(rowp(Vb, pos(blk, i)));
     float sc[GH][IT], mx[GH];
 #pragma unroll
     for (int j = 0; j < GH; ++j) mx[j] = -FLT_MAX;
@@ -873,12 +883,12 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
     }
     if (blk + 1 < nblk) {
 #pragma unroll
-      for (int i = 0; i < IT; ++i) kr[i].load(K + min(pos(blk + 1, i), plast) * kd);
+      for (int i = 0; i < IT; ++i) kr[i].load(rowp(Kb, pos(blk + 1, i)));
     }
 #pragma unroll
     for (int j = 0; j < GH; ++j) {
       const float mn = fmaxf(m[j], wave_max(mx[j]));  // (>= -FLT_MAX: finite)
-      const float alpha = expf(m[j] - mn);
+      const float alpha = __builtin_amdgcn_exp2f(m[j] - mn);
       m[j] = mn;
       l[j] *= alpha;
 #pragma unroll
@@ -890,7 +900,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
       vr[i].get(x);
 #pragma unroll
       for (int j = 0; j < GH; ++j) {
-        const float w = expf(sc[j][i] - m[j]);
+        const float w = __builtin_amdgcn_exp2f(sc[j][i] - m[j]);
         l[j] += w;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[j][e] += w * x[e];
@@ -911,13 +921,13 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
       for (int e = 0; e < 8; ++e) v += qv[j][e] * kx[e];
       const float sc = row_sum<LPP>(v) * scale;
       const float mn = fmaxf(m[j], sc);
-      const float alpha = expf(m[j] - mn);
+      const float alpha = __builtin_amdgcn_exp2f(m[j] - mn);
       m[j] = mn;
       l[j] *= alpha;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[j][e] *= alpha;
       if (sub == 0) {
-        const float w = expf(sc - mn);
+        const float w = __builtin_amdgcn_exp2f(sc - mn);
         l[j] += w;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[j][e] += w * vx[e];
@@ -936,7 +946,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
     float mw = red[0][0][j];
 #pragma unroll
     for (int w = 1; w < NWV; ++w) mw = fmaxf(mw, red[0][w][j]);
-    const float f = expf(m[j] - mw);
+    const float f = __builtin_amdgcn_exp2f(m[j] - mw);
     float4* dst = (float4*)&so[wv * PPW + sub][j][8 * dl];
     dst[0] = make_float4(o[j][0] * f, o[j][1] * f, o[j][2] * f, o[j][3] * f);
     dst[1] = make_float4(o[j][4] * f, o[j][5] * f, o[j][6] * f, o[j][7] * f);
@@ -967,7 +977,7 @@ __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
     } else {
       float* P = a.part + (bh * a.nchunk + c) * dec_pstride(HD);
       *(float4*)(P + d) = t;
-      if (d == 0) *(float2*)(P + HD) = make_float2(red[2][0][j], lj);
+      if (d == 0) *(float2*)(P + HD) = make_float2(red[2][0][j] * 0.693147180559945309f, lj);
     }
   }
 }
