@@ -3,6 +3,7 @@
 // gpt_forward / gpt_step / gpt_step_multi (14NGiestas/autoresearch
 // src/lib/fortran_gpt.f90:54-199, src/lib/fortran_kv.f90:26-289).
 #include <stdarg.h>
+#include <stddef.h>
 #include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
@@ -1394,18 +1395,24 @@ bool fused_applies(const fg_model* m, const fg_kv* kv, int n_steps) {
          kv->len + n_steps <= FUSED_MAX_LEN;
 }
 
-// The whole greedy loop as one persistent launch: ids go to kv->d_out,
-// logits (when wanted) to kv->d_lgs, the cache rows of the n_steps positions
-// are written in place.
-int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, int with_logits) {
+// n_steps greedy steps as one persistent launch from the id at d_id0 (on
+// the device) at position len0: the steps' argmax ids go to ids_out, their
+// logits (when logits_out is set) to logits_out, the cache rows of the
+// n_steps positions are written in place. The launch's placement counters
+// are cleared first, and its error flag too when clear_err is set (a caller
+// running several launches clears it once and reads it after the last).
+int32_t fused_launch(fg_model* m, fg_kv* kv, const int32_t* d_id0, int len0, int n_steps,
+                     int32_t* ids_out, float* logits_out, bool clear_err) {
   hipStream_t s = m->stream;
   const uint32_t eps = fused_epochs(m->d, n_steps);
   if ((uint64_t)m->fused_ep + eps >= 0xFFFFFF00ull) {  // epochs would wrap: start over
     HIPCHK(hipMemsetAsync(m->fused_slots, 0, (size_t)m->fl.slots * 8, s));
     m->fused_ep = 1;
   }
-  HIPCHK(hipMemcpyAsync(kv->d_ids, ids, 4, hipMemcpyHostToDevice, s));
-  HIPCHK(hipMemsetAsync(m->fused_err, 0, 4 * (1 + FUSED_NX), s));
+  if (clear_err)
+    HIPCHK(hipMemsetAsync(m->fused_err, 0, 4 * (1 + FUSED_NX), s));
+  else
+    HIPCHK(hipMemsetAsync(m->fused_err + 1, 0, 4 * FUSED_NX, s));
   FusedArgs a;
   a.arena = m->fused_w;
   a.wte = m->w.wte;
@@ -1414,11 +1421,11 @@ int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, in
   a.kc = kv->k;
   a.vc = kv->v;
   a.maxT = kv->maxT;
-  a.len0 = kv->len;
+  a.len0 = len0;
   a.n_steps = n_steps;
-  a.d_id0 = kv->d_ids;
-  a.ids_out = kv->d_out;
-  a.logits_out = with_logits ? kv->d_lgs : nullptr;
+  a.d_id0 = d_id0;
+  a.ids_out = ids_out;
+  a.logits_out = logits_out;
   a.slots = m->fused_slots;
   a.ep_base = m->fused_ep;
   a.err = m->fused_err;
@@ -1436,7 +1443,7 @@ int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, in
   const double wbytes = (double)m->w.bytes - 2.0 * d.V * d.D;
   double bytes = 0, flops = 0;
   for (int st = 0; st < n_steps; ++st) {
-    const double len = kv->len + st + 1;
+    const double len = len0 + st + 1;
     bytes += wbytes + 2.0 * d.D + (double)d.L * d.kvd() * 4 * 2 * (len + 1);
     flops += wbytes + (double)d.L * 4 * d.hd * d.H * len;
   }
@@ -1470,6 +1477,26 @@ int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, in
     }
   }
   if (e != hipSuccess) return seterr(FG_EHIP, "persistent decode launch: %s", hipGetErrorString(e));
+  return FG_OK;
+}
+
+// The whole greedy loop as one persistent launch: ids go to kv->d_out,
+// logits (when wanted) to kv->d_lgs.
+int32_t fused_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, int with_logits) {
+  HIPCHK(hipMemcpyAsync(kv->d_ids, ids, 4, hipMemcpyHostToDevice, m->stream));
+  return fused_launch(m, kv, kv->d_ids, kv->len, n_steps, kv->d_out,
+                      with_logits ? kv->d_lgs : nullptr, true);
+}
+
+// The persistent launch's error flag, after the device is idle: 0, or the
+// engine error for it.
+int32_t fused_check(fg_model* m) {
+  uint32_t err = 0;
+  HIPCHK(hipMemcpy(&err, m->fused_err, 4, hipMemcpyDeviceToHost));
+  if (err != 0)
+    return seterr(FG_EHIP, "persistent decode: %s",
+                  err == 2 ? "an XCD held more than 32 of its workgroups"
+                           : "a hand-over between workgroups timed out");
   return FG_OK;
 }
 
@@ -1658,14 +1685,7 @@ extern "C" int32_t fg_decode_greedy(fg_model* m, fg_kv* kv, const int32_t* ids, 
   HIPCHK(hipMemcpyAsync(ids_out, kv->d_out, nout * 4, hipMemcpyDeviceToHost, s));
   if (logits_out) RCCHK(copy_out(m, logits_out, kv->d_lgs, (size_t)nout * m->d.V * 4, s));
   HIPCHK(hipStreamSynchronize(s));
-  if (fused) {
-    uint32_t err = 0;
-    HIPCHK(hipMemcpy(&err, m->fused_err, 4, hipMemcpyDeviceToHost));
-    if (err != 0)
-      return seterr(FG_EHIP, "persistent decode: %s",
-                    err == 2 ? "an XCD held more than 32 of its workgroups"
-                             : "a hand-over between workgroups timed out");
-  }
+  if (fused) RCCHK(fused_check(m));
   kv->len += n_steps;
   kv->filled = std::max(kv->filled, kv->len);
   return FG_OK;
@@ -1956,6 +1976,26 @@ extern "C" int32_t fg_decode_sample(fg_model* m, fg_kv* kv, int32_t* ids, int32_
   HIPCHK(hipMemcpyAsync(kv->d_smp, h, sizeof *h, hipMemcpyHostToDevice, s));
   int done = 0;
   const int total = n_total - n_known;
+  const bool fused = fused_applies(m, kv, total);
+  if (fused) {
+    // each step the persistent kernel for one step (its logits; its own
+    // argmax goes to the spare inp[1]), then the draw, which leaves the next
+    // input in inp[0]; the error flag is cleared once and read at the end
+    int32_t* inp = (int32_t*)((char*)kv->d_smp + offsetof(SampleDev, inp));
+    HIPCHK(hipMemsetAsync(m->fused_err, 0, 4, s));
+    for (; done < total; ++done) {
+      const int32_t rc = fused_launch(m, kv, inp, n_known - 1 + done, 1, inp + 1,
+                                      m->ws.logits, false);
+      if (rc != FG_OK) {
+        (void)hipStreamSynchronize(s);
+        kv->len = n_known - 1;
+        return rc;
+      }
+      timed(m, s, FG_K_OTHER, 0, (double)m->d.V * 4, [&] {
+        launch_sample_step(s, kv->d_smp, m->ws.logits, m->d.V, kv->d_sids);
+      });
+    }
+  }
   while (done < total) {
     int run = 32;
     while (run > total - done) run >>= 1;
@@ -1971,6 +2011,13 @@ extern "C" int32_t fg_decode_sample(fg_model* m, fg_kv* kv, int32_t* ids, int32_
   HIPCHK(hipMemcpyAsync(ids + n_known, kv->d_sids + n_known, (size_t)total * 4,
                         hipMemcpyDeviceToHost, s));
   HIPCHK(hipStreamSynchronize(s));
+  if (fused) {
+    const int32_t rc = fused_check(m);
+    if (rc != FG_OK) {
+      kv->len = n_known - 1;
+      return rc;
+    }
+  }
   if (h->pp != n_total) return seterr(FG_EHIP, "sampling loop ended at %d of %d", h->pp, n_total);
   *state = h->rng;
   kv->len = n_total - 1;

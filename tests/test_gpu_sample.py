@@ -146,6 +146,67 @@ def test_decode_sample_loop(m):
     kv.close()
 
 
+SMALL_MHA = Dims(n_layer=2, d_model=256, n_head=2, n_kv_head=2, head_dim=128, vocab=1024)
+
+
+def test_decode_sample_loop_persistent():
+    """On a shape the persistent B=1 kernel serves, each sampled step's
+    forward is one persistent launch (the timing records one per id) and
+    the draw a kernel of its own. temp 0 gives decode_greedy's stream bit
+    for bit (the same kernel); with penalties, the stream against stepping
+    the engine one position at a time with the oracle choosing ids (the
+    per-step logits come from the single-row kernels there, ~1e-6 apart),
+    up to a near-boundary draw."""
+    d = SMALL_MHA
+    m = engine.Model(d, stacks=seeded_weights(d, 7))
+    assert m.fused_decode()[0], m.fused_decode()[1]
+    prompt = uniform_ids(18, 12, d.vocab)
+    n_gen = 40
+    ntot = prompt.size + n_gen
+    c, s = rope_tables(ntot, d.head_dim)
+    m.set_rope(c.reshape(-1), s.reshape(-1))
+
+    def fresh():
+        kv = m.kv(1, ntot)
+        kv.step_multi(prompt[:-1], want_logits=False)
+        return kv
+
+    kv = fresh()
+    g, _ = kv.decode_greedy(prompt[-1:], n_gen)
+    kv.close()
+    kv = fresh()
+    m.timing(True)
+    out, st = kv.decode_sample(prompt, n_gen, seed=3, temp=0.0)
+    tm = m.timing_read()
+    m.timing(False)
+    kv.close()
+    assert tm["decode_fused"][0] == n_gen, tm
+    assert np.array_equal(out, g[:, 0]) and st == 3
+    cfg = dict(temp=0.8, topp=0.9, pres=0.2, freq=0.1, rep=1.2, nblock=3)
+    kv = fresh()
+    out, st_dev = kv.decode_sample(prompt, n_gen, seed=77, **cfg)
+    kv.close()
+    m.set_fused_decode(False)  # (single steps on the per-kernel path)
+    kv = fresh()
+    ids, st = [int(prompt[-1])], 77
+    gen = []
+    for t in range(n_gen):
+        lg, _ = kv.step(np.array([ids[-1]], np.int32))
+        want, st, det = S.sample_next(lg[0], cfg["temp"], cfg["topp"], cfg["pres"], cfg["freq"],
+                                      cfg["rep"], 0, 0.0, gen, len(gen), cfg["nblock"], st)
+        if want != out[t]:
+            mg = margin(det, det["u"])
+            assert mg < 1e-5, f"step {t}: {out[t]} vs {want}, margin {mg}"
+            print(f"near-boundary divergence at step {t}; stream compared up to it", flush=True)
+            break
+        gen.append(want)
+        ids.append(want)
+    else:
+        assert st == st_dev
+    kv.close()
+    m.close()
+
+
 def test_sample_errors(m):
     with pytest.raises(engine.FgptError):
         m.sample(np.zeros(8193, np.float32))
