@@ -781,7 +781,10 @@ __device__ void fold_finish(const DecArgs& a, int row, int h0, int kvh, int pos,
 // rescaled to the workgroup maximum, and leave as
 // k_attn_dec's do (the output, or a partial for k_attn_dec_merge). While a
 // block's scores are formed its V rows load, and the next block's K rows
-// load while its V rows are weighed.
+// load while its V rows are weighed. With FOLD the kernel also finishes the
+// step's QKV projection (fold_load / fold_finish): the query comes from the
+// split-K partials, and the new position, not cached yet, is added by the
+// last chunk from the k and v it computed (and appended to the cache).
 template <int HD, int DPC, int GH, class KT, int NWV = 4, bool FOLD = false>
 __global__ __launch_bounds__(64 * NWV) void k_attn_dec_loop(DecArgs a) {
   constexpr int LPP = HD / 8;        // lanes per cached row
