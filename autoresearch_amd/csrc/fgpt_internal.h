@@ -357,7 +357,13 @@ constexpr int FUSED_MAX_LEN = 2048;  // attention positions a step may see
 // XCD; below it every workgroup of the XCD computes the whole attention of
 // the head itself.
 constexpr int FUSED_SPLIT_MIN = 128;
-constexpr int FUSED_SPLIT_WG = 16;  // (1 032 positions: 13.4 us a layer; 8 workgroups 14.6)
+// 18: one batch of cache rows per position group up to 18 x 8 groups x 8
+// = 1 152 positions (chat_text's 1 024-position contexts and a little
+// beyond); at 1 032-1 094 positions 154.1 against 162.9 us a token with 16
+// (some workgroups then fetched a second batch), 14.6 us a layer with 8;
+// more would take the kernel past its 256 VGPRs (the merge gathers
+// FUSED_SPLIT_WG partials of hd + 2 slots at once)
+constexpr int FUSED_SPLIT_WG = 18;
 
 struct FusedLayout {
   bool ok = false;
