@@ -286,7 +286,7 @@ int32_t fg_decode_sample(fg_model *m, fg_kv *kv, int32_t *ids, int32_t n_known, 
  * (all layers, lm_head and the argmax of every step; the weights stream
  * through LDS one layer ahead, activations pass between workgroups through
  * epoch-tagged slots; from 128 positions on a head's attention is split
- * over 16 workgroups), for the model shapes the library compiles it for
+ * over 18 workgroups), for the model shapes the library compiles it for
  * (head_dim 128, d_ff = 4 d_model: d_model 768 with 6 heads and vocab 8192,
  * d_model 256 with 2 heads and vocab 1024) on a device of 256 CUs in 8 XCDs
  * that allows cooperative launches; 0 keeps the captured per-kernel steps.
