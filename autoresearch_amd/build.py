@@ -22,7 +22,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLANG = os.environ.get("FC_AMD", "/opt/rocm/bin/amdflang")
 
 HIP_SOURCES = ["fgpt_engine.hip", "fgpt_weights.hip", "fgpt_spec.hip", "kern_core.hip",
-               "kern_gemm.hip", "kern_attn.hip", "kern_sample.hip", "kern_fused.hip"]
+               "kern_gemm.hip", "kern_attn.hip", "kern_sample.hip", "kern_fused.hip",
+               "kern_fused_gqa.hip"]
 HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wall", "-Wno-unused-function", "-Wno-unused-result"]

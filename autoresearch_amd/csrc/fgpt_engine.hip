@@ -1392,7 +1392,7 @@ int32_t graph_decode(fg_model* m, fg_kv* kv, const int32_t* ids, int n_steps, in
 
 bool fused_applies(const fg_model* m, const fg_kv* kv, int n_steps) {
   return m->fused_on && m->fused_w && kv->B == 1 && !kv->kv16 &&
-         kv->len + n_steps <= FUSED_MAX_LEN;
+         kv->len + n_steps <= m->fl.max_len;
 }
 
 // n_steps greedy steps as one persistent launch from the id at d_id0 (on
@@ -1469,7 +1469,7 @@ int32_t fused_launch(fg_model* m, fg_kv* kv, const int32_t* d_id0, int len0, int
     if (e == hipSuccess) {
       FILE* fp = fopen(tpath, "ab");
       if (fp) {
-        const int32_t hdr[4] = {FUSED_NWG, d.L + 1, 32, n_steps};
+        const int32_t hdr[4] = {FUSED_NWG, d.L + 1, 32 | (m->fl.kind << 16), n_steps};
         fwrite(hdr, 4, 4, fp);
         fwrite(ht.data(), 8, tn, fp);
         fclose(fp);

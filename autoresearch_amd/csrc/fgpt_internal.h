@@ -367,6 +367,11 @@ constexpr int FUSED_SPLIT_WG = 18;
 
 struct FusedLayout {
   bool ok = false;
+  // 0: one KV head per query head (kern_fused.hip); 1: two KV heads, each
+  // shared by a group of query heads (kern_fused_gqa.hip)
+  int kind = 0;
+  int max_len = FUSED_MAX_LEN;  // attention positions a step may see
+  int64_t off_xp = 0;           // (kind 1) slot offset of the XCD-level attention partials
   int QR, C, FR, HN, LR;  // rows per workgroup: qkv, proj/proj2 outputs, fc, proj2 K, lm_head
   int64_t wq, wp, wf, w2;   // segment byte offsets within a layer slice
   int64_t slice, lmb;       // bytes of a layer slice and of the lm_head slice
@@ -379,10 +384,14 @@ struct FusedLayout {
 // The layout for dims d; ok = false (with the reason in *why) when the
 // fused kernel does not serve them.
 FusedLayout fused_layout(const Dims& d, const char** why);
+// The same for two KV heads shared by groups of query heads (kind 1).
+FusedLayout fused_layout_gqa(const Dims& d, const char** why);
 // Copy the main arena's weights (host bf16, the Weights layout) into the
 // fused layout (host buffer of FUSED_NWG * cu_bytes bytes).
 void fused_pack(const Dims& d, const FusedLayout& f, const Weights& w, const bf16_t* host_main,
                 bf16_t* host_fused);
+void fused_pack_gqa(const Dims& d, const FusedLayout& f, const Weights& w, const bf16_t* host_main,
+                    bf16_t* host_fused);
 
 struct FusedArgs {
   const bf16_t* arena;  // fused weight copy
@@ -409,5 +418,7 @@ struct FusedArgs {
 uint32_t fused_epochs(const Dims& d, int n_steps);
 hipError_t launch_fused_decode(hipStream_t s, const Dims& d, const FusedLayout& f,
                                const FusedArgs& a);
+hipError_t launch_fused_gqa(hipStream_t s, const Dims& d, const FusedLayout& f,
+                            const FusedArgs& a);
 
 }  // namespace fgpt

@@ -48,153 +48,11 @@
 
 #include <algorithm>
 
-#include "fgpt_internal.h"
-#include "kern_common.h"
+#include "kern_fused.h"
 
 namespace fgpt {
 
 namespace {
-
-constexpr int FUSED_HD = 128;            // head dim this kernel is built for
-constexpr int FUSED_THREADS = 320;       // 4 compute waves + 1 loader wave
-constexpr long FUSED_MAX_SPIN = 1l << 20;  // polls before a hand-over is given up
-// copies of the lm_head argmax candidates, each read by 256 / FUSED_LMC
-// workgroups (the lm_head pseudo-layer: one copy read by all 256 5.4 us,
-// 8 copies 4.6, 16 4.9, 64 5.3: more copies cost more write-through stores)
-constexpr int FUSED_LMC = 8;
-
-__device__ __forceinline__ uint64_t slot_pack(float v, uint32_t ep) {
-  return ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v);
-}
-__device__ __forceinline__ uint64_t slot_load(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// hand-over to workgroups of other XCDs: write-through to memory
-__device__ __forceinline__ void slot_put_dev(uint64_t* p, float v, uint32_t ep) {
-  __hip_atomic_store(p, slot_pack(v, ep), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// hand-over within the XCD: a plain store into the shared L2
-__device__ __forceinline__ void slot_put_xcd(uint64_t* p, float v, uint32_t ep) {
-  __hip_atomic_store(p, slot_pack(v, ep), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// Wait until the n (<= NMAX) slots p[i * stride] carry epoch ep, then
-// return their values in out. All loads go out at once; only slots still
-// short of the epoch are read again. false: the bound was reached or the
-// error flag was raised elsewhere (the flag is then raised here too).
-template <int NMAX>
-__device__ bool slots_wait(const uint64_t* p, int64_t stride, int n, uint32_t ep, float* out,
-                           uint32_t* err) {
-  uint64_t v[NMAX];
-#pragma unroll
-  for (int i = 0; i < NMAX; ++i) v[i] = i < n ? slot_load(p + i * stride) : slot_pack(0.f, ep);
-  for (long spin = 0;; ++spin) {
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < NMAX; ++i) ok = ok && (uint32_t)(v[i] >> 32) == ep;
-    if (ok) break;
-    if (spin >= FUSED_MAX_SPIN ||
-        ((spin & 255) == 255 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-      __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return false;
-    }
-#pragma unroll
-    for (int i = 0; i < NMAX; ++i)
-      if (i < n && (uint32_t)(v[i] >> 32) != ep) v[i] = slot_load(p + i * stride);
-  }
-#pragma unroll
-  for (int i = 0; i < NMAX; ++i)
-    if (i < n) out[i] = __uint_as_float((uint32_t)v[i]);
-  return true;
-}
-
-// Gather n slots (lane-strided over the 256 compute threads) into dst.
-template <int NMAX>
-__device__ bool gather_slots(const uint64_t* p, int n, uint32_t ep, float* dst, int tid,
-                             uint32_t* err) {
-  float v[NMAX];
-  const int cnt = tid < n ? (n - tid + 255) / 256 : 0;
-  if (!slots_wait<NMAX>(p + tid, 256, cnt, ep, v, err)) return false;
-#pragma unroll
-  for (int i = 0; i < NMAX; ++i)
-    if (i < cnt) dst[tid + 256 * i] = v[i];
-  return true;
-}
-
-// The lane's part of the dot products of NR bf16 rows (LDS, at byte
-// offsets roff from w) with fp32 x (LDS) over K (a multiple of 128): the
-// lane takes elements [CE k, CE k + CE) for k = lane, lane+64, ... (CE = 4
-// when K is a multiple of 256, else 2, so every lane has the same count).
-// Every load of the lane's chunks is issued before any arithmetic.
-template <int NR, int K>
-__device__ __forceinline__ void dot_rows(const uint8_t* w, const int (&roff)[NR], const float* x,
-                                         int lane, float (&acc)[NR]) {
-  static_assert(K % 128 == 0, "K a multiple of 128");
-  constexpr int CE = K % 256 == 0 ? 4 : 2;
-  constexpr int IT = K / (64 * CE);
-  if constexpr (CE == 4) {
-    float4 xv[IT];
-    uint2 wv[IT][NR];
-#pragma unroll
-    for (int i = 0; i < IT; ++i) {
-      xv[i] = *(const float4*)(x + 4 * (lane + 64 * i));
-#pragma unroll
-      for (int r = 0; r < NR; ++r) wv[i][r] = *(const uint2*)(w + roff[r] + 8 * (lane + 64 * i));
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float t = 0.f;
-#pragma unroll
-      for (int i = 0; i < IT; ++i)
-        t += xv[i].x * __uint_as_float(wv[i][r].x << 16) +
-             xv[i].y * __uint_as_float(wv[i][r].x & 0xFFFF0000u) +
-             xv[i].z * __uint_as_float(wv[i][r].y << 16) +
-             xv[i].w * __uint_as_float(wv[i][r].y & 0xFFFF0000u);
-      acc[r] = t;
-    }
-  } else {
-    float2 xv[IT];
-    uint32_t wv[IT][NR];
-#pragma unroll
-    for (int i = 0; i < IT; ++i) {
-      xv[i] = *(const float2*)(x + 2 * (lane + 64 * i));
-#pragma unroll
-      for (int r = 0; r < NR; ++r) wv[i][r] = *(const uint32_t*)(w + roff[r] + 4 * (lane + 64 * i));
-    }
-#pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      float t = 0.f;
-#pragma unroll
-      for (int i = 0; i < IT; ++i)
-        t += xv[i].x * __uint_as_float(wv[i][r] << 16) +
-             xv[i].y * __uint_as_float(wv[i][r] & 0xFFFF0000u);
-      acc[r] = t;
-    }
-  }
-}
-
-// sum(x^2) over the wave, x (LDS) of K elements in dot_rows' lane split
-template <int K>
-__device__ __forceinline__ float sumsq(const float* x, int lane) {
-  constexpr int IT = K / 256;
-  float4 xv[IT];
-#pragma unroll
-  for (int i = 0; i < IT; ++i) xv[i] = *(const float4*)(x + 4 * (lane + 64 * i));
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < IT; ++i)
-    ss += xv[i].x * xv[i].x + xv[i].y * xv[i].y + xv[i].z * xv[i].z + xv[i].w * xv[i].w;
-  return wave_sum(ss);
-}
-
-__device__ __forceinline__ void amax_take(float& v, int& i, float v2, int i2) {
-  if (v2 > v || (v2 == v && i2 < i)) {
-    v = v2;
-    i = i2;
-  }
-}
-
-constexpr int64_t round1k(int64_t x) { return (x + 1023) / 1024 * 1024; }
 
 // The work split's sizes for one model shape (head_dim 128, d_ff = 4
 // d_model); fused_layout computes the same values at run time.
@@ -222,36 +80,6 @@ struct FusedShape {
 // 6 heads, vocab 8192) and a small one the tests run.
 typedef FusedShape<768, 6, 8192> ShapeD12;
 typedef FusedShape<256, 2, 1024> ShapeSmall;
-
-// Sums over the wave of RP (4 or 8) per-lane values at once: v[r] of every
-// lane lands in this wave's LDS scratch (RP x 64 floats), each group of
-// LPO = 64/RP lanes adds RP consecutive partials of one value, then a DPP
-// butterfly over the group (quad permutes, then the half-row and row
-// mirrors, which pair the same lanes as strides 4 and 8 once the smaller
-// groups are uniform). The sum of v[r] is left in lanes [r*LPO, (r+1)*LPO).
-template <int RP>
-__device__ __forceinline__ float multi_sum(const float (&v)[RP], float* scr, int lane) {
-  constexpr int LPO = 64 / RP;
-  static_assert(RP == 4 || RP == 8, "groups of 16 or 8 lanes");
-#pragma unroll
-  for (int r = 0; r < RP; ++r) scr[r * 64 + lane] = v[r];
-  const float* p = scr + (lane / LPO) * 64 + (lane % LPO) * RP;
-  const float4 a = *(const float4*)p;
-  float t = (a.x + a.y) + (a.z + a.w);
-  if (RP == 8) {
-    const float4 b = *(const float4*)(p + 4);
-    t += (b.x + b.y) + (b.z + b.w);
-  }
-  t += dpp_f<0xB1>(t);
-  t += dpp_f<0x4E>(t);
-  t += dpp_f<0x141>(t);
-  if (LPO == 16) t += dpp_f<0x140>(t);
-  return t;
-}
-
-__device__ __forceinline__ float lane_value(float v, int src) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), src));
-}
 
 template <class Sh, bool TRACE>
 __global__ __launch_bounds__(FUSED_THREADS) void k_fused_decode(FusedArgs a) {
@@ -765,9 +593,9 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
     f.ok = false;
     return f;
   };
+  if (d.KH != d.H) return fused_layout_gqa(d, why);
   if (d.hd != FUSED_HD) return no("head_dim is not 128");
   if (d.H > FUSED_NX) return no("more heads than XCDs");
-  if (d.KH != d.H) return no("grouped KV heads");
   if (d.D % FUSED_NC != 0 || d.D / FUSED_NC > 64) return no("d_model not a multiple of 32 up to 2048");
   if (d.dff % (FUSED_NWG * 2) != 0) return no("d_ff not a multiple of 512");
   if (d.V % FUSED_NWG != 0) return no("vocab not a multiple of 256");
@@ -813,6 +641,7 @@ FusedLayout fused_layout(const Dims& d, const char** why) {
 
 void fused_pack(const Dims& d, const FusedLayout& f, const Weights& w, const bf16_t* hm,
                 bf16_t* hf) {
+  if (f.kind == 1) return fused_pack_gqa(d, f, w, hm, hf);
   const int D = d.D, hd = d.hd, H = d.H, qd = d.qd(), kd = d.kvd();
   memset(hf, 0, (size_t)FUSED_NWG * f.cu_bytes);
   for (int b = 0; b < FUSED_NWG; ++b) {
@@ -866,6 +695,7 @@ static hipError_t launch_shape(hipStream_t s, const FusedLayout& f, const FusedA
 
 hipError_t launch_fused_decode(hipStream_t s, const Dims& d, const FusedLayout& f,
                                const FusedArgs& a) {
+  if (f.kind == 1) return launch_fused_gqa(s, d, f, a);
   if (d.D == ShapeD12::D && d.H == ShapeD12::H && d.V == ShapeD12::V)
     return launch_shape<ShapeD12>(s, f, a);
   if (d.D == ShapeSmall::D && d.H == ShapeSmall::H && d.V == ShapeSmall::V)

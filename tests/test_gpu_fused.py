@@ -20,6 +20,8 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 SMALL_MHA = Dims(n_layer=2, d_model=256, n_head=2, n_kv_head=2, head_dim=128, vocab=1024)
 SMALL_GQA = Dims(n_layer=2, d_model=128, n_head=2, n_kv_head=1, head_dim=64, vocab=512)
+# the grouped-KV persistent kernel's small build: 4 heads over 2 KV heads
+SMALL_GQA2 = Dims(n_layer=2, d_model=512, n_head=4, n_kv_head=2, head_dim=128, vocab=1024)
 
 
 def relerr(a, b):
@@ -210,5 +212,55 @@ def test_fused_not_for_unsupported_dims():
     kv.step_multi(prompt[:-1], want_logits=False)
     ids, _ = kv.decode_greedy(prompt[-1:], 20)
     assert np.array_equal(ids[:, 0], ref_ids)
+    kv.close()
+    m.close()
+
+
+def test_fused_gqa_small_vs_oracle():
+    """The grouped-KV persistent kernel (4 heads over 2 KV heads): one call
+    from position 6 to 305, so the group's positions first sit in the first
+    quarter's 32 workgroups only (the other three quarters' partials empty),
+    then in all 128 and on past 256 (two and three positions per
+    workgroup); against the oracle (ids identical, logits and the cache rows
+    the loop wrote within the bar), the per-kernel path (ids identical,
+    logits within 1e-5 x max|logit|), and a replay bit for bit."""
+    d = SMALL_GQA2
+    w, m, c, s = setup(d, 31, 320)
+    on, why = m.fused_decode()
+    print("grouped-KV persistent decode active:", on, why)
+    assert on, why
+    prompt = uniform_ids(13, 7, d.vocab)
+    n, maxT = 300, 320
+    ref_ids, ref_lg = O.greedy_decode(prompt, w, d, n, c, s, maxT=maxT)
+    kv = m.kv(1, maxT)
+    kv.step_multi(prompt[:-1], want_logits=False)
+    ids, lg = kv.decode_greedy(prompt[-1:], n, want_logits=True)   # positions 6..305
+    e = relerr(lg[:, 0], ref_lg)
+    first = int(np.argmax(ids[:, 0] != ref_ids)) if not np.array_equal(ids[:, 0], ref_ids) else -1
+    print("small gqa: ids equal", first < 0, "first mismatch", first, "relerr", e)
+    assert np.array_equal(ids[:, 0], ref_ids)
+    assert e < TOL
+    k, v = kv.read()
+    rk, rv = oracle_cache(prompt, w, d, n, c, s, maxT)
+    kd = d.n_kv_head * d.head_dim
+    P = len(prompt) + n - 1
+    k = k.reshape(d.n_layer, maxT, kd)[:, :P]
+    v = v.reshape(d.n_layer, maxT, kd)[:, :P]
+    rk = rk.reshape(d.n_layer, maxT, kd)[:, :P]
+    rv = rv.reshape(d.n_layer, maxT, kd)[:, :P]
+    print("cache rows relerr", relerr(k, rk), relerr(v, rv))
+    assert relerr(k, rk) < TOL and relerr(v, rv) < TOL
+    kv.len = 6
+    ids2, lg2 = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    assert np.array_equal(ids, ids2) and np.array_equal(lg, lg2)
+    m.set_fused_decode(False)
+    try:
+        kv.len = 6
+        ids_g, lg_g = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    finally:
+        m.set_fused_decode(True)
+    assert np.array_equal(ids, ids_g)
+    print("vs per-kernel path: logits relerr", relerr(lg, lg_g))
+    assert relerr(lg, lg_g) < 1e-5
     kv.close()
     m.close()
