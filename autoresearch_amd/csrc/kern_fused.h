@@ -18,6 +18,9 @@ constexpr long FUSED_MAX_SPIN = 1l << 20;  // polls before a hand-over is given 
 // workgroups (the lm_head pseudo-layer: one copy read by all 256 5.4 us,
 // 8 copies 4.6, 16 4.9, 64 5.3: more copies cost more write-through stores)
 constexpr int FUSED_LMC = 8;
+// sleeps (s_sleep units) before the first read and between reads of a
+// hand-over across XCDs in kern_fused_gqa.hip (see slots_wait)
+constexpr int XPRE = 16, XGAP = 4;
 
 __device__ __forceinline__ uint64_t slot_pack(float v, uint32_t ep) {
   return ((uint64_t)ep << 32) | (uint64_t)__float_as_uint(v);
@@ -38,9 +41,19 @@ __device__ __forceinline__ void slot_put_xcd(uint64_t* p, float v, uint32_t ep) 
 // return their values in out. All loads go out at once; only slots still
 // short of the epoch are read again. false: the bound was reached or the
 // error flag was raised elsewhere (the flag is then raised here too).
-template <int NMAX>
+// PRE, GAP: s_sleep units (64 clocks) before the first read and before each
+// read again. Where the weights stream from HBM (kern_fused_gqa.hip), slots
+// written through from other XCDs arrive later than a poll issued right
+// after the reader's own publish, and polls that go out early slow the
+// hand-over down (the depth-20 q/k/v hand-over: 3.0 us polling at once, 1.6
+// us after a sleep of 16); where everything stays in the Infinity Cache
+// (kern_fused.hip) polling at once is faster (the depth-12 loop with
+// XPRE/XGAP on its hand-overs across XCDs: 0.1206 against 0.1147 ms a token,
+// A/B on one box).
+template <int NMAX, int PRE = 0, int GAP = 0>
 __device__ bool slots_wait(const uint64_t* p, int64_t stride, int n, uint32_t ep, float* out,
                            uint32_t* err) {
+  if (PRE > 0) __builtin_amdgcn_s_sleep(PRE);
   uint64_t v[NMAX];
 #pragma unroll
   for (int i = 0; i < NMAX; ++i) v[i] = i < n ? slot_load(p + i * stride) : slot_pack(0.f, ep);
@@ -54,6 +67,7 @@ __device__ bool slots_wait(const uint64_t* p, int64_t stride, int n, uint32_t ep
       __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return false;
     }
+    if (GAP > 0) __builtin_amdgcn_s_sleep(GAP);
 #pragma unroll
     for (int i = 0; i < NMAX; ++i)
       if (i < n && (uint32_t)(v[i] >> 32) != ep) v[i] = slot_load(p + i * stride);
@@ -65,12 +79,12 @@ __device__ bool slots_wait(const uint64_t* p, int64_t stride, int n, uint32_t ep
 }
 
 // Gather n slots (lane-strided over the 256 compute threads) into dst.
-template <int NMAX>
+template <int NMAX, int PRE = 0, int GAP = 0>
 __device__ bool gather_slots(const uint64_t* p, int n, uint32_t ep, float* dst, int tid,
                              uint32_t* err) {
   float v[NMAX];
   const int cnt = tid < n ? (n - tid + 255) / 256 : 0;
-  if (!slots_wait<NMAX>(p + tid, 256, cnt, ep, v, err)) return false;
+  if (!slots_wait<NMAX, PRE, GAP>(p + tid, 256, cnt, ep, v, err)) return false;
 #pragma unroll
   for (int i = 0; i < NMAX; ++i)
     if (i < cnt) dst[tid + 256 * i] = v[i];

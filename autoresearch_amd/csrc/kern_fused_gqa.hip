@@ -378,7 +378,7 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
           }
         }
         mark(s, l, 1);
-        if (!gather_slots<((G + 2) * HD + 255) / 256>(QL + (int64_t)q * (G + 2) * HD, (G + 2) * HD, ep,
+        if (!gather_slots<((G + 2) * HD + 255) / 256, XPRE, XGAP>(QL + (int64_t)q * (G + 2) * HD, (G + 2) * HD, ep,
                                                        qkv_lds, tid, err))
           *stop = 1;
         mark(s, l, 19);
@@ -399,19 +399,22 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
 #pragma unroll
         for (int j = 0; j < G; ++j) qv[j] = *(const float2*)(qkv_lds + j * HD + 2 * lane);
         // position li = w + 4 i: cached rows from the c_proj2 region, the
-        // new position's k and v from the hand-over
+        // new position's k and v from the hand-over. Branch-free: every
+        // slot is read and weighed, those past pos masked (a read in bounds
+        // of the region: li < NPW), so the G x AB score reductions, each a
+        // dependent chain, interleave.
         float2 kr[AB], vr[AB];
+        bool ok[AB];
 #pragma unroll
         for (int i = 0; i < AB; ++i) {
           const int li = wv + 4 * i, pp = gi + 128 * li;
+          ok[i] = pp <= pos;
           const float* r = pp == pos ? qkv_lds + GQ
                                      : (const float*)(lds + Sh::OFF_2 + 1024 * li);
-          kr[i] = make_float2(0.f, 0.f);
-          vr[i] = make_float2(0.f, 0.f);
-          if (pp <= pos) {
-            kr[i] = *(const float2*)(r + 2 * lane);
-            vr[i] = *(const float2*)(r + (pp == pos ? HD : 128) + 2 * lane);
-          }
+          const float2 kk = *(const float2*)(r + 2 * lane);
+          const float2 vv = *(const float2*)(r + HD + 2 * lane);
+          kr[i] = ok[i] ? kk : make_float2(0.f, 0.f);
+          vr[i] = ok[i] ? vv : make_float2(0.f, 0.f);
         }
         // one head at a time (its AB scores live, not G x AB)
 #pragma unroll
@@ -420,20 +423,17 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
           float m = -FLT_MAX;  // (no position: max -FLT_MAX, sum 0, O 0)
 #pragma unroll
           for (int i = 0; i < AB; ++i) {
-            sc[i] = gi + 128 * (wv + 4 * i) <= pos
-                        ? wave_sum(qv[j].x * kr[i].x + qv[j].y * kr[i].y) * scale
-                        : -INFINITY;
+            const float t = wave_sum(qv[j].x * kr[i].x + qv[j].y * kr[i].y) * scale;
+            sc[i] = ok[i] ? t : -INFINITY;
             m = fmaxf(m, sc[i]);
           }
           float ls = 0.f, ox = 0.f, oy = 0.f;
 #pragma unroll
           for (int i = 0; i < AB; ++i) {
-            if (gi + 128 * (wv + 4 * i) <= pos) {
-              const float e = __expf(sc[i] - m);
-              ls += e;
-              ox += e * vr[i].x;
-              oy += e * vr[i].y;
-            }
+            const float e = ok[i] ? __expf(sc[i] - m) : 0.f;
+            ls += e;
+            ox += e * vr[i].x;
+            oy += e * vr[i].y;
           }
           float* rj = rec + (wv * G + j) * REC;
           *(float2*)(rj + 2 * lane) = make_float2(ox, oy);
@@ -522,7 +522,7 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
         }
         mark(s, l, 6);
         // the group's 4 quarter results
-        if (!gather_slots<(4 * APS + 255) / 256>(XP + (int64_t)q * 4 * APS, 4 * APS, ep + 2, gg,
+        if (!gather_slots<(4 * APS + 255) / 256, XPRE, XGAP>(XP + (int64_t)q * 4 * APS, 4 * APS, ep + 2, gg,
                                                   tid, err))
           *stop = 1;
       }
@@ -572,7 +572,7 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
       // residual += the two groups' c_proj partials (groups in order)
       if (wv == 0 && lane < C) {
         float pv[2];
-        if (!slots_wait<2>(PP + c * C + lane, D, KH, ep + 3, pv, err)) *stop = 1;
+        if (!slots_wait<2, XPRE, XGAP>(PP + c * C + lane, D, KH, ep + 3, pv, err)) *stop = 1;
         const float t = pv[0] + pv[1];
         x_own = x_own + t;
         slot_put_xcd(XL + c * C + lane, x_own, ep + 4);
@@ -601,17 +601,23 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
       // takes rows w, w+4, ... (four at a time)
       if (comp) {
         const float inv = 1.0f / sqrtf(sumsq<D>(x_lds, lane) / (float)D + eps);
-        for (int r0 = wv; r0 < FR; r0 += 16) {
-          float acc[4];
-          int ro[4];
+        // wave w takes rows w, w + 4, ..., FR / 4 of them in one pass
+        constexpr int NRF = FR / 4;
+        static_assert(FR % 4 == 0 && NRF <= 8, "fc rows per wave");
+        float acc[8];
+        int ro[NRF];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) ro[i] = min(r0 + 4 * i, FR - 1) * D * 2;  // (rows past FR: ignored)
-          dot_rows<4, D>(lds + Sh::OFF_F, ro, x_lds, lane, acc);
-          float t = multi_sum<4>(acc, scr, lane) * inv;
-          t = t < 0.f ? 0.f : t;
-          const int r = r0 + 4 * (lane >> 4);
-          if ((lane & 15) == 0 && r < FR) slot_put_xcd(HL + c * FR + r, t * t, ep + 5);
+        for (int i = 0; i < NRF; ++i) ro[i] = (wv + 4 * i) * D * 2;
+        {
+          float t[NRF];
+          dot_rows<NRF, D>(lds + Sh::OFF_F, ro, x_lds, lane, t);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = i < NRF ? t[i] : 0.f;
         }
+        float t = multi_sum<8>(acc, scr, lane) * inv;
+        t = t < 0.f ? 0.f : t;
+        const int r = wv + 4 * (lane >> 3);
+        if ((lane & 7) == 0 && (lane >> 3) < NRF) slot_put_xcd(HL + c * FR + r, t * t, ep + 5);
         mark(s, l, 12);
         if (!gather_slots<(HN + 255) / 256>(HL, HN, ep + 5, hy, tid, err)) *stop = 1;
       }
@@ -634,22 +640,32 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
       // c_proj2 partial over this XCD's fc block: wave w takes outputs w,
       // w+4, ... (eight at a time)
       if (comp) {
-        for (int j0 = wv; j0 < C; j0 += 32) {
-          float v[8];
-          int ro[8];
+        // wave w takes outputs w, w + 4, ..., C / 4 of them, their dot
+        // products in one pass, summed eight at a time
+        constexpr int NOC = C / 4;
+        static_assert(C % 4 == 0 && NOC <= 16, "c_proj2 outputs per wave");
+        float v[NOC];
+        {
+          int ro[NOC];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) ro[i] = min(j0 + 4 * i, C - 1) * HN * 2;  // (outputs past C: ignored)
-          dot_rows<8, HN>(lds + Sh::OFF_2, ro, hy, lane, v);
-          const float t = multi_sum<8>(v, scr, lane);
-          const int j = j0 + 4 * (lane >> 3);
-          if ((lane & 7) == 0 && j < C) slot_put_dev(P2 + (int64_t)g * D + c * C + j, t, ep + 6);
+          for (int i = 0; i < NOC; ++i) ro[i] = (wv + 4 * i) * HN * 2;
+          dot_rows<NOC, HN>(lds + Sh::OFF_2, ro, hy, lane, v);
+        }
+#pragma unroll
+        for (int i0 = 0; i0 < NOC; i0 += 8) {
+          float u[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) u[i] = i0 + i < NOC ? v[i0 + i] : 0.f;
+          const float t = multi_sum<8>(u, scr, lane);
+          const int i = i0 + (lane >> 3), j = wv + 4 * i;
+          if ((lane & 7) == 0 && i < NOC) slot_put_dev(P2 + (int64_t)g * D + c * C + j, t, ep + 6);
         }
         mark(s, l, 16);
       }
       // residual += the 8 blocks' c_proj2 partials (blocks in order)
       if (wv == 0 && lane < C) {
         float pv[8];
-        if (!slots_wait<8>(P2 + c * C + lane, D, FUSED_NX, ep + 6, pv, err)) *stop = 1;
+        if (!slots_wait<8, XPRE, XGAP>(P2 + c * C + lane, D, FUSED_NX, ep + 6, pv, err)) *stop = 1;
         float t = pv[0];
 #pragma unroll
         for (int kk = 1; kk < FUSED_NX; ++kk) t += pv[kk];
@@ -722,8 +738,8 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
         float cv[8];
         float bv = -INFINITY;
         int bi = 0x7fffffff;
-        if (slots_wait<8>(LMC + (int64_t)(b % FUSED_LMC) * 2 * FUSED_NWG + lane, 64, 8, ep, cv,
-                          err)) {
+        if (slots_wait<8, XPRE, XGAP>(LMC + (int64_t)(b % FUSED_LMC) * 2 * FUSED_NWG + lane, 64, 8,
+                                      ep, cv, err)) {
 #pragma unroll
           for (int kk = 0; kk < 4; ++kk) amax_take(bv, bi, cv[kk], __float_as_int(cv[4 + kk]));
         } else {
