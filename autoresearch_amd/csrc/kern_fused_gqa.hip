@@ -145,6 +145,28 @@ __device__ __forceinline__ void dma16_nt(const void* g, uint32_t lds) {
                : "memory", "m0");
 }
 
+// Sum (maximum) over the four 16-lane rows of the wave: every lane gets
+// the sum of lanes l, l^16, l^32, l^48, by gfx950's lane-half and row swaps
+// (v_permlane32_swap: lanes 32-63 of the first operand with lanes 0-31 of
+// the second; v_permlane16_swap: odd rows of the first with even rows of
+// the second), in the order (r0 + r2) + (r1 + r3).
+__device__ __forceinline__ float rows4_sum(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float t = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t w = __float_as_uint(t);
+  const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ float rows4_max(float v) {
+  const uint32_t u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float t = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t w = __float_as_uint(t);
+  const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -391,52 +413,72 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
       if (*stop) goto done;
       if (ldA) piece(l, 2, 2, NFP);
       if (comp) {
-        // the wave's scores for the G heads, one softmax over its positions
-        // (the new position's k and v from the hand-over); the lane holds
-        // head dims 2 lane, 2 lane + 1
+        // the wave's scores for the G heads, one softmax over its slots.
+        // 16 lanes a cached row (8 head dims each), 4 rows a wave: slot
+        // (h, r) of wave w is position li = w + 4 (4 h + r), cached rows
+        // from the c_proj2 region, the new position's k and v from the
+        // hand-over. A score is a sum over the row's 16 lanes (DPP, no
+        // lane reads); the rows' maxima, weight sums and weighted V sums
+        // meet by lane swaps (rows4_max, rows4_sum).
+        // Branch-free: every slot is read (in bounds: li clamped below NPW)
+        // and weighed, those past pos masked.
+        constexpr int NH = (AB + 3) / 4;
         const float scale = 1.0f / sqrtf((float)HD);
-        float2 qv[G];
+        const int r = lane >> 4, d0 = 8 * (lane & 15);
+        float k8[NH][8], v8[NH][8];
+        bool ok[NH];
 #pragma unroll
-        for (int j = 0; j < G; ++j) qv[j] = *(const float2*)(qkv_lds + j * HD + 2 * lane);
-        // position li = w + 4 i: cached rows from the c_proj2 region, the
-        // new position's k and v from the hand-over. Branch-free: every
-        // slot is read and weighed, those past pos masked (a read in bounds
-        // of the region: li < NPW), so the G x AB score reductions, each a
-        // dependent chain, interleave.
-        float2 kr[AB], vr[AB];
-        bool ok[AB];
+        for (int h = 0; h < NH; ++h) {
+          const int li = wv + 4 * (4 * h + r), pp = gi + 128 * li;
+          ok[h] = pp <= pos;
+          const float* rp = pp == pos ? qkv_lds + GQ
+                                      : (const float*)(lds + Sh::OFF_2 + 1024 * min(li, Sh::NPW - 1));
+          const float4 ka = *(const float4*)(rp + d0), kb = *(const float4*)(rp + d0 + 4);
+          const float4 va = *(const float4*)(rp + HD + d0), vb = *(const float4*)(rp + HD + d0 + 4);
+          const float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+          const float vv[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
-        for (int i = 0; i < AB; ++i) {
-          const int li = wv + 4 * i, pp = gi + 128 * li;
-          ok[i] = pp <= pos;
-          const float* r = pp == pos ? qkv_lds + GQ
-                                     : (const float*)(lds + Sh::OFF_2 + 1024 * li);
-          const float2 kk = *(const float2*)(r + 2 * lane);
-          const float2 vv = *(const float2*)(r + HD + 2 * lane);
-          kr[i] = ok[i] ? kk : make_float2(0.f, 0.f);
-          vr[i] = ok[i] ? vv : make_float2(0.f, 0.f);
+          for (int e = 0; e < 8; ++e) {
+            k8[h][e] = ok[h] ? kk[e] : 0.f;
+            v8[h][e] = ok[h] ? vv[e] : 0.f;
+          }
         }
-        // one head at a time (its AB scores live, not G x AB)
 #pragma unroll
         for (int j = 0; j < G; ++j) {
-          float sc[AB];
+          const float4 qa = *(const float4*)(qkv_lds + j * HD + d0);
+          const float4 qb = *(const float4*)(qkv_lds + j * HD + d0 + 4);
+          const float q8[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+          float sc[NH];
           float m = -FLT_MAX;  // (no position: max -FLT_MAX, sum 0, O 0)
 #pragma unroll
-          for (int i = 0; i < AB; ++i) {
-            const float t = wave_sum(qv[j].x * kr[i].x + qv[j].y * kr[i].y) * scale;
-            sc[i] = ok[i] ? t : -INFINITY;
-            m = fmaxf(m, sc[i]);
-          }
-          float ls = 0.f, ox = 0.f, oy = 0.f;
+          for (int h = 0; h < NH; ++h) {
+            float t = q8[0] * k8[h][0];
 #pragma unroll
-          for (int i = 0; i < AB; ++i) {
-            const float e = ok[i] ? __expf(sc[i] - m) : 0.f;
-            ls += e;
-            ox += e * vr[i].x;
-            oy += e * vr[i].y;
+            for (int e = 1; e < 8; ++e) t += q8[e] * k8[h][e];
+            t += dpp_f<0xB1>(t);   // the row's 16 lanes: quad permutes, then
+            t += dpp_f<0x4E>(t);   // the half-row and row mirrors
+            t += dpp_f<0x141>(t);
+            t += dpp_f<0x140>(t);
+            sc[h] = ok[h] ? t * scale : -INFINITY;
+            m = fmaxf(m, sc[h]);
           }
+          m = rows4_max(m);
+          float ls = 0.f, o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int h = 0; h < NH; ++h) {
+            const float e = ok[h] ? __expf(sc[h] - m) : 0.f;
+            ls += e;
+#pragma unroll
+            for (int x = 0; x < 8; ++x) o[x] += e * v8[h][x];
+          }
+          ls = rows4_sum(ls);
+#pragma unroll
+          for (int x = 0; x < 8; ++x) o[x] = rows4_sum(o[x]);
           float* rj = rec + (wv * G + j) * REC;
-          *(float2*)(rj + 2 * lane) = make_float2(ox, oy);
+          if (lane < 16) {
+            *(float4*)(rj + d0) = make_float4(o[0], o[1], o[2], o[3]);
+            *(float4*)(rj + d0 + 4) = make_float4(o[4], o[5], o[6], o[7]);
+          }
           if (lane == 0) {
             rj[HD] = m;
             rj[HD + 1] = ls;
