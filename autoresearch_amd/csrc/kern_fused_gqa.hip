@@ -540,20 +540,36 @@ __global__ __launch_bounds__(GQA_THREADS) void k_fused_gqa(FusedArgs a) {
 
       if (comp) {
         // the XCD's result for outputs [c OPW, (c+1) OPW) of the group's
-        // query dims, and (max, sum) of the heads whose first dim is here
-        if (tid < OPW + G) {
-          const int o = c * OPW + (tid < OPW ? tid : 0);
-          const int j = tid < OPW ? o / HD : tid - OPW;
-          if (tid < OPW || c == j * HD / OPW) {
-            float mx = xg[OPW + 2 * j];
-            for (int w = 1; w < 32; ++w) mx = fmaxf(mx, xg[w * XW + OPW + 2 * j]);
-            float t = 0.f;
-            const int e = tid < OPW ? tid : OPW + 2 * j + 1;
-            for (int w = 0; w < 32; ++w) t += __expf(xg[w * XW + OPW + 2 * j] - mx) * xg[w * XW + e];
+        // query dims, and (max, sum) of the heads whose first dim is here:
+        // item it on 8 lanes, each over partials k, k + 8, k + 16, k + 24,
+        // the 8 lanes met by DPP (quad permutes, then the half-row mirror)
+        const int it = tid >> 3, k8 = tid & 7;
+        static_assert(OPW + G <= 32, "XCD-merge items on 8 lanes each");
+        if (it < OPW + G) {
+          const int o = c * OPW + (it < OPW ? it : 0);
+          const int j = it < OPW ? o / HD : it - OPW;
+          if (it < OPW || c == j * HD / OPW) {
+            const int e = it < OPW ? it : OPW + 2 * j + 1;
+            float mw[4], vw[4];
 #pragma unroll
-            for (int x = 0; x < GQA_COPIES; ++x) {
-              uint64_t* xp = XP + (int64_t)(x * 4 + q) * APS;
-              if (tid < OPW) {
+            for (int i = 0; i < 4; ++i) {
+              const float* xw = xg + (k8 + 8 * i) * XW;
+              mw[i] = xw[OPW + 2 * j];
+              vw[i] = xw[e];
+            }
+            float mx = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+            mx = fmaxf(mx, dpp_f<0xB1>(mx));
+            mx = fmaxf(mx, dpp_f<0x4E>(mx));
+            mx = fmaxf(mx, dpp_f<0x141>(mx));
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) t += __expf(mw[i] - mx) * vw[i];
+            t += dpp_f<0xB1>(t);
+            t += dpp_f<0x4E>(t);
+            t += dpp_f<0x141>(t);
+            if (k8 < GQA_COPIES) {  // lane x of the item writes copy x
+              uint64_t* xp = XP + (int64_t)(k8 * 4 + q) * APS;
+              if (it < OPW) {
                 slot_put_dev(xp + o, t, ep + 2);
               } else {
                 slot_put_dev(xp + GQ + 2 * j, mx, ep + 2);
