@@ -264,3 +264,33 @@ def test_fused_gqa_small_vs_oracle():
     assert relerr(lg, lg_g) < 1e-5
     kv.close()
     m.close()
+
+
+def test_fused_gqa_small_long_context():
+    """The grouped-KV persistent kernel past 512 positions (a 600-id prompt
+    cached by one chunked pass, then 80 steps at positions 599..678): a
+    workgroup then holds up to six of the group's positions, so its waves
+    weigh slots on more than one 16-lane row; against the oracle and the
+    per-kernel path."""
+    d = SMALL_GQA2
+    P, n, maxT = 600, 80, 700
+    w, m, c, s = setup(d, 37, maxT)
+    prompt = uniform_ids(19, P, d.vocab)
+    ref_ids, ref_lg = O.greedy_decode(prompt, w, d, n, c, s, maxT=maxT, prefill_multi=True)
+    kv = m.kv(1, maxT)
+    kv.step_multi(prompt[:-1], want_logits=False)
+    ids, lg = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    e = relerr(lg[:, 0], ref_lg)
+    print("small gqa at 599..678: ids equal", np.array_equal(ids[:, 0], ref_ids), "relerr", e)
+    assert np.array_equal(ids[:, 0], ref_ids)
+    assert e < TOL
+    m.set_fused_decode(False)
+    try:
+        kv.len = P - 1
+        ids_g, lg_g = kv.decode_greedy(prompt[-1:], n, want_logits=True)
+    finally:
+        m.set_fused_decode(True)
+    assert np.array_equal(ids, ids_g)
+    assert relerr(lg, lg_g) < 1e-5
+    kv.close()
+    m.close()
