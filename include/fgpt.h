@@ -282,16 +282,19 @@ int32_t fg_decode_sample(fg_model *m, fg_kv *kv, int32_t *ids, int32_t n_known, 
 /* Handle options (no counterpart in the reference, which has one CPU path).
  *
  * FG_OPT_FUSED_DECODE: 1 (the default) lets fg_decode_greedy run a B=1 loop
- * on an fp32 cache whose positions stay below 2048 as ONE persistent launch
- * (all layers, lm_head and the argmax of every step; the weights stream
- * through LDS one layer ahead, activations pass between workgroups through
- * epoch-tagged slots; from 128 positions on a head's attention is split
- * over 18 workgroups), for the model shapes the library compiles it for
- * (head_dim 128, d_ff = 4 d_model: d_model 768 with 6 heads and vocab 8192,
- * d_model 256 with 2 heads and vocab 1024) on a device of 256 CUs in 8 XCDs
- * that allows cooperative launches; 0 keeps the captured per-kernel steps.
- * Both paths compute the same functions of the same inputs; their fp32
- * sums run in different orders.
+ * on an fp32 cache as ONE persistent launch (all layers, lm_head and the
+ * argmax of every step; the weights stream through LDS ahead of their use,
+ * activations pass between workgroups through epoch-tagged slots), for the
+ * model shapes the library compiles it for (head_dim 128, d_ff = 4
+ * d_model), on a device of 256 CUs in 8 XCDs that allows cooperative
+ * launches: one KV head per query head with d_model 768, 6 heads and vocab
+ * 8192, or d_model 256, 2 heads and vocab 1024, positions below 2048 (from
+ * 128 positions on a head's attention is split over 18 workgroups); two KV
+ * heads shared by the query heads with d_model 1280, 10 heads and vocab
+ * 8192 (positions below 4096) or d_model 512, 4 heads and vocab 1024
+ * (below 1024). 0 keeps the captured per-kernel steps. Both paths compute
+ * the same functions of the same inputs; their fp32 sums run in different
+ * orders.
  *
  * FG_OPT_FORWARD_F16: 1 runs fg_forward / fg_forward_dev / fg_eval_bpb
  * passes of more than 128 token rows as single-term fp16 MFMA work: one
