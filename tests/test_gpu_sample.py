@@ -147,17 +147,20 @@ def test_decode_sample_loop(m):
 
 
 SMALL_MHA = Dims(n_layer=2, d_model=256, n_head=2, n_kv_head=2, head_dim=128, vocab=1024)
+# the grouped-KV persistent kernel's small build: 4 heads over 2 KV heads
+SMALL_GQA2 = Dims(n_layer=2, d_model=512, n_head=4, n_kv_head=2, head_dim=128, vocab=1024)
 
 
-def test_decode_sample_loop_persistent():
-    """On a shape the persistent B=1 kernel serves, each sampled step's
-    forward is one persistent launch (the timing records one per id) and
-    the draw a kernel of its own. temp 0 gives decode_greedy's stream bit
-    for bit (the same kernel); with penalties, the stream against stepping
-    the engine one position at a time with the oracle choosing ids (the
-    per-step logits come from the single-row kernels there, ~1e-6 apart),
-    up to a near-boundary draw."""
-    d = SMALL_MHA
+@pytest.mark.parametrize("d", [SMALL_MHA, SMALL_GQA2], ids=["mha", "gqa"])
+def test_decode_sample_loop_persistent(d):
+    """On a shape a persistent B=1 kernel serves (one KV head per query
+    head, or two shared KV heads), each sampled step's forward is one
+    persistent launch (the timing records one per id) and the draw a kernel
+    of its own. temp 0 gives decode_greedy's stream bit for bit (the same
+    kernel); with penalties, the stream against stepping the engine one
+    position at a time with the oracle choosing ids (the per-step logits
+    come from the single-row kernels there, ~1e-6 apart), up to a
+    near-boundary draw."""
     m = engine.Model(d, stacks=seeded_weights(d, 7))
     assert m.fused_decode()[0], m.fused_decode()[1]
     prompt = uniform_ids(18, 12, d.vocab)
