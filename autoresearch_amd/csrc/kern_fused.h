@@ -22,7 +22,8 @@ constexpr int FUSED_LMC = 8;
 // hand-over across XCDs in kern_fused_gqa.hip (see slots_wait); depth-20
 // GQA decode at 2047-2302 positions, ms a token: XPRE 8 0.382, 16 0.349,
 // 24 0.390 (XGAP 4); XGAP 0 0.3477, 1 0.3475, 2 0.3484, 4 0.3502, 10 0.3585
-// (XPRE 16, means of runs on one box)
+// (XPRE 16, means of runs on one box); at XGAP 1, XPRE 12 0.357, 16 0.346,
+// 20 0.356
 constexpr int XPRE = 16, XGAP = 1;
 
 __device__ __forceinline__ uint64_t slot_pack(float v, uint32_t ep) {
